@@ -1,0 +1,226 @@
+#!/usr/bin/env python3
+"""Benchmark: cascade verify attention at Qwen3-8B shape on one MI355X.
+
+Workload (one "step" = one verify step of the target model): all 36 layers of
+cascade verify attention, Qwen3-8B shape (32 query / 8 kv heads, head_dim 128,
+bf16), prefix 4096 tokens paged at 16 with a random page permutation, and the
+D2SD candidate tree of generation/d3_generator.py:116-180 (DFlash block 16 +
+top-4 DTA branches of block 32; N unique nodes).  Each layer has its own KV
+pool (604 MB in total, beyond the 256 MB Infinity Cache).  The 36 layer calls
+(attention + merge launch each) are captured in one hipGraph and replayed.
+
+Prints ONE JSON line.  value = microseconds per layer-call (lower is better).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "d2-sd_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "cascade-verify attn µs/layer + HBM GB/s (% roofline), Qwen3-8B shape, 1 GPU"
+HBM_PEAK_GBPS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def time_graph(graph, reps: int, torch) -> float:
+    """Average milliseconds per replay of `graph` (HIP events on the stream the
+    replays are launched on)."""
+    s = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(s)
+    for _ in range(reps):
+        graph.replay(s)
+    e1.record(s)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def cpu_baseline(mp, reps: int, torch) -> dict:
+    """The oracle's fp32 torch-sdpa form of one layer on the host cores."""
+    from oracle import cascade_oracle as orc
+    prob = mp.problem
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    threads = max(1, min(threads, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    lt = mp.layers[0]
+    req = prob.requests[0]
+    L = req.prefix_len
+    pages = mp.page_table[mp.page_indptr[0]:mp.page_indptr[1]].cpu().tolist()
+    kp = orc.gather_paged(lt.k_prefix.cpu(), pages, L).float()
+    vp = orc.gather_paged(lt.v_prefix.cpu(), pages, L).float()
+    q, ks, vs = lt.q.cpu().float(), lt.k_suffix.cpu().float(), lt.v_suffix.cpu().float()
+    m = torch.as_tensor(req.tree.ancestor_mask())
+    sm = prob.head_dim ** -0.5
+
+    def once():
+        return orc.cascade_tree_ref(q, ks, vs, kp, vp, m, sm, prob.window_left, None, dtype=torch.float32,
+                                    use_sdpa=True)
+
+    for _ in range(3):
+        once()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        once()
+        times.append(time.perf_counter() - t0)
+    us = statistics.median(times) * 1e6
+    return {"value": us, "unit": "us/layer", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"layer 0 of 36 (N={prob.total_q} queries, prefix {L} + tree), fp32 torch "
+                      f"scaled_dot_product_attention + logsumexp on the host, median of {reps} after 3 warm-ups",
+            "queries_per_s": prob.total_q / (us * 1e-6), "cpu_model": cpu_model()}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200, help="timed graph replays (verify steps)")
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--layers", type=int, default=36)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--cpu-reps", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernel-reps", type=int, default=50)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: every path here runs on a single MI355X "
+              "(multi-GPU sharding is a design note, not a measured configuration).", file=sys.stderr)
+        return 2
+
+    import torch
+    import d2sd
+    from d2sd import workloads as wl
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    prob = wl.config2(args.seed, layers=args.layers)
+    log(f"materialising {prob.name}: N={prob.total_q} nodes, {args.layers} layers")
+    mp = wl.materialize(prob, dev)
+    attn = d2sd.CascadeVerifyAttention(dev)
+    wl.plan_for(attn, mp)
+    info = attn.info
+    T, hq, d = prob.total_q, prob.num_qo_heads, prob.head_dim
+    outs = [(torch.empty(T, hq, d, dtype=torch.bfloat16, device=dev),
+             torch.empty(T, hq, dtype=torch.float32, device=dev)) for _ in mp.layers]
+
+    def layer_call(i, fn):
+        lt = mp.layers[i]
+        o, l = outs[i]
+        fn(lt.q, lt.k_suffix, lt.v_suffix, lt.k_prefix, lt.v_prefix, out=o, lse=l)
+
+    for i in range(len(mp.layers)):  # eager warm-up
+        layer_call(i, attn.run)
+    torch.cuda.synchronize()
+    step = d2sd.HipGraph()
+    with step.capture():
+        for i in range(len(mp.layers)):
+            layer_call(i, attn.run)
+    g_attn = d2sd.HipGraph()
+    with g_attn.capture():
+        for i in range(len(mp.layers)):
+            layer_call(i, attn.run_attention)
+    g_merge = d2sd.HipGraph()
+    with g_merge.capture():
+        for i in range(len(mp.layers)):
+            layer_call(i, attn.run_merge)
+    log(f"plan: {info.num_work} attention workgroups ({info.waves_per_block} waves), {info.num_merge} merge "
+        f"items, {info.num_slots} partial slots, max splits {info.max_splits_used}")
+
+    for _ in range(args.warmup):
+        step.replay()
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(args.steps):
+        step.replay(s)
+    e1.record(s)
+    torch.cuda.synchronize()
+    ms_per_step = e0.elapsed_time(e1) / args.steps
+    us_layer = ms_per_step * 1000.0 / len(mp.layers)
+    log(f"timed {args.steps} steps: {ms_per_step:.4f} ms/step, {us_layer:.3f} us/layer")
+
+    # per-kernel averages (graphs of the 36 launches of one kernel)
+    attn_us = time_graph(g_attn, args.kernel_reps, torch) * 1000.0 / len(mp.layers)
+    merge_us = time_graph(g_merge, args.kernel_reps, torch) * 1000.0 / len(mp.layers)
+    log(f"attention kernel {attn_us:.3f} us/launch, merge kernel {merge_us:.3f} us/launch")
+
+    vb, vf = wl.verify_bytes_flops(prob)
+    pb, pf = wl.prefix_bytes_flops(prob)
+    t_hbm, t_mfma = vb / (HBM_PEAK_GBPS * 1e9), vf / (MFMA_BF16_PEAK_TFLOPS * 1e12)
+    bound = "mfma" if t_mfma > t_hbm else "hbm"
+    if bound == "mfma":
+        achieved = vf / (attn_us * 1e-6) / 1e12
+        roof = {"bound": "mfma", "achieved": achieved, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": achieved / MFMA_BF16_PEAK_TFLOPS}
+    else:
+        achieved = vb / (attn_us * 1e-6) / 1e9
+        roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": achieved / HBM_PEAK_GBPS}
+    roof["traffic"] = None
+    roof["kernel"] = "d2sd::attn_kernel<128, %d, false>" % info.waves_per_block
+    roof["kernel_us"] = attn_us
+    roof["algorithmic_bytes"] = vb
+    roof["algorithmic_flops"] = vf
+    roof["hbm_frac_of_kernel"] = vb / (attn_us * 1e-6) / 1e9 / HBM_PEAK_GBPS
+
+    layer_gbps = vb / (us_layer * 1e-6) / 1e9
+    result = {
+        "metric": METRIC,
+        "value": us_layer,
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: Q/K/V ~ N(0,1) rounded to bf16, seeded; tree from seeded DFlash confidences",
+        "config": {"workload": prob.name, "layers": len(mp.layers), "prefix_len": 4096, "page_size": 16,
+                   "tree_nodes": T, "tree_rows": 5, "row_len": 32, "num_qo_heads": hq, "num_kv_heads": 8,
+                   "head_dim": d, "replay": "hipGraph of 36 x (attention + merge launch)"},
+        "queries_per_s": T / (us_layer * 1e-6),
+        "hbm_gbps": layer_gbps,
+        "hbm_frac": layer_gbps / HBM_PEAK_GBPS,
+        "mfma_frac": vf / (us_layer * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+        "roofline_floor_us": max(t_hbm, t_mfma) * 1e6,
+        "prefix_level": {"bytes": pb, "flops": pf},
+        "kernels_us": {"attention": attn_us, "merge": merge_us},
+        "roofline": roof,
+    }
+    if not args.no_cpu_baseline:
+        log("timing the CPU baseline (oracle, fp32 torch sdpa)")
+        result["cpu_baseline"] = cpu_baseline(mp, args.cpu_reps, torch)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

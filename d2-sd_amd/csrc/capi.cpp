@@ -1,0 +1,421 @@
+// extern "C" entry points of libd2sd.so (declared in include/d2sd.h).
+// Argument validation, work planning and kernel launches; no device memory is
+// allocated here except the executable of a captured graph.
+#include <hip/hip_runtime_api.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/d2sd.h"
+#include "d2sd_internal.h"
+#include "plan.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int fail_hip(hipError_t e, const char* what) {
+  g_last_error = std::string(what) + ": " + hipGetErrorString(e);
+  return D2SD_ERR_HIP;
+}
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+int device_num_cus() {
+  static std::mutex mu;
+  static std::vector<int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  std::lock_guard<std::mutex> lk(mu);
+  if ((int)cache.size() <= dev) cache.resize(dev + 1, 0);
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+      (void)hipGetLastError();
+      n = 256;
+    }
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+bool stride_ok(int64_t s) { return s % 8 == 0; }
+
+int check_heads(int hq, int hkv, int d) {
+  if (hq <= 0 || hkv <= 0 || hq % hkv != 0)
+    return fail(D2SD_ERR_INVALID_ARG, "num_qo_heads must be a positive multiple of num_kv_heads");
+  if (d != 64 && d != 128) return fail(D2SD_ERR_UNSUPPORTED, "head_dim must be 64 or 128");
+  return D2SD_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* d2sd_last_error(void) { return g_last_error.c_str(); }
+
+const char* d2sd_version(void) { return "d2sd-mi355x 0.1.0 (gfx950)"; }
+
+int d2sd_merge_state_in_place(void* v, int64_t v_stride_n, int64_t v_stride_h, float* s, int64_t s_stride_n,
+                              const void* v_other, int64_t vo_stride_n, int64_t vo_stride_h,
+                              const float* s_other, int64_t so_stride_n, int seq_len, int num_heads,
+                              int head_dim, int lse_base2, d2sd_stream_t stream) {
+  g_last_error.clear();
+  if (seq_len < 0 || num_heads <= 0 || head_dim <= 0 || head_dim % 8 != 0)
+    return fail(D2SD_ERR_INVALID_ARG, "merge_state: bad sizes");
+  if (seq_len == 0) return D2SD_OK;
+  if (!v || !s || !v_other || !s_other) return fail(D2SD_ERR_INVALID_ARG, "merge_state: null pointer");
+  if (!aligned16(v) || !aligned16(v_other) || !stride_ok(v_stride_n) || !stride_ok(v_stride_h) ||
+      !stride_ok(vo_stride_n) || !stride_ok(vo_stride_h))
+    return fail(D2SD_ERR_INVALID_ARG, "merge_state: v / v_other must be 16-byte aligned with strides % 8 == 0");
+  hipError_t e = d2sd::launch_merge_state(v, v_stride_n, v_stride_h, s, s_stride_n, v_other, vo_stride_n,
+                                          vo_stride_h, s_other, so_stride_n, seq_len, num_heads, head_dim,
+                                          lse_base2, (hipStream_t)stream);
+  return e == hipSuccess ? D2SD_OK : fail_hip(e, "merge_state launch");
+}
+
+size_t d2sd_single_prefill_workspace_size(int qo_len, int kv_len, int num_qo_heads, int num_kv_heads,
+                                          int head_dim, int window_left) {
+  if (qo_len <= 0 || kv_len <= 0 || num_kv_heads <= 0 || num_qo_heads % num_kv_heads) return 0;
+  d2sd::ImplicitWork imp{};
+  int waves = 0;
+  size_t ws = 0;
+  d2sd::plan_single(qo_len, kv_len, num_qo_heads, num_kv_heads, head_dim, window_left, device_num_cus(), imp,
+                    waves, ws);
+  return ws;
+}
+
+int d2sd_single_prefill_with_kv_cache(const void* q, int64_t q_stride_n, int64_t q_stride_h, const void* k,
+                                      const void* v, int64_t kv_stride_n, int64_t kv_stride_h, void* o,
+                                      int64_t o_stride_n, int64_t o_stride_h, float* lse, int qo_len, int kv_len,
+                                      int num_qo_heads, int num_kv_heads, int head_dim, int causal,
+                                      int window_left, float sm_scale, int lse_base2, void* workspace,
+                                      size_t workspace_bytes, d2sd_stream_t stream) {
+  g_last_error.clear();
+  if (int rc = check_heads(num_qo_heads, num_kv_heads, head_dim)) return rc;
+  if (qo_len < 0 || kv_len < 0) return fail(D2SD_ERR_INVALID_ARG, "single_prefill: negative length");
+  if (qo_len == 0) return D2SD_OK;
+  if (kv_len == 0) return fail(D2SD_ERR_INVALID_ARG, "single_prefill: kv_len must be > 0");
+  if (!q || !k || !v || !o) return fail(D2SD_ERR_INVALID_ARG, "single_prefill: null pointer");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !stride_ok(q_stride_n) ||
+      !stride_ok(q_stride_h) || !stride_ok(kv_stride_n) || !stride_ok(kv_stride_h) || !stride_ok(o_stride_n) ||
+      !stride_ok(o_stride_h))
+    return fail(D2SD_ERR_INVALID_ARG, "single_prefill: tensors must be 16-byte aligned with strides % 8 == 0");
+  if (!(sm_scale > 0.f) || !std::isfinite(sm_scale)) return fail(D2SD_ERR_INVALID_ARG, "single_prefill: bad sm_scale");
+
+  d2sd::AttnParams p{};
+  int waves = 0;
+  size_t ws = 0;
+  d2sd::plan_single(qo_len, kv_len, num_qo_heads, num_kv_heads, head_dim, window_left, device_num_cus(), p.imp,
+                    waves, ws);
+  if (ws > workspace_bytes || (ws > 0 && !workspace))
+    return fail(D2SD_ERR_WORKSPACE, "single_prefill: workspace too small (need " + std::to_string(ws) + " bytes)");
+  const int rows = 32 * waves;
+  const long long slots = (long long)num_kv_heads * p.imp.qtiles * p.imp.splits;
+  p.q = q;
+  p.q_stride_n = q_stride_n;
+  p.q_stride_h = q_stride_h;
+  p.o = o;
+  p.o_stride_n = o_stride_n;
+  p.o_stride_h = o_stride_h;
+  p.lse = lse;
+  p.lse_stride_n = num_qo_heads;
+  p.part_o = (float*)workspace;
+  p.part_lse = workspace ? (float*)workspace + slots * rows * head_dim : nullptr;
+  d2sd::KvSource& s0 = p.src[0];
+  s0.k = k;
+  s0.v = v;
+  s0.stride_tok = kv_stride_n;
+  s0.stride_head = kv_stride_h;
+  s0.mask_mode = causal ? d2sd::MASK_CAUSAL : d2sd::MASK_NONE;
+  s0.dtype = d2sd::KV_BF16;
+  p.src[1] = s0;
+  p.sm_scale = sm_scale;
+  p.sm_scale_log2 = sm_scale * kLog2e;
+  p.num_kv_heads = num_kv_heads;
+  p.group = num_qo_heads / num_kv_heads;
+  p.lse_base2 = lse_base2;
+  const int nblocks = num_kv_heads * p.imp.qtiles * p.imp.splits;
+  hipError_t e = d2sd::launch_attention(p, head_dim, waves, false, nblocks, (hipStream_t)stream);
+  if (e != hipSuccess) return fail_hip(e, "single_prefill attention launch");
+  if (p.imp.splits > 1) {
+    e = d2sd::launch_merge(p, head_dim, rows, num_kv_heads * p.imp.qtiles, (hipStream_t)stream);
+    if (e != hipSuccess) return fail_hip(e, "single_prefill merge launch");
+  }
+  return D2SD_OK;
+}
+
+int d2sd_local_attention_merge(const void* q, int64_t q_stride_b, int64_t q_stride_n, int64_t q_stride_h,
+                               const void* k, const void* v, int64_t kv_stride_b, int64_t kv_stride_n,
+                               int64_t kv_stride_h, void* out, int64_t o_stride_b, int64_t o_stride_n,
+                               int64_t o_stride_h, float* lse, int64_t lse_stride_b, int64_t lse_stride_n,
+                               int bsz, int block_len, int num_qo_heads, int num_kv_heads, int head_dim,
+                               int causal, float sm_scale, const float* sinks, int lse_base2,
+                               d2sd_stream_t stream) {
+  g_last_error.clear();
+  if (int rc = check_heads(num_qo_heads, num_kv_heads, head_dim)) return rc;
+  if (bsz < 0 || block_len < 0) return fail(D2SD_ERR_INVALID_ARG, "local_attention_merge: negative size");
+  if (bsz == 0 || block_len == 0) return D2SD_OK;
+  if (!q || !k || !v || !out || !lse) return fail(D2SD_ERR_INVALID_ARG, "local_attention_merge: null pointer");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) || !stride_ok(q_stride_b) ||
+      !stride_ok(q_stride_n) || !stride_ok(q_stride_h) || !stride_ok(kv_stride_b) || !stride_ok(kv_stride_n) ||
+      !stride_ok(kv_stride_h) || !stride_ok(o_stride_b) || !stride_ok(o_stride_n) || !stride_ok(o_stride_h))
+    return fail(D2SD_ERR_INVALID_ARG,
+                "local_attention_merge: tensors must be 16-byte aligned with strides % 8 == 0");
+  d2sd::AttnParams p{};
+  const int g = num_qo_heads / num_kv_heads;
+  const int waves = d2sd::choose_waves(block_len * g);
+  const int rows = 32 * waves;
+  p.imp.num_reqs = bsz;
+  p.imp.qtiles = (block_len * g + rows - 1) / rows;
+  p.imp.splits = 1;
+  p.imp.chunk_keys = ((block_len + 63) / 64) * 64;
+  p.imp.qo_len = block_len;
+  p.imp.kv_len = block_len;
+  p.imp.kv_begin = 0;
+  p.imp.single_mode = d2sd::MODE_INPLACE;
+  p.q = q;
+  p.q_stride_n = q_stride_n;
+  p.q_stride_h = q_stride_h;
+  p.q_stride_req = q_stride_b;
+  p.o = out;
+  p.o_stride_n = o_stride_n;
+  p.o_stride_h = o_stride_h;
+  p.o_stride_req = o_stride_b;
+  p.lse = lse;
+  p.lse_stride_n = lse_stride_n;
+  p.lse_stride_req = lse_stride_b;
+  p.sinks = sinks;
+  d2sd::KvSource& s0 = p.src[0];
+  s0.k = k;
+  s0.v = v;
+  s0.stride_tok = kv_stride_n;
+  s0.stride_head = kv_stride_h;
+  s0.stride_req = kv_stride_b;
+  s0.mask_mode = causal ? d2sd::MASK_CAUSAL : d2sd::MASK_NONE;
+  s0.dtype = d2sd::KV_BF16;
+  p.src[1] = s0;
+  p.sm_scale = sm_scale;
+  p.sm_scale_log2 = sm_scale * kLog2e;
+  p.num_kv_heads = num_kv_heads;
+  p.group = g;
+  p.lse_base2 = lse_base2;
+  const int nblocks = bsz * num_kv_heads * p.imp.qtiles;
+  hipError_t e = d2sd::launch_attention(p, head_dim, waves, false, nblocks, (hipStream_t)stream);
+  return e == hipSuccess ? D2SD_OK : fail_hip(e, "local_attention_merge launch");
+}
+
+int d2sd_graph_begin_capture(d2sd_stream_t stream) {
+  g_last_error.clear();
+  if (!stream) return fail(D2SD_ERR_INVALID_ARG, "graph capture needs a non-null stream");
+  hipError_t e = hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal);
+  return e == hipSuccess ? D2SD_OK : fail_hip(e, "hipStreamBeginCapture");
+}
+
+int d2sd_graph_end_capture(d2sd_stream_t stream, void** graph_exec) {
+  g_last_error.clear();
+  if (!graph_exec) return fail(D2SD_ERR_INVALID_ARG, "graph_exec is null");
+  hipGraph_t graph = nullptr;
+  hipError_t e = hipStreamEndCapture((hipStream_t)stream, &graph);
+  if (e != hipSuccess) return fail_hip(e, "hipStreamEndCapture");
+  hipGraphExec_t exec = nullptr;
+  e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  if (e != hipSuccess) return fail_hip(e, "hipGraphInstantiate");
+  *graph_exec = (void*)exec;
+  return D2SD_OK;
+}
+
+int d2sd_graph_launch(void* graph_exec, d2sd_stream_t stream) {
+  g_last_error.clear();
+  if (!graph_exec) return fail(D2SD_ERR_INVALID_ARG, "graph_exec is null");
+  hipError_t e = hipGraphLaunch((hipGraphExec_t)graph_exec, (hipStream_t)stream);
+  return e == hipSuccess ? D2SD_OK : fail_hip(e, "hipGraphLaunch");
+}
+
+int d2sd_graph_destroy(void* graph_exec) {
+  g_last_error.clear();
+  if (!graph_exec) return D2SD_OK;
+  hipError_t e = hipGraphExecDestroy((hipGraphExec_t)graph_exec);
+  return e == hipSuccess ? D2SD_OK : fail_hip(e, "hipGraphExecDestroy");
+}
+
+int d2sd_cascade_plan(const d2sd_cascade_plan_desc* desc, int32_t* host_plan, size_t host_plan_ints,
+                      d2sd_cascade_plan_info* info) {
+  g_last_error.clear();
+  if (!desc || !info) return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: null desc/info");
+  if (int rc = check_heads(desc->num_qo_heads, desc->num_kv_heads, desc->head_dim)) return rc;
+  if (desc->num_reqs <= 0 || !desc->qo_indptr || !desc->prefix_len)
+    return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: need num_reqs > 0, qo_indptr and prefix_len");
+  if (desc->kv_dtype != D2SD_KV_BF16 && desc->kv_dtype != D2SD_KV_FP8_E4M3)
+    return fail(D2SD_ERR_UNSUPPORTED, "cascade_plan: kv_dtype");
+  if (desc->waves_per_block != 0 && desc->waves_per_block != 4 && desc->waves_per_block != 8)
+    return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: waves_per_block must be 0, 4 or 8");
+  if (desc->qo_indptr[0] != 0) return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: qo_indptr[0] must be 0");
+  for (int r = 0; r < desc->num_reqs; ++r) {
+    if (desc->qo_indptr[r + 1] < desc->qo_indptr[r])
+      return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: qo_indptr must be non-decreasing");
+    if (desc->prefix_len[r] < 0) return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: negative prefix_len");
+  }
+  d2sd::PlanInput in{};
+  in.num_reqs = desc->num_reqs;
+  in.qo_indptr = desc->qo_indptr;
+  in.prefix_len = desc->prefix_len;
+  in.num_qo_heads = desc->num_qo_heads;
+  in.num_kv_heads = desc->num_kv_heads;
+  in.head_dim = desc->head_dim;
+  in.window_left = desc->window_left;
+  in.num_cus = desc->num_cus > 0 ? desc->num_cus : device_num_cus();
+  in.max_splits = desc->max_splits;
+  in.waves = desc->waves_per_block;
+  std::vector<d2sd::WorkItem> work;
+  std::vector<d2sd::MergeItem> merge;
+  d2sd::PlanOutput out{};
+  d2sd::plan_cascade(in, work, merge, out);
+  static_assert(sizeof(d2sd::WorkItem) == 8 * sizeof(int32_t), "WorkItem layout");
+  static_assert(sizeof(d2sd::MergeItem) == 8 * sizeof(int32_t), "MergeItem layout");
+  std::memset(info, 0, sizeof(*info));
+  info->num_work = (int)work.size();
+  info->num_merge = (int)merge.size();
+  info->waves_per_block = out.waves;
+  info->rows_per_tile = out.rows_per_tile;
+  info->num_slots = out.num_slots;
+  info->plan_ints = 8 * (info->num_work + info->num_merge);
+  info->workspace_bytes = out.workspace_bytes;
+  info->max_splits_used = out.max_splits_used;
+  info->num_reqs = desc->num_reqs;
+  info->num_qo_heads = desc->num_qo_heads;
+  info->num_kv_heads = desc->num_kv_heads;
+  info->head_dim = desc->head_dim;
+  info->kv_dtype = desc->kv_dtype;
+  if (host_plan) {
+    if (host_plan_ints < (size_t)info->plan_ints)
+      return fail(D2SD_ERR_WORKSPACE, "cascade_plan: host_plan too small (need " +
+                                          std::to_string(info->plan_ints) + " int32)");
+    std::memcpy(host_plan, work.data(), work.size() * sizeof(d2sd::WorkItem));
+    std::memcpy(host_plan + 8 * work.size(), merge.data(), merge.size() * sizeof(d2sd::MergeItem));
+  }
+  return D2SD_OK;
+}
+
+static int build_cascade_params(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* a,
+                                d2sd::AttnParams& p) {
+  if (!info || !a) return fail(D2SD_ERR_INVALID_ARG, "cascade_run: null info/args");
+  const int D = info->head_dim;
+  if (int rc = check_heads(info->num_qo_heads, info->num_kv_heads, D)) return rc;
+  if (!a->plan || !a->qo_indptr || !a->q || !a->k_suffix || !a->v_suffix || !a->out || !a->prefix_len)
+    return fail(D2SD_ERR_INVALID_ARG, "cascade_run: null pointer");
+  if (info->num_slots > 0 && (!a->workspace || a->workspace_bytes < info->workspace_bytes))
+    return fail(D2SD_ERR_WORKSPACE, "cascade_run: workspace too small (need " +
+                                        std::to_string(info->workspace_bytes) + " bytes)");
+  if (!aligned16(a->q) || !aligned16(a->k_suffix) || !aligned16(a->v_suffix) || !aligned16(a->out) ||
+      !stride_ok(a->q_stride_n) || !stride_ok(a->q_stride_h) || !stride_ok(a->suffix_stride_n) ||
+      !stride_ok(a->suffix_stride_h) || !stride_ok(a->o_stride_n) || !stride_ok(a->o_stride_h))
+    return fail(D2SD_ERR_INVALID_ARG, "cascade_run: tensors must be 16-byte aligned with strides % 8 == 0");
+  const bool has_prefix = a->k_prefix != nullptr;
+  if (has_prefix) {
+    if (!a->v_prefix || !aligned16(a->k_prefix) || !aligned16(a->v_prefix) || !stride_ok(a->prefix_stride_tok) ||
+        !stride_ok(a->prefix_stride_head) || (a->page_size > 0 && !stride_ok(a->prefix_stride_page)))
+      return fail(D2SD_ERR_INVALID_ARG, "cascade_run: prefix K/V must be 16-byte aligned with strides % 8 == 0");
+    if (a->page_size > 0 && ((a->page_size & (a->page_size - 1)) || !a->page_table || !a->page_indptr))
+      return fail(D2SD_ERR_INVALID_ARG, "cascade_run: paged prefix needs a power-of-two page_size, page_table and page_indptr");
+  }
+  if (info->max_splits_used > 0 && !has_prefix)
+    return fail(D2SD_ERR_INVALID_ARG, "cascade_run: the plan has prefix keys but k_prefix is null");
+  if (a->mask_mode == D2SD_MASK_TREE && (!a->tree_mask || a->mask_words <= 0))
+    return fail(D2SD_ERR_INVALID_ARG, "cascade_run: tree mask needs tree_mask and mask_words");
+  if (info->kv_dtype == D2SD_KV_FP8_E4M3 && (!a->k_scale || !a->v_scale))
+    return fail(D2SD_ERR_INVALID_ARG, "cascade_run: fp8 prefix needs k_scale and v_scale");
+
+  p = d2sd::AttnParams{};
+  p.q = a->q;
+  p.q_stride_n = a->q_stride_n;
+  p.q_stride_h = a->q_stride_h;
+  p.qo_indptr = a->qo_indptr;
+  p.o = a->out;
+  p.o_stride_n = a->o_stride_n;
+  p.o_stride_h = a->o_stride_h;
+  p.lse = a->lse;
+  p.lse_stride_n = a->lse_stride_n;
+  const long long rows = info->rows_per_tile;
+  p.part_o = (float*)a->workspace;
+  p.part_lse = a->workspace ? (float*)a->workspace + (long long)info->num_slots * rows * D : nullptr;
+  p.work = (const d2sd::WorkItem*)a->plan;
+  p.merge = (const d2sd::MergeItem*)(a->plan + 8LL * info->num_work);
+  p.sinks = a->sinks;
+  d2sd::KvSource& pre = p.src[0];
+  pre.k = a->k_prefix;
+  pre.v = a->v_prefix;
+  pre.stride_tok = a->prefix_stride_tok;
+  pre.stride_head = a->prefix_stride_head;
+  pre.stride_page = a->prefix_stride_page;
+  pre.tok_indptr = a->prefix_tok_indptr;
+  pre.page_indptr = a->page_size > 0 ? a->page_indptr : nullptr;
+  pre.page_table = a->page_size > 0 ? a->page_table : nullptr;
+  pre.kv_len = a->prefix_len;
+  pre.k_scale = a->k_scale;
+  pre.v_scale = a->v_scale;
+  int lg = 0;
+  while (a->page_size > 0 && (1 << lg) < a->page_size) ++lg;
+  pre.log2_page = lg;
+  pre.mask_mode = d2sd::MASK_NONE;
+  pre.dtype = info->kv_dtype == D2SD_KV_FP8_E4M3 ? d2sd::KV_FP8 : d2sd::KV_BF16;
+  d2sd::KvSource& suf = p.src[1];
+  suf.k = a->k_suffix;
+  suf.v = a->v_suffix;
+  suf.stride_tok = a->suffix_stride_n;
+  suf.stride_head = a->suffix_stride_h;
+  suf.tok_indptr = a->qo_indptr;
+  suf.kv_len = nullptr;  // suffix keys == the request's queries
+  suf.tree_mask = (const unsigned long long*)a->tree_mask;
+  suf.mask_mode = a->mask_mode;
+  suf.mask_words = a->mask_words;
+  suf.dtype = d2sd::KV_BF16;
+  p.sm_scale = a->sm_scale;
+  p.sm_scale_log2 = a->sm_scale * kLog2e;
+  p.num_kv_heads = info->num_kv_heads;
+  p.group = info->num_qo_heads / info->num_kv_heads;
+  p.lse_base2 = a->lse_base2;
+  p.num_merge = info->num_merge;
+  return D2SD_OK;
+}
+
+int d2sd_cascade_attention(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* a,
+                           d2sd_stream_t stream) {
+  g_last_error.clear();
+  d2sd::AttnParams p{};
+  if (int rc = build_cascade_params(info, a, p)) return rc;
+  const bool fp8 = info->kv_dtype == D2SD_KV_FP8_E4M3;
+  hipError_t e =
+      d2sd::launch_attention(p, info->head_dim, info->waves_per_block, fp8, info->num_work, (hipStream_t)stream);
+  return e == hipSuccess ? D2SD_OK : fail_hip(e, "cascade attention launch");
+}
+
+int d2sd_cascade_merge(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* a, d2sd_stream_t stream) {
+  g_last_error.clear();
+  d2sd::AttnParams p{};
+  if (int rc = build_cascade_params(info, a, p)) return rc;
+  hipError_t e = d2sd::launch_merge(p, info->head_dim, info->rows_per_tile, info->num_merge, (hipStream_t)stream);
+  return e == hipSuccess ? D2SD_OK : fail_hip(e, "cascade merge launch");
+}
+
+int d2sd_cascade_run(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* a, d2sd_stream_t stream) {
+  if (int rc = d2sd_cascade_attention(info, a, stream)) return rc;
+  return d2sd_cascade_merge(info, a, stream);
+}
+
+}  // extern "C"

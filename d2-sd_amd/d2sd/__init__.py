@@ -1,0 +1,21 @@
+"""d2sd — MI355X (gfx950) cascade tree-verification attention for D2SD.
+
+Drop-in surface of the reference's verify path:
+  single_prefill_with_kv_cache, merge_state_in_place   (flashinfer names)
+  CascadeGraphRunner                                    (model/cascade_graph.py)
+and the tree-level API
+  CascadeVerifyAttention.plan() / .run()
+All device work runs hand-written HIP kernels in libd2sd.so (C ABI:
+include/d2sd.h); importing raises if the library has not been built.
+"""
+from ._lib import LIB_PATH, version
+from .ops import local_attention_merge, merge_state, merge_state_in_place, single_prefill_with_kv_cache
+from .graph import HipGraph
+from .cascade_graph import CascadeGraphRunner
+from .cascade import CascadeVerifyAttention
+from . import tree
+
+__all__ = [
+    "LIB_PATH", "version", "single_prefill_with_kv_cache", "merge_state_in_place", "merge_state",
+    "local_attention_merge", "HipGraph", "CascadeGraphRunner", "CascadeVerifyAttention", "tree",
+]

@@ -1,0 +1,71 @@
+"""Builds libd2sd.so (the C-ABI library) in-tree with hipcc for gfx950.
+
+    python d2-sd_amd/d2sd/_build.py     (or __graft_entry__.build())
+
+Every call compiles from source; objects go to d2-sd_amd/_build/.
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent          # d2-sd_amd/d2sd
+ROOT = PKG_DIR.parent                               # d2-sd_amd
+CSRC = ROOT / "csrc"
+OBJ_DIR = ROOT / "_build"
+LIB_PATH = PKG_DIR / "libd2sd.so"
+INCLUDE = ROOT.parent / "include"
+
+ARCH = "gfx950"
+SOURCES = ["attention.hip", "plan.cpp", "capi.cpp"]
+
+COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function", f"-I{INCLUDE}", f"-I{CSRC}"]
+# Device code: never let the compiler emit packed-fp32 VALU forms.
+DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          "-ffp-contract=fast"]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (ROCm is required to build libd2sd.so)")
+
+
+def _compile(src: str) -> Path:
+    path = CSRC / src
+    obj = OBJ_DIR / (path.stem + ".o")
+    cmd = [hipcc(), *COMMON]
+    if path.suffix == ".hip":
+        cmd += DEVICE
+    else:
+        cmd += ["-x", "c++", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include"]
+    cmd += ["-c", str(path), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    return obj
+
+
+def build(verbose: bool = False) -> Path:
+    OBJ_DIR.mkdir(parents=True, exist_ok=True)
+    with cf.ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
+        objs = list(ex.map(_compile, SOURCES))
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, LIB_PATH)
+    if verbose:
+        print(f"built {LIB_PATH}")
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    build(verbose=True)
+    sys.exit(0)

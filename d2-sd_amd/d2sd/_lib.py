@@ -1,0 +1,161 @@
+"""ctypes binding of libd2sd.so (C ABI declared in include/d2sd.h).
+
+The library is loaded at import; a missing library raises ImportError — there
+is no fallback path.  Device work additionally requires ROCm device tensors.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libd2sd.so"
+
+D2SD_OK = 0
+D2SD_KV_BF16 = 0
+D2SD_KV_FP8_E4M3 = 1
+D2SD_MASK_NONE = 0
+D2SD_MASK_CAUSAL = 1
+D2SD_MASK_TREE = 2
+
+# Every symbol include/d2sd.h declares.
+EXPORTED_SYMBOLS = (
+    "d2sd_last_error",
+    "d2sd_version",
+    "d2sd_merge_state_in_place",
+    "d2sd_single_prefill_workspace_size",
+    "d2sd_single_prefill_with_kv_cache",
+    "d2sd_local_attention_merge",
+    "d2sd_graph_begin_capture",
+    "d2sd_graph_end_capture",
+    "d2sd_graph_launch",
+    "d2sd_graph_destroy",
+    "d2sd_cascade_plan",
+    "d2sd_cascade_run",
+    "d2sd_cascade_attention",
+    "d2sd_cascade_merge",
+)
+
+
+class PlanDesc(C.Structure):
+    _fields_ = [
+        ("num_reqs", C.c_int),
+        ("qo_indptr", C.POINTER(C.c_int32)),
+        ("prefix_len", C.POINTER(C.c_int32)),
+        ("num_qo_heads", C.c_int),
+        ("num_kv_heads", C.c_int),
+        ("head_dim", C.c_int),
+        ("window_left", C.c_int),
+        ("kv_dtype", C.c_int),
+        ("num_cus", C.c_int),
+        ("max_splits", C.c_int),
+        ("waves_per_block", C.c_int),
+    ]
+
+
+class PlanInfo(C.Structure):
+    _fields_ = [
+        ("num_work", C.c_int),
+        ("num_merge", C.c_int),
+        ("waves_per_block", C.c_int),
+        ("rows_per_tile", C.c_int),
+        ("num_slots", C.c_int),
+        ("plan_ints", C.c_int),
+        ("workspace_bytes", C.c_size_t),
+        ("max_splits_used", C.c_int),
+        ("num_reqs", C.c_int),
+        ("num_qo_heads", C.c_int),
+        ("num_kv_heads", C.c_int),
+        ("head_dim", C.c_int),
+        ("kv_dtype", C.c_int),
+    ]
+
+
+class RunArgs(C.Structure):
+    _fields_ = [
+        ("plan", C.c_void_p),
+        ("qo_indptr", C.c_void_p),
+        ("q", C.c_void_p),
+        ("q_stride_n", C.c_int64),
+        ("q_stride_h", C.c_int64),
+        ("k_suffix", C.c_void_p),
+        ("v_suffix", C.c_void_p),
+        ("suffix_stride_n", C.c_int64),
+        ("suffix_stride_h", C.c_int64),
+        ("mask_mode", C.c_int),
+        ("mask_words", C.c_int),
+        ("tree_mask", C.c_void_p),
+        ("k_prefix", C.c_void_p),
+        ("v_prefix", C.c_void_p),
+        ("prefix_stride_tok", C.c_int64),
+        ("prefix_stride_head", C.c_int64),
+        ("prefix_stride_page", C.c_int64),
+        ("page_size", C.c_int),
+        ("page_indptr", C.c_void_p),
+        ("page_table", C.c_void_p),
+        ("prefix_tok_indptr", C.c_void_p),
+        ("prefix_len", C.c_void_p),
+        ("k_scale", C.c_void_p),
+        ("v_scale", C.c_void_p),
+        ("sinks", C.c_void_p),
+        ("out", C.c_void_p),
+        ("o_stride_n", C.c_int64),
+        ("o_stride_h", C.c_int64),
+        ("lse", C.c_void_p),
+        ("lse_stride_n", C.c_int64),
+        ("sm_scale", C.c_float),
+        ("lse_base2", C.c_int),
+        ("workspace", C.c_void_p),
+        ("workspace_bytes", C.c_size_t),
+    ]
+
+
+def _load() -> C.CDLL:
+    if not LIB_PATH.exists():
+        raise ImportError(
+            f"{LIB_PATH} is missing: build it first (python -c 'import __graft_entry__ as g; g.build()' "
+            "or python d2-sd_amd/d2sd/_build.py)")
+    lib = C.CDLL(str(LIB_PATH))
+    vp, i64, i32, f32, sz = C.c_void_p, C.c_int64, C.c_int, C.c_float, C.c_size_t
+    lib.d2sd_last_error.restype = C.c_char_p
+    lib.d2sd_last_error.argtypes = []
+    lib.d2sd_version.restype = C.c_char_p
+    lib.d2sd_version.argtypes = []
+    lib.d2sd_merge_state_in_place.restype = i32
+    lib.d2sd_merge_state_in_place.argtypes = [vp, i64, i64, vp, i64, vp, i64, i64, vp, i64, i32, i32, i32, i32, vp]
+    lib.d2sd_single_prefill_workspace_size.restype = sz
+    lib.d2sd_single_prefill_workspace_size.argtypes = [i32, i32, i32, i32, i32, i32]
+    lib.d2sd_single_prefill_with_kv_cache.restype = i32
+    lib.d2sd_single_prefill_with_kv_cache.argtypes = [
+        vp, i64, i64, vp, vp, i64, i64, vp, i64, i64, vp, i32, i32, i32, i32, i32, i32, i32, f32, i32, vp, sz, vp]
+    lib.d2sd_local_attention_merge.restype = i32
+    lib.d2sd_local_attention_merge.argtypes = [
+        vp, i64, i64, i64, vp, vp, i64, i64, i64, vp, i64, i64, i64, vp, i64, i64,
+        i32, i32, i32, i32, i32, i32, f32, vp, i32, vp]
+    lib.d2sd_graph_begin_capture.restype = i32
+    lib.d2sd_graph_begin_capture.argtypes = [vp]
+    lib.d2sd_graph_end_capture.restype = i32
+    lib.d2sd_graph_end_capture.argtypes = [vp, C.POINTER(C.c_void_p)]
+    lib.d2sd_graph_launch.restype = i32
+    lib.d2sd_graph_launch.argtypes = [vp, vp]
+    lib.d2sd_graph_destroy.restype = i32
+    lib.d2sd_graph_destroy.argtypes = [vp]
+    lib.d2sd_cascade_plan.restype = i32
+    lib.d2sd_cascade_plan.argtypes = [C.POINTER(PlanDesc), C.POINTER(C.c_int32), sz, C.POINTER(PlanInfo)]
+    for name in ("d2sd_cascade_run", "d2sd_cascade_attention", "d2sd_cascade_merge"):
+        fn = getattr(lib, name)
+        fn.restype = i32
+        fn.argtypes = [C.POINTER(PlanInfo), C.POINTER(RunArgs), vp]
+    return lib
+
+
+lib = _load()
+
+
+def check(rc: int, what: str) -> None:
+    if rc != D2SD_OK:
+        msg = lib.d2sd_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (status {rc}): {msg}")
+
+
+def version() -> str:
+    return lib.d2sd_version().decode()

@@ -1,0 +1,286 @@
+"""CascadeVerifyAttention — plan()/run() for cascade tree-verification attention.
+
+One run() computes, for every request r, what generation/verification.py:127-176
+computes per layer with three FlashInfer calls, a CUDA graph and torch
+elementwise ops:
+
+  * prefix fetch + sliding-window truncation (verification.py:127-135),
+  * shared-prefix attention of every suffix query (verification.py:145-150),
+  * suffix attention under the tree (ancestor) mask — the per-row causal
+    local level of verification.py:155-162 over unique tree nodes,
+  * log-sum-exp merge (verification.py:163-165) and the GPT-OSS sink rescale
+    (verification.py:173-176),
+
+with the queries of request r = its tree nodes q[qo_indptr[r]:qo_indptr[r+1]].
+plan() does all host work and device uploads; run() only launches kernels
+(two per call: split-KV attention over prefix chunks and suffix trees, then the
+merge), allocates nothing when `out`/`lse` are given, and can be captured into
+a HipGraph.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import Optional, Sequence, Tuple, Union
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import check, lib
+from .tree import pack_tree_masks
+
+_MASK_MODES = {"none": _lib.D2SD_MASK_NONE, "causal": _lib.D2SD_MASK_CAUSAL, "tree": _lib.D2SD_MASK_TREE}
+
+
+def _i32(x) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(x, dtype=np.int32))
+
+
+class CascadeVerifyAttention:
+    def __init__(self, device: Union[str, torch.device, None] = None):
+        self.device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        self._planned = False
+
+    # ------------------------------------------------------------------ plan
+    def plan(
+        self,
+        qo_indptr: Sequence[int],
+        prefix_len: Sequence[int],
+        num_qo_heads: int,
+        num_kv_heads: int,
+        head_dim: int,
+        *,
+        tree_masks: Optional[Sequence[np.ndarray]] = None,
+        mask_mode: str = "tree",
+        page_size: int = 0,
+        page_indptr: Optional[Sequence[int]] = None,
+        page_table: Optional[Union[Sequence[int], torch.Tensor]] = None,
+        prefix_tok_indptr: Optional[Sequence[int]] = None,
+        kv_layout: str = "HND",
+        sm_scale: Optional[float] = None,
+        window_left: int = -1,
+        sinks: Optional[torch.Tensor] = None,
+        kv_dtype: torch.dtype = torch.bfloat16,
+        k_scale: Optional[torch.Tensor] = None,
+        v_scale: Optional[torch.Tensor] = None,
+        lse_base2: bool = False,
+        max_splits: int = 0,
+        waves_per_block: int = 0,
+        num_cus: int = 0,
+    ) -> "CascadeVerifyAttention":
+        """Plan one verify call.
+
+        qo_indptr [R+1]: tree nodes of request r are rows qo_indptr[r]:qo_indptr[r+1]
+        of q / k_suffix / v_suffix / out / lse.  prefix_len [R]: shared-prefix keys.
+        tree_masks: per request a bool [n_r, n_r] ancestor mask (M[i, j] = node j
+        is i or an ancestor of i) when mask_mode == "tree".
+        Prefix KV at run(): paged (page_size > 0) pool of shape
+        [pages, Hkv, P, D] (kv_layout "HND") or [pages, P, Hkv, D] ("NHD") with
+        request r's pages page_table[page_indptr[r]:page_indptr[r+1]]; or
+        contiguous [Hkv, L, D] ("HND", the DynamicCache layout) / [L, Hkv, D]
+        ("NHD"), request r at token offset prefix_tok_indptr[r] (default 0).
+        window_left >= 0 keeps the last window_left prefix keys for all queries
+        (verification.py:133-135).  sinks [Hq] fp32 applies O *= sigmoid(lse - sink).
+        kv_dtype torch.float8_e4m3fn takes per-kv-head fp32 k_scale / v_scale.
+        """
+        qo = _i32(qo_indptr)
+        pl = _i32(prefix_len)
+        R = int(pl.shape[0])
+        if qo.shape[0] != R + 1:
+            raise ValueError("qo_indptr must have len(prefix_len) + 1 entries")
+        if mask_mode not in _MASK_MODES:
+            raise ValueError(f"mask_mode must be one of {sorted(_MASK_MODES)}")
+        if kv_layout not in ("HND", "NHD"):
+            raise ValueError("kv_layout must be 'HND' or 'NHD'")
+        if kv_dtype not in (torch.bfloat16, torch.float8_e4m3fn):
+            raise TypeError("kv_dtype must be torch.bfloat16 or torch.float8_e4m3fn")
+        fp8 = kv_dtype == torch.float8_e4m3fn
+        dev = self.device
+        desc = _lib.PlanDesc()
+        desc.num_reqs = R
+        desc.qo_indptr = qo.ctypes.data_as(C.POINTER(C.c_int32))
+        desc.prefix_len = pl.ctypes.data_as(C.POINTER(C.c_int32))
+        desc.num_qo_heads = num_qo_heads
+        desc.num_kv_heads = num_kv_heads
+        desc.head_dim = head_dim
+        desc.window_left = window_left
+        desc.kv_dtype = _lib.D2SD_KV_FP8_E4M3 if fp8 else _lib.D2SD_KV_BF16
+        desc.num_cus = num_cus
+        desc.max_splits = max_splits
+        desc.waves_per_block = waves_per_block
+        info = _lib.PlanInfo()
+        check(lib.d2sd_cascade_plan(C.byref(desc), None, 0, C.byref(info)), "cascade_plan (size)")
+        host = np.zeros(max(info.plan_ints, 8), dtype=np.int32)
+        check(lib.d2sd_cascade_plan(C.byref(desc), host.ctypes.data_as(C.POINTER(C.c_int32)), host.size,
+                                    C.byref(info)), "cascade_plan")
+        self.info = info
+        self.plan_host = host
+        self.qo_indptr_host = qo
+        self.prefix_len_host = pl
+        self.plan_dev = torch.from_numpy(host).to(dev)
+        self.qo_indptr_dev = torch.from_numpy(qo).to(dev)
+        self.prefix_len_dev = torch.from_numpy(pl).to(dev)
+        self.workspace = torch.empty(max(int(info.workspace_bytes), 16), dtype=torch.uint8, device=dev)
+        self.mask_mode = _MASK_MODES[mask_mode]
+        self.total_q = int(qo[-1])
+        if self.mask_mode == _lib.D2SD_MASK_TREE:
+            if tree_masks is None or len(tree_masks) != R:
+                raise ValueError("mask_mode 'tree' needs one ancestor mask per request")
+            for r, m in enumerate(tree_masks):
+                n = int(qo[r + 1] - qo[r])
+                if m.shape != (n, n):
+                    raise ValueError(f"tree_masks[{r}] must be [{n}, {n}], got {m.shape}")
+            packed = pack_tree_masks([np.asarray(m, dtype=bool) for m in tree_masks])
+            self.mask_words = int(packed.shape[1])
+            self.tree_mask_dev = torch.from_numpy(packed.view(np.int64)).to(dev)
+        else:
+            self.mask_words = 0
+            self.tree_mask_dev = None
+        self.page_size = int(page_size)
+        if self.page_size > 0:
+            if page_indptr is None or page_table is None:
+                raise ValueError("paged prefix needs page_indptr and page_table")
+            pi = _i32(page_indptr)
+            if pi.shape[0] != R + 1:
+                raise ValueError("page_indptr must have R + 1 entries")
+            need = (pl + self.page_size - 1) // self.page_size
+            if np.any(pi[1:] - pi[:-1] < need):
+                raise ValueError("page_indptr gives a request fewer pages than its prefix_len needs")
+            self.page_indptr_dev = torch.from_numpy(pi).to(dev)
+            pt = page_table if isinstance(page_table, torch.Tensor) else torch.from_numpy(_i32(page_table))
+            self.page_table_dev = pt.to(device=dev, dtype=torch.int32).contiguous()
+            if self.page_table_dev.numel() < int(pi[-1]):
+                raise ValueError("page_table shorter than page_indptr[-1]")
+            self.prefix_tok_indptr_dev = None
+        else:
+            self.page_indptr_dev = None
+            self.page_table_dev = None
+            self.prefix_tok_indptr_dev = (torch.from_numpy(_i32(prefix_tok_indptr)).to(dev)
+                                          if prefix_tok_indptr is not None else None)
+        self.kv_layout = kv_layout
+        self.num_qo_heads, self.num_kv_heads, self.head_dim = num_qo_heads, num_kv_heads, head_dim
+        self.sm_scale = float(sm_scale) if sm_scale is not None else head_dim ** -0.5
+        self.window_left = window_left
+        self.sinks = sinks.to(device=dev, dtype=torch.float32).contiguous() if sinks is not None else None
+        if self.sinks is not None and self.sinks.numel() != num_qo_heads:
+            raise ValueError("sinks must have num_qo_heads entries")
+        self.kv_dtype = kv_dtype
+        if fp8:
+            if k_scale is None or v_scale is None:
+                raise ValueError("fp8 KV needs k_scale and v_scale")
+            self.k_scale = k_scale.to(device=dev, dtype=torch.float32).contiguous()
+            self.v_scale = v_scale.to(device=dev, dtype=torch.float32).contiguous()
+        else:
+            self.k_scale = self.v_scale = None
+        self.lse_base2 = bool(lse_base2)
+        self._planned = True
+        return self
+
+    # ------------------------------------------------------------------- run
+    def _prefix_strides(self, k_prefix: torch.Tensor) -> Tuple[int, int, int]:
+        """(stride_tok, stride_head, stride_page) in elements."""
+        if self.page_size > 0:
+            if k_prefix.dim() != 4:
+                raise ValueError("paged prefix pool must be 4-D")
+            if self.kv_layout == "HND":   # [pages, Hkv, P, D]
+                _, hkv, P, D = k_prefix.shape
+                st, sh, sp = k_prefix.stride(2), k_prefix.stride(1), k_prefix.stride(0)
+            else:                         # [pages, P, Hkv, D]
+                _, P, hkv, D = k_prefix.shape
+                st, sh, sp = k_prefix.stride(1), k_prefix.stride(2), k_prefix.stride(0)
+            if P != self.page_size:
+                raise ValueError(f"pool page size {P} != planned {self.page_size}")
+        else:
+            if k_prefix.dim() == 4 and k_prefix.shape[0] == 1:
+                k_prefix = k_prefix[0]   # DynamicCache [1, Hkv, L, D]
+            if k_prefix.dim() != 3:
+                raise ValueError("contiguous prefix must be [Hkv, L, D] (HND) or [L, Hkv, D] (NHD)")
+            if self.kv_layout == "HND":
+                hkv, _, D = k_prefix.shape
+                st, sh, sp = k_prefix.stride(1), k_prefix.stride(0), 0
+            else:
+                _, hkv, D = k_prefix.shape
+                st, sh, sp = k_prefix.stride(0), k_prefix.stride(1), 0
+        if hkv != self.num_kv_heads or D != self.head_dim or k_prefix.stride(-1) != 1:
+            raise ValueError("prefix KV head count / head_dim / contiguity mismatch")
+        return st, sh, sp
+
+    def run(
+        self,
+        q: torch.Tensor,
+        k_suffix: torch.Tensor,
+        v_suffix: torch.Tensor,
+        k_prefix: Optional[torch.Tensor] = None,
+        v_prefix: Optional[torch.Tensor] = None,
+        out: Optional[torch.Tensor] = None,
+        lse: Optional[torch.Tensor] = None,
+    ) -> Tuple[torch.Tensor, torch.Tensor]:
+        """q [total_q, Hq, D], k/v_suffix [total_q, Hkv, D] (bf16); prefix KV as
+        planned.  Returns (out [total_q, Hq, D] bf16, lse [total_q, Hq] fp32)."""
+        return self._launch("d2sd_cascade_run", q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse)
+
+    def run_attention(self, q, k_suffix, v_suffix, k_prefix=None, v_prefix=None, out=None, lse=None):
+        """First half of run(): the attention launch alone (partials in the
+        plan's workspace).  run_merge() with the same arguments finishes it."""
+        return self._launch("d2sd_cascade_attention", q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse)
+
+    def run_merge(self, q, k_suffix, v_suffix, k_prefix=None, v_prefix=None, out=None, lse=None):
+        """Second half of run(): merge of the workspace partials into out / lse."""
+        return self._launch("d2sd_cascade_merge", q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse)
+
+    def _launch(self, fn_name, q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse):
+        if not self._planned:
+            raise RuntimeError("run() before plan()")
+        T, hq, d = self.total_q, self.num_qo_heads, self.head_dim
+        for name, t, h in (("q", q, hq), ("k_suffix", k_suffix, self.num_kv_heads),
+                           ("v_suffix", v_suffix, self.num_kv_heads)):
+            if t.shape != (T, h, d) or t.dtype != torch.bfloat16 or t.stride(-1) != 1 or not t.is_cuda:
+                raise ValueError(f"{name} must be a bf16 device tensor [{T}, {h}, {d}] with contiguous head_dim")
+        if k_suffix.stride() != v_suffix.stride():
+            raise ValueError("k_suffix and v_suffix must share strides")
+        if out is None:
+            out = torch.empty((T, hq, d), dtype=torch.bfloat16, device=q.device)
+        if lse is None:
+            lse = torch.empty((T, hq), dtype=torch.float32, device=q.device)
+        if out.shape != (T, hq, d) or out.dtype != torch.bfloat16 or out.stride(-1) != 1:
+            raise ValueError("out must be bf16 [total_q, Hq, D] with contiguous head_dim")
+        if lse.shape != (T, hq) or lse.dtype != torch.float32 or lse.stride(-1) != 1:
+            raise ValueError("lse must be float32 [total_q, Hq] with contiguous heads")
+        a = _lib.RunArgs()
+        a.plan = self.plan_dev.data_ptr()
+        a.qo_indptr = self.qo_indptr_dev.data_ptr()
+        a.q = q.data_ptr()
+        a.q_stride_n, a.q_stride_h = q.stride(0), q.stride(1)
+        a.k_suffix, a.v_suffix = k_suffix.data_ptr(), v_suffix.data_ptr()
+        a.suffix_stride_n, a.suffix_stride_h = k_suffix.stride(0), k_suffix.stride(1)
+        a.mask_mode = self.mask_mode
+        a.mask_words = self.mask_words
+        a.tree_mask = self.tree_mask_dev.data_ptr() if self.tree_mask_dev is not None else None
+        if k_prefix is not None:
+            if v_prefix is None or v_prefix.shape != k_prefix.shape or v_prefix.stride() != k_prefix.stride():
+                raise ValueError("v_prefix must match k_prefix in shape and strides")
+            if k_prefix.dtype != self.kv_dtype or v_prefix.dtype != self.kv_dtype:
+                raise TypeError(f"prefix KV must be {self.kv_dtype}")
+            st, sh, sp = self._prefix_strides(k_prefix)
+            a.k_prefix, a.v_prefix = k_prefix.data_ptr(), v_prefix.data_ptr()
+            a.prefix_stride_tok, a.prefix_stride_head, a.prefix_stride_page = st, sh, sp
+        a.page_size = self.page_size
+        a.page_indptr = self.page_indptr_dev.data_ptr() if self.page_indptr_dev is not None else None
+        a.page_table = self.page_table_dev.data_ptr() if self.page_table_dev is not None else None
+        a.prefix_tok_indptr = (self.prefix_tok_indptr_dev.data_ptr()
+                               if self.prefix_tok_indptr_dev is not None else None)
+        a.prefix_len = self.prefix_len_dev.data_ptr()
+        a.k_scale = self.k_scale.data_ptr() if self.k_scale is not None else None
+        a.v_scale = self.v_scale.data_ptr() if self.v_scale is not None else None
+        a.sinks = self.sinks.data_ptr() if self.sinks is not None else None
+        a.out = out.data_ptr()
+        a.o_stride_n, a.o_stride_h = out.stride(0), out.stride(1)
+        a.lse = lse.data_ptr()
+        a.lse_stride_n = lse.stride(0)
+        a.sm_scale = self.sm_scale
+        a.lse_base2 = int(self.lse_base2)
+        a.workspace = self.workspace.data_ptr()
+        a.workspace_bytes = self.workspace.numel()
+        fn = getattr(lib, fn_name)
+        check(fn(C.byref(self.info), C.byref(a), C.c_void_p(torch.cuda.current_stream().cuda_stream)), fn_name)
+        return out, lse

@@ -1,0 +1,99 @@
+"""CascadeGraphRunner — drop-in for model/cascade_graph.py:5-112.
+
+Same constructor, `_capture(bsz)` and `run(q, k, v, out_shared, lse_shared)`
+contract as the reference: per bsz, static buffers + a captured graph of the
+local (per-row) attention and its merge into the shared-prefix state; `run`
+copies inputs in, replays and copies the merged `out_shared` and `lse_shared`
+back (cascade_graph.py:100-112).  The captured body is ONE fused kernel
+launch (local attention of every row + merge_state epilogue) instead of
+2*bsz FlashInfer launches (cascade_graph.py:52-60).
+"""
+from __future__ import annotations
+
+from typing import Dict, Optional
+
+import torch
+
+from .graph import HipGraph
+from .ops import local_attention_merge
+
+
+class CascadeGraphRunner:
+    def __init__(
+        self,
+        block_size: int,
+        num_heads: int,
+        num_kv_heads: int,
+        head_dim: int,
+        dtype: torch.dtype,
+        device: torch.device,
+        sm_scale: float,
+        causal: bool,
+        sinks: Optional[torch.Tensor] = None,
+    ):
+        if dtype != torch.bfloat16:
+            raise TypeError("CascadeGraphRunner supports bfloat16")
+        self.block_size = block_size
+        self.num_heads = num_heads
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.dtype = dtype
+        self.device = torch.device(device)
+        self.sm_scale = sm_scale
+        self.causal = causal
+        # Optional GPT-OSS sink rescale fused after the merge
+        # (generation/verification.py:173-176); None keeps the reference
+        # runner's behaviour (no sink inside the runner).
+        self.sinks = sinks.to(device=self.device, dtype=torch.float32).contiguous() if sinks is not None else None
+        self._graphs: Dict[int, HipGraph] = {}
+        self._buffers: Dict[int, Dict[str, torch.Tensor]] = {}
+
+    def _run_local_merge(self, bufs: Dict[str, torch.Tensor]) -> None:
+        local_attention_merge(bufs["q"], bufs["k"], bufs["v"], bufs["out_shared"], bufs["lse_shared"],
+                              causal=self.causal, sm_scale=self.sm_scale, sinks=self.sinks)
+
+    def _capture(self, bsz: int) -> None:
+        """Pre-allocate buffers, warm up, and capture the graph for `bsz`
+        (model/cascade_graph.py:37-74)."""
+        dev, dt = self.device, self.dtype
+        lb, hq, hkv, d = self.block_size, self.num_heads, self.num_kv_heads, self.head_dim
+        bufs = {
+            "q": torch.zeros(bsz, lb, hq, d, dtype=dt, device=dev),
+            "k": torch.zeros(bsz, lb, hkv, d, dtype=dt, device=dev),
+            "v": torch.zeros(bsz, lb, hkv, d, dtype=dt, device=dev),
+            "out_shared": torch.zeros(bsz, lb, hq, d, dtype=dt, device=dev),
+            "lse_shared": torch.full((bsz, lb, hq), float("-inf"), dtype=torch.float32, device=dev),
+        }
+        for _ in range(3):
+            self._run_local_merge(bufs)
+        torch.cuda.synchronize()
+        g = HipGraph()
+        with g.capture():
+            self._run_local_merge(bufs)
+        self._graphs[bsz] = g
+        self._buffers[bsz] = bufs
+
+    def run(self, q_local: torch.Tensor, k_local: torch.Tensor, v_local: torch.Tensor,
+            out_shared: torch.Tensor, lse_shared: torch.Tensor) -> None:
+        """q_local [bsz, Lb, Hq, D], k/v_local [bsz, Lb, Hkv, D],
+        out_shared [bsz, Lb, Hq, D] and lse_shared [bsz, Lb, Hq] (in/out).
+        After return out_shared / lse_shared hold the merged state."""
+        bsz = q_local.shape[0]
+        if bsz not in self._graphs:
+            self._capture(bsz)
+        bufs = self._buffers[bsz]
+        bufs["q"].copy_(q_local)
+        bufs["k"].copy_(k_local)
+        bufs["v"].copy_(v_local)
+        bufs["out_shared"].copy_(out_shared)
+        bufs["lse_shared"].copy_(lse_shared)
+        self._graphs[bsz].replay()
+        out_shared.copy_(bufs["out_shared"])
+        lse_shared.copy_(bufs["lse_shared"])
+
+    def run_direct(self, q_local: torch.Tensor, k_local: torch.Tensor, v_local: torch.Tensor,
+                   out_shared: torch.Tensor, lse_shared: torch.Tensor) -> None:
+        """Same result as run() with no staging copies: one kernel launch on
+        the caller's tensors (any strides with a contiguous head_dim)."""
+        local_attention_merge(q_local, k_local, v_local, out_shared, lse_shared,
+                              causal=self.causal, sm_scale=self.sm_scale, sinks=self.sinks)

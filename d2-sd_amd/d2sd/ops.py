@@ -1,0 +1,183 @@
+"""FlashInfer-compatible entry points used by the reference's verify path.
+
+    single_prefill_with_kv_cache  <- flashinfer.single_prefill_with_kv_cache
+                                     (generation/verification.py:145, 159;
+                                      model/cascade_graph.py:54; model/dflash.py:112, 127)
+    merge_state_in_place          <- flashinfer.merge_state_in_place
+                                     (generation/verification.py:163;
+                                      model/cascade_graph.py:58; model/dflash.py:131)
+    merge_state                   <- flashinfer.merge_state (out-of-place form)
+
+Same names, argument meaning and return convention as the FlashInfer calls the
+reference makes; every call runs the gfx950 kernels of libd2sd.so on the
+current HIP stream.  The returned LSE is the natural logarithm of the softmax
+denominator (pass lse_base2=True for base 2).
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import Optional, Tuple, Union
+
+import torch
+
+from . import _lib
+from ._lib import check, lib
+
+
+def _stream() -> C.c_void_p:
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _need_device(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if not t.is_cuda:
+            raise ValueError("d2sd kernels need ROCm device tensors (got a CPU tensor)")
+
+
+def _need_bf16(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"d2sd kernels take bfloat16 q/k/v/o (got {t.dtype})")
+
+
+def _need_rows(name: str, t: torch.Tensor) -> None:
+    if t.dim() != 3 or t.stride(-1) != 1:
+        raise ValueError(f"{name} must be 3-D with a contiguous last dimension, got shape "
+                         f"{tuple(t.shape)} strides {t.stride()}")
+
+
+def single_prefill_with_kv_cache(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    custom_mask: Optional[torch.Tensor] = None,
+    packed_custom_mask: Optional[torch.Tensor] = None,
+    causal: bool = False,
+    kv_layout: str = "NHD",
+    pos_encoding_mode: str = "NONE",
+    use_fp16_qk_reduction: bool = False,
+    sm_scale: Optional[float] = None,
+    window_left: int = -1,
+    logits_soft_cap: Optional[float] = None,
+    rope_scale: Optional[float] = None,
+    rope_theta: Optional[float] = None,
+    return_lse: bool = False,
+    lse_base2: bool = False,
+) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
+    """Attention of q [qo_len, Hq, D] over k, v [kv_len, Hkv, D] (kv_layout
+    "NHD") or [Hkv, kv_len, D] ("HND"), GQA head map h -> h // (Hq // Hkv).
+
+    causal=True keeps key j for query i iff j <= i + kv_len - qo_len.
+    Returns out (q's shape, bf16) or (out, lse [qo_len, Hq] fp32).
+    """
+    if custom_mask is not None or packed_custom_mask is not None:
+        raise NotImplementedError("custom masks: use CascadeVerifyAttention (tree mask)")
+    if pos_encoding_mode != "NONE" or logits_soft_cap not in (None, 0.0) or rope_scale or rope_theta:
+        raise NotImplementedError("only pos_encoding_mode='NONE' without soft-cap is supported")
+    if window_left != -1:
+        raise NotImplementedError("window_left: use CascadeVerifyAttention(window_left=...)")
+    if use_fp16_qk_reduction:
+        raise NotImplementedError("use_fp16_qk_reduction")
+    _need_device(q, k, v)
+    _need_bf16(q, k, v)
+    _need_rows("q", q)
+    _need_rows("k", k)
+    _need_rows("v", v)
+    if k.stride() != v.stride() or k.shape != v.shape:
+        raise ValueError("k and v must have the same shape and strides")
+    qo_len, hq, d = q.shape
+    if kv_layout == "NHD":
+        kv_len, hkv, dk = k.shape
+        s_n, s_h = k.stride(0), k.stride(1)
+    elif kv_layout == "HND":
+        hkv, kv_len, dk = k.shape
+        s_n, s_h = k.stride(1), k.stride(0)
+    else:
+        raise ValueError(f"kv_layout must be 'NHD' or 'HND', got {kv_layout!r}")
+    if dk != d:
+        raise ValueError("q and k head_dim differ")
+    if sm_scale is None:
+        sm_scale = d ** -0.5
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    lse = torch.empty((qo_len, hq), dtype=torch.float32, device=q.device) if return_lse else None
+    ws_bytes = lib.d2sd_single_prefill_workspace_size(qo_len, kv_len, hq, hkv, d, -1)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+    with torch.cuda.device(q.device):
+        rc = lib.d2sd_single_prefill_with_kv_cache(
+            q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), v.data_ptr(), s_n, s_h,
+            out.data_ptr(), out.stride(0), out.stride(1), lse.data_ptr() if lse is not None else None,
+            qo_len, kv_len, hq, hkv, d, int(bool(causal)), -1, float(sm_scale), int(bool(lse_base2)),
+            ws.data_ptr(), ws.numel(), _stream())
+    check(rc, "single_prefill_with_kv_cache")
+    return (out, lse) if return_lse else out
+
+
+def merge_state_in_place(v: torch.Tensor, s: torch.Tensor, v_other: torch.Tensor, s_other: torch.Tensor,
+                         mask: Optional[torch.Tensor] = None, lse_base2: bool = False) -> None:
+    """v [n, H, D] bf16 and s [n, H] fp32 become the merge of (v, s) and
+    (v_other, s_other): s' = logaddexp(s, s_other),
+    v' = v*exp(s - s') + v_other*exp(s_other - s')."""
+    if mask is not None:
+        raise NotImplementedError("merge_state_in_place(mask=...)")
+    _need_device(v, s, v_other, s_other)
+    _need_bf16(v, v_other)
+    _need_rows("v", v)
+    _need_rows("v_other", v_other)
+    if v.shape != v_other.shape or s.shape != v.shape[:2] or s_other.shape != v.shape[:2]:
+        raise ValueError("merge_state_in_place: shape mismatch")
+    if s.dtype != torch.float32 or s_other.dtype != torch.float32:
+        raise TypeError("merge_state_in_place: s and s_other must be float32")
+    if s.stride(1) != 1 or s_other.stride(1) != 1:
+        raise ValueError("merge_state_in_place: s / s_other need a contiguous head dimension")
+    n, h, d = v.shape
+    with torch.cuda.device(v.device):
+        rc = lib.d2sd_merge_state_in_place(
+            v.data_ptr(), v.stride(0), v.stride(1), s.data_ptr(), s.stride(0),
+            v_other.data_ptr(), v_other.stride(0), v_other.stride(1), s_other.data_ptr(), s_other.stride(0),
+            n, h, d, int(bool(lse_base2)), _stream())
+    check(rc, "merge_state_in_place")
+
+
+def merge_state(v_a: torch.Tensor, s_a: torch.Tensor, v_b: torch.Tensor, s_b: torch.Tensor,
+                lse_base2: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Out-of-place merge of two attention states; returns (v, s)."""
+    v = v_a.clone()
+    s = s_a.clone()
+    merge_state_in_place(v, s, v_b, s_b, lse_base2=lse_base2)
+    return v, s
+
+
+def local_attention_merge(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor,
+                          lse: torch.Tensor, causal: bool, sm_scale: float,
+                          sinks: Optional[torch.Tensor] = None, lse_base2: bool = False) -> None:
+    """One launch of the per-row local attention + in-place merge loop of
+    model/cascade_graph.py:52-60: q/out [bsz, Lb, Hq, D], k/v [bsz, Lb, Hkv, D],
+    lse [bsz, Lb, Hq]; out/lse are updated in place."""
+    _need_device(q, k, v, out, lse)
+    _need_bf16(q, k, v, out)
+    if q.dim() != 4 or k.dim() != 4 or out.shape != q.shape or k.shape != v.shape:
+        raise ValueError("local_attention_merge: q/out [bsz, Lb, Hq, D], k/v [bsz, Lb, Hkv, D]")
+    if k.stride() != v.stride() or q.stride(-1) != 1 or k.stride(-1) != 1 or out.stride(-1) != 1:
+        raise ValueError("local_attention_merge: contiguous head_dim and equal k/v strides required")
+    if lse.dtype != torch.float32 or lse.shape != q.shape[:3] or lse.stride(-1) != 1:
+        raise ValueError("local_attention_merge: lse must be float32 [bsz, Lb, Hq] with contiguous heads")
+    bsz, lb, hq, d = q.shape
+    hkv = k.shape[2]
+    if k.shape[0] != bsz or k.shape[1] != lb or k.shape[3] != d:
+        raise ValueError("local_attention_merge: k/v shape mismatch")
+    sk = None
+    if sinks is not None:
+        if sinks.dtype != torch.float32 or sinks.numel() != hq or not sinks.is_contiguous():
+            raise ValueError("sinks must be a contiguous float32 [Hq] tensor")
+        sk = sinks.data_ptr()
+    with torch.cuda.device(q.device):
+        rc = lib.d2sd_local_attention_merge(
+            q.data_ptr(), q.stride(0), q.stride(1), q.stride(2), k.data_ptr(), v.data_ptr(),
+            k.stride(0), k.stride(1), k.stride(2), out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
+            lse.data_ptr(), lse.stride(0), lse.stride(1), bsz, lb, hq, hkv, d, int(bool(causal)),
+            float(sm_scale), sk, int(bool(lse_base2)), _stream())
+    check(rc, "local_attention_merge")
+
+
+__all__ = ["single_prefill_with_kv_cache", "merge_state_in_place", "merge_state", "local_attention_merge"]
+_ = _lib

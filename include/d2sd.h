@@ -1,0 +1,233 @@
+/*
+ * d2sd.h — C ABI of the MI355X (gfx950) cascade tree-verification attention
+ * library `libd2sd.so`.
+ *
+ * Every entry point takes raw device pointers, element strides (int64, in
+ * units of elements, not bytes), plain sizes and a hipStream_t, and returns
+ * 0 (D2SD_OK) or a non-zero status; d2sd_last_error() then holds a message.
+ * Nothing here allocates device memory except d2sd_graph_end_capture (the
+ * graph executable) — scratch space is always caller-provided.  The launch
+ * entry points never synchronise the host, so they may be captured into a
+ * hipGraph.
+ *
+ * Tensor conventions (all bf16 = bfloat16, lse = float32):
+ *   q   : [qo_len, num_qo_heads, head_dim]      (NHD; head_dim contiguous)
+ *   k,v : [kv_len, num_kv_heads, head_dim]      (NHD), or any layout
+ *         expressible with (stride_tok, stride_head) — e.g. the
+ *         [num_kv_heads, kv_len, head_dim] DynamicCache layout (HND)
+ *   o   : like q
+ *   lse : [qo_len, num_qo_heads], natural log unless lse_base2 != 0
+ * Query head h reads kv head h / (num_qo_heads / num_kv_heads)  (GQA).
+ * head_dim must be 64 or 128; pointers must be 16-byte aligned and every
+ * stride a multiple of 8 elements.
+ */
+#ifndef D2SD_H_
+#define D2SD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* d2sd_stream_t; /* == hipStream_t */
+
+#define D2SD_OK 0
+#define D2SD_ERR_INVALID_ARG 1
+#define D2SD_ERR_UNSUPPORTED 2
+#define D2SD_ERR_WORKSPACE 3
+#define D2SD_ERR_HIP 4
+
+#define D2SD_KV_BF16 0
+#define D2SD_KV_FP8_E4M3 1 /* OCP e4m3fn bytes, dequantised with per-kv-head fp32 scales */
+
+#define D2SD_MASK_NONE 0
+#define D2SD_MASK_CAUSAL 1 /* key j visible to query i iff j <= i + (kv_len - qo_len) */
+#define D2SD_MASK_TREE 2   /* ancestor bitmask, see d2sd_cascade_run_args */
+
+/* Message for the last failed call on this thread ("" if none). */
+const char* d2sd_last_error(void);
+/* Library version string. */
+const char* d2sd_version(void);
+
+/* ------------------------------------------------------------------------
+ * merge_state_in_place
+ * Replaces flashinfer.merge_state_in_place(v, s, v_other, s_other) as called
+ * at generation/verification.py:163-165, model/cascade_graph.py:58-60 and
+ * model/dflash.py:131-133.
+ *   s' = logaddexp(s, s_other);  v' = v*e^(s-s') + v_other*e^(s_other-s')
+ * v: [seq_len, num_heads, head_dim] bf16 (updated), s: [seq_len, num_heads]
+ * fp32 (updated).  An operand with lse = -inf contributes nothing.
+ * ---------------------------------------------------------------------- */
+int d2sd_merge_state_in_place(void* v, int64_t v_stride_n, int64_t v_stride_h,
+                              float* s, int64_t s_stride_n,
+                              const void* v_other, int64_t vo_stride_n, int64_t vo_stride_h,
+                              const float* s_other, int64_t so_stride_n,
+                              int seq_len, int num_heads, int head_dim, int lse_base2,
+                              d2sd_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * single_prefill_with_kv_cache
+ * Replaces flashinfer.single_prefill_with_kv_cache(q, k, v, causal=...,
+ * return_lse=True, sm_scale=...) as called at generation/verification.py:145
+ * (shared prefix, causal=False), verification.py:159 (per-branch local,
+ * causal=True), model/cascade_graph.py:54 and model/dflash.py:112,127.
+ * window_left >= 0 keeps only the last window_left keys for every query
+ * (the prefix truncation rule of generation/verification.py:133-135);
+ * -1 disables it.  lse may be NULL.  The workspace (device memory, at least
+ * d2sd_single_prefill_workspace_size() bytes) holds split-KV partials.
+ * ---------------------------------------------------------------------- */
+size_t d2sd_single_prefill_workspace_size(int qo_len, int kv_len, int num_qo_heads,
+                                          int num_kv_heads, int head_dim, int window_left);
+int d2sd_single_prefill_with_kv_cache(const void* q, int64_t q_stride_n, int64_t q_stride_h,
+                                      const void* k, const void* v,
+                                      int64_t kv_stride_n, int64_t kv_stride_h,
+                                      void* o, int64_t o_stride_n, int64_t o_stride_h,
+                                      float* lse, int qo_len, int kv_len, int num_qo_heads,
+                                      int num_kv_heads, int head_dim, int causal,
+                                      int window_left, float sm_scale, int lse_base2,
+                                      void* workspace, size_t workspace_bytes,
+                                      d2sd_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * local_attention_merge
+ * One launch for the whole per-row loop that CascadeGraphRunner captures
+ * (model/cascade_graph.py:52-60): for every row i < bsz,
+ *   (o_l, lse_l) = attention(q[i], k[i], v[i], causal)   (block_len x block_len)
+ *   merge_state_in_place(out[i], lse[i], o_l, lse_l)
+ * q/out: [bsz, block_len, num_qo_heads, head_dim]; k/v: [bsz, block_len,
+ * num_kv_heads, head_dim]; lse: [bsz, block_len, num_qo_heads] fp32.
+ * sinks (nullable, [num_qo_heads] fp32) additionally applies the GPT-OSS
+ * rescale out *= sigmoid(lse - sink) of generation/verification.py:173-176
+ * after the merge (lse itself keeps the merged value).
+ * ---------------------------------------------------------------------- */
+int d2sd_local_attention_merge(const void* q, int64_t q_stride_b, int64_t q_stride_n,
+                               int64_t q_stride_h, const void* k, const void* v,
+                               int64_t kv_stride_b, int64_t kv_stride_n, int64_t kv_stride_h,
+                               void* out, int64_t o_stride_b, int64_t o_stride_n,
+                               int64_t o_stride_h, float* lse, int64_t lse_stride_b,
+                               int64_t lse_stride_n, int bsz, int block_len, int num_qo_heads,
+                               int num_kv_heads, int head_dim, int causal, float sm_scale,
+                               const float* sinks, int lse_base2, d2sd_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * hipGraph capture / replay owned by the library.
+ * Replaces torch.cuda.CUDAGraph capture (model/cascade_graph.py:67-71) and
+ * replay (cascade_graph.py:107).  Capture runs on `stream` (which must not
+ * be the null stream) in thread-local capture mode.
+ * ---------------------------------------------------------------------- */
+int d2sd_graph_begin_capture(d2sd_stream_t stream);
+int d2sd_graph_end_capture(d2sd_stream_t stream, void** graph_exec);
+int d2sd_graph_launch(void* graph_exec, d2sd_stream_t stream);
+int d2sd_graph_destroy(void* graph_exec);
+
+/* ------------------------------------------------------------------------
+ * Cascade verify attention: plan() / run().
+ * No reference counterpart calls a plan(); this pair is the single-call form
+ * of generation/verification.py:127-176 (prefix fetch + window, shared-prefix
+ * attention, per-branch attention, merge, GPT-OSS sink) over a token TREE of
+ * unique candidate nodes instead of bsz duplicated rows, for a batch of
+ * requests.
+ *
+ * Request r owns query/suffix tokens [qo_indptr[r], qo_indptr[r+1]) of q,
+ * k_suffix, v_suffix, out and lse, and a prefix of prefix_len[r] keys.
+ * Suffix key j is visible to suffix query i of request r iff bit j of
+ *   tree_mask[(qo_indptr[r] + i) * mask_words + j / 64]
+ * is set (bit (j % 64), little-endian 64-bit words).  mask_mode may instead
+ * be D2SD_MASK_CAUSAL (chain) or D2SD_MASK_NONE (all suffix keys visible,
+ * the non-causal DTA-draft case of model/dflash.py:127-130).
+ *
+ * The prefix is either contiguous (page_size == 0): key t of request r at
+ *   k_prefix + (prefix_tok_indptr[r] + t)*prefix_stride_tok + h*prefix_stride_head
+ * (prefix_tok_indptr may be NULL: all requests then start at token 0), or
+ * paged (page_size a power of two): key t at
+ *   k_prefix + page_table[page_indptr[r] + t/page_size]*prefix_stride_page
+ *            + (t % page_size)*prefix_stride_tok + h*prefix_stride_head.
+ * window_left >= 0 keeps the last window_left prefix keys (all queries).
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  int num_reqs;
+  const int32_t* qo_indptr;  /* host, [num_reqs + 1] */
+  const int32_t* prefix_len; /* host, [num_reqs] */
+  int num_qo_heads;
+  int num_kv_heads;
+  int head_dim;
+  int window_left;     /* -1: full prefix */
+  int kv_dtype;        /* D2SD_KV_* of the prefix cache */
+  int num_cus;         /* 0: query the device */
+  int max_splits;      /* 0: no limit */
+  int waves_per_block; /* 0: choose; else 4 or 8 */
+} d2sd_cascade_plan_desc;
+
+typedef struct {
+  int num_work;         /* attention workgroups */
+  int num_merge;        /* merge items (tile groups with > 1 partial) */
+  int waves_per_block;  /* 4 or 8 */
+  int rows_per_tile;    /* 32 * waves_per_block */
+  int num_slots;        /* split-KV partial slots */
+  int plan_ints;        /* int32 entries written to host_plan */
+  size_t workspace_bytes; /* float workspace for partials */
+  int max_splits_used;  /* 0: no prefix work at all */
+  int num_reqs;
+  int num_qo_heads;
+  int num_kv_heads;
+  int head_dim;
+  int kv_dtype;
+} d2sd_cascade_plan_info;
+
+/* Fills host_plan (capacity host_plan_ints int32) with the work list; the
+ * caller copies these plan_ints int32 values to device memory and passes that
+ * pointer to d2sd_cascade_run.  Pass host_plan = NULL to only fill info. */
+int d2sd_cascade_plan(const d2sd_cascade_plan_desc* desc, int32_t* host_plan,
+                      size_t host_plan_ints, d2sd_cascade_plan_info* info);
+
+typedef struct {
+  const int32_t* plan;      /* device copy of the host plan */
+  const int32_t* qo_indptr; /* device, [num_reqs + 1] */
+  const void* q;            /* [total_q, Hq, D] bf16 */
+  int64_t q_stride_n, q_stride_h;
+  const void* k_suffix;     /* [total_q, Hkv, D] bf16 */
+  const void* v_suffix;
+  int64_t suffix_stride_n, suffix_stride_h;
+  int mask_mode;            /* D2SD_MASK_* for the suffix level */
+  int mask_words;           /* 64-bit words per tree-mask row */
+  const uint64_t* tree_mask;
+  const void* k_prefix;     /* bf16 or fp8 bytes */
+  const void* v_prefix;
+  int64_t prefix_stride_tok, prefix_stride_head, prefix_stride_page;
+  int page_size;            /* 0: contiguous */
+  const int32_t* page_indptr;       /* device, [num_reqs + 1] (paged) */
+  const int32_t* page_table;        /* device (paged) */
+  const int32_t* prefix_tok_indptr; /* device, [num_reqs] (contiguous; nullable) */
+  const int32_t* prefix_len;        /* device, [num_reqs] */
+  const float* k_scale;     /* fp8: [Hkv] */
+  const float* v_scale;
+  const float* sinks;       /* nullable, [Hq] */
+  void* out;                /* [total_q, Hq, D] bf16 */
+  int64_t o_stride_n, o_stride_h;
+  float* lse;               /* nullable, [total_q, Hq] */
+  int64_t lse_stride_n;
+  float sm_scale;
+  int lse_base2;
+  void* workspace;
+  size_t workspace_bytes;
+} d2sd_cascade_run_args;
+
+/* run = attention then merge.  The two halves are also exported: attention
+ * (prefix chunks + suffix trees, one launch) writes split partials to the
+ * workspace (or the final output for rows with a single producer); merge
+ * (one launch) combines the partials, applies the sink and writes out / lse.
+ * Between the two, the workspace holds the only copy of the partial state. */
+int d2sd_cascade_run(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* args,
+                     d2sd_stream_t stream);
+int d2sd_cascade_attention(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* args,
+                           d2sd_stream_t stream);
+int d2sd_cascade_merge(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* args,
+                       d2sd_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* D2SD_H_ */

@@ -1,0 +1,234 @@
+"""CPU oracle for cascade tree-verification attention.
+
+TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and bench.py's
+CPU-baseline leg may import this module, and only as the checker / the timed
+CPU baseline — never as a product path.
+
+It restates the reference's verify-attention algorithm on the CPU in float64
+(or float32 for the timed baseline):
+
+  reference path                                   function here
+  generation/verification.py:127-135 prefix+window  window_prefix_ref
+  verification.py:145-150 (flashinfer single prefill, shared level, non-causal)
+  verification.py:159-162 (local level, causal)    single_prefill_ref / attention_ref
+  verification.py:163-165, cascade_graph.py:58-60 (flashinfer merge_state_in_place)
+                                                   merge_state_ref
+  verification.py:173-176 (GPT-OSS sink)           sink_rescale_ref
+  verification.py:127-176 as a whole (row layout)  cascade_verify_rows_ref
+  the same over unique tree nodes, single pass     cascade_tree_ref
+
+FlashInfer itself (flashinfer-python>=0.2.0, requirements.txt:13) is not
+vendored in the reference and not installed here.  Its published algorithm for
+the two calls the reference makes is restated from its documentation:
+softmax attention with scale sm_scale, query head h reading kv head
+h // (Hq // Hkv), causal alignment to the bottom-right corner
+(key j visible to query i iff j <= i + kv_len - qo_len), and merge_state
+  s = log(e^{s_a} + e^{s_b}),  v = (v_a e^{s_a} + v_b e^{s_b}) / e^{s}.
+The LSE here is the natural log; FlashInfer's own LSE base (its kernels work
+in the exp2 domain) is parity unpinned, as are its bf16 rounding of P before
+P.V and its accumulation order (bit-level parity).
+
+How each function is pinned (tests/test_oracle.py): against pure-Python
+float64 loops in tests/golden/make_golden.py (written independently of this
+module) and the committed fixtures they produce; against invariants (split
+prefix merged == unsplit; merge commutative / associative; empty prefix ->
+pure tree attention; chain tree == causal; constant V -> that V; page-table
+permutation invariance); against the reference's three-step row-layout
+algorithm vs. the single-pass tree form; and, for the sink, against the
+installed transformers GPT-OSS eager attention (a library routine).
+"""
+from __future__ import annotations
+
+import math
+from typing import List, Optional, Tuple
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+Tensor = torch.Tensor
+
+
+def _expand_kv(k: Tensor, hq: int) -> Tensor:
+    """[L, Hkv, D] -> [L, Hq, D] with query head h reading kv head h // g."""
+    hkv = k.shape[1]
+    if hq % hkv:
+        raise ValueError("Hq must be a multiple of Hkv")
+    return k.repeat_interleave(hq // hkv, dim=1)
+
+
+def attention_ref(q: Tensor, k: Tensor, v: Tensor, mask: Optional[Tensor], sm_scale: float,
+                  dtype: torch.dtype = torch.float64) -> Tuple[Tensor, Tensor]:
+    """Masked GQA softmax attention.  q [n, Hq, D], k/v [L, Hkv, D],
+    mask bool [n, L] (True = visible) or None.  Returns (o [n, Hq, D],
+    lse [n, Hq]) in `dtype`; rows with no visible key give o = 0, lse = -inf."""
+    n, hq, d = q.shape
+    L = k.shape[0]
+    qd, kd, vd = q.to(dtype), _expand_kv(k.to(dtype), hq), _expand_kv(v.to(dtype), hq)
+    if L == 0:
+        return torch.zeros(n, hq, d, dtype=dtype), torch.full((n, hq), -math.inf, dtype=dtype)
+    scores = torch.einsum("nhd,lhd->hnl", qd, kd) * sm_scale          # [Hq, n, L]
+    if mask is not None:
+        scores = scores.masked_fill(~mask.bool()[None], -math.inf)
+    lse = torch.logsumexp(scores, dim=-1)                              # [Hq, n]
+    empty = torch.isinf(lse) & (lse < 0)
+    p = torch.exp(scores - torch.where(empty, torch.zeros_like(lse), lse)[..., None])
+    p = torch.where(empty[..., None], torch.zeros_like(p), p)
+    o = torch.einsum("hnl,lhd->nhd", p, vd)
+    return o, lse.transpose(0, 1).contiguous()
+
+
+def attention_sdpa_ref(q: Tensor, k: Tensor, v: Tensor, mask: Optional[Tensor], sm_scale: float,
+                       dtype: torch.dtype = torch.float32) -> Tuple[Tensor, Tensor]:
+    """Same contract via torch.nn.functional.scaled_dot_product_attention
+    (enable_gqa) for O and torch.logsumexp for LSE — the formulation the CPU
+    baseline times.  Every row must have at least one visible key."""
+    n, hq, d = q.shape
+    qd = q.to(dtype).transpose(0, 1)[None]                             # [1, Hq, n, D]
+    kd = k.to(dtype).transpose(0, 1)[None]                             # [1, Hkv, L, D]
+    vd = v.to(dtype).transpose(0, 1)[None]
+    m = mask.bool()[None, None] if mask is not None else None
+    o = F.scaled_dot_product_attention(qd, kd, vd, attn_mask=m, scale=sm_scale, enable_gqa=True)
+    scores = torch.matmul(qd, _expand_kv(k.to(dtype), hq).transpose(0, 1)[None].transpose(-1, -2)) * sm_scale
+    if m is not None:
+        scores = scores.masked_fill(~m, -math.inf)
+    lse = torch.logsumexp(scores, dim=-1)[0].transpose(0, 1)
+    return o[0].transpose(0, 1).contiguous(), lse.contiguous()
+
+
+def causal_mask(qo_len: int, kv_len: int) -> Tensor:
+    """FlashInfer causal rule: key j visible to query i iff j <= i + kv_len - qo_len."""
+    i = torch.arange(qo_len)[:, None]
+    j = torch.arange(kv_len)[None, :]
+    return j <= i + (kv_len - qo_len)
+
+
+def single_prefill_ref(q: Tensor, k: Tensor, v: Tensor, causal: bool, sm_scale: float,
+                       dtype: torch.dtype = torch.float64) -> Tuple[Tensor, Tensor]:
+    """flashinfer.single_prefill_with_kv_cache(q, k, v, causal, return_lse=True,
+    sm_scale) as called at generation/verification.py:145-148 and 159-162."""
+    mask = causal_mask(q.shape[0], k.shape[0]) if causal else None
+    return attention_ref(q, k, v, mask, sm_scale, dtype)
+
+
+def merge_state_ref(v: Tensor, s: Tensor, v_other: Tensor, s_other: Tensor) -> Tuple[Tensor, Tensor]:
+    """flashinfer.merge_state_in_place semantics (generation/verification.py:163-165;
+    model/cascade_graph.py:58-60), out of place, in float64.  An operand with
+    s = -inf contributes nothing; both -inf leaves (v, -inf)."""
+    v, s, v_other, s_other = (x.to(torch.float64) for x in (v, s, v_other, s_other))
+    m = torch.maximum(s, s_other)
+    both_empty = torch.isinf(m) & (m < 0)
+    m_safe = torch.where(both_empty, torch.zeros_like(m), m)
+    ea, eb = torch.exp(s - m_safe), torch.exp(s_other - m_safe)
+    tot = ea + eb
+    tot_safe = torch.where(both_empty, torch.ones_like(tot), tot)
+    out = (v * ea[..., None] + v_other * eb[..., None]) / tot_safe[..., None]
+    out = torch.where(both_empty[..., None], v, out)
+    lse = torch.where(both_empty, s, m_safe + torch.log(tot_safe))
+    return out, lse
+
+
+def sink_rescale_ref(o: Tensor, lse: Tensor, sinks: Tensor) -> Tensor:
+    """GPT-OSS sink (generation/verification.py:173-176): O * sigmoid(lse - sink_h),
+    lse = the merged natural-log LSE [..., Hq], sinks [Hq]."""
+    return o * torch.sigmoid(lse.to(torch.float64) - sinks.to(torch.float64))[..., None]
+
+
+def window_prefix_ref(k: Tensor, v: Tensor, window: int) -> Tuple[Tensor, Tensor]:
+    """Sliding-window prefix rule (generation/verification.py:132-135): if the
+    prefix [L, Hkv, D] is longer than `window`, keep its last `window` keys for
+    every query; -1 / None keeps all."""
+    if window is not None and window >= 0 and k.shape[0] > window:
+        return k[k.shape[0] - window:], v[v.shape[0] - window:]
+    return k, v
+
+
+def cascade_verify_rows_ref(q_rows: Tensor, k_rows: Tensor, v_rows: Tensor, k_prefix: Tensor,
+                            v_prefix: Tensor, sm_scale: float, window: int = -1,
+                            sinks: Optional[Tensor] = None, causal: bool = True) -> Tuple[Tensor, Tensor]:
+    """The reference's per-layer attention block, step by step
+    (generation/verification.py:127-176), on bsz candidate rows:
+      q_rows [bsz, Lb, Hq, D]; k_rows / v_rows [bsz, Lb, Hkv, D] (the rows' new
+      KV); k_prefix / v_prefix [L, Hkv, D] (NHD).
+    1. window truncation of the prefix (132-135)
+    2. shared level: all bsz*Lb queries vs the prefix, non-causal (142-150)
+    3. per row i: local causal attention over the row's own Lb keys (158-162)
+    4. merge_state_in_place of the local into the shared state (163-165)
+    5. GPT-OSS sink rescale with the merged LSE (173-176)
+    Returns (out [bsz, Lb, Hq, D], lse [bsz, Lb, Hq]) in float64."""
+    bsz, lb, hq, d = q_rows.shape
+    kp, vp = window_prefix_ref(k_prefix, v_prefix, window)
+    q_all = q_rows.reshape(bsz * lb, hq, d)
+    o_sh, lse_sh = single_prefill_ref(q_all, kp, vp, causal=False, sm_scale=sm_scale)
+    o_sh = o_sh.view(bsz, lb, hq, d)
+    lse_sh = lse_sh.view(bsz, lb, hq)
+    outs, lses = [], []
+    for i in range(bsz):
+        o_l, lse_l = single_prefill_ref(q_rows[i], k_rows[i], v_rows[i], causal=causal, sm_scale=sm_scale)
+        o_m, lse_m = merge_state_ref(o_sh[i], lse_sh[i], o_l, lse_l)
+        outs.append(o_m)
+        lses.append(lse_m)
+    out = torch.stack(outs)
+    lse = torch.stack(lses)
+    if sinks is not None:
+        out = sink_rescale_ref(out, lse, sinks)
+    return out, lse
+
+
+def cascade_tree_ref(q: Tensor, k_suffix: Tensor, v_suffix: Tensor, k_prefix: Optional[Tensor],
+                     v_prefix: Optional[Tensor], anc_mask: Tensor, sm_scale: float, window: int = -1,
+                     sinks: Optional[Tensor] = None, dtype: torch.dtype = torch.float64,
+                     use_sdpa: bool = False) -> Tuple[Tensor, Tensor]:
+    """Single-pass form over unique tree nodes: one masked softmax over
+    [prefix || suffix] keys with mask [ones(N, L_eff) || M], M[i, j] = node j is
+    i or an ancestor of i.  q [N, Hq, D], k/v_suffix [N, Hkv, D],
+    k/v_prefix [L, Hkv, D] or None."""
+    n = q.shape[0]
+    if k_prefix is not None and k_prefix.shape[0] > 0:
+        kp, vp = window_prefix_ref(k_prefix, v_prefix, window)
+        k_all = torch.cat([kp.to(k_suffix.dtype), k_suffix], 0)
+        v_all = torch.cat([vp.to(v_suffix.dtype), v_suffix], 0)
+        mask = torch.cat([torch.ones(n, kp.shape[0], dtype=torch.bool), anc_mask.bool()], 1)
+    else:
+        k_all, v_all, mask = k_suffix, v_suffix, anc_mask.bool()
+    fn = attention_sdpa_ref if use_sdpa else attention_ref
+    o, lse = fn(q, k_all, v_all, mask, sm_scale, dtype)
+    if sinks is not None:
+        o = o * torch.sigmoid(lse.to(dtype) - sinks.to(dtype))[..., None]
+    return o, lse
+
+
+def ancestor_mask_from_rows(node_index: np.ndarray, num_nodes: int) -> np.ndarray:
+    """Ancestor mask rebuilt from the row layout alone: node j is visible to
+    node i iff some row holds i at position p and j at a position <= p (the
+    reference's per-row causal rule, verification.py:161)."""
+    m = np.zeros((num_nodes, num_nodes), dtype=bool)
+    for row in np.asarray(node_index):
+        for p, i in enumerate(row):
+            m[int(i), [int(x) for x in row[:p + 1]]] = True
+    return m
+
+
+def fp8_dequant_ref(x: Tensor, scale: Tensor) -> Tensor:
+    """fp8 e4m3fn [.., Hkv, D] (or [pages, Hkv, P, D]) times a per-kv-head scale,
+    in float32.  `head_dim_axis` of the scale is the Hkv axis given by the caller
+    via broadcasting."""
+    return x.to(torch.float32) * scale.to(torch.float32)
+
+
+def gather_paged(pool: Tensor, page_table: List[int], length: int, layout: str = "HND") -> Tensor:
+    """Paged pool [pages, Hkv, P, D] (HND) or [pages, P, Hkv, D] (NHD) ->
+    contiguous [length, Hkv, D] in page_table order."""
+    if layout == "HND":
+        pages = pool[torch.as_tensor(list(page_table), dtype=torch.long)].permute(0, 2, 1, 3)
+    else:
+        pages = pool[torch.as_tensor(list(page_table), dtype=torch.long)]
+    flat = pages.reshape(-1, pages.shape[2], pages.shape[3])
+    return flat[:length]
+
+
+__all__ = [
+    "attention_ref", "attention_sdpa_ref", "causal_mask", "single_prefill_ref", "merge_state_ref",
+    "sink_rescale_ref", "window_prefix_ref", "cascade_verify_rows_ref", "cascade_tree_ref",
+    "ancestor_mask_from_rows", "fp8_dequant_ref", "gather_paged",
+]

@@ -1,0 +1,352 @@
+"""GPU parity of the HIP kernels against the CPU oracle (oracle/cascade_oracle.py).
+
+Tolerances (bf16 outputs vs the float64 oracle on the same bf16 inputs):
+  O   : max |err| <= 2e-2 and mean |err| <= 2e-3
+  LSE : max |err| <= 1e-3 (natural log)
+  greedy argmax of a fixed random lm_head projection: identical.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import cascade_oracle as orc
+import d2sd
+from d2sd import tree as dtree
+from d2sd import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+O_MAX, O_MEAN, LSE_MAX = 2e-2, 2e-3, 1e-3
+DEV = "cuda"
+
+
+def check_close(o, o_ref, lse=None, lse_ref=None, tag=""):
+    o = o.detach().float().cpu().double()
+    o_ref = o_ref.double()
+    err = (o - o_ref).abs()
+    assert torch.isfinite(o).all(), f"{tag}: non-finite output"
+    assert err.max().item() <= O_MAX, f"{tag}: O max err {err.max().item():.3e}"
+    assert err.mean().item() <= O_MEAN, f"{tag}: O mean err {err.mean().item():.3e}"
+    if lse is not None:
+        lse = lse.detach().cpu().double()
+        lse_ref = lse_ref.double()
+        fin = torch.isfinite(lse_ref)
+        assert torch.equal(torch.isfinite(lse), fin), f"{tag}: LSE finiteness differs"
+        if fin.any():
+            e = (lse[fin] - lse_ref[fin]).abs().max().item()
+            assert e <= LSE_MAX, f"{tag}: LSE max err {e:.3e}"
+
+
+def bf16_randn(gen, *shape):
+    return torch.randn(*shape, generator=gen).to(torch.bfloat16)
+
+
+# ------------------------------------------------------------ merge_state
+def test_merge_state_golden(golden):
+    c = golden["merge"]
+    v = torch.from_numpy(c["va"]).to(torch.bfloat16).to(DEV)
+    s = torch.from_numpy(c["sa"]).float().to(DEV)
+    vb = torch.from_numpy(c["vb"]).to(torch.bfloat16).to(DEV)
+    sb = torch.from_numpy(c["sb"]).float().to(DEV)
+    d2sd.merge_state_in_place(v, s, vb, sb)
+    torch.cuda.synchronize()
+    check_close(v, torch.from_numpy(c["v"]), s, torch.from_numpy(c["s"]), "merge golden")
+
+
+@pytest.mark.parametrize("n,h,d", [(160, 32, 128), (33, 64, 64), (1, 8, 128)])
+def test_merge_state_random(n, h, d):
+    gen = torch.Generator().manual_seed(n + h + d)
+    va, vb = bf16_randn(gen, n, h, d), bf16_randn(gen, n, h, d)
+    sa, sb = torch.randn(n, h, generator=gen) * 3, torch.randn(n, h, generator=gen) * 3
+    sa[0, 0] = -math.inf
+    ref_v, ref_s = orc.merge_state_ref(va, sa, vb, sb)
+    v, s = va.to(DEV), sa.to(DEV)
+    d2sd.merge_state_in_place(v, s, vb.to(DEV), sb.to(DEV))
+    torch.cuda.synchronize()
+    check_close(v, ref_v, s, ref_s, "merge random")
+
+
+# --------------------------------------------------- single_prefill (drop-in)
+@pytest.mark.parametrize("qo,kv,hq,hkv,d,causal,layout", [
+    (160, 4096, 32, 8, 128, False, "NHD"),   # verification.py:145 shared level, 5 rows x 32
+    (32, 32, 32, 8, 128, True, "NHD"),       # verification.py:159 local level
+    (5, 70, 8, 2, 64, False, "NHD"),
+    (37, 300, 64, 8, 64, True, "HND"),
+    (1, 1000, 32, 8, 128, False, "HND"),
+    (64, 1024, 32, 8, 128, False, "HND"),
+    (200, 130, 8, 8, 128, True, "NHD"),
+])
+def test_single_prefill(qo, kv, hq, hkv, d, causal, layout):
+    gen = torch.Generator().manual_seed(qo * 7 + kv)
+    q = bf16_randn(gen, qo, hq, d)
+    k, v = bf16_randn(gen, kv, hkv, d), bf16_randn(gen, kv, hkv, d)
+    o_ref, lse_ref = orc.single_prefill_ref(q, k, v, causal, d ** -0.5)
+    kd, vd = k.to(DEV), v.to(DEV)
+    if layout == "HND":
+        kd, vd = kd.transpose(0, 1).contiguous(), vd.transpose(0, 1).contiguous()
+    o, lse = d2sd.single_prefill_with_kv_cache(q.to(DEV), kd, vd, causal=causal, kv_layout=layout,
+                                               sm_scale=d ** -0.5, return_lse=True)
+    torch.cuda.synchronize()
+    check_close(o, o_ref, lse, lse_ref, f"single_prefill {qo}x{kv}")
+
+
+def test_single_prefill_strided_q():
+    """q as the transposed view the reference builds (verification.py:142-144)."""
+    gen = torch.Generator().manual_seed(11)
+    bsz, lb, hq, hkv, d, L = 4, 32, 32, 8, 128, 777
+    q4 = bf16_randn(gen, bsz, hq, lb, d)           # [bsz, Hq, Lb, D] as after RoPE
+    k, v = bf16_randn(gen, L, hkv, d), bf16_randn(gen, L, hkv, d)
+    q_fi = q4.to(DEV).transpose(1, 2)              # [bsz, Lb, Hq, D] view
+    q_flat = q_fi.reshape(bsz * lb, hq, d)
+    o, lse = d2sd.single_prefill_with_kv_cache(q_flat, k.to(DEV), v.to(DEV), causal=False,
+                                               sm_scale=d ** -0.5, return_lse=True)
+    torch.cuda.synchronize()
+    o_ref, lse_ref = orc.single_prefill_ref(q4.transpose(1, 2).reshape(bsz * lb, hq, d), k, v, False, d ** -0.5)
+    check_close(o, o_ref, lse, lse_ref, "strided q")
+
+
+# ----------------------------------------- CascadeGraphRunner (drop-in path)
+@pytest.mark.parametrize("bsz,causal,with_sinks", [(5, True, False), (3, False, False), (2, True, True)])
+def test_reference_row_flow(bsz, causal, with_sinks):
+    """The reference's flow (verification.py:142-176): shared single prefill over
+    all rows, then CascadeGraphRunner.run (local attention + merge), then sink."""
+    gen = torch.Generator().manual_seed(bsz)
+    lb, hq, hkv, d, L = 32, 32, 8, 128, 1000
+    q = bf16_randn(gen, bsz, lb, hq, d)
+    kl, vl = bf16_randn(gen, bsz, lb, hkv, d), bf16_randn(gen, bsz, lb, hkv, d)
+    kp, vp = bf16_randn(gen, L, hkv, d), bf16_randn(gen, L, hkv, d)
+    sinks = torch.randn(hq, generator=gen) if with_sinks else None
+    o_ref, lse_ref = orc.cascade_verify_rows_ref(q, kl, vl, kp, vp, d ** -0.5, -1, sinks, causal=causal)
+    runner = d2sd.CascadeGraphRunner(lb, hq, hkv, d, torch.bfloat16, torch.device(DEV), d ** -0.5, causal,
+                                     sinks=sinks)
+    qd = q.to(DEV)
+    o_sh, lse_sh = d2sd.single_prefill_with_kv_cache(qd.reshape(bsz * lb, hq, d), kp.to(DEV), vp.to(DEV),
+                                                     causal=False, return_lse=True, sm_scale=d ** -0.5)
+    o_sh = o_sh.view(bsz, lb, hq, d)
+    lse_sh = lse_sh.view(bsz, lb, hq)
+    runner.run(qd, kl.to(DEV), vl.to(DEV), o_sh, lse_sh)
+    torch.cuda.synchronize()
+    check_close(o_sh, o_ref, lse_sh, lse_ref, "row flow")
+    # run_direct (no staging copies) gives the same numbers
+    o2, l2 = d2sd.single_prefill_with_kv_cache(qd.reshape(bsz * lb, hq, d), kp.to(DEV), vp.to(DEV),
+                                               causal=False, return_lse=True, sm_scale=d ** -0.5)
+    o2, l2 = o2.view(bsz, lb, hq, d), l2.view(bsz, lb, hq)
+    runner.run_direct(qd, kl.to(DEV), vl.to(DEV), o2, l2)
+    torch.cuda.synchronize()
+    assert torch.equal(o2, o_sh) and torch.equal(l2, lse_sh)
+
+
+# --------------------------------------------------- cascade plan / run
+def _run_problem(prob, layers=1, **plan_kw):
+    mp = wl.materialize(prob, DEV, layers=layers)
+    attn = d2sd.CascadeVerifyAttention(DEV)
+    wl.plan_for(attn, mp, **plan_kw)
+    outs = []
+    for lt in mp.layers:
+        o, lse = attn.run(lt.q, lt.k_suffix, lt.v_suffix, lt.k_prefix, lt.v_prefix)
+        outs.append((o, lse))
+    torch.cuda.synchronize()
+    return mp, attn, outs
+
+
+def _oracle_request(mp, li, r, dtype=torch.float64):
+    prob = mp.problem
+    lt = mp.layers[li]
+    qo = prob.qo_indptr
+    a, b = qo[r], qo[r + 1]
+    req = prob.requests[r]
+    L = req.prefix_len
+    if L > 0:
+        if prob.page_size > 0:
+            pages = mp.page_table[mp.page_indptr[r]:mp.page_indptr[r + 1]].cpu().tolist()
+            kp = orc.gather_paged(lt.k_prefix.cpu(), pages, L)
+            vp = orc.gather_paged(lt.v_prefix.cpu(), pages, L)
+        else:
+            s = mp.prefix_tok_indptr[r]
+            kp = lt.k_prefix.cpu()[:, s:s + L].transpose(0, 1)
+            vp = lt.v_prefix.cpu()[:, s:s + L].transpose(0, 1)
+        if prob.kv_dtype == torch.float8_e4m3fn:
+            kp = kp.float() * mp.k_scale.cpu()[None, :, None]
+            vp = vp.float() * mp.v_scale.cpu()[None, :, None]
+    else:
+        kp = vp = None
+    m = torch.as_tensor(req.tree.ancestor_mask())
+    sinks = mp.sinks.cpu() if mp.sinks is not None else None
+    return orc.cascade_tree_ref(lt.q.cpu()[a:b], lt.k_suffix.cpu()[a:b], lt.v_suffix.cpu()[a:b], kp, vp, m,
+                                prob.head_dim ** -0.5, prob.window_left, sinks, dtype=dtype)
+
+
+def _check_problem(mp, outs, reqs=None, layers=None, dtype=torch.float64, tag=""):
+    prob = mp.problem
+    qo = prob.qo_indptr
+    for li in (layers if layers is not None else range(len(outs))):
+        o, lse = outs[li]
+        for r in (reqs if reqs is not None else range(len(prob.requests))):
+            o_ref, lse_ref = _oracle_request(mp, li, r, dtype)
+            a, b = qo[r], qo[r + 1]
+            check_close(o[a:b], o_ref, lse[a:b], lse_ref, f"{tag} layer {li} req {r}")
+
+
+def test_cascade_golden_d64(golden):
+    _cascade_golden(golden["tree_d64"])
+
+
+def test_cascade_golden_d128(golden):
+    _cascade_golden(golden["tree_d128"])
+
+
+def _cascade_golden(c):
+    q = torch.from_numpy(c["q"]).to(torch.bfloat16).to(DEV)
+    ks = torch.from_numpy(c["k_suffix"]).to(torch.bfloat16).to(DEV)
+    vs = torch.from_numpy(c["v_suffix"]).to(torch.bfloat16).to(DEV)
+    kp = torch.from_numpy(c["k_prefix"]).to(torch.bfloat16).to(DEV)
+    vp = torch.from_numpy(c["v_prefix"]).to(torch.bfloat16).to(DEV)
+    n, hq, d = q.shape
+    hkv = ks.shape[1]
+    sinks = torch.from_numpy(c["sinks"]).float() if "sinks" in c else None
+    attn = d2sd.CascadeVerifyAttention(DEV).plan(
+        [0, n], [kp.shape[0]], hq, hkv, d, tree_masks=[dtree.ancestor_mask(c["parents"])], kv_layout="NHD",
+        window_left=int(c["window"]), sinks=sinks, sm_scale=float(c["sm_scale"]))
+    o, lse = attn.run(q, ks, vs, kp, vp)
+    torch.cuda.synchronize()
+    check_close(o, torch.from_numpy(c["o"]), lse, torch.from_numpy(c["lse"]), "golden")
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_cascade_config1(seed):
+    mp, _, outs = _run_problem(wl.config1(seed))
+    _check_problem(mp, outs, tag="cfg1")
+
+
+def test_cascade_config2_two_layers():
+    mp, _, outs = _run_problem(wl.config2(0, layers=2))
+    assert 106 <= mp.problem.total_q <= 150
+    _check_problem(mp, outs, tag="cfg2")
+
+
+def test_cascade_config3_subset():
+    mp, _, outs = _run_problem(wl.config3(0, num_reqs=8))
+    _check_problem(mp, outs, reqs=[0, 5], dtype=torch.float32, tag="cfg3")
+
+
+@pytest.mark.parametrize("sliding", [False, True])
+def test_cascade_config4(sliding):
+    mp, _, outs = _run_problem(wl.config4(0, sliding=sliding))
+    _check_problem(mp, outs, tag="cfg4")
+
+
+def test_cascade_config5_subset():
+    mp, _, outs = _run_problem(wl.config5(0, num_reqs=32))
+    _check_problem(mp, outs, reqs=[0, 31], dtype=torch.float32, tag="cfg5")
+
+
+@pytest.mark.parametrize("L,shared,window,waves", [
+    (0, [16, 4, 9], -1, 0),        # empty prefix: suffix level alone
+    (1, [1], -1, 0),               # single key, single node
+    (65, [40, 1, 39], -1, 4),      # N > 64 nodes (two mask words), L % 64 == 1
+    (130, [30, 0, 17], 100, 8),    # forest (p=0), window inside the prefix
+    (50, [20, 5], 500, 0),         # window longer than the prefix
+])
+def test_cascade_edges(L, shared, window, waves):
+    t = dtree.tree_from_shared_prefixes(shared[0], shared)
+    prob = wl.VerifyProblem("edge", 32, 8, 128, [wl.Request(t, L)], page_size=16 if L % 2 else 0,
+                            window_left=window, seed=L)
+    mp, _, outs = _run_problem(prob, waves_per_block=waves)
+    _check_problem(mp, outs, tag="edge")
+
+
+def test_split_count_does_not_change_result():
+    """Split-KV merge == unsplit (size-independent property at full size)."""
+    prob = wl.config2(3, layers=1)
+    _, _, outs_a = _run_problem(prob)
+    _, _, outs_b = _run_problem(prob, max_splits=1)
+    check_close(outs_a[0][0], outs_b[0][0].float().cpu(), outs_a[0][1], outs_b[0][1].cpu(), "splits")
+
+
+def test_page_permutation_is_bit_invariant():
+    prob = wl.config2(4, layers=1)
+    mp, attn, outs = _run_problem(prob)
+    lt = mp.layers[0]
+    perm = torch.randperm(lt.k_prefix.shape[0], generator=torch.Generator().manual_seed(0)).to(DEV)
+    kp2 = torch.empty_like(lt.k_prefix)
+    vp2 = torch.empty_like(lt.v_prefix)
+    kp2[perm] = lt.k_prefix
+    vp2[perm] = lt.v_prefix
+    table2 = perm[mp.page_table.long()].to(torch.int32)
+    attn2 = d2sd.CascadeVerifyAttention(DEV)
+    p = mp.problem
+    attn2.plan(p.qo_indptr, p.prefix_lens, p.num_qo_heads, p.num_kv_heads, p.head_dim,
+               tree_masks=p.tree_masks(), page_size=16, page_indptr=mp.page_indptr, page_table=table2)
+    o2, l2 = attn2.run(lt.q, lt.k_suffix, lt.v_suffix, kp2, vp2)
+    torch.cuda.synchronize()
+    assert torch.equal(o2, outs[0][0]) and torch.equal(l2, outs[0][1])
+
+
+def test_tree_flow_equals_reference_row_flow():
+    """plan/run over unique nodes == the reference's row flow (single prefill +
+    CascadeGraphRunner) gathered through node_index."""
+    prob = wl.config2(5, layers=1)
+    prob.page_size = 0
+    mp, _, outs = _run_problem(prob)
+    t = prob.requests[0].tree
+    idx = torch.as_tensor(t.node_index, dtype=torch.long, device=DEV)
+    lt = mp.layers[0]
+    bsz, lb = idx.shape
+    hq, hkv, d = prob.num_qo_heads, prob.num_kv_heads, prob.head_dim
+    q_rows = lt.q[idx]
+    kp = lt.k_prefix.transpose(0, 1)              # [L, Hkv, D] view of [Hkv, L, D]
+    vp = lt.v_prefix.transpose(0, 1)
+    o_sh, lse_sh = d2sd.single_prefill_with_kv_cache(q_rows.reshape(bsz * lb, hq, d), kp, vp, causal=False,
+                                                     return_lse=True, sm_scale=d ** -0.5)
+    o_sh, lse_sh = o_sh.view(bsz, lb, hq, d), lse_sh.view(bsz, lb, hq)
+    runner = d2sd.CascadeGraphRunner(lb, hq, hkv, d, torch.bfloat16, torch.device(DEV), d ** -0.5, True)
+    runner.run(q_rows, lt.k_suffix[idx], lt.v_suffix[idx], o_sh, lse_sh)
+    torch.cuda.synchronize()
+    check_close(o_sh, outs[0][0][idx].float().cpu(), lse_sh, outs[0][1][idx].cpu(), "row vs tree")
+
+
+@pytest.mark.parametrize("cfg", ["config1", "config2"])
+def test_greedy_argmax_bit_identical(cfg):
+    prob = getattr(wl, cfg)(0) if cfg == "config1" else wl.config2(0, layers=1)
+    mp, _, outs = _run_problem(prob)
+    o_ref, _ = _oracle_request(mp, 0, 0)
+    n = prob.total_q
+    w = torch.randn(prob.num_qo_heads * prob.head_dim, 32000, generator=torch.Generator().manual_seed(1234))
+    logits_ref = o_ref.reshape(n, -1).float() @ w
+    logits_gpu = outs[0][0].reshape(n, -1).float().cpu() @ w
+    top2 = logits_ref.topk(2, dim=-1).values
+    margin = (top2[:, 0] - top2[:, 1]).min().item()
+    err = (logits_gpu - logits_ref).abs().max().item()
+    assert margin > 4 * err, f"seed gives a near-tie: margin {margin:.4g} vs err {err:.4g}"
+    assert torch.equal(logits_gpu.argmax(-1), logits_ref.argmax(-1))
+
+
+def test_hipgraph_replays_match_eager():
+    """Capture 3 layers of cascade run into one HipGraph; replay several times
+    with eager work in between; every replay equals the eager result."""
+    prob = wl.config2(6, layers=3)
+    mp = wl.materialize(prob, DEV)
+    attn = d2sd.CascadeVerifyAttention(DEV)
+    wl.plan_for(attn, mp)
+    T, hq, d = prob.total_q, prob.num_qo_heads, prob.head_dim
+    outs = [(torch.empty(T, hq, d, dtype=torch.bfloat16, device=DEV),
+             torch.empty(T, hq, dtype=torch.float32, device=DEV)) for _ in mp.layers]
+    eager = []
+    for lt in mp.layers:
+        o, l = attn.run(lt.q, lt.k_suffix, lt.v_suffix, lt.k_prefix, lt.v_prefix)
+        eager.append((o.clone(), l.clone()))
+    g = d2sd.HipGraph()
+    with g.capture():
+        for lt, (o, l) in zip(mp.layers, outs):
+            attn.run(lt.q, lt.k_suffix, lt.v_suffix, lt.k_prefix, lt.v_prefix, out=o, lse=l)
+    for rep in range(4):
+        for o, l in outs:
+            o.zero_()
+            l.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        for (o, l), (eo, el) in zip(outs, eager):
+            assert torch.equal(o, eo) and torch.equal(l, el), f"replay {rep}"
+        _ = (torch.randn(1000, device=DEV) * 2).sum().item()   # eager work between replays

@@ -1,0 +1,295 @@
+"""Pins the CPU oracle (oracle/cascade_oracle.py) — CPU only.
+
+Each oracle function is checked against something other than its own formula:
+the loop-computed fixtures of tests/golden/make_golden.py, invariants of the
+mathematics, the reference's three-step row-layout algorithm vs the single-pass
+tree form, and the installed transformers GPT-OSS eager attention for the sink.
+A few tests plant a mistake in the oracle and require the pins to catch it.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import cascade_oracle as orc
+from d2sd import tree as dtree
+from d2sd import workloads as wl
+
+T = torch.from_numpy
+
+
+def _close(a, b, tol=1e-9):
+    a = torch.as_tensor(a, dtype=torch.float64)
+    b = torch.as_tensor(b, dtype=torch.float64)
+    fin = torch.isfinite(b)
+    assert torch.equal(torch.isfinite(a), fin)
+    assert torch.all(a[~fin] == b[~fin])
+    if fin.any():
+        err = (a[fin] - b[fin]).abs().max().item()
+        assert err <= tol, err
+
+
+# --------------------------------------------------------------- fixtures
+def test_golden_gqa_nomask(golden):
+    c = golden["gqa_nomask"]
+    o, lse = orc.single_prefill_ref(T(c["q"]), T(c["k"]), T(c["v"]), causal=False, sm_scale=float(c["sm_scale"]))
+    _close(o, c["o"])
+    _close(lse, c["lse"])
+
+
+def test_golden_causal(golden):
+    c = golden["causal"]
+    o, lse = orc.single_prefill_ref(T(c["q"]), T(c["k"]), T(c["v"]), causal=True, sm_scale=float(c["sm_scale"]))
+    _close(o, c["o"])
+    _close(lse, c["lse"])
+
+
+@pytest.mark.parametrize("case", ["tree_small", "tree_d64", "tree_d128"])
+def test_golden_tree_single_pass(golden, case):
+    c = golden[case]
+    m = dtree.ancestor_mask(c["parents"])
+    sinks = T(c["sinks"]) if "sinks" in c else None
+    o, lse = orc.cascade_tree_ref(T(c["q"]), T(c["k_suffix"]), T(c["v_suffix"]), T(c["k_prefix"]),
+                                  T(c["v_prefix"]), T(m), float(c["sm_scale"]), int(c["window"]), sinks)
+    _close(o, c["o"])
+    _close(lse, c["lse"])
+
+
+@pytest.mark.parametrize("case", ["tree_small", "tree_d64", "tree_d128"])
+def test_golden_tree_row_layout(golden, case):
+    """The reference's own 3-step algorithm (shared prefill over all rows,
+    per-row causal local prefill, merge_state, sink) reproduces the fixture
+    after gathering node values into rows."""
+    c = golden[case]
+    idx = torch.as_tensor(c["node_index"], dtype=torch.long)
+    q, ks, vs = T(c["q"]), T(c["k_suffix"]), T(c["v_suffix"])
+    sinks = T(c["sinks"]) if "sinks" in c else None
+    o, lse = orc.cascade_verify_rows_ref(q[idx], ks[idx], vs[idx], T(c["k_prefix"]), T(c["v_prefix"]),
+                                         float(c["sm_scale"]), int(c["window"]), sinks)
+    _close(o, T(c["o"])[idx])
+    _close(lse, T(c["lse"])[idx])
+
+
+def test_golden_merge(golden):
+    c = golden["merge"]
+    v, s = orc.merge_state_ref(T(c["va"]), T(c["sa"]), T(c["vb"]), T(c["sb"]))
+    _close(v, c["v"], 1e-12)
+    _close(s, c["s"], 1e-12)
+
+
+# ------------------------------------------------------------- invariants
+def _rand(gen, *shape):
+    return torch.randn(*shape, generator=gen, dtype=torch.float64)
+
+
+def test_sdpa_form_matches_explicit_form():
+    gen = torch.Generator().manual_seed(1)
+    q, k, v = _rand(gen, 7, 8, 32), _rand(gen, 19, 2, 32), _rand(gen, 19, 2, 32)
+    mask = torch.rand(7, 19, generator=gen) < 0.7
+    mask[:, 0] = True
+    o1, l1 = orc.attention_ref(q, k, v, mask, 0.2)
+    o2, l2 = orc.attention_sdpa_ref(q, k, v, mask, 0.2, dtype=torch.float64)
+    _close(o1, o2, 1e-10)
+    _close(l1, l2, 1e-10)
+
+
+@pytest.mark.parametrize("splits", [[5, 11], [1, 2, 3, 30], [17]])
+def test_split_prefix_merge_equals_unsplit(splits):
+    gen = torch.Generator().manual_seed(2)
+    q, k, v = _rand(gen, 6, 4, 16), _rand(gen, 40, 2, 16), _rand(gen, 40, 2, 16)
+    o_ref, l_ref = orc.single_prefill_ref(q, k, v, False, 0.25)
+    bounds = [0] + splits + [40]
+    o_acc = torch.zeros_like(o_ref)
+    l_acc = torch.full_like(l_ref, -math.inf)
+    for a, b in zip(bounds[:-1], bounds[1:]):
+        o_p, l_p = orc.single_prefill_ref(q, k[a:b], v[a:b], False, 0.25)
+        o_acc, l_acc = orc.merge_state_ref(o_acc, l_acc, o_p, l_p)
+    _close(o_acc, o_ref, 1e-12)
+    _close(l_acc, l_ref, 1e-12)
+
+
+def test_merge_commutative_associative():
+    gen = torch.Generator().manual_seed(3)
+    st = [(_rand(gen, 3, 2, 8), _rand(gen, 3, 2) * 3) for _ in range(3)]
+    ab = orc.merge_state_ref(*st[0], *st[1])
+    ba = orc.merge_state_ref(*st[1], *st[0])
+    _close(ab[0], ba[0], 1e-12)
+    _close(ab[1], ba[1], 1e-12)
+    left = orc.merge_state_ref(*ab, *st[2])
+    bc = orc.merge_state_ref(*st[1], *st[2])
+    right = orc.merge_state_ref(*st[0], *bc)
+    _close(left[0], right[0], 1e-12)
+    _close(left[1], right[1], 1e-12)
+
+
+def test_empty_prefix_is_pure_tree_attention():
+    gen = torch.Generator().manual_seed(4)
+    t = dtree.tree_from_shared_prefixes(6, [6, 2, 4])
+    m = torch.as_tensor(t.ancestor_mask())
+    n = t.num_nodes
+    q, ks, vs = _rand(gen, n, 4, 16), _rand(gen, n, 2, 16), _rand(gen, n, 2, 16)
+    o1, l1 = orc.cascade_tree_ref(q, ks, vs, None, None, m, 0.3)
+    o2, l2 = orc.attention_ref(q, ks, vs, m, 0.3)
+    _close(o1, o2, 1e-12)
+    _close(l1, l2, 1e-12)
+
+
+def test_chain_tree_equals_causal_prefill():
+    gen = torch.Generator().manual_seed(5)
+    n, L = 9, 23
+    t = dtree.tree_from_shared_prefixes(n, [n])
+    q, ks, vs = _rand(gen, n, 4, 16), _rand(gen, n, 1, 16), _rand(gen, n, 1, 16)
+    kp, vp = _rand(gen, L, 1, 16), _rand(gen, L, 1, 16)
+    o1, l1 = orc.cascade_tree_ref(q, ks, vs, kp, vp, torch.as_tensor(t.ancestor_mask()), 0.25)
+    o2, l2 = orc.single_prefill_ref(q, torch.cat([kp, ks]), torch.cat([vp, vs]), True, 0.25)
+    _close(o1, o2, 1e-12)
+    _close(l1, l2, 1e-12)
+
+
+def test_constant_v_gives_v():
+    gen = torch.Generator().manual_seed(6)
+    q, k = _rand(gen, 5, 4, 8), _rand(gen, 12, 2, 8)
+    v = torch.ones(12, 2, 8, dtype=torch.float64) * torch.tensor([1.5, -2.0], dtype=torch.float64)[None, :, None]
+    o, _ = orc.single_prefill_ref(q, k, v, True, 0.5)
+    expect = torch.tensor([1.5] * 2 + [-2.0] * 2, dtype=torch.float64)[None, :, None].expand_as(o)
+    _close(o, expect, 1e-12)
+
+
+def test_page_permutation_invariance():
+    gen = torch.Generator().manual_seed(7)
+    P, pages, hkv, d, L = 4, 6, 2, 8, 21
+    pool = _rand(gen, pages, hkv, P, d)
+    table = [3, 0, 5, 1, 4, 2]
+    k1 = orc.gather_paged(pool, table, L)
+    perm = [2, 4, 0, 5, 1, 3]                      # pool2[perm[i]] = pool[i]
+    pool2 = torch.empty_like(pool)
+    for i, pi in enumerate(perm):
+        pool2[pi] = pool[i]
+    k2 = orc.gather_paged(pool2, [perm[t] for t in table], L)
+    assert torch.equal(k1, k2)
+    assert torch.equal(k1[:4], pool[3].permute(1, 0, 2))
+
+
+def test_window_keeps_last_keys():
+    gen = torch.Generator().manual_seed(8)
+    k, v = _rand(gen, 30, 2, 8), _rand(gen, 30, 2, 8)
+    kw, vw = orc.window_prefix_ref(k, v, 7)
+    assert torch.equal(kw, k[23:]) and torch.equal(vw, v[23:])
+    assert orc.window_prefix_ref(k, v, 64)[0] is k
+    assert orc.window_prefix_ref(k, v, -1)[0] is k
+
+
+def test_sink_matches_transformers_gpt_oss_eager():
+    from types import SimpleNamespace
+    from transformers.models.gpt_oss.modeling_gpt_oss import eager_attention_forward
+    gen = torch.Generator().manual_seed(9)
+    t = dtree.tree_from_shared_prefixes(5, [5, 1, 3])
+    m = torch.as_tensor(t.ancestor_mask())
+    n, L, hq, hkv, d = t.num_nodes, 13, 8, 2, 16
+    q, ks, vs = _rand(gen, n, hq, d), _rand(gen, n, hkv, d), _rand(gen, n, hkv, d)
+    kp, vp = _rand(gen, L, hkv, d), _rand(gen, L, hkv, d)
+    sinks = _rand(gen, hq)
+    o, _ = orc.cascade_tree_ref(q, ks, vs, kp, vp, m, d ** -0.5, sinks=sinks)
+    full = torch.cat([torch.ones(n, L, dtype=torch.bool), m], 1)
+    add = torch.zeros(n, L + n, dtype=torch.float64).masked_fill(~full, -math.inf)[None, None]
+    mod = SimpleNamespace(num_key_value_groups=hq // hkv, sinks=sinks, training=False)
+    k_all = torch.cat([kp, ks]).transpose(0, 1)[None]
+    v_all = torch.cat([vp, vs]).transpose(0, 1)[None]
+    ref, _ = eager_attention_forward(mod, q.transpose(0, 1)[None], k_all, v_all, add, d ** -0.5)
+    _close(o, ref[0], 1e-12)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2, 3])
+def test_row_layout_equals_tree_layout_d3(seed):
+    rng = np.random.default_rng(seed)
+    t = dtree.d3_verify_tree(rng.uniform(size=7), block_size=8, block_size_2=12, topk=3)
+    idx = torch.as_tensor(t.node_index, dtype=torch.long)
+    gen = torch.Generator().manual_seed(seed)
+    n = t.num_nodes
+    q, ks, vs = _rand(gen, n, 4, 16), _rand(gen, n, 2, 16), _rand(gen, n, 2, 16)
+    kp, vp = _rand(gen, 20, 2, 16), _rand(gen, 20, 2, 16)
+    sinks = _rand(gen, 4)
+    o_t, l_t = orc.cascade_tree_ref(q, ks, vs, kp, vp, torch.as_tensor(t.ancestor_mask()), 0.25, 9, sinks)
+    o_r, l_r = orc.cascade_verify_rows_ref(q[idx], ks[idx], vs[idx], kp, vp, 0.25, 9, sinks)
+    _close(o_r, o_t[idx], 1e-12)
+    _close(l_r, l_t[idx], 1e-12)
+
+
+def test_fp8_dequant_exact():
+    x = torch.tensor([0.0, 1.0, -1.5, 448.0, 2.0 ** -9, -(2.0 ** -6) * 0.875], dtype=torch.float32)
+    f8 = x.to(torch.float8_e4m3fn)
+    assert torch.equal(orc.fp8_dequant_ref(f8, torch.tensor(1.0)), x)
+
+
+# ------------------------------------------------- planted-mistake checks
+def test_planted_wrong_gqa_map_is_caught(golden, monkeypatch):
+    c = golden["gqa_nomask"]
+    monkeypatch.setattr(orc, "_expand_kv", lambda k, hq: k.repeat(1, hq // k.shape[1], 1))
+    o, _ = orc.single_prefill_ref(T(c["q"]), T(c["k"]), T(c["v"]), causal=False, sm_scale=float(c["sm_scale"]))
+    assert (o - T(c["o"])).abs().max() > 1e-3
+
+
+def test_planted_top_left_causal_is_caught(golden, monkeypatch):
+    c = golden["causal"]
+    monkeypatch.setattr(orc, "causal_mask", lambda n, L: torch.arange(L)[None, :] <= torch.arange(n)[:, None])
+    o, _ = orc.single_prefill_ref(T(c["q"]), T(c["k"]), T(c["v"]), causal=True, sm_scale=float(c["sm_scale"]))
+    assert (o - T(c["o"])).abs().max() > 1e-3
+
+
+def test_planted_missing_window_is_caught(golden, monkeypatch):
+    c = golden["tree_small"]
+    monkeypatch.setattr(orc, "window_prefix_ref", lambda k, v, w: (k, v))
+    o, _ = orc.cascade_tree_ref(T(c["q"]), T(c["k_suffix"]), T(c["v_suffix"]), T(c["k_prefix"]),
+                                T(c["v_prefix"]), T(dtree.ancestor_mask(c["parents"])), float(c["sm_scale"]),
+                                int(c["window"]), T(c["sinks"]))
+    assert (o - T(c["o"])).abs().max() > 1e-3
+
+
+def test_planted_base2_lse_is_caught(golden):
+    c = golden["gqa_nomask"]
+    _, lse = orc.single_prefill_ref(T(c["q"]), T(c["k"]), T(c["v"]), causal=False, sm_scale=float(c["sm_scale"]))
+    assert (lse / math.log(2) - T(c["lse"])).abs().max() > 1e-2
+
+
+# ------------------------------------------------ tree geometry (host code)
+@pytest.mark.parametrize("seed", range(6))
+def test_tree_mask_two_constructions_agree(seed):
+    rng = np.random.default_rng(seed)
+    trees = [dtree.d3_verify_tree(rng.uniform(size=15)),
+             dtree.d3_verify_tree(rng.uniform(size=15), 16, 16, 4),
+             wl.random_branch_tree(rng, 8, 32, chain_to_row0=False),
+             wl.random_branch_tree(rng, 4, 16)]
+    for t in trees:
+        m1 = dtree.ancestor_mask(t.parents)
+        m2 = orc.ancestor_mask_from_rows(t.node_index, t.num_nodes)
+        assert np.array_equal(m1, m2)
+
+
+def test_d3_tree_sizes_match_reference_geometry():
+    sizes = []
+    for seed in range(200):
+        rng = np.random.default_rng(seed)
+        t = dtree.d3_verify_tree(rng.uniform(size=15), 16, 32, 4)
+        assert t.num_rows == 5 and t.row_len == 32
+        # row j shares pl_j + 1 tokens with row 0, pl_j distinct in [0, 14]
+        assert all(1 <= s <= 15 for s in t.shared[1:]) and len(set(t.shared[1:])) == 4
+        assert t.num_nodes == 32 + sum(32 - s for s in t.shared[1:])
+        sizes.append(t.num_nodes)
+    assert 106 <= min(sizes) and max(sizes) <= 150
+
+
+def test_d3_rates_formula():
+    conf = np.array([0.9, 0.5, 0.8, 0.3])
+    r = dtree.d3_rejection_rates(conf)
+    assert np.allclose(r, [0.1, 0.9 * 0.5, 0.9 * 0.5 * 0.2, 0.9 * 0.5 * 0.8 * 0.7])
+
+
+def test_pack_mask_bits():
+    m = np.zeros((2, 70), dtype=bool)
+    m[0, [0, 5, 63]] = True
+    m[1, [64, 69]] = True
+    p = dtree.pack_mask_rows(m)
+    assert p.shape == (2, 2)
+    assert int(p[0, 0]) == (1 | (1 << 5) | (1 << 63)) and int(p[0, 1]) == 0
+    assert int(p[1, 0]) == 0 and int(p[1, 1]) == (1 | (1 << 5))
