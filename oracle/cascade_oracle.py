@@ -186,8 +186,10 @@ def cascade_tree_ref(q: Tensor, k_suffix: Tensor, v_suffix: Tensor, k_prefix: Op
     n = q.shape[0]
     if k_prefix is not None and k_prefix.shape[0] > 0:
         kp, vp = window_prefix_ref(k_prefix, v_prefix, window)
-        k_all = torch.cat([kp.to(k_suffix.dtype), k_suffix], 0)
-        v_all = torch.cat([vp.to(v_suffix.dtype), v_suffix], 0)
+        # concatenate in the computation dtype: a dequantised (fp32) prefix
+        # must not be rounded to the suffix's bf16
+        k_all = torch.cat([kp.to(dtype), k_suffix.to(dtype)], 0)
+        v_all = torch.cat([vp.to(dtype), v_suffix.to(dtype)], 0)
         mask = torch.cat([torch.ones(n, kp.shape[0], dtype=torch.bool), anc_mask.bool()], 1)
     else:
         k_all, v_all, mask = k_suffix, v_suffix, anc_mask.bool()

@@ -216,6 +216,23 @@ def test_row_layout_equals_tree_layout_d3(seed):
     _close(l_r, l_t[idx], 1e-12)
 
 
+def test_tree_ref_keeps_prefix_precision():
+    """A float prefix (e.g. fp8 dequantised with an fp32 scale) is used at full
+    precision next to a bf16 suffix."""
+    gen = torch.Generator().manual_seed(10)
+    t = dtree.tree_from_shared_prefixes(4, [4, 2])
+    m = torch.as_tensor(t.ancestor_mask())
+    n = t.num_nodes
+    q = _rand(gen, n, 4, 16).to(torch.bfloat16)
+    ks, vs = _rand(gen, n, 2, 16).to(torch.bfloat16), _rand(gen, n, 2, 16).to(torch.bfloat16)
+    kp, vp = _rand(gen, 9, 2, 16) * 1.0009765, _rand(gen, 9, 2, 16) * 1.0009765
+    o1, l1 = orc.cascade_tree_ref(q, ks, vs, kp, vp, m, 0.25)
+    full = torch.cat([torch.ones(n, 9, dtype=torch.bool), m], 1)
+    o2, l2 = orc.attention_ref(q.double(), torch.cat([kp, ks.double()]), torch.cat([vp, vs.double()]), full, 0.25)
+    _close(o1, o2, 1e-12)
+    _close(l1, l2, 1e-12)
+
+
 def test_fp8_dequant_exact():
     x = torch.tensor([0.0, 1.0, -1.5, 448.0, 2.0 ** -9, -(2.0 ** -6) * 0.875], dtype=torch.float32)
     f8 = x.to(torch.float8_e4m3fn)
