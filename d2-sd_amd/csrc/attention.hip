@@ -1,13 +1,13 @@
 // gfx950 (CDNA4) kernels for cascade tree-verification attention.
 //
-//   attn_kernel     GQA-packed split-KV attention over one key source (the
-//                   shared prefix — contiguous or paged, bf16 or fp8 — or the
-//                   suffix tree), with a partial / final / in-place-merge
-//                   epilogue.  Replaces flashinfer.single_prefill_with_kv_cache
+//   attn_kernel     GQA-packed split-KV attention of packed (token, query head)
+//                   rows over one key source — the shared prefix (contiguous or
+//                   paged, bf16 or fp8) or the suffix tree — with a partial /
+//                   final / in-place-merge / merge-partials epilogue.  Replaces
+//                   flashinfer.single_prefill_with_kv_cache
 //                   (generation/verification.py:145-162, model/cascade_graph.py:54-57).
-//   merge_kernel    log-sum-exp merge of split partials (+ optional merge into
-//                   an existing state and the GPT-OSS sink rescale of
-//                   generation/verification.py:173-176).
+//   merge_kernel    log-sum-exp merge of split partials (+ the GPT-OSS sink
+//                   rescale of generation/verification.py:173-176).
 //   merge_state_kernel  flashinfer.merge_state_in_place
 //                   (generation/verification.py:163-165, model/cascade_graph.py:58-60).
 //
@@ -25,9 +25,18 @@
 // O^T += V^T . P^T straight from those registers; V^T is staged in LDS with
 // the key order inside every 16-key group permuted so that the A operand a
 // lane reads matches the key order of the P^T values it already holds.
+//
+// Register image.  Lane l of wave w holds O^T[d][row] for row = 32w + l%32
+// and d = 32*mt + 8*q4 + 4*(l/32) + e (mt < D/32, q4 < 4, e < 4).  Split
+// partials (normalised O in bf16, LSE in fp32) are stored in exactly this
+// image — the 4 values (mt, q4) of lane l at element
+// ((w*(D/32) + mt)*4 + q4)*256 + 4*l of the slot — so that every partial
+// store and every merge load is one contiguous 512-byte wave access.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
+
+#include <type_traits>
 
 #include "d2sd_internal.h"
 
@@ -35,7 +44,6 @@ namespace d2sd {
 
 typedef __bf16 bf16_t;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -48,6 +56,8 @@ constexpr float kLn2 = 0.6931471805599453f;
 // Lazy rescaling: the running max used for exponentiation may trail the true
 // row max by up to 2^kRescaleSlack before O and l are rescaled.
 constexpr float kRescaleSlack = 8.0f;
+// Tree-mask words held in registers per row (rows of up to 256 nodes).
+constexpr int kMaskRegWords = 4;
 
 __device__ __forceinline__ bf16x8 zero_bf16x8() {
   u32x4 z = {0u, 0u, 0u, 0u};
@@ -61,6 +71,36 @@ __device__ __forceinline__ unsigned pack_bf16x2(float a, float b) {
 
 __device__ __forceinline__ float bf16_lo(unsigned w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(unsigned w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ float load_lse_nat(const float* lse, int base2) {
+  const float v = *lse;
+  return base2 ? v * kLn2 : v;
+}
+
+// Element offset of (wave, mt, q4, lane) inside one partial slot (register image).
+template <int D>
+__device__ __forceinline__ int image_offset(int wave, int mt, int q4, int lane) {
+  return ((wave * (D / 32) + mt) * 4 + q4) * 256 + 4 * lane;
+}
+
+// fp8 e4m3fn (OCP) -> bf16, exact.  Bytes b0..b3 of w -> 4 bf16 in a u32x2.
+__device__ __forceinline__ u32x2 fp8x4_to_bf16x4(unsigned w) {
+  // e4m3fn placed in the top of an fp16: value(fp16) * 2^8 == value(e4m3fn)
+  // for normals and subnormals alike (exponent bias 15 vs 7).  The 2^8 is
+  // folded into the dequantisation scale by the caller.
+  u32x2 r;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const unsigned b0 = (w >> (16 * h)) & 0xffu, b1 = (w >> (16 * h + 8)) & 0xffu;
+    const unsigned h0 = ((b0 & 0x80u) << 8) | ((b0 & 0x7fu) << 7);
+    const unsigned h1 = ((b1 & 0x80u) << 8) | ((b1 & 0x7fu) << 7);
+    const float f0 = (float)__builtin_bit_cast(_Float16, (unsigned short)h0);
+    const float f1 = (float)__builtin_bit_cast(_Float16, (unsigned short)h1);
+    // fp16 values with a 3-bit mantissa are exact in bf16: truncate.
+    r[h] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
+  }
+  return r;
+}
 
 // ---------------------------------------------------------------------------
 // Work items
@@ -94,75 +134,191 @@ __device__ __forceinline__ WorkItem implicit_work(const AttnParams& p, int b) {
   return w;
 }
 
-__device__ __forceinline__ long long tok_offset(const KvSource& s, int req, int t) {
-  if (s.page_table != nullptr) {
-    const int pg = s.page_table[s.page_indptr[req] + (t >> s.log2_page)];
-    return (long long)pg * s.stride_page + (long long)(t & ((1 << s.log2_page) - 1)) * s.stride_tok;
+// ---------------------------------------------------------------------------
+// Output store of one lane's part of a row (register image), with the
+// GPT-OSS sink factor sigmoid(lse - sink); o_scale normalises the values.
+// ---------------------------------------------------------------------------
+template <int D>
+__device__ __forceinline__ void store_row(const AttnParams& p, int req, int q0, int n, int qh, int hh,
+                                          const f32x16 (&o)[D / 32], float o_scale, float lse) {
+  bf16_t* orow = (bf16_t*)p.o + (long long)req * p.o_stride_req + (long long)(q0 + n) * p.o_stride_n +
+                 (long long)qh * p.o_stride_h;
+  float* lrow = p.lse ? p.lse + (long long)req * p.lse_stride_req + (long long)(q0 + n) * p.lse_stride_n + qh
+                      : nullptr;
+  if (p.sinks) {
+    const float sk = p.sinks[qh];
+    o_scale *= (lse == -INFINITY) ? 0.f : 1.f / (1.f + __expf(sk - lse));
   }
-  const int base = s.tok_indptr ? s.tok_indptr[req] : 0;
-  return (long long)req * s.stride_req + (long long)(base + t) * s.stride_tok;
-}
-
-// fp8 e4m3fn (OCP) -> bf16, exact.  Bytes b0..b3 of w -> 4 bf16 in a u32x2.
-__device__ __forceinline__ u32x2 fp8x4_to_bf16x4(unsigned w) {
-  // e4m3fn placed in the top of an fp16: value(fp16) * 2^8 == value(e4m3fn)
-  // for normals and subnormals alike (exponent bias 15 vs 7).  The 2^8 is
-  // folded into the dequantisation scale by the caller.
-  u32x2 r;
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const unsigned b0 = (w >> (16 * h)) & 0xffu, b1 = (w >> (16 * h + 8)) & 0xffu;
-    const unsigned h0 = ((b0 & 0x80u) << 8) | ((b0 & 0x7fu) << 7);
-    const unsigned h1 = ((b1 & 0x80u) << 8) | ((b1 & 0x7fu) << 7);
-    const float f0 = (float)__builtin_bit_cast(_Float16, (unsigned short)h0);
-    const float f1 = (float)__builtin_bit_cast(_Float16, (unsigned short)h1);
-    // fp16 values with a 3-bit mantissa are exact in bf16: truncate.
-    r[h] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
-  }
-  return r;
+  for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      bf16_t* dst = orow + 32 * mt + 8 * q4 + 4 * hh;
+      *(u32x2*)dst = (u32x2){pack_bf16x2(o[mt][4 * q4] * o_scale, o[mt][4 * q4 + 1] * o_scale),
+                             pack_bf16x2(o[mt][4 * q4 + 2] * o_scale, o[mt][4 * q4 + 3] * o_scale)};
+    }
+  if (lrow && hh == 0) *lrow = p.lse_base2 ? lse * kLog2e : lse;
 }
 
-// ---------------------------------------------------------------------------
-// Output epilogue shared by attn_kernel (FINAL / INPLACE) and merge_kernel.
-// o4 holds 4 consecutive head-dim values (already normalised), lse is natural.
-// ---------------------------------------------------------------------------
-struct RowOut {
-  bf16_t* o;     // row base (head-dim 0)
-  float* lse;    // lse slot of this (token, head), nullable
-};
+// Merge `nslots` split partials (register image, slots slot0.. of a tile of
+// `prows` rows; this lane's row is `prow` of it) into the lane's state
+// (o, lse); o holds normalised values on entry and on return.
+template <int D>
+__device__ __forceinline__ void merge_partials(const AttnParams& p, int slot0, int nslots, int prows, int prow,
+                                               int lane, f32x16 (&o)[D / 32], float& lse) {
+  const float* lse_base = p.part_lse + (long long)slot0 * prows + prow;
+  float m = lse;
+  for (int s = 0; s < nslots; ++s) m = fmaxf(m, lse_base[(long long)s * prows]);
+  if (m == -INFINITY) return;  // nothing anywhere: o stays 0, lse -inf
+  const float w_own = __expf(lse - m);
+  float wsum = w_own;
+#pragma unroll
+  for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[mt][r] *= w_own;
+  const long long slot_elems = (long long)prows * D;
+  const bf16_t* img = (const bf16_t*)p.part_o + (long long)slot0 * slot_elems;
+  const int wave = prow >> 5;
+  // kMergeBatch slots per round, all loads issued before any is consumed
+  // (slots past nslots reload the last one with weight 0).
+  constexpr int kMergeBatch = 4;
+  for (int s0 = 0; s0 < nslots; s0 += kMergeBatch) {
+    u32x2 v[kMergeBatch][D / 32][4];
+    float wt[kMergeBatch];
+#pragma unroll
+    for (int b = 0; b < kMergeBatch; ++b) {
+      const int s = min(s0 + b, nslots - 1);
+      wt[b] = (s0 + b < nslots) ? __expf(lse_base[(long long)s * prows] - m) : 0.f;  // 0 for an empty split
+      const bf16_t* po = img + (long long)s * slot_elems;
+#pragma unroll
+      for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) v[b][mt][q4] = *(const u32x2*)(po + image_offset<D>(wave, mt, q4, lane));
+    }
+#pragma unroll
+    for (int b = 0; b < kMergeBatch; ++b) {
+#pragma unroll
+      for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          o[mt][4 * q4] += wt[b] * bf16_lo(v[b][mt][q4][0]);
+          o[mt][4 * q4 + 1] += wt[b] * bf16_hi(v[b][mt][q4][0]);
+          o[mt][4 * q4 + 2] += wt[b] * bf16_lo(v[b][mt][q4][1]);
+          o[mt][4 * q4 + 3] += wt[b] * bf16_hi(v[b][mt][q4][1]);
+        }
+      wsum += wt[b];
+    }
+  }
+  const float inv = 1.f / wsum;
+#pragma unroll
+  for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[mt][r] *= inv;
+  lse = m + logf(wsum);
+}
 
-__device__ __forceinline__ float load_lse_nat(const float* lse, int base2) {
-  const float v = *lse;
-  return base2 ? v * kLn2 : v;
+// Epilogue shared by the attention kernels: normalise the accumulators and
+// write a split partial, the final output, or merge with stored state /
+// prefix partials first.
+template <int D, int W>
+__device__ __forceinline__ void finish_rows(const AttnParams& p, const WorkItem& w, f32x16 (&o)[D / 32],
+                                            float m_run, float l_run, float vscale, float cn, int row,
+                                            bool rvalid, int q0, int n, int qh) {
+  constexpr int ROWS = 32 * W;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, l32 = lane & 31, hh = lane >> 5;
+  const int mode = w.mode & 0xff;
+  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const bool nonempty = l_tot > 0.f;
+  const float inv = nonempty ? vscale / l_tot : 0.f;
+  float lse = nonempty ? m_run * cn + logf(l_tot) : -INFINITY;
+#pragma unroll
+  for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[mt][r] *= inv;
+
+  if (mode == MODE_PARTIAL) {
+    bf16_t* po = (bf16_t*)p.part_o + (long long)w.slot * ROWS * D;
+#pragma unroll
+    for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4)
+        *(u32x2*)(po + image_offset<D>(wv, mt, q4, lane)) =
+            (u32x2){pack_bf16x2(o[mt][4 * q4], o[mt][4 * q4 + 1]), pack_bf16x2(o[mt][4 * q4 + 2], o[mt][4 * q4 + 3])};
+    if (hh == 0) p.part_lse[(long long)w.slot * ROWS + wv * 32 + l32] = lse;
+    return;
+  }
+  if (!rvalid) return;
+
+  if (mode == MODE_MERGE_SLOTS) {
+    // merge the prefix launch's split partials for this row (prefix tiles of
+    // prefix_rows rows; this launch's row blocks never straddle one)
+    const int prows = p.prefix_rows;
+    merge_partials<D>(p, w.slot, w.mode >> 8, prows, row % prows, lane, o, lse);
+  } else if (mode == MODE_INPLACE) {
+    // merge with the (bf16 O, LSE) state stored at the output
+    const bf16_t* orow = (const bf16_t*)p.o + (long long)w.req * p.o_stride_req +
+                         (long long)(q0 + n) * p.o_stride_n + (long long)qh * p.o_stride_h;
+    const float* lrow = p.lse + (long long)w.req * p.lse_stride_req + (long long)(q0 + n) * p.lse_stride_n + qh;
+    const float lo = load_lse_nat(lrow, p.lse_base2);
+    const float m = fmaxf(lo, lse);
+    float wa = 1.f, wb = 0.f;  // both empty: keep the stored state
+    if (m != -INFINITY) {
+      const float ea = __expf(lo - m), eb = __expf(lse - m);
+      const float sum = ea + eb;
+      wa = ea / sum;
+      wb = eb / sum;
+      lse = m + logf(sum);
+    } else {
+      lse = lo;
+    }
+#pragma unroll
+    for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const u32x2 old = *(const u32x2*)(orow + 32 * mt + 8 * q4 + 4 * hh);
+        o[mt][4 * q4] = o[mt][4 * q4] * wb + wa * bf16_lo(old[0]);
+        o[mt][4 * q4 + 1] = o[mt][4 * q4 + 1] * wb + wa * bf16_hi(old[0]);
+        o[mt][4 * q4 + 2] = o[mt][4 * q4 + 2] * wb + wa * bf16_lo(old[1]);
+        o[mt][4 * q4 + 3] = o[mt][4 * q4 + 3] * wb + wa * bf16_hi(old[1]);
+      }
+  }
+  store_row<D>(p, w.req, q0, n, qh, hh, o, 1.f, lse);
 }
 
 // ---------------------------------------------------------------------------
 // Attention kernel
 // ---------------------------------------------------------------------------
-template <int D, int W, bool FP8>
-__global__ __launch_bounds__(64 * W) void attn_kernel(const AttnParams p) {
+template <int D>
+struct Smem {
+  bf16_t Ks[2][64 * (D + 8)];
+  bf16_t Vt[2][D * (64 + 8)];
+  int pages[kMaxStagedPages];  // page ids of the workgroup's key range
+};
+
+// One workgroup: rows [qtile*32W, +32W) of (req, kvh) against keys
+// [kv_begin, kv_end) of source S.
+//   FP8    : S holds e4m3fn bytes (dequantised with per-kv-head scales)
+//   PAGED  : S is a paged pool (page ids staged in LDS)
+//   MASKED : causal / tree masks (else only the key-range tail is masked)
+template <int D, int W, bool FP8, bool PAGED, bool MASKED>
+__device__ __forceinline__ void attn_body(const AttnParams& p, const WorkItem& w, const KvSource& S,
+                                          Smem<D>& sm) {
   constexpr int ROWS = 32 * W;
   constexpr int NT = 64 * W;
   constexpr int KP = D + 8;   // K tile pitch (elements)
   constexpr int VP = 64 + 8;  // V^T tile pitch (elements)
-  constexpr int KCH = D / 8;  // 16-byte chunks per key row (bf16)
+  constexpr int KCH = D / 8;  // 8-element chunks per key row
   constexpr int NK = 64 * KCH / NT;  // K chunks per thread == V keys per thread
   constexpr int VKG = 64 / NK;       // V key groups per d-chunk
-  static_assert(NK >= 1 && NK <= 4, "tile/thread mismatch");
-
-  __shared__ __attribute__((aligned(16))) bf16_t Ks[2][64 * KP];
-  __shared__ __attribute__((aligned(16))) bf16_t Vt[2][D * VP];
+  constexpr int ESZ = FP8 ? 1 : 2;
+  static_assert(NK == 1 || NK == 2 || NK == 4 || NK == 8, "tile/thread mismatch");
+  typedef typename std::conditional<FP8, u32x2, u32x4>::type Raw;  // 8 elements
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = tid >> 6;
   const int l32 = lane & 31;
   const int hh = lane >> 5;
-
-  const WorkItem w = p.work ? p.work[blockIdx.x] : implicit_work(p, blockIdx.x);
-  if (w.mode == MODE_NOOP) return;
-  const KvSource S = w.src ? p.src[1] : p.src[0];
-  const bool fp8 = FP8 && (S.dtype == KV_FP8);
 
   const int g = p.group;
   const int q0 = p.qo_indptr ? p.qo_indptr[w.req] : 0;
@@ -173,6 +329,7 @@ __global__ __launch_bounds__(64 * W) void attn_kernel(const AttnParams p) {
   const int n = rvalid ? row / g : 0;
   const int j = rvalid ? row - n * g : 0;
   const int qh = w.kvh * g + j;
+  const int mode = w.mode & 0xff;
 
   // Q fragments (B operand of S^T = K Q^T): lane holds 8 consecutive head
   // dims at offset 8*hh of every 16-wide k step, for query row `row`.
@@ -186,7 +343,8 @@ __global__ __launch_bounds__(64 * W) void attn_kernel(const AttnParams p) {
   }
 
   float kscale = 1.f, vscale = 1.f;
-  if (fp8) {
+  if constexpr (FP8) {
+    // e4m3fn bytes are expanded as value / 2^8 (see fp8x4_to_bf16x4)
     kscale = (S.k_scale ? S.k_scale[w.kvh] : 1.f) * 256.f;
     vscale = (S.v_scale ? S.v_scale[w.kvh] : 1.f) * 256.f;
   }
@@ -195,52 +353,76 @@ __global__ __launch_bounds__(64 * W) void attn_kernel(const AttnParams p) {
 
   const int kv_begin = w.kv_begin, kv_end = w.kv_end;
   const int ntiles = (kv_end - kv_begin + 63) >> 6;
-  const long long head_off = (long long)w.kvh * S.stride_head;
-  const int mask_mode = S.mask_mode;
-  const int kvlen_req = S.kv_len ? S.kv_len[w.req] : (p.work ? nq : p.imp.kv_len);
-  const int causal_off = kvlen_req - nq;  // key j visible iff j <= i + causal_off
-  const unsigned long long* mrow =
-      (mask_mode == MASK_TREE && rvalid) ? S.tree_mask + (long long)(q0 + n) * S.mask_words : nullptr;
 
-  // ---- global -> register tile loads ----
-  u32x4 kr[NK], vr[NK];
+  // masks: the causal offset, or the row's tree-mask words held in registers
+  int mask_mode = MASK_NONE, causal_off = 0;
+  unsigned long long mreg[kMaskRegWords] = {0ull, 0ull, 0ull, 0ull};
+  const unsigned long long* mrow = nullptr;
+  if constexpr (MASKED) {
+    mask_mode = S.mask_mode;
+    const int kvlen_req = S.kv_len ? S.kv_len[w.req] : (p.work ? nq : p.imp.kv_len);
+    causal_off = kvlen_req - nq;  // key j visible iff j <= i + causal_off
+    if (mask_mode == MASK_TREE && rvalid) {
+      mrow = S.tree_mask + (long long)(q0 + n) * S.mask_words;
+#pragma unroll
+      for (int k = 0; k < kMaskRegWords; ++k) mreg[k] = (k < S.mask_words) ? mrow[k] : 0ull;
+    }
+  }
+
+  // ---- source addressing: byte offset of token t (head folded into the base) ----
+  const char* kbase = (const char*)S.k + (long long)w.kvh * S.stride_head * ESZ;
+  const char* vbase = (const char*)S.v + (long long)w.kvh * S.stride_head * ESZ;
+  const long long tok_b = S.stride_tok * ESZ;
+  const long long page_b = S.stride_page * ESZ;
+  const int log2p = S.log2_page;
+  const int pmask = (1 << log2p) - 1;
+  int pg_first = 0;
+  if constexpr (PAGED) {
+    if (ntiles > 0) {
+      pg_first = kv_begin >> log2p;
+      const int npg = ((kv_end - 1) >> log2p) - pg_first + 1;  // <= kMaxStagedPages (planner)
+      const int* pt = S.page_table + S.page_indptr[w.req] + pg_first;
+      for (int i = tid; i < npg; i += NT) sm.pages[i] = pt[i];
+    }
+    __syncthreads();  // page ids visible to every thread
+  } else {
+    const long long base_tok = S.tok_indptr ? S.tok_indptr[w.req] : 0;
+    const long long off = ((long long)w.req * S.stride_req + base_tok * S.stride_tok) * ESZ;
+    kbase += off;
+    vbase += off;
+  }
+  auto tok_off = [&](int t) -> long long {
+    if constexpr (PAGED)
+      return (long long)sm.pages[(t >> log2p) - pg_first] * page_b + (long long)(t & pmask) * tok_b;
+    else
+      return (long long)t * tok_b;
+  };
+
+  // ---- global -> register tile loads.  Keys past kv_end load the last valid
+  // key instead (finite data whose scores the tail mask removes), so no load
+  // result is inspected before it is stored to LDS.
+  Raw kr[NK], vr[NK];
   auto load_tile = [&](int kb) {
-    const bf16_t* kbase = (const bf16_t*)S.k;
-    const bf16_t* vbase = (const bf16_t*)S.v;
 #pragma unroll
     for (int i = 0; i < NK; ++i) {
       const int c_ = tid + i * NT;
-      const int key = c_ / KCH, dc = c_ % KCH;
-      const int t = kb + key;
-      u32x4 val = {0u, 0u, 0u, 0u};
-      if (t < kv_end) {
-        const long long off = tok_offset(S, w.req, t) + head_off + dc * 8;
-        if (fp8) {
-          const u32x2 raw = *(const u32x2*)((const unsigned char*)S.k + off);
-          const u32x2 lo = fp8x4_to_bf16x4(raw[0]), hi = fp8x4_to_bf16x4(raw[1]);
-          val = (u32x4){lo[0], lo[1], hi[0], hi[1]};
-        } else {
-          val = *(const u32x4*)(kbase + off);
-        }
-      }
-      kr[i] = val;
+      const int t = min(kb + c_ / KCH, kv_end - 1);
+      kr[i] = *(const Raw*)(kbase + tok_off(t) + (c_ % KCH) * 8 * ESZ);
     }
     const int kg = tid % VKG, dc = tid / VKG;
 #pragma unroll
     for (int i = 0; i < NK; ++i) {
-      const int t = kb + kg * NK + i;
-      u32x4 val = {0u, 0u, 0u, 0u};
-      if (t < kv_end) {
-        const long long off = tok_offset(S, w.req, t) + head_off + dc * 8;
-        if (fp8) {
-          const u32x2 raw = *(const u32x2*)((const unsigned char*)S.v + off);
-          const u32x2 lo = fp8x4_to_bf16x4(raw[0]), hi = fp8x4_to_bf16x4(raw[1]);
-          val = (u32x4){lo[0], lo[1], hi[0], hi[1]};
-        } else {
-          val = *(const u32x4*)(vbase + off);
-        }
-      }
-      vr[i] = val;
+      const int t = min(kb + kg * NK + i, kv_end - 1);
+      vr[i] = *(const Raw*)(vbase + tok_off(t) + dc * 8 * ESZ);
+    }
+  };
+
+  auto to_bf16 = [&](const Raw& r) -> u32x4 {
+    if constexpr (FP8) {
+      const u32x2 lo = fp8x4_to_bf16x4(r[0]), hi = fp8x4_to_bf16x4(r[1]);
+      return (u32x4){lo[0], lo[1], hi[0], hi[1]};
+    } else {
+      return r;
     }
   };
 
@@ -249,29 +431,33 @@ __global__ __launch_bounds__(64 * W) void attn_kernel(const AttnParams p) {
 #pragma unroll
     for (int i = 0; i < NK; ++i) {
       const int c_ = tid + i * NT;
-      const int key = c_ / KCH, dc = c_ % KCH;
-      *(u32x4*)(&Ks[buf][key * KP + dc * 8]) = kr[i];
+      *(u32x4*)(&sm.Ks[buf][(c_ / KCH) * KP + (c_ % KCH) * 8]) = to_bf16(kr[i]);
     }
     const int kg = tid % VKG, dc = tid / VKG;
-    const int kk = kg * NK;  // first key of this thread (NK consecutive keys)
+    u32x4 vv[NK];
+#pragma unroll
+    for (int i = 0; i < NK; ++i) vv[i] = to_bf16(vr[i]);
     // slot of key kk inside its 16-key group: keys 4h+{0..3} and 4h+8+{0..3}
     // of half h are stored at slots 8h..8h+7 (the order in which a lane of
     // half h holds them in the S^T accumulator).
-    const int slot = (kk & ~15) + 8 * ((kk >> 2) & 1) + (kk & 3) + 4 * ((kk >> 3) & 1);
+    auto slot_of = [](int kk) { return (kk & ~15) + 8 * ((kk >> 2) & 1) + (kk & 3) + 4 * ((kk >> 3) & 1); };
 #pragma unroll
     for (int dd = 0; dd < 8; ++dd) {
-      bf16_t* dst = &Vt[buf][(dc * 8 + dd) * VP + slot];
       const int wi = dd >> 1;
       const int sh = (dd & 1) * 16;
-      if constexpr (NK == 4) {
-        const unsigned e0 = (vr[0][wi] >> sh) & 0xffffu, e1 = (vr[1][wi] >> sh) & 0xffffu;
-        const unsigned e2 = (vr[2][wi] >> sh) & 0xffffu, e3 = (vr[3][wi] >> sh) & 0xffffu;
-        *(u32x2*)dst = (u32x2){e0 | (e1 << 16), e2 | (e3 << 16)};
+      bf16_t* rowp = &sm.Vt[buf][(dc * 8 + dd) * VP];
+      if constexpr (NK >= 4) {
+#pragma unroll
+        for (int q = 0; q < NK / 4; ++q) {
+          const unsigned e0 = (vv[4 * q][wi] >> sh) & 0xffffu, e1 = (vv[4 * q + 1][wi] >> sh) & 0xffffu;
+          const unsigned e2 = (vv[4 * q + 2][wi] >> sh) & 0xffffu, e3 = (vv[4 * q + 3][wi] >> sh) & 0xffffu;
+          *(u32x2*)(rowp + slot_of(kg * NK + 4 * q)) = (u32x2){e0 | (e1 << 16), e2 | (e3 << 16)};
+        }
       } else if constexpr (NK == 2) {
-        const unsigned e0 = (vr[0][wi] >> sh) & 0xffffu, e1 = (vr[1][wi] >> sh) & 0xffffu;
-        *(unsigned*)dst = e0 | (e1 << 16);
+        const unsigned e0 = (vv[0][wi] >> sh) & 0xffffu, e1 = (vv[1][wi] >> sh) & 0xffffu;
+        *(unsigned*)(rowp + slot_of(kg * 2)) = e0 | (e1 << 16);
       } else {
-        *(unsigned short*)dst = (unsigned short)((vr[0][wi] >> sh) & 0xffffu);
+        *(unsigned short*)(rowp + slot_of(kg)) = (unsigned short)((vv[0][wi] >> sh) & 0xffffu);
       }
     }
   };
@@ -300,7 +486,7 @@ __global__ __launch_bounds__(64 * W) void attn_kernel(const AttnParams p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) { s0[r] = 0.f; s1[r] = 0.f; }
     {
-      const bf16_t* ka = &Ks[buf][l32 * KP + 8 * hh];
+      const bf16_t* ka = &sm.Ks[buf][l32 * KP + 8 * hh];
 #pragma unroll
       for (int ks = 0; ks < D / 16; ++ks) {
         const bf16x8 a0 = *(const bf16x8*)(ka + 16 * ks);
@@ -312,25 +498,34 @@ __global__ __launch_bounds__(64 * W) void attn_kernel(const AttnParams p) {
 
     // ---- masking ----
     // register r of 32-key tile kt holds key 32*kt + 8*(r/4) + 4*hh + r%4.
-    const bool tail = kb + 64 > kv_end;
-    if (tail || mask_mode != MASK_NONE) {
+    bool apply = kb + 64 > kv_end;
+    if constexpr (MASKED) apply = apply || mask_mode != MASK_NONE;
+    if (apply) {
       unsigned long long mw = ~0ull;
-      if (mask_mode == MASK_TREE) mw = mrow ? mrow[kb >> 6] : 0ull;
+      if constexpr (MASKED) {
+        if (mask_mode == MASK_TREE) {
+          const int wi = kb >> 6;  // suffix tiles start at key 0: one word per tile
+          mw = wi == 0 ? mreg[0] : wi == 1 ? mreg[1] : wi == 2 ? mreg[2] : wi == 3 ? mreg[3]
+                                                                                  : (mrow ? mrow[wi] : 0ull);
+          if (!rvalid) mw = 0ull;
+        }
+      }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int kk0 = 8 * (r >> 2) + 4 * hh + (r & 3);
         const int kk1 = kk0 + 32;
-        const int t0 = kb + kk0, t1 = kb + kk1;
-        bool v0 = t0 < kv_end, v1 = t1 < kv_end;
-        if (mask_mode == MASK_CAUSAL) {
-          v0 = v0 && (t0 <= n + causal_off);
-          v1 = v1 && (t1 <= n + causal_off);
-        } else if (mask_mode == MASK_TREE) {
-          v0 = v0 && ((mw >> kk0) & 1ull);
-          v1 = v1 && ((mw >> kk1) & 1ull);
+        bool v0 = kb + kk0 < kv_end, v1 = kb + kk1 < kv_end;
+        if constexpr (MASKED) {
+          if (mask_mode == MASK_CAUSAL) {
+            v0 = v0 && (kb + kk0 <= n + causal_off);
+            v1 = v1 && (kb + kk1 <= n + causal_off);
+          } else if (mask_mode == MASK_TREE) {
+            v0 = v0 && ((mw >> kk0) & 1ull);
+            v1 = v1 && ((mw >> kk1) & 1ull);
+          }
         }
-        if (!v0) s0[r] = -INFINITY;
-        if (!v1) s1[r] = -INFINITY;
+        s0[r] = v0 ? s0[r] : -INFINITY;
+        s1[r] = v1 ? s1[r] : -INFINITY;
       }
     }
 
@@ -374,7 +569,7 @@ __global__ __launch_bounds__(64 * W) void attn_kernel(const AttnParams p) {
       pb[ks] = __builtin_bit_cast(bf16x8, u);
     }
     {
-      const bf16_t* va = &Vt[buf][l32 * VP + 8 * hh];
+      const bf16_t* va = &sm.Vt[buf][l32 * VP + 8 * hh];
 #pragma unroll
       for (int mt = 0; mt < D / 32; ++mt)
 #pragma unroll
@@ -388,150 +583,372 @@ __global__ __launch_bounds__(64 * W) void attn_kernel(const AttnParams p) {
     __syncthreads();
   }
 
-  // ---- epilogue ----
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
-  const bool nonempty = l_tot > 0.f;
-  const float inv = nonempty ? vscale / l_tot : 0.f;
-  const float lse = nonempty ? m_run * cn + logf(l_tot) : -INFINITY;
+  finish_rows<D, W>(p, w, o, m_run, l_run, vscale, cn, row, rvalid, q0, n, qh);
+}
 
-  if (w.mode == MODE_PARTIAL) {
-    const long long prow = (long long)w.slot * ROWS + wv * 32 + l32;
-    float* po = p.part_o + prow * D;
-#pragma unroll
-    for (int mt = 0; mt < D / 32; ++mt)
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        f32x4 v = {o[mt][4 * q4] * inv, o[mt][4 * q4 + 1] * inv, o[mt][4 * q4 + 2] * inv,
-                   o[mt][4 * q4 + 3] * inv};
-        *(f32x4*)(po + 32 * mt + 8 * q4 + 4 * hh) = v;
-      }
-    if (hh == 0) p.part_lse[prow] = lse;
-    return;
-  }
-  if (!rvalid) return;
-
-  // FINAL / INPLACE: merge with the stored state if asked, then sink.
-  bf16_t* orow = (bf16_t*)p.o + (long long)w.req * p.o_stride_req + (long long)(q0 + n) * p.o_stride_n +
-                 (long long)qh * p.o_stride_h;
-  float* lrow = p.lse ? p.lse + (long long)w.req * p.lse_stride_req + (long long)(q0 + n) * p.lse_stride_n + qh
-                      : nullptr;
-  float wa = 0.f, wb = 1.f, lse_out = lse;
-  if (w.mode == MODE_INPLACE) {
-    const float lo = load_lse_nat(lrow, p.lse_base2);
-    const float m = fmaxf(lo, lse);
-    if (m == -INFINITY) {
-      wa = 1.f; wb = 0.f; lse_out = -INFINITY;
-    } else {
-      const float ea = __expf(lo - m), eb = __expf(lse - m);
-      const float sum = ea + eb;
-      wa = ea / sum; wb = eb / sum;
-      lse_out = m + logf(sum);
-    }
-  }
-  float sink_f = 1.f;
-  if (p.sinks) {
-    const float sk = p.sinks[qh];
-    sink_f = (lse_out == -INFINITY) ? 0.f : 1.f / (1.f + __expf(sk - lse_out));
-  }
-#pragma unroll
-  for (int mt = 0; mt < D / 32; ++mt)
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      bf16_t* dst = orow + 32 * mt + 8 * q4 + 4 * hh;
-      float v0 = o[mt][4 * q4] * inv * wb, v1 = o[mt][4 * q4 + 1] * inv * wb;
-      float v2 = o[mt][4 * q4 + 2] * inv * wb, v3 = o[mt][4 * q4 + 3] * inv * wb;
-      if (w.mode == MODE_INPLACE && wa != 0.f) {
-        const u32x2 old = *(const u32x2*)dst;
-        v0 += wa * bf16_lo(old[0]); v1 += wa * bf16_hi(old[0]);
-        v2 += wa * bf16_lo(old[1]); v3 += wa * bf16_hi(old[1]);
-      }
-      *(u32x2*)dst = (u32x2){pack_bf16x2(v0 * sink_f, v1 * sink_f), pack_bf16x2(v2 * sink_f, v3 * sink_f)};
-    }
-  if (lrow && hh == 0) *lrow = p.lse_base2 ? lse_out * kLog2e : lse_out;
+template <int D, int W, bool FP8, bool PAGED, bool MASKED, int SRC>
+__global__ __launch_bounds__(64 * W) void attn_kernel(const AttnParams p) {
+  __shared__ __attribute__((aligned(16))) Smem<D> sm;
+  const WorkItem w = p.work ? p.work[blockIdx.x] : implicit_work(p, blockIdx.x);
+  if ((w.mode & 0xff) == MODE_NOOP) return;
+  attn_body<D, W, FP8, PAGED, MASKED>(p, w, p.src[SRC], sm);
 }
 
 // ---------------------------------------------------------------------------
-// Split-KV merge: rows of one tile group, ROWS rows, nslots partials each.
-// Thread layout: D/4 threads per row (4 head dims each).
+// bf16 attention with direct global->LDS tile loads (gfx950).
+//
+// K and V tiles travel global -> LDS with global_load_lds_dwordx4 (each wave
+// instruction writes 1 KB: lane l's 16 bytes at +16*l), into a ring of
+// kStages tiles, so up to kStages-1 tiles are in flight per workgroup without
+// holding any of them in registers.  Both tiles are stored row-major with the
+// 16-byte chunk c of key row r at chunk c ^ swz(r), which makes the K reads
+// of the QK MFMA conflict-free.  V is read straight from that row-major tile
+// as the A operand of O^T += V^T P^T with ds_read_b64_tr_b16: in every 16-lane
+// group lane k names 4 bf16 of key row k/4 and receives column k of the 4 keys,
+// so two reads give a lane the 8 keys of its half of a 16-key MFMA step in the
+// same order the P^T registers hold them.
 // ---------------------------------------------------------------------------
-template <int D>
-__global__ __launch_bounds__(256) void merge_kernel(const AttnParams p, int rows_per_tile, int row_blocks) {
-  constexpr int TPR = D / 4;      // threads per row
-  constexpr int RPB = 256 / TPR;  // rows per block
-  const int item_idx = blockIdx.x / row_blocks;
-  const int rb = blockIdx.x % row_blocks;
-  MergeItem mi;
-  if (p.merge) {
-    mi = p.merge[item_idx];
-  } else {
-    const int Q = p.imp.qtiles;
-    mi.qtile = item_idx % Q;
-    const int rest = item_idx / Q;
-    mi.kvh = rest % p.num_kv_heads;
-    mi.req = rest / p.num_kv_heads;
-    mi.slot_begin = item_idx * p.imp.splits;
-    mi.nslots = p.imp.splits;
-    mi.mode = p.imp.single_mode;
-  }
-  const int lr = rb * RPB + threadIdx.x / TPR;
-  const int d0 = (threadIdx.x % TPR) * 4;
-  if (lr >= rows_per_tile) return;
-  const int g = p.group;
-  const int q0 = p.qo_indptr ? p.qo_indptr[mi.req] : 0;
-  const int nq = p.qo_indptr ? p.qo_indptr[mi.req + 1] - q0 : p.imp.qo_len;
-  const int row = mi.qtile * rows_per_tile + lr;
-  if (row >= nq * g) return;
-  const int n = row / g, j = row - n * g;
-  const int qh = mi.kvh * g + j;
+constexpr int kStages = 4;
 
-  float m = -INFINITY;
-  for (int s = 0; s < mi.nslots; ++s)
-    m = fmaxf(m, p.part_lse[(long long)(mi.slot_begin + s) * rows_per_tile + lr]);
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  float wsum = 0.f;
-  if (m != -INFINITY) {
-    for (int s = 0; s < mi.nslots; ++s) {
-      const long long prow = (long long)(mi.slot_begin + s) * rows_per_tile + lr;
-      const float ls = p.part_lse[prow];
-      const float wgt = __expf(ls - m);  // 0 for an empty split (-inf)
-      if (wgt > 0.f) {
-        const f32x4 v = *(const f32x4*)(p.part_o + prow * D + d0);
-        acc += wgt * v;
-        wsum += wgt;
+template <int D>
+struct DmaSmem {
+  bf16_t ring[kStages][2][64 * D];  // [stage][K, V][key row * D]
+  int pages[kMaxStagedPages];
+};
+
+// XOR swizzle of 16-byte chunks in a key row (row pitch 256 B for D = 128,
+// 128 B for D = 64): 16 consecutive rows map one chunk to 16 distinct banks.
+template <int D>
+__device__ __forceinline__ int chunk_swizzle(int row) {
+  return D == 128 ? (row & 15) : ((row >> 1) & 7);
+}
+
+// One global_load_lds_dwordx4: lane l copies 16 bytes from `src` to LDS byte
+// address lds_addr + 16*l (lds_addr wave-uniform, passed through M0).  Issued
+// as inline asm so that the compiler does not track these LDS writes: its own
+// tracking waits for every outstanding DMA (vmcnt(0)) before transposing LDS
+// reads, which would drain the whole prefetch ring each tile.  Completion is
+// enforced explicitly (wait_vmcnt + s_barrier).  M0 is saved and restored.
+__device__ __forceinline__ void dma16(const void* src, unsigned lds_addr) {
+  unsigned saved;
+  __asm__ volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(src)
+      : "memory");
+}
+
+__device__ __forceinline__ unsigned lds_address(const void* p) {
+  return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+// s_waitcnt with vmcnt <= N and no wait on the other counters (gfx9 encoding:
+// vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int D, int W, bool PAGED, bool MASKED>
+__device__ __forceinline__ void attn_dma_body(const AttnParams& p, const WorkItem& w, const KvSource& S,
+                                              DmaSmem<D>& sm) {
+  constexpr int ROWS = 32 * W;
+  constexpr int NT = 64 * W;
+  constexpr int CH = D / 8;                 // 16-byte chunks per key row
+  constexpr int RPI = 64 / CH;              // key rows per 1 KB wave instruction
+  constexpr int IPT = 64 / RPI;             // instructions per 64-key tile (K or V)
+  constexpr int IPW = IPT / W;              // ... per wave
+  constexpr int LPT = 2 * IPW;              // DMA loads per tile per wave (K + V)
+  static_assert(IPW >= 1 && IPT % W == 0, "tile/wave mismatch");
+  (void)ROWS;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = tid >> 6;
+  const int l32 = lane & 31;
+  const int hh = lane >> 5;
+
+  const int g = p.group;
+  const int q0 = p.qo_indptr ? p.qo_indptr[w.req] : 0;
+  const int nq = p.qo_indptr ? p.qo_indptr[w.req + 1] - q0 : p.imp.qo_len;
+  const int R = nq * g;
+  const int row = w.qtile * (32 * W) + wv * 32 + l32;
+  const bool rvalid = row < R;
+  const int n = rvalid ? row / g : 0;
+  const int j = rvalid ? row - n * g : 0;
+  const int qh = w.kvh * g + j;
+
+  const float c = p.sm_scale_log2;
+  const float cn = p.sm_scale;
+  const int kv_begin = w.kv_begin, kv_end = w.kv_end;
+  const int ntiles = (kv_end - kv_begin + 63) >> 6;
+
+  int mask_mode = MASK_NONE, causal_off = 0;
+  unsigned long long mreg[kMaskRegWords] = {0ull, 0ull, 0ull, 0ull};
+  const unsigned long long* mrow = nullptr;
+  if constexpr (MASKED) {
+    mask_mode = S.mask_mode;
+    const int kvlen_req = S.kv_len ? S.kv_len[w.req] : (p.work ? nq : p.imp.kv_len);
+    causal_off = kvlen_req - nq;
+    if (mask_mode == MASK_TREE && rvalid) {
+      mrow = S.tree_mask + (long long)(q0 + n) * S.mask_words;
+#pragma unroll
+      for (int k = 0; k < kMaskRegWords; ++k) mreg[k] = (k < S.mask_words) ? mrow[k] : 0ull;
+    }
+  }
+
+  // ---- source addressing (bytes; the kv head is folded into the bases) ----
+  const char* kbase = (const char*)S.k + (long long)w.kvh * S.stride_head * 2;
+  const char* vbase = (const char*)S.v + (long long)w.kvh * S.stride_head * 2;
+  const long long tok_b = S.stride_tok * 2;
+  const long long page_b = S.stride_page * 2;
+  const int log2p = S.log2_page;
+  const int pmask = (1 << log2p) - 1;
+  int pg_first = 0;
+  if constexpr (PAGED) {
+    if (ntiles > 0) {
+      pg_first = kv_begin >> log2p;
+      const int npg = ((kv_end - 1) >> log2p) - pg_first + 1;  // <= kMaxStagedPages (planner)
+      const int* pt = S.page_table + S.page_indptr[w.req] + pg_first;
+      for (int i = tid; i < npg; i += NT) sm.pages[i] = pt[i];
+    }
+  } else {
+    const long long base_tok = S.tok_indptr ? S.tok_indptr[w.req] : 0;
+    const long long off = ((long long)w.req * S.stride_req + base_tok * S.stride_tok) * 2;
+    kbase += off;
+    vbase += off;
+  }
+
+  // Q fragments (B operand of S^T = K Q^T), loaded while the page ids land
+  bf16x8 qf[D / 16];
+  {
+    const bf16_t* qp = (const bf16_t*)p.q + (long long)w.req * p.q_stride_req +
+                       (long long)(q0 + n) * p.q_stride_n + (long long)qh * p.q_stride_h + 8 * hh;
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks)
+      qf[ks] = rvalid ? *(const bf16x8*)(qp + 16 * ks) : zero_bf16x8();
+  }
+  // Complete the Q loads here, visibly to the compiler: otherwise it keeps
+  // them pending into the tile loop and waits vmcnt(0) there every tile,
+  // which would also drain the DMA ring.
+  wait_vmcnt<0>();
+  __syncthreads();  // page ids visible
+
+  auto tok_off = [&](int t) -> long long {
+    if constexpr (PAGED)
+      return (long long)sm.pages[(t >> log2p) - pg_first] * page_b + (long long)(t & pmask) * tok_b;
+    else
+      return (long long)t * tok_b;
+  };
+
+  // DMA of tile `it` into ring stage it % kStages.  Keys past kv_end load the
+  // last valid key (finite data whose scores the tail mask removes).
+  auto issue = [&](int it) {
+    const int kb = kv_begin + it * 64;
+    bf16_t* kst = &sm.ring[it % kStages][0][0];
+    bf16_t* vst = &sm.ring[it % kStages][1][0];
+#pragma unroll
+    for (int i = 0; i < IPW; ++i) {
+      const int inst = wv * IPW + i;
+      const int r = inst * RPI + lane / CH;           // key row in the tile
+      const int cs = lane % CH;                        // stored chunk
+      const int cg = cs ^ chunk_swizzle<D>(r);         // global chunk it holds
+      const long long off = tok_off(min(kb + r, kv_end - 1)) + cg * 16;
+      dma16(kbase + off, lds_address(kst + inst * 512));
+      dma16(vbase + off, lds_address(vst + inst * 512));
+    }
+  };
+
+  f32x16 o[D / 32];
+#pragma unroll
+  for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[mt][r] = 0.f;
+  float m_run = -INFINITY;
+  float l_run = 0.f;
+
+#pragma unroll
+  for (int t = 0; t < kStages - 1; ++t)
+    if (t < ntiles) issue(t);
+
+  for (int it = 0; it < ntiles; ++it) {
+    // tile `it` has landed once at most min(kStages-2, tiles issued after it)
+    // tiles of this wave's DMA are still outstanding; then every wave's share
+    // is visible after the barrier, and stage (it-1) % kStages is free.
+    const int ahead = min(kStages - 2, ntiles - 1 - it);
+    __asm__ volatile("" ::: "memory");  // no LDS access crosses the barrier
+    if (ahead >= 2) wait_vmcnt<2 * LPT>();
+    else if (ahead == 1) wait_vmcnt<LPT>();
+    else wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+    if (it + kStages - 1 < ntiles) issue(it + kStages - 1);
+
+    const int kb = kv_begin + it * 64;
+    const bf16_t* kst = &sm.ring[it % kStages][0][0];
+    const bf16_t* vst = &sm.ring[it % kStages][1][0];
+
+    // ---- S^T = K Q^T : two 32-key tiles ----
+    f32x16 s0, s1;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) { s0[r] = 0.f; s1[r] = 0.f; }
+    {
+      const int sw0 = chunk_swizzle<D>(l32), sw1 = chunk_swizzle<D>(l32 + 32);
+      const bf16_t* k0 = kst + l32 * D;
+      const bf16_t* k1 = kst + (l32 + 32) * D;
+#pragma unroll
+      for (int ks = 0; ks < D / 16; ++ks) {
+        const int cidx = 2 * ks + hh;
+        const bf16x8 a0 = *(const bf16x8*)(k0 + 8 * (cidx ^ sw0));
+        const bf16x8 a1 = *(const bf16x8*)(k1 + 8 * (cidx ^ sw1));
+        s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[ks], s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[ks], s1, 0, 0, 0);
       }
     }
-  }
-  float lse = (wsum > 0.f) ? m + logf(wsum) : -INFINITY;
-  const float inv = (wsum > 0.f) ? 1.f / wsum : 0.f;
-  acc *= inv;
 
-  bf16_t* dst = (bf16_t*)p.o + (long long)mi.req * p.o_stride_req + (long long)(q0 + n) * p.o_stride_n +
-                (long long)qh * p.o_stride_h + d0;
-  float* lrow = p.lse ? p.lse + (long long)mi.req * p.lse_stride_req + (long long)(q0 + n) * p.lse_stride_n + qh
-                      : nullptr;
-  if (mi.mode == MODE_INPLACE) {
-    const float lo = load_lse_nat(lrow, p.lse_base2);
-    const float mm = fmaxf(lo, lse);
-    if (mm != -INFINITY) {
-      const float ea = __expf(lo - mm), eb = __expf(lse - mm);
-      const float sum = ea + eb;
-      const u32x2 old = *(const u32x2*)dst;
-      const f32x4 ov = {bf16_lo(old[0]), bf16_hi(old[0]), bf16_lo(old[1]), bf16_hi(old[1])};
-      acc = (ea / sum) * ov + (eb / sum) * acc;
-      lse = mm + logf(sum);
-    } else {
-      const u32x2 old = *(const u32x2*)dst;
-      acc = (f32x4){bf16_lo(old[0]), bf16_hi(old[0]), bf16_lo(old[1]), bf16_hi(old[1])};
-      lse = -INFINITY;
+    // ---- masking: register r of 32-key tile kt holds key 32*kt + 8*(r/4) + 4*hh + r%4 ----
+    bool apply = kb + 64 > kv_end;
+    if constexpr (MASKED) apply = apply || mask_mode != MASK_NONE;
+    if (apply) {
+      unsigned long long mw = ~0ull;
+      if constexpr (MASKED) {
+        if (mask_mode == MASK_TREE) {
+          const int wi = kb >> 6;
+          mw = wi == 0 ? mreg[0] : wi == 1 ? mreg[1] : wi == 2 ? mreg[2] : wi == 3 ? mreg[3]
+                                                                                  : (mrow ? mrow[wi] : 0ull);
+          if (!rvalid) mw = 0ull;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kk0 = 8 * (r >> 2) + 4 * hh + (r & 3);
+        const int kk1 = kk0 + 32;
+        bool v0 = kb + kk0 < kv_end, v1 = kb + kk1 < kv_end;
+        if constexpr (MASKED) {
+          if (mask_mode == MASK_CAUSAL) {
+            v0 = v0 && (kb + kk0 <= n + causal_off);
+            v1 = v1 && (kb + kk1 <= n + causal_off);
+          } else if (mask_mode == MASK_TREE) {
+            v0 = v0 && ((mw >> kk0) & 1ull);
+            v1 = v1 && ((mw >> kk1) & 1ull);
+          }
+        }
+        s0[r] = v0 ? s0[r] : -INFINITY;
+        s1[r] = v1 ? s1[r] : -INFINITY;
+      }
+    }
+
+    // ---- online softmax ----
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const bool grow = (mx > m_run) && ((m_run == -INFINITY) || (mx - m_run) * c > kRescaleSlack);
+    if (__any(grow)) {
+      const float m_new = grow ? mx : m_run;
+      const float alpha = (m_run == -INFINITY) ? 0.f : exp2f((m_run - m_new) * c);
+      l_run *= alpha;
+#pragma unroll
+      for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[mt][r] *= alpha;
+      m_run = m_new;
+    }
+    const float mc = (m_run == -INFINITY) ? 0.f : m_run * c;
+    float lsum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      s0[r] = __builtin_amdgcn_exp2f(fmaf(s0[r], c, -mc));
+      s1[r] = __builtin_amdgcn_exp2f(fmaf(s1[r], c, -mc));
+      lsum += s0[r] + s1[r];
+    }
+    l_run += lsum;
+
+    // ---- O^T += V^T P^T (A operand by transposing LDS reads) ----
+    bf16x8 pb[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const f32x16& sv = (ks < 2) ? s0 : s1;
+      const int base = 8 * (ks & 1);
+      u32x4 u;
+      u[0] = pack_bf16x2(sv[base + 0], sv[base + 1]);
+      u[1] = pack_bf16x2(sv[base + 2], sv[base + 3]);
+      u[2] = pack_bf16x2(sv[base + 4], sv[base + 5]);
+      u[3] = pack_bf16x2(sv[base + 6], sv[base + 7]);
+      pb[ks] = __builtin_bit_cast(bf16x8, u);
+    }
+    {
+      // lane k of 16-lane group G names key row 4*hh + k/4 (+8 for the second
+      // read) and head dims 16*(G&1) + 4*(k&3) .. +3 of the 32-wide block mt
+      const int k16 = lane & 15;
+      const int krow = 4 * hh + (k16 >> 2);
+      const int dsub = 16 * ((lane >> 4) & 1) + 4 * (k16 & 3);
+#pragma unroll
+      for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const int key0 = 16 * ks + krow, key1 = key0 + 8;
+          const int d = 32 * mt + dsub;
+          const bf16_t* p0 = vst + key0 * D + 8 * ((d >> 3) ^ chunk_swizzle<D>(key0)) + (d & 7);
+          const bf16_t* p1 = vst + key1 * D + 8 * ((d >> 3) ^ chunk_swizzle<D>(key1)) + (d & 7);
+          typedef short s16x4 __attribute__((ext_vector_type(4)));
+          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p0);
+          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p1);
+          const u32x2 ulo = __builtin_bit_cast(u32x2, lo), uhi = __builtin_bit_cast(u32x2, hi);
+          const bf16x8 a = __builtin_bit_cast(bf16x8, (u32x4){ulo[0], ulo[1], uhi[0], uhi[1]});
+          o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[ks], o[mt], 0, 0, 0);
+        }
     }
   }
-  if (p.sinks) {
-    const float sk = p.sinks[qh];
-    acc *= (lse == -INFINITY) ? 0.f : 1.f / (1.f + __expf(sk - lse));
-  }
-  // all TPR threads of a row have read the stored lse above (same wave)
-  *(u32x2*)dst = (u32x2){pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
-  if (lrow && d0 == 0) *lrow = p.lse_base2 ? lse * kLog2e : lse;
+
+  finish_rows<D, W>(p, w, o, m_run, l_run, 1.f, cn, row, rvalid, q0, n, qh);
+}
+
+template <int D, int W, bool PAGED, bool MASKED, int SRC>
+__global__ __launch_bounds__(64 * W) void attn_dma_kernel(const AttnParams p) {
+  __shared__ __attribute__((aligned(16))) DmaSmem<D> sm;
+  const WorkItem w = p.work ? p.work[blockIdx.x] : implicit_work(p, blockIdx.x);
+  if ((w.mode & 0xff) == MODE_NOOP) return;
+  attn_dma_body<D, W, PAGED, MASKED>(p, w, p.src[SRC], sm);
+}
+
+// ---------------------------------------------------------------------------
+// Split-KV merge (single_prefill): one wave per 32 rows of a tile group; the
+// partials are read in their register image, the output written like the
+// attention kernel's FINAL epilogue.
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(256) void merge_kernel(const AttnParams p, int rows_per_tile) {
+  const int waves_per_tile = rows_per_tile / 32;
+  const int gwave = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int item_idx = gwave / waves_per_tile;
+  const int wt = gwave % waves_per_tile;
+  if (item_idx >= p.num_merge) return;
+  const int lane = threadIdx.x & 63, l32 = lane & 31, hh = lane >> 5;
+  const int Q = p.imp.qtiles;
+  const int qt = item_idx % Q;
+  const int rest = item_idx / Q;
+  const int kvh = rest % p.num_kv_heads;
+  const int req = rest / p.num_kv_heads;
+  const int g = p.group;
+  const int nq = p.imp.qo_len;
+  const int row = qt * rows_per_tile + wt * 32 + l32;
+  if (row >= nq * g) return;
+  const int n = row / g, j = row - n * g;
+  const int qh = kvh * g + j;
+  f32x16 o[D / 32];
+#pragma unroll
+  for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[mt][r] = 0.f;
+  float lse = -INFINITY;
+  merge_partials<D>(p, item_idx * p.imp.splits, p.imp.splits, rows_per_tile, wt * 32 + l32, lane, o, lse);
+  store_row<D>(p, req, 0, n, qh, hh, o, 1.f, lse);
 }
 
 // ---------------------------------------------------------------------------
@@ -586,34 +1003,72 @@ __global__ __launch_bounds__(256) void merge_state_kernel(const MergeStateArgs a
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
-template <int D, int W, bool FP8>
+template <int D, int W, bool FP8, bool PAGED, bool MASKED, int SRC>
 static hipError_t launch_attn_t(const AttnParams& p, int nblocks, hipStream_t s) {
-  hipLaunchKernelGGL((attn_kernel<D, W, FP8>), dim3(nblocks), dim3(64 * W), 0, s, p);
+  hipLaunchKernelGGL((attn_kernel<D, W, FP8, PAGED, MASKED, SRC>), dim3(nblocks), dim3(64 * W), 0, s, p);
   return hipGetLastError();
 }
 
-hipError_t launch_attention(const AttnParams& p, int head_dim, int waves, bool fp8, int nblocks,
-                            hipStream_t s) {
-  if (nblocks <= 0) return hipSuccess;
-  if (head_dim == 128) {
-    if (waves == 4) return fp8 ? launch_attn_t<128, 4, true>(p, nblocks, s) : launch_attn_t<128, 4, false>(p, nblocks, s);
-    if (waves == 8) return fp8 ? launch_attn_t<128, 8, true>(p, nblocks, s) : launch_attn_t<128, 8, false>(p, nblocks, s);
-  } else if (head_dim == 64) {
-    if (waves == 4) return fp8 ? launch_attn_t<64, 4, true>(p, nblocks, s) : launch_attn_t<64, 4, false>(p, nblocks, s);
-    if (waves == 8) return fp8 ? launch_attn_t<64, 8, true>(p, nblocks, s) : launch_attn_t<64, 8, false>(p, nblocks, s);
+// Kernel variants: the shared-prefix level (unmasked; contiguous or paged,
+// bf16 or fp8), the suffix tree level (masked, contiguous, kSuffixWaves waves)
+// and the single-source drop-in (contiguous bf16, optionally causal).
+template <int D, int W, bool PAGED, bool MASKED, int SRC>
+static hipError_t launch_dma_t(const AttnParams& p, int nblocks, hipStream_t s) {
+  hipLaunchKernelGGL((attn_dma_kernel<D, W, PAGED, MASKED, SRC>), dim3(nblocks), dim3(64 * W), 0, s, p);
+  return hipGetLastError();
+}
+
+// Kernel variants: bf16 sources use the direct-to-LDS kernel — the shared
+// prefix level (unmasked; contiguous or paged), the suffix tree level
+// (masked, contiguous, kSuffixWaves waves) and the single-source drop-in
+// (contiguous, optionally causal); an fp8 prefix uses the register-staged
+// kernel, which converts e4m3fn to bf16 on its way into LDS.
+template <int D>
+static hipError_t launch_attention_d(const AttnParams& p, int waves, int src, bool fp8, bool paged, bool masked,
+                                     int nblocks, hipStream_t s) {
+  if (src == 1) {
+    if (waves == kSuffixWaves && masked && !fp8 && !paged)
+      return launch_dma_t<D, kSuffixWaves, false, true, 1>(p, nblocks, s);
+    return hipErrorInvalidValue;
   }
+  if (masked) {
+    if (fp8 || paged) return hipErrorInvalidValue;
+    if (waves == 4) return launch_dma_t<D, 4, false, true, 0>(p, nblocks, s);
+    if (waves == 8) return launch_dma_t<D, 8, false, true, 0>(p, nblocks, s);
+    return hipErrorInvalidValue;
+  }
+  if (!fp8) {
+    if (waves == 4) return paged ? launch_dma_t<D, 4, true, false, 0>(p, nblocks, s)
+                                 : launch_dma_t<D, 4, false, false, 0>(p, nblocks, s);
+    if (waves == 8) return paged ? launch_dma_t<D, 8, true, false, 0>(p, nblocks, s)
+                                 : launch_dma_t<D, 8, false, false, 0>(p, nblocks, s);
+    return hipErrorInvalidValue;
+  }
+  if (waves == 4) return paged ? launch_attn_t<D, 4, true, true, false, 0>(p, nblocks, s)
+                               : launch_attn_t<D, 4, true, false, false, 0>(p, nblocks, s);
+  if (waves == 8) return paged ? launch_attn_t<D, 8, true, true, false, 0>(p, nblocks, s)
+                               : launch_attn_t<D, 8, true, false, false, 0>(p, nblocks, s);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_attention(const AttnParams& p, int head_dim, int waves, int src, bool fp8, bool paged,
+                            bool masked, int nblocks, hipStream_t s) {
+  if (nblocks <= 0) return hipSuccess;
+  if (head_dim == 128) return launch_attention_d<128>(p, waves, src, fp8, paged, masked, nblocks, s);
+  if (head_dim == 64) return launch_attention_d<64>(p, waves, src, fp8, paged, masked, nblocks, s);
   return hipErrorInvalidValue;
 }
 
 hipError_t launch_merge(const AttnParams& p, int head_dim, int rows_per_tile, int nitems, hipStream_t s) {
   if (nitems <= 0) return hipSuccess;
-  const int tpr = head_dim / 4;
-  const int rpb = 256 / tpr;
-  const int row_blocks = (rows_per_tile + rpb - 1) / rpb;
+  AttnParams q = p;
+  q.num_merge = nitems;
+  const int waves = nitems * (rows_per_tile / 32);
+  const int blocks = (waves + 3) / 4;
   if (head_dim == 128)
-    hipLaunchKernelGGL(merge_kernel<128>, dim3(nitems * row_blocks), dim3(256), 0, s, p, rows_per_tile, row_blocks);
+    hipLaunchKernelGGL(merge_kernel<128>, dim3(blocks), dim3(256), 0, s, q, rows_per_tile);
   else if (head_dim == 64)
-    hipLaunchKernelGGL(merge_kernel<64>, dim3(nitems * row_blocks), dim3(256), 0, s, p, rows_per_tile, row_blocks);
+    hipLaunchKernelGGL(merge_kernel<64>, dim3(blocks), dim3(256), 0, s, q, rows_per_tile);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

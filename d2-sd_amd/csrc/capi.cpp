@@ -134,8 +134,8 @@ int d2sd_single_prefill_with_kv_cache(const void* q, int64_t q_stride_n, int64_t
   p.o_stride_h = o_stride_h;
   p.lse = lse;
   p.lse_stride_n = num_qo_heads;
-  p.part_o = (float*)workspace;
-  p.part_lse = workspace ? (float*)workspace + slots * rows * head_dim : nullptr;
+  p.part_o = workspace;
+  p.part_lse = workspace ? (float*)((char*)workspace + slots * rows * head_dim * 2) : nullptr;
   d2sd::KvSource& s0 = p.src[0];
   s0.k = k;
   s0.v = v;
@@ -150,7 +150,8 @@ int d2sd_single_prefill_with_kv_cache(const void* q, int64_t q_stride_n, int64_t
   p.group = num_qo_heads / num_kv_heads;
   p.lse_base2 = lse_base2;
   const int nblocks = num_kv_heads * p.imp.qtiles * p.imp.splits;
-  hipError_t e = d2sd::launch_attention(p, head_dim, waves, false, nblocks, (hipStream_t)stream);
+  hipError_t e = d2sd::launch_attention(p, head_dim, waves, 0, false, false, causal != 0, nblocks,
+                                        (hipStream_t)stream);
   if (e != hipSuccess) return fail_hip(e, "single_prefill attention launch");
   if (p.imp.splits > 1) {
     e = d2sd::launch_merge(p, head_dim, rows, num_kv_heads * p.imp.qtiles, (hipStream_t)stream);
@@ -215,7 +216,8 @@ int d2sd_local_attention_merge(const void* q, int64_t q_stride_b, int64_t q_stri
   p.group = g;
   p.lse_base2 = lse_base2;
   const int nblocks = bsz * num_kv_heads * p.imp.qtiles;
-  hipError_t e = d2sd::launch_attention(p, head_dim, waves, false, nblocks, (hipStream_t)stream);
+  hipError_t e = d2sd::launch_attention(p, head_dim, waves, 0, false, false, causal != 0, nblocks,
+                                        (hipStream_t)stream);
   return e == hipSuccess ? D2SD_OK : fail_hip(e, "local_attention_merge launch");
 }
 
@@ -271,6 +273,8 @@ int d2sd_cascade_plan(const d2sd_cascade_plan_desc* desc, int32_t* host_plan, si
       return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: qo_indptr must be non-decreasing");
     if (desc->prefix_len[r] < 0) return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: negative prefix_len");
   }
+  if (desc->page_size < 0 || (desc->page_size & (desc->page_size - 1)))
+    return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: page_size must be 0 or a power of two");
   d2sd::PlanInput in{};
   in.num_reqs = desc->num_reqs;
   in.qo_indptr = desc->qo_indptr;
@@ -282,19 +286,18 @@ int d2sd_cascade_plan(const d2sd_cascade_plan_desc* desc, int32_t* host_plan, si
   in.num_cus = desc->num_cus > 0 ? desc->num_cus : device_num_cus();
   in.max_splits = desc->max_splits;
   in.waves = desc->waves_per_block;
-  std::vector<d2sd::WorkItem> work;
-  std::vector<d2sd::MergeItem> merge;
+  in.page_size = desc->page_size;
   d2sd::PlanOutput out{};
-  d2sd::plan_cascade(in, work, merge, out);
+  d2sd::plan_cascade(in, out);
   static_assert(sizeof(d2sd::WorkItem) == 8 * sizeof(int32_t), "WorkItem layout");
-  static_assert(sizeof(d2sd::MergeItem) == 8 * sizeof(int32_t), "MergeItem layout");
   std::memset(info, 0, sizeof(*info));
-  info->num_work = (int)work.size();
-  info->num_merge = (int)merge.size();
-  info->waves_per_block = out.waves;
-  info->rows_per_tile = out.rows_per_tile;
+  info->num_prefix_work = (int)out.prefix_work.size();
+  info->num_suffix_work = (int)out.suffix_work.size();
+  info->prefix_waves = out.waves;
+  info->suffix_waves = out.suffix_waves;
+  info->prefix_rows = out.rows_per_tile;
   info->num_slots = out.num_slots;
-  info->plan_ints = 8 * (info->num_work + info->num_merge);
+  info->plan_ints = 8 * (info->num_prefix_work + info->num_suffix_work);
   info->workspace_bytes = out.workspace_bytes;
   info->max_splits_used = out.max_splits_used;
   info->num_reqs = desc->num_reqs;
@@ -302,12 +305,14 @@ int d2sd_cascade_plan(const d2sd_cascade_plan_desc* desc, int32_t* host_plan, si
   info->num_kv_heads = desc->num_kv_heads;
   info->head_dim = desc->head_dim;
   info->kv_dtype = desc->kv_dtype;
+  info->page_size = desc->page_size;
   if (host_plan) {
     if (host_plan_ints < (size_t)info->plan_ints)
       return fail(D2SD_ERR_WORKSPACE, "cascade_plan: host_plan too small (need " +
                                           std::to_string(info->plan_ints) + " int32)");
-    std::memcpy(host_plan, work.data(), work.size() * sizeof(d2sd::WorkItem));
-    std::memcpy(host_plan + 8 * work.size(), merge.data(), merge.size() * sizeof(d2sd::MergeItem));
+    std::memcpy(host_plan, out.prefix_work.data(), out.prefix_work.size() * sizeof(d2sd::WorkItem));
+    std::memcpy(host_plan + 8 * out.prefix_work.size(), out.suffix_work.data(),
+                out.suffix_work.size() * sizeof(d2sd::WorkItem));
   }
   return D2SD_OK;
 }
@@ -333,6 +338,8 @@ static int build_cascade_params(const d2sd_cascade_plan_info* info, const d2sd_c
       return fail(D2SD_ERR_INVALID_ARG, "cascade_run: prefix K/V must be 16-byte aligned with strides % 8 == 0");
     if (a->page_size > 0 && ((a->page_size & (a->page_size - 1)) || !a->page_table || !a->page_indptr))
       return fail(D2SD_ERR_INVALID_ARG, "cascade_run: paged prefix needs a power-of-two page_size, page_table and page_indptr");
+    if (a->page_size != info->page_size)
+      return fail(D2SD_ERR_INVALID_ARG, "cascade_run: page_size differs from the planned one");
   }
   if (info->max_splits_used > 0 && !has_prefix)
     return fail(D2SD_ERR_INVALID_ARG, "cascade_run: the plan has prefix keys but k_prefix is null");
@@ -351,11 +358,12 @@ static int build_cascade_params(const d2sd_cascade_plan_info* info, const d2sd_c
   p.o_stride_h = a->o_stride_h;
   p.lse = a->lse;
   p.lse_stride_n = a->lse_stride_n;
-  const long long rows = info->rows_per_tile;
-  p.part_o = (float*)a->workspace;
-  p.part_lse = a->workspace ? (float*)a->workspace + (long long)info->num_slots * rows * D : nullptr;
+  const long long rows = info->prefix_rows;
+  p.part_o = a->workspace;
+  p.part_lse = a->workspace ? (float*)((char*)a->workspace + (long long)info->num_slots * rows * D * 2) : nullptr;
   p.work = (const d2sd::WorkItem*)a->plan;
-  p.merge = (const d2sd::MergeItem*)(a->plan + 8LL * info->num_work);
+  p.merge = nullptr;
+  p.prefix_rows = info->prefix_rows;
   p.sinks = a->sinks;
   d2sd::KvSource& pre = p.src[0];
   pre.k = a->k_prefix;
@@ -390,32 +398,33 @@ static int build_cascade_params(const d2sd_cascade_plan_info* info, const d2sd_c
   p.num_kv_heads = info->num_kv_heads;
   p.group = info->num_qo_heads / info->num_kv_heads;
   p.lse_base2 = a->lse_base2;
-  p.num_merge = info->num_merge;
+  p.num_merge = 0;
   return D2SD_OK;
 }
 
-int d2sd_cascade_attention(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* a,
-                           d2sd_stream_t stream) {
+int d2sd_cascade_prefix(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* a, d2sd_stream_t stream) {
   g_last_error.clear();
   d2sd::AttnParams p{};
   if (int rc = build_cascade_params(info, a, p)) return rc;
   const bool fp8 = info->kv_dtype == D2SD_KV_FP8_E4M3;
-  hipError_t e =
-      d2sd::launch_attention(p, info->head_dim, info->waves_per_block, fp8, info->num_work, (hipStream_t)stream);
-  return e == hipSuccess ? D2SD_OK : fail_hip(e, "cascade attention launch");
+  hipError_t e = d2sd::launch_attention(p, info->head_dim, info->prefix_waves, 0, fp8, info->page_size > 0,
+                                        false, info->num_prefix_work, (hipStream_t)stream);
+  return e == hipSuccess ? D2SD_OK : fail_hip(e, "cascade prefix launch");
 }
 
-int d2sd_cascade_merge(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* a, d2sd_stream_t stream) {
+int d2sd_cascade_suffix(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* a, d2sd_stream_t stream) {
   g_last_error.clear();
   d2sd::AttnParams p{};
   if (int rc = build_cascade_params(info, a, p)) return rc;
-  hipError_t e = d2sd::launch_merge(p, info->head_dim, info->rows_per_tile, info->num_merge, (hipStream_t)stream);
-  return e == hipSuccess ? D2SD_OK : fail_hip(e, "cascade merge launch");
+  p.work += info->num_prefix_work;
+  hipError_t e = d2sd::launch_attention(p, info->head_dim, info->suffix_waves, 1, false, false, true,
+                                        info->num_suffix_work, (hipStream_t)stream);
+  return e == hipSuccess ? D2SD_OK : fail_hip(e, "cascade suffix launch");
 }
 
 int d2sd_cascade_run(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* a, d2sd_stream_t stream) {
-  if (int rc = d2sd_cascade_attention(info, a, stream)) return rc;
-  return d2sd_cascade_merge(info, a, stream);
+  if (int rc = d2sd_cascade_prefix(info, a, stream)) return rc;
+  return d2sd_cascade_suffix(info, a, stream);
 }
 
 }  // extern "C"

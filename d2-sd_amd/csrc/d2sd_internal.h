@@ -12,14 +12,21 @@ enum : int {
   MODE_FINAL = 1,    // only producer for its rows: write bf16 O and LSE directly
   MODE_INPLACE = 2,  // merge into the (O, LSE) already stored at the output
   MODE_NOOP = 3,     // padding item, exits immediately
+  MODE_MERGE_SLOTS = 4,  // merge (mode >> 8) prefix partials at `slot` with its own state
 };
 
 enum : int { MASK_NONE = 0, MASK_CAUSAL = 1, MASK_TREE = 2 };
+
+// Page ids one attention workgroup stages in LDS (its split's pages).
+constexpr int kMaxStagedPages = 1024;
+// Waves of the suffix (tree attention + merge) launch: 64-row blocks.
+constexpr int kSuffixWaves = 2;
 enum : int { KV_BF16 = 0, KV_FP8 = 1 };
 
 // One attention workgroup: rows [qtile*ROWS, (qtile+1)*ROWS) of the packed
 // (token, query-head) rows that read kv head `kvh` of request `req`, against
-// keys [kv_begin, kv_end) of key source `src`.
+// keys [kv_begin, kv_end) of key source `src`.  `mode` holds the epilogue in
+// its low 8 bits and, for MODE_MERGE_SLOTS, the partial count above them.
 struct WorkItem {
   int req, kvh, qtile, src, kv_begin, kv_end, slot, mode;
 };
@@ -74,7 +81,7 @@ struct AttnParams {
   long long o_stride_n, o_stride_h, o_stride_req;
   float* lse;
   long long lse_stride_n, lse_stride_req;
-  float* part_o;                 // [slot][ROWS][D]
+  void* part_o;                  // bf16 [slot][ROWS * D], register image
   float* part_lse;               // [slot][ROWS]
   const WorkItem* work;          // nullable => implicit
   const MergeItem* merge;        // nullable => implicit
@@ -87,6 +94,7 @@ struct AttnParams {
   int group;                     // Hq / Hkv
   int lse_base2;
   int num_merge;
+  int prefix_rows;               // rows per partial slot (MODE_MERGE_SLOTS)
 };
 
 }  // namespace d2sd

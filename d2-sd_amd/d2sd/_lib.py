@@ -31,8 +31,8 @@ EXPORTED_SYMBOLS = (
     "d2sd_graph_destroy",
     "d2sd_cascade_plan",
     "d2sd_cascade_run",
-    "d2sd_cascade_attention",
-    "d2sd_cascade_merge",
+    "d2sd_cascade_prefix",
+    "d2sd_cascade_suffix",
 )
 
 
@@ -46,6 +46,7 @@ class PlanDesc(C.Structure):
         ("head_dim", C.c_int),
         ("window_left", C.c_int),
         ("kv_dtype", C.c_int),
+        ("page_size", C.c_int),
         ("num_cus", C.c_int),
         ("max_splits", C.c_int),
         ("waves_per_block", C.c_int),
@@ -54,10 +55,11 @@ class PlanDesc(C.Structure):
 
 class PlanInfo(C.Structure):
     _fields_ = [
-        ("num_work", C.c_int),
-        ("num_merge", C.c_int),
-        ("waves_per_block", C.c_int),
-        ("rows_per_tile", C.c_int),
+        ("num_prefix_work", C.c_int),
+        ("num_suffix_work", C.c_int),
+        ("prefix_waves", C.c_int),
+        ("suffix_waves", C.c_int),
+        ("prefix_rows", C.c_int),
         ("num_slots", C.c_int),
         ("plan_ints", C.c_int),
         ("workspace_bytes", C.c_size_t),
@@ -67,6 +69,7 @@ class PlanInfo(C.Structure):
         ("num_kv_heads", C.c_int),
         ("head_dim", C.c_int),
         ("kv_dtype", C.c_int),
+        ("page_size", C.c_int),
     ]
 
 
@@ -141,7 +144,7 @@ def _load() -> C.CDLL:
     lib.d2sd_graph_destroy.argtypes = [vp]
     lib.d2sd_cascade_plan.restype = i32
     lib.d2sd_cascade_plan.argtypes = [C.POINTER(PlanDesc), C.POINTER(C.c_int32), sz, C.POINTER(PlanInfo)]
-    for name in ("d2sd_cascade_run", "d2sd_cascade_attention", "d2sd_cascade_merge"):
+    for name in ("d2sd_cascade_run", "d2sd_cascade_prefix", "d2sd_cascade_suffix"):
         fn = getattr(lib, name)
         fn.restype = i32
         fn.argtypes = [C.POINTER(PlanInfo), C.POINTER(RunArgs), vp]

@@ -105,6 +105,7 @@ class CascadeVerifyAttention:
         desc.head_dim = head_dim
         desc.window_left = window_left
         desc.kv_dtype = _lib.D2SD_KV_FP8_E4M3 if fp8 else _lib.D2SD_KV_BF16
+        desc.page_size = int(page_size)
         desc.num_cus = num_cus
         desc.max_splits = max_splits
         desc.waves_per_block = waves_per_block
@@ -219,14 +220,16 @@ class CascadeVerifyAttention:
         planned.  Returns (out [total_q, Hq, D] bf16, lse [total_q, Hq] fp32)."""
         return self._launch("d2sd_cascade_run", q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse)
 
-    def run_attention(self, q, k_suffix, v_suffix, k_prefix=None, v_prefix=None, out=None, lse=None):
-        """First half of run(): the attention launch alone (partials in the
-        plan's workspace).  run_merge() with the same arguments finishes it."""
-        return self._launch("d2sd_cascade_attention", q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse)
+    def run_prefix(self, q, k_suffix, v_suffix, k_prefix=None, v_prefix=None, out=None, lse=None):
+        """First half of run(): the shared-prefix launch alone (split-KV
+        partials in the plan's workspace).  run_suffix() with the same
+        arguments finishes the call."""
+        return self._launch("d2sd_cascade_prefix", q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse)
 
-    def run_merge(self, q, k_suffix, v_suffix, k_prefix=None, v_prefix=None, out=None, lse=None):
-        """Second half of run(): merge of the workspace partials into out / lse."""
-        return self._launch("d2sd_cascade_merge", q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse)
+    def run_suffix(self, q, k_suffix, v_suffix, k_prefix=None, v_prefix=None, out=None, lse=None):
+        """Second half of run(): tree-masked suffix level + merge of the
+        workspace partials + sink, into out / lse."""
+        return self._launch("d2sd_cascade_suffix", q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse)
 
     def _launch(self, fn_name, q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse):
         if not self._planned:

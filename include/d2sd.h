@@ -155,16 +155,18 @@ typedef struct {
   int head_dim;
   int window_left;     /* -1: full prefix */
   int kv_dtype;        /* D2SD_KV_* of the prefix cache */
+  int page_size;       /* 0: contiguous prefix; else the run's page size */
   int num_cus;         /* 0: query the device */
   int max_splits;      /* 0: no limit */
-  int waves_per_block; /* 0: choose; else 4 or 8 */
+  int waves_per_block; /* prefix launch: 0 = choose, else 4 or 8 */
 } d2sd_cascade_plan_desc;
 
 typedef struct {
-  int num_work;         /* attention workgroups */
-  int num_merge;        /* merge items (tile groups with > 1 partial) */
-  int waves_per_block;  /* 4 or 8 */
-  int rows_per_tile;    /* 32 * waves_per_block */
+  int num_prefix_work;  /* workgroups of the prefix launch */
+  int num_suffix_work;  /* workgroups of the suffix (tree + merge) launch */
+  int prefix_waves;     /* 4 or 8 */
+  int suffix_waves;     /* waves per suffix workgroup */
+  int prefix_rows;      /* 32 * prefix_waves: rows per partial slot */
   int num_slots;        /* split-KV partial slots */
   int plan_ints;        /* int32 entries written to host_plan */
   size_t workspace_bytes; /* float workspace for partials */
@@ -174,6 +176,7 @@ typedef struct {
   int num_kv_heads;
   int head_dim;
   int kv_dtype;
+  int page_size;
 } d2sd_cascade_plan_info;
 
 /* Fills host_plan (capacity host_plan_ints int32) with the work list; the
@@ -214,17 +217,17 @@ typedef struct {
   size_t workspace_bytes;
 } d2sd_cascade_run_args;
 
-/* run = attention then merge.  The two halves are also exported: attention
- * (prefix chunks + suffix trees, one launch) writes split partials to the
- * workspace (or the final output for rows with a single producer); merge
- * (one launch) combines the partials, applies the sink and writes out / lse.
- * Between the two, the workspace holds the only copy of the partial state. */
+/* run = prefix launch then suffix launch.  Both halves are also exported:
+ * prefix (one launch) writes the split-KV partial states of the shared-prefix
+ * level to the workspace; suffix (one launch) computes the tree-masked suffix
+ * level and, in its epilogue, merges the prefix partials, applies the sink and
+ * writes out / lse.  Between the two the workspace holds the partial state. */
 int d2sd_cascade_run(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* args,
                      d2sd_stream_t stream);
-int d2sd_cascade_attention(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* args,
-                           d2sd_stream_t stream);
-int d2sd_cascade_merge(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* args,
-                       d2sd_stream_t stream);
+int d2sd_cascade_prefix(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* args,
+                        d2sd_stream_t stream);
+int d2sd_cascade_suffix(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* args,
+                        d2sd_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -35,7 +35,7 @@ def test_version_and_error_strings():
     assert _lib.lib.d2sd_last_error() is not None
 
 
-def _plan(qo, pl, hq=32, hkv=8, d=128, window=-1, num_cus=256, waves=0, max_splits=0):
+def _plan(qo, pl, hq=32, hkv=8, d=128, window=-1, num_cus=256, waves=0, max_splits=0, page_size=16):
     desc = _lib.PlanDesc()
     qo = np.asarray(qo, dtype=np.int32)
     pl = np.asarray(pl, dtype=np.int32)
@@ -45,6 +45,7 @@ def _plan(qo, pl, hq=32, hkv=8, d=128, window=-1, num_cus=256, waves=0, max_spli
     desc.num_qo_heads, desc.num_kv_heads, desc.head_dim = hq, hkv, d
     desc.window_left = window
     desc.kv_dtype = 0
+    desc.page_size = page_size
     desc.num_cus = num_cus
     desc.max_splits = max_splits
     desc.waves_per_block = waves
@@ -54,75 +55,98 @@ def _plan(qo, pl, hq=32, hkv=8, d=128, window=-1, num_cus=256, waves=0, max_spli
     rc = _lib.lib.d2sd_cascade_plan(C.byref(desc), host.ctypes.data_as(C.POINTER(C.c_int32)), host.size,
                                     C.byref(info))
     assert rc == 0, _lib.lib.d2sd_last_error()
-    work = host[: 8 * info.num_work].reshape(-1, 8)
-    merge = host[8 * info.num_work: 8 * (info.num_work + info.num_merge)].reshape(-1, 8)
-    return info, work, merge
+    npre, nsuf = info.num_prefix_work, info.num_suffix_work
+    pre = host[: 8 * npre].reshape(-1, 8)
+    suf = host[8 * npre: 8 * (npre + nsuf)].reshape(-1, 8)
+    return info, pre, suf
 
 
-@pytest.mark.parametrize("qo,pl,window", [
-    ([0, 128], [4096], -1),
-    ([0, 41], [1024], -1),
-    ([0, 256], [8192], 128),
-    ([0, 64, 100, 164], [8192, 20000, 0], -1),
-    ([0, 30], [0], -1),
-    ([0, 150, 300], [777, 33], 500),
+MODE_PARTIAL, MODE_FINAL, MODE_NOOP, MODE_MERGE = 0, 1, 3, 4
+
+
+@pytest.mark.parametrize("qo,pl,window,page,hq", [
+    ([0, 128], [4096], -1, 16, 32),
+    ([256 * i for i in range(33)], [8192] * 32, -1, 16, 64),   # more tile groups than CUs
+    ([0, 256], [8192], -1, 16, 64),
+    ([0, 150], [4096], -1, 16, 32),
+    ([0, 41], [1024], -1, 0, 32),
+    ([0, 256], [8192], 128, 16, 32),
+    ([0, 64, 100, 164], [8192, 20000, 0], -1, 16, 32),
+    ([0, 30], [0], -1, 0, 32),
+    ([0, 150, 300], [777, 33], 500, 1, 32),
+    ([64 * i for i in range(33)], [8192] * 32, -1, 16, 32),
 ])
-def test_plan_partitions_work(qo, pl, window):
-    hq, hkv = 32, 8
+def test_plan_partitions_work(qo, pl, window, page, hq):
+    hkv = 8
     g = hq // hkv
-    info, work, merge = _plan(qo, pl, hq, hkv, 128, window)
-    rows = info.rows_per_tile
-    assert info.waves_per_block in (4, 8) and rows == 32 * info.waves_per_block
-    live = work[work[:, 7] != 3]
-    # NOOP padding only between live items, never at the end
-    assert work.shape[0] == 0 or work[-1, 7] != 3
-    cover = {}
-    slots = []
-    for req, kvh, qt, src, kb, ke, slot, mode in live.tolist():
-        cover.setdefault((req, kvh, qt, src), []).append((kb, ke))
-        if mode == 0:
-            slots.append(slot)
-        else:
-            assert mode == 1 and slot == -1
-    assert len(slots) == len(set(slots)) == info.num_slots
+    info, pre, suf = _plan(qo, pl, hq, hkv, 128, window, page_size=page)
+    rows = info.prefix_rows
+    assert info.prefix_waves in (4, 8) and rows == 32 * info.prefix_waves
+    srows = 32 * info.suffix_waves
+    assert rows % srows == 0
+    for lst in (pre, suf):
+        assert lst.shape[0] == 0 or lst[-1, 7] != MODE_NOOP
+    cover, slots = {}, {}
+    for req, kvh, qt, src, kb, ke, slot, mode in pre[pre[:, 7] != MODE_NOOP].tolist():
+        assert src == 0 and mode == MODE_PARTIAL
+        cover.setdefault((req, kvh, qt), []).append((kb, ke, slot))
+    all_slots = [c[2] for v in cover.values() for c in v]
+    assert len(all_slots) == len(set(all_slots)) == info.num_slots
+    blocks = {}
+    for req, kvh, qt, src, kb, ke, slot, mode in suf[suf[:, 7] != MODE_NOOP].tolist():
+        assert src == 1
+        blocks.setdefault((req, kvh), []).append((qt, kb, ke, slot, mode))
     for r in range(len(pl)):
         n = qo[r + 1] - qo[r]
-        qtiles = (n * g + rows - 1) // rows
         L = pl[r]
         Leff = min(L, window) if window >= 0 else L
         for h in range(hkv):
+            qtiles = (n * g + rows - 1) // rows
             for qt in range(qtiles):
-                # suffix level: exactly one item over [0, n)
-                assert cover.get((r, h, qt, 1)) == [(0, n)]
-                # prefix level: chunks partition [L - Leff, L), aligned to 64 from the start
-                ch = sorted(cover.get((r, h, qt, 0), []))
+                ch = sorted(cover.get((r, h, qt), []))
                 if Leff == 0:
                     assert ch == []
                     continue
+                # chunks partition [L - Leff, L) on 64-key tile boundaries
                 assert ch[0][0] == L - Leff and ch[-1][1] == L
-                for (a, b), (c, _) in zip(ch[:-1], ch[1:]):
+                for (a, b, _), (c, _, _) in zip(ch[:-1], ch[1:]):
                     assert b == c and (b - ch[0][0]) % 64 == 0
-    # merge items: one per group with > 1 item, slots contiguous and matching
-    groups = {}
-    for req, kvh, qt, src, kb, ke, slot, mode in live.tolist():
-        groups.setdefault((req, kvh, qt), []).append(slot)
-    for req, kvh, qt, sb, ns, mode, _, _ in merge.tolist():
-        s = sorted(groups[(req, kvh, qt)])
-        assert s == list(range(sb, sb + ns)) and ns > 1 and mode == 1
-    assert len(merge) == sum(1 for v in groups.values() if len(v) > 1)
-    assert info.workspace_bytes == info.num_slots * rows * (128 + 1) * 4
+                # the group's slots are consecutive in key order
+                assert [c[2] for c in ch] == list(range(ch[0][2], ch[0][2] + len(ch)))
+                if page:
+                    for a, b, _ in ch:
+                        assert (b - 1) // page - a // page + 1 <= 1024
+            nb = (n * g + srows - 1) // srows
+            bl = sorted(blocks.get((r, h), []))
+            assert [b[0] for b in bl] == list(range(nb))
+            for b, kb, ke, slot, mode in bl:
+                assert (kb, ke) == (0, n)
+                ch = sorted(cover.get((r, h, (b * srows) // rows), []))
+                if ch:
+                    assert mode & 0xff == MODE_MERGE and mode >> 8 == len(ch) and slot == ch[0][2]
+                else:
+                    assert mode == MODE_FINAL and slot == -1
+    assert info.workspace_bytes == info.num_slots * rows * (128 * 2 + 4)
+
+
+def test_plan_prefix_fits_one_wave_of_workgroups():
+    info, pre, _ = _plan([0, 150], [4096])
+    live = (pre[:, 7] != MODE_NOOP).sum()
+    assert info.prefix_waves == 8 and live <= 256
+    info, pre, _ = _plan([0, 41], [1024])
+    assert (pre[:, 7] != MODE_NOOP).sum() <= 256 * (2 if info.prefix_waves == 4 else 1)
 
 
 def test_plan_xcd_grouping():
-    """All q-tiles of one (request, head, key chunk) sit on the same XCD
-    (work index % 8)."""
-    info, work, _ = _plan([0, 128], [4096])
-    xcd = {}
-    for i, (req, kvh, qt, src, kb, ke, slot, mode) in enumerate(work.tolist()):
-        if mode == 3:
-            continue
-        xcd.setdefault((req, kvh, src, kb), set()).add(i % 8)
-    assert all(len(s) == 1 for s in xcd.values())
+    """Items reading the same keys sit on one XCD (work index % 8)."""
+    info, pre, suf = _plan([0, 150, 200], [4096, 3000])
+    for lst, key in ((pre, lambda w: (w[0], w[1], w[4])), (suf, lambda w: (w[0], w[1]))):
+        xcd = {}
+        for i, w in enumerate(lst.tolist()):
+            if w[7] == MODE_NOOP:
+                continue
+            xcd.setdefault(key(w), set()).add(i % 8)
+        assert all(len(s) == 1 for s in xcd.values())
 
 
 def test_plan_rejects_bad_input():
