@@ -7,7 +7,8 @@ bf16), prefix 4096 tokens paged at 16 with a random page permutation, and the
 D2SD candidate tree of generation/d3_generator.py:116-180 (DFlash block 16 +
 top-4 DTA branches of block 32; N unique nodes).  Each layer has its own KV
 pool (604 MB in total, beyond the 256 MB Infinity Cache).  The 36 layer calls
-(attention + merge launch each) are captured in one hipGraph and replayed.
+(attention launch + merge launch each) are captured in one hipGraph and
+replayed.
 
 Prints ONE JSON line.  value = microseconds per layer-call (lower is better).
 """
@@ -139,17 +140,17 @@ def main() -> int:
     with step.capture():
         for i in range(len(mp.layers)):
             layer_call(i, attn.run)
-    g_prefix = d2sd.HipGraph()
-    with g_prefix.capture():
+    g_attn = d2sd.HipGraph()
+    with g_attn.capture():
         for i in range(len(mp.layers)):
-            layer_call(i, attn.run_prefix)
-    g_suffix = d2sd.HipGraph()
-    with g_suffix.capture():
+            layer_call(i, attn.run_attention)
+    g_merge = d2sd.HipGraph()
+    with g_merge.capture():
         for i in range(len(mp.layers)):
-            layer_call(i, attn.run_suffix)
-    log(f"plan: prefix {info.num_prefix_work} workgroups x {info.prefix_waves} waves, suffix "
-        f"{info.num_suffix_work} x {info.suffix_waves} waves, {info.num_slots} partial slots, "
-        f"{info.max_splits_used} splits")
+            layer_call(i, attn.run_merge)
+    log(f"plan: attention {info.num_items} workgroups x {info.waves_per_block} waves "
+        f"({info.rows_per_tile} rows each), {info.max_splits_used} prefix splits, {info.num_slots} partial "
+        f"slots, {info.num_merges} merge groups")
 
     for _ in range(args.warmup):
         step.replay()
@@ -167,31 +168,32 @@ def main() -> int:
     log(f"timed {args.steps} steps: {ms_per_step:.4f} ms/step, {us_layer:.3f} us/layer")
 
     # per-kernel averages (graphs of the 36 launches of one kernel)
-    prefix_us = time_graph(g_prefix, args.kernel_reps, torch) * 1000.0 / len(mp.layers)
-    suffix_us = time_graph(g_suffix, args.kernel_reps, torch) * 1000.0 / len(mp.layers)
-    log(f"prefix kernel {prefix_us:.3f} us/launch, suffix+merge kernel {suffix_us:.3f} us/launch")
+    attn_us = time_graph(g_attn, args.kernel_reps, torch) * 1000.0 / len(mp.layers)
+    merge_us = time_graph(g_merge, args.kernel_reps, torch) * 1000.0 / len(mp.layers)
+    log(f"attention kernel {attn_us:.3f} us/launch, merge kernel {merge_us:.3f} us/launch")
 
     vb, vf = wl.verify_bytes_flops(prob)
-    pb, pf = wl.prefix_bytes_flops(prob)
-    # dominant kernel: the shared-prefix launch, priced at the prefix level's
-    # algorithmic bytes / flops (KV once, Q, O, LSE, page table)
-    t_hbm, t_mfma = pb / (HBM_PEAK_GBPS * 1e9), pf / (MFMA_BF16_PEAK_TFLOPS * 1e12)
+    ab, af = wl.attention_launch_bytes_flops(prob)
+    # dominant kernel: the attention launch (prefix key chunks + suffix trees),
+    # priced at its algorithmic bytes / flops (K/V, Q, page table, tree mask;
+    # visible (query, key) pairs)
+    t_hbm, t_mfma = ab / (HBM_PEAK_GBPS * 1e9), af / (MFMA_BF16_PEAK_TFLOPS * 1e12)
     if t_mfma > t_hbm:
-        achieved = pf / (prefix_us * 1e-6) / 1e12
+        achieved = af / (attn_us * 1e-6) / 1e12
         roof = {"bound": "mfma", "achieved": achieved, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": achieved / MFMA_BF16_PEAK_TFLOPS}
     else:
-        achieved = pb / (prefix_us * 1e-6) / 1e9
+        achieved = ab / (attn_us * 1e-6) / 1e9
         roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": achieved / HBM_PEAK_GBPS}
     roof["traffic"] = None
-    roof["kernel"] = "d2sd::attn_kernel<128, %d, false> (shared-prefix level)" % info.prefix_waves
-    roof["kernel_us"] = prefix_us
-    roof["algorithmic_bytes"] = pb
-    roof["algorithmic_flops"] = pf
-    roof["hbm_gbps"] = pb / (prefix_us * 1e-6) / 1e9
+    roof["kernel"] = "d2sd::verify_attn_kernel<128, %d, ...> (prefix chunks + suffix trees)" % info.waves_per_block
+    roof["kernel_us"] = attn_us
+    roof["algorithmic_bytes"] = ab
+    roof["algorithmic_flops"] = af
+    roof["hbm_gbps"] = ab / (attn_us * 1e-6) / 1e9
     roof["hbm_frac"] = roof["hbm_gbps"] / HBM_PEAK_GBPS
-    roof["mfma_frac"] = pf / (prefix_us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS
+    roof["mfma_frac"] = af / (attn_us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS
 
     layer_gbps = vb / (us_layer * 1e-6) / 1e9
     result = {
@@ -209,7 +211,7 @@ def main() -> int:
         "data": "synthetic: Q/K/V ~ N(0,1) rounded to bf16, seeded; tree from seeded DFlash confidences",
         "config": {"workload": prob.name, "layers": len(mp.layers), "prefix_len": 4096, "page_size": 16,
                    "tree_nodes": T, "tree_rows": 5, "row_len": 32, "num_qo_heads": hq, "num_kv_heads": 8,
-                   "head_dim": d, "replay": "hipGraph of 36 x (attention + merge launch)"},
+                   "head_dim": d, "replay": "hipGraph of 36 x (attention launch + merge launch)"},
         "queries_per_s": T / (us_layer * 1e-6),
         "hbm_gbps": layer_gbps,
         "hbm_frac": layer_gbps / HBM_PEAK_GBPS,
@@ -217,7 +219,7 @@ def main() -> int:
         "roofline_floor_us": max(vb / (HBM_PEAK_GBPS * 1e9), vf / (MFMA_BF16_PEAK_TFLOPS * 1e12)) * 1e6,
         "layer_bytes": vb,
         "layer_flops": vf,
-        "kernels_us": {"prefix": prefix_us, "suffix_merge": suffix_us},
+        "kernels_us": {"attention": attn_us, "merge": merge_us},
         "roofline": roof,
     }
     if not args.no_cpu_baseline:

@@ -1,15 +1,18 @@
-// gfx950 (CDNA4) kernels for cascade tree-verification attention.
+// gfx950 (CDNA4) kernels of the single-call drop-ins for the reference's
+// FlashInfer calls (the cascade plan()/run() path lives in verify_attention.hip):
 //
-//   attn_kernel     GQA-packed split-KV attention of packed (token, query head)
-//                   rows over one key source — the shared prefix (contiguous or
-//                   paged, bf16 or fp8) or the suffix tree — with a partial /
-//                   final / in-place-merge / merge-partials epilogue.  Replaces
-//                   flashinfer.single_prefill_with_kv_cache
-//                   (generation/verification.py:145-162, model/cascade_graph.py:54-57).
-//   merge_kernel    log-sum-exp merge of split partials (+ the GPT-OSS sink
-//                   rescale of generation/verification.py:173-176).
+//   attn_dma_kernel     GQA-packed split-KV attention of packed (token, query
+//                       head) rows over one contiguous K/V source, unmasked or
+//                       causal, with a partial / final / in-place-merge
+//                       epilogue.  Replaces flashinfer.single_prefill_with_kv_cache
+//                       (generation/verification.py:145-162,
+//                       model/cascade_graph.py:54-57) and, with the in-place
+//                       epilogue, the per-row local attention + merge loop of
+//                       model/cascade_graph.py:52-60.
+//   merge_kernel        log-sum-exp merge of split partials (+ the GPT-OSS sink
+//                       rescale of generation/verification.py:173-176).
 //   merge_state_kernel  flashinfer.merge_state_in_place
-//                   (generation/verification.py:163-165, model/cascade_graph.py:58-60).
+//                       (generation/verification.py:163-165, model/cascade_graph.py:58-60).
 //
 // Work decomposition.  The rows of one (request, kv head) are the packed
 // (token n, query head j) pairs, row = n*g + j, so all g query heads that
@@ -22,9 +25,9 @@
 // registers for the whole loop), so lane l holds the scores of ONE query
 // row (l % 32) for 32 keys: the softmax max / sum are in-lane plus one
 // exchange with lane l^32.  P^T is fed back as the B operand of
-// O^T += V^T . P^T straight from those registers; V^T is staged in LDS with
-// the key order inside every 16-key group permuted so that the A operand a
-// lane reads matches the key order of the P^T values it already holds.
+// O^T += V^T . P^T straight from those registers; V^T is read from the
+// row-major V tile with ds_read_b64_tr_b16 in the key order of the P^T
+// registers.
 //
 // Register image.  Lane l of wave w holds O^T[d][row] for row = 32w + l%32
 // and d = 32*mt + 8*q4 + 4*(l/32) + e (mt < D/32, q4 < 4, e < 4).  Split
@@ -39,67 +42,13 @@
 #include <type_traits>
 
 #include "d2sd_internal.h"
+#include "kernel_common.h"
 
 namespace d2sd {
-
-typedef __bf16 bf16_t;
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kLn2 = 0.6931471805599453f;
-// Lazy rescaling: the running max used for exponentiation may trail the true
-// row max by up to 2^kRescaleSlack before O and l are rescaled.
-constexpr float kRescaleSlack = 8.0f;
-// Tree-mask words held in registers per row (rows of up to 256 nodes).
-constexpr int kMaskRegWords = 4;
-
-__device__ __forceinline__ bf16x8 zero_bf16x8() {
-  u32x4 z = {0u, 0u, 0u, 0u};
-  return __builtin_bit_cast(bf16x8, z);
-}
-
-__device__ __forceinline__ unsigned pack_bf16x2(float a, float b) {
-  f32x2 v = {a, b};
-  return __builtin_bit_cast(unsigned, __builtin_convertvector(v, bf16x2));
-}
-
-__device__ __forceinline__ float bf16_lo(unsigned w) { return __uint_as_float(w << 16); }
-__device__ __forceinline__ float bf16_hi(unsigned w) { return __uint_as_float(w & 0xffff0000u); }
 
 __device__ __forceinline__ float load_lse_nat(const float* lse, int base2) {
   const float v = *lse;
   return base2 ? v * kLn2 : v;
-}
-
-// Element offset of (wave, mt, q4, lane) inside one partial slot (register image).
-template <int D>
-__device__ __forceinline__ int image_offset(int wave, int mt, int q4, int lane) {
-  return ((wave * (D / 32) + mt) * 4 + q4) * 256 + 4 * lane;
-}
-
-// fp8 e4m3fn (OCP) -> bf16, exact.  Bytes b0..b3 of w -> 4 bf16 in a u32x2.
-__device__ __forceinline__ u32x2 fp8x4_to_bf16x4(unsigned w) {
-  // e4m3fn placed in the top of an fp16: value(fp16) * 2^8 == value(e4m3fn)
-  // for normals and subnormals alike (exponent bias 15 vs 7).  The 2^8 is
-  // folded into the dequantisation scale by the caller.
-  u32x2 r;
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const unsigned b0 = (w >> (16 * h)) & 0xffu, b1 = (w >> (16 * h + 8)) & 0xffu;
-    const unsigned h0 = ((b0 & 0x80u) << 8) | ((b0 & 0x7fu) << 7);
-    const unsigned h1 = ((b1 & 0x80u) << 8) | ((b1 & 0x7fu) << 7);
-    const float f0 = (float)__builtin_bit_cast(_Float16, (unsigned short)h0);
-    const float f1 = (float)__builtin_bit_cast(_Float16, (unsigned short)h1);
-    // fp16 values with a 3-bit mantissa are exact in bf16: truncate.
-    r[h] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
-  }
-  return r;
 }
 
 // ---------------------------------------------------------------------------
@@ -217,9 +166,8 @@ __device__ __forceinline__ void merge_partials(const AttnParams& p, int slot0, i
   lse = m + logf(wsum);
 }
 
-// Epilogue shared by the attention kernels: normalise the accumulators and
-// write a split partial, the final output, or merge with stored state /
-// prefix partials first.
+// Epilogue of the attention kernel: normalise the accumulators and write a
+// split partial or the final output, or merge with the stored state first.
 template <int D, int W>
 __device__ __forceinline__ void finish_rows(const AttnParams& p, const WorkItem& w, f32x16 (&o)[D / 32],
                                             float m_run, float l_run, float vscale, float cn, int row,
@@ -249,12 +197,7 @@ __device__ __forceinline__ void finish_rows(const AttnParams& p, const WorkItem&
   }
   if (!rvalid) return;
 
-  if (mode == MODE_MERGE_SLOTS) {
-    // merge the prefix launch's split partials for this row (prefix tiles of
-    // prefix_rows rows; this launch's row blocks never straddle one)
-    const int prows = p.prefix_rows;
-    merge_partials<D>(p, w.slot, w.mode >> 8, prows, row % prows, lane, o, lse);
-  } else if (mode == MODE_INPLACE) {
+  if (mode == MODE_INPLACE) {
     // merge with the (bf16 O, LSE) state stored at the output
     const bf16_t* orow = (const bf16_t*)p.o + (long long)w.req * p.o_stride_req +
                          (long long)(q0 + n) * p.o_stride_n + (long long)qh * p.o_stride_h;
@@ -286,315 +229,6 @@ __device__ __forceinline__ void finish_rows(const AttnParams& p, const WorkItem&
 }
 
 // ---------------------------------------------------------------------------
-// Attention kernel
-// ---------------------------------------------------------------------------
-template <int D>
-struct Smem {
-  bf16_t Ks[2][64 * (D + 8)];
-  bf16_t Vt[2][D * (64 + 8)];
-  int pages[kMaxStagedPages];  // page ids of the workgroup's key range
-};
-
-// One workgroup: rows [qtile*32W, +32W) of (req, kvh) against keys
-// [kv_begin, kv_end) of source S.
-//   FP8    : S holds e4m3fn bytes (dequantised with per-kv-head scales)
-//   PAGED  : S is a paged pool (page ids staged in LDS)
-//   MASKED : causal / tree masks (else only the key-range tail is masked)
-template <int D, int W, bool FP8, bool PAGED, bool MASKED>
-__device__ __forceinline__ void attn_body(const AttnParams& p, const WorkItem& w, const KvSource& S,
-                                          Smem<D>& sm) {
-  constexpr int ROWS = 32 * W;
-  constexpr int NT = 64 * W;
-  constexpr int KP = D + 8;   // K tile pitch (elements)
-  constexpr int VP = 64 + 8;  // V^T tile pitch (elements)
-  constexpr int KCH = D / 8;  // 8-element chunks per key row
-  constexpr int NK = 64 * KCH / NT;  // K chunks per thread == V keys per thread
-  constexpr int VKG = 64 / NK;       // V key groups per d-chunk
-  constexpr int ESZ = FP8 ? 1 : 2;
-  static_assert(NK == 1 || NK == 2 || NK == 4 || NK == 8, "tile/thread mismatch");
-  typedef typename std::conditional<FP8, u32x2, u32x4>::type Raw;  // 8 elements
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wv = tid >> 6;
-  const int l32 = lane & 31;
-  const int hh = lane >> 5;
-
-  const int g = p.group;
-  const int q0 = p.qo_indptr ? p.qo_indptr[w.req] : 0;
-  const int nq = p.qo_indptr ? p.qo_indptr[w.req + 1] - q0 : p.imp.qo_len;
-  const int R = nq * g;
-  const int row = w.qtile * ROWS + wv * 32 + l32;
-  const bool rvalid = row < R;
-  const int n = rvalid ? row / g : 0;
-  const int j = rvalid ? row - n * g : 0;
-  const int qh = w.kvh * g + j;
-  const int mode = w.mode & 0xff;
-
-  // Q fragments (B operand of S^T = K Q^T): lane holds 8 consecutive head
-  // dims at offset 8*hh of every 16-wide k step, for query row `row`.
-  bf16x8 qf[D / 16];
-  {
-    const bf16_t* qp = (const bf16_t*)p.q + (long long)w.req * p.q_stride_req +
-                       (long long)(q0 + n) * p.q_stride_n + (long long)qh * p.q_stride_h + 8 * hh;
-#pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks)
-      qf[ks] = rvalid ? *(const bf16x8*)(qp + 16 * ks) : zero_bf16x8();
-  }
-
-  float kscale = 1.f, vscale = 1.f;
-  if constexpr (FP8) {
-    // e4m3fn bytes are expanded as value / 2^8 (see fp8x4_to_bf16x4)
-    kscale = (S.k_scale ? S.k_scale[w.kvh] : 1.f) * 256.f;
-    vscale = (S.v_scale ? S.v_scale[w.kvh] : 1.f) * 256.f;
-  }
-  const float c = p.sm_scale_log2 * kscale;  // raw score -> log2 domain
-  const float cn = p.sm_scale * kscale;      // raw score -> natural domain
-
-  const int kv_begin = w.kv_begin, kv_end = w.kv_end;
-  const int ntiles = (kv_end - kv_begin + 63) >> 6;
-
-  // masks: the causal offset, or the row's tree-mask words held in registers
-  int mask_mode = MASK_NONE, causal_off = 0;
-  unsigned long long mreg[kMaskRegWords] = {0ull, 0ull, 0ull, 0ull};
-  const unsigned long long* mrow = nullptr;
-  if constexpr (MASKED) {
-    mask_mode = S.mask_mode;
-    const int kvlen_req = S.kv_len ? S.kv_len[w.req] : (p.work ? nq : p.imp.kv_len);
-    causal_off = kvlen_req - nq;  // key j visible iff j <= i + causal_off
-    if (mask_mode == MASK_TREE && rvalid) {
-      mrow = S.tree_mask + (long long)(q0 + n) * S.mask_words;
-#pragma unroll
-      for (int k = 0; k < kMaskRegWords; ++k) mreg[k] = (k < S.mask_words) ? mrow[k] : 0ull;
-    }
-  }
-
-  // ---- source addressing: byte offset of token t (head folded into the base) ----
-  const char* kbase = (const char*)S.k + (long long)w.kvh * S.stride_head * ESZ;
-  const char* vbase = (const char*)S.v + (long long)w.kvh * S.stride_head * ESZ;
-  const long long tok_b = S.stride_tok * ESZ;
-  const long long page_b = S.stride_page * ESZ;
-  const int log2p = S.log2_page;
-  const int pmask = (1 << log2p) - 1;
-  int pg_first = 0;
-  if constexpr (PAGED) {
-    if (ntiles > 0) {
-      pg_first = kv_begin >> log2p;
-      const int npg = ((kv_end - 1) >> log2p) - pg_first + 1;  // <= kMaxStagedPages (planner)
-      const int* pt = S.page_table + S.page_indptr[w.req] + pg_first;
-      for (int i = tid; i < npg; i += NT) sm.pages[i] = pt[i];
-    }
-    __syncthreads();  // page ids visible to every thread
-  } else {
-    const long long base_tok = S.tok_indptr ? S.tok_indptr[w.req] : 0;
-    const long long off = ((long long)w.req * S.stride_req + base_tok * S.stride_tok) * ESZ;
-    kbase += off;
-    vbase += off;
-  }
-  auto tok_off = [&](int t) -> long long {
-    if constexpr (PAGED)
-      return (long long)sm.pages[(t >> log2p) - pg_first] * page_b + (long long)(t & pmask) * tok_b;
-    else
-      return (long long)t * tok_b;
-  };
-
-  // ---- global -> register tile loads.  Keys past kv_end load the last valid
-  // key instead (finite data whose scores the tail mask removes), so no load
-  // result is inspected before it is stored to LDS.
-  Raw kr[NK], vr[NK];
-  auto load_tile = [&](int kb) {
-#pragma unroll
-    for (int i = 0; i < NK; ++i) {
-      const int c_ = tid + i * NT;
-      const int t = min(kb + c_ / KCH, kv_end - 1);
-      kr[i] = *(const Raw*)(kbase + tok_off(t) + (c_ % KCH) * 8 * ESZ);
-    }
-    const int kg = tid % VKG, dc = tid / VKG;
-#pragma unroll
-    for (int i = 0; i < NK; ++i) {
-      const int t = min(kb + kg * NK + i, kv_end - 1);
-      vr[i] = *(const Raw*)(vbase + tok_off(t) + dc * 8 * ESZ);
-    }
-  };
-
-  auto to_bf16 = [&](const Raw& r) -> u32x4 {
-    if constexpr (FP8) {
-      const u32x2 lo = fp8x4_to_bf16x4(r[0]), hi = fp8x4_to_bf16x4(r[1]);
-      return (u32x4){lo[0], lo[1], hi[0], hi[1]};
-    } else {
-      return r;
-    }
-  };
-
-  // ---- register -> LDS (K row-major, V transposed with permuted key slots) ----
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < NK; ++i) {
-      const int c_ = tid + i * NT;
-      *(u32x4*)(&sm.Ks[buf][(c_ / KCH) * KP + (c_ % KCH) * 8]) = to_bf16(kr[i]);
-    }
-    const int kg = tid % VKG, dc = tid / VKG;
-    u32x4 vv[NK];
-#pragma unroll
-    for (int i = 0; i < NK; ++i) vv[i] = to_bf16(vr[i]);
-    // slot of key kk inside its 16-key group: keys 4h+{0..3} and 4h+8+{0..3}
-    // of half h are stored at slots 8h..8h+7 (the order in which a lane of
-    // half h holds them in the S^T accumulator).
-    auto slot_of = [](int kk) { return (kk & ~15) + 8 * ((kk >> 2) & 1) + (kk & 3) + 4 * ((kk >> 3) & 1); };
-#pragma unroll
-    for (int dd = 0; dd < 8; ++dd) {
-      const int wi = dd >> 1;
-      const int sh = (dd & 1) * 16;
-      bf16_t* rowp = &sm.Vt[buf][(dc * 8 + dd) * VP];
-      if constexpr (NK >= 4) {
-#pragma unroll
-        for (int q = 0; q < NK / 4; ++q) {
-          const unsigned e0 = (vv[4 * q][wi] >> sh) & 0xffffu, e1 = (vv[4 * q + 1][wi] >> sh) & 0xffffu;
-          const unsigned e2 = (vv[4 * q + 2][wi] >> sh) & 0xffffu, e3 = (vv[4 * q + 3][wi] >> sh) & 0xffffu;
-          *(u32x2*)(rowp + slot_of(kg * NK + 4 * q)) = (u32x2){e0 | (e1 << 16), e2 | (e3 << 16)};
-        }
-      } else if constexpr (NK == 2) {
-        const unsigned e0 = (vv[0][wi] >> sh) & 0xffffu, e1 = (vv[1][wi] >> sh) & 0xffffu;
-        *(unsigned*)(rowp + slot_of(kg * 2)) = e0 | (e1 << 16);
-      } else {
-        *(unsigned short*)(rowp + slot_of(kg)) = (unsigned short)((vv[0][wi] >> sh) & 0xffffu);
-      }
-    }
-  };
-
-  f32x16 o[D / 32];
-#pragma unroll
-  for (int mt = 0; mt < D / 32; ++mt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[mt][r] = 0.f;
-  float m_run = -INFINITY;
-  float l_run = 0.f;
-
-  if (ntiles > 0) {
-    load_tile(kv_begin);
-    store_tile(0);
-  }
-  __syncthreads();
-
-  for (int it = 0; it < ntiles; ++it) {
-    const int buf = it & 1;
-    const int kb = kv_begin + it * 64;
-    if (it + 1 < ntiles) load_tile(kb + 64);
-
-    // ---- S^T = K Q^T : two 32-key tiles ----
-    f32x16 s0, s1;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) { s0[r] = 0.f; s1[r] = 0.f; }
-    {
-      const bf16_t* ka = &sm.Ks[buf][l32 * KP + 8 * hh];
-#pragma unroll
-      for (int ks = 0; ks < D / 16; ++ks) {
-        const bf16x8 a0 = *(const bf16x8*)(ka + 16 * ks);
-        const bf16x8 a1 = *(const bf16x8*)(ka + 32 * KP + 16 * ks);
-        s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[ks], s0, 0, 0, 0);
-        s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[ks], s1, 0, 0, 0);
-      }
-    }
-
-    // ---- masking ----
-    // register r of 32-key tile kt holds key 32*kt + 8*(r/4) + 4*hh + r%4.
-    bool apply = kb + 64 > kv_end;
-    if constexpr (MASKED) apply = apply || mask_mode != MASK_NONE;
-    if (apply) {
-      unsigned long long mw = ~0ull;
-      if constexpr (MASKED) {
-        if (mask_mode == MASK_TREE) {
-          const int wi = kb >> 6;  // suffix tiles start at key 0: one word per tile
-          mw = wi == 0 ? mreg[0] : wi == 1 ? mreg[1] : wi == 2 ? mreg[2] : wi == 3 ? mreg[3]
-                                                                                  : (mrow ? mrow[wi] : 0ull);
-          if (!rvalid) mw = 0ull;
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int kk0 = 8 * (r >> 2) + 4 * hh + (r & 3);
-        const int kk1 = kk0 + 32;
-        bool v0 = kb + kk0 < kv_end, v1 = kb + kk1 < kv_end;
-        if constexpr (MASKED) {
-          if (mask_mode == MASK_CAUSAL) {
-            v0 = v0 && (kb + kk0 <= n + causal_off);
-            v1 = v1 && (kb + kk1 <= n + causal_off);
-          } else if (mask_mode == MASK_TREE) {
-            v0 = v0 && ((mw >> kk0) & 1ull);
-            v1 = v1 && ((mw >> kk1) & 1ull);
-          }
-        }
-        s0[r] = v0 ? s0[r] : -INFINITY;
-        s1[r] = v1 ? s1[r] : -INFINITY;
-      }
-    }
-
-    // ---- online softmax (lane-local row, partner lane l^32) ----
-    float mx = -INFINITY;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const bool grow = (mx > m_run) && ((m_run == -INFINITY) || (mx - m_run) * c > kRescaleSlack);
-    if (__any(grow)) {
-      const float m_new = grow ? mx : m_run;
-      const float alpha = (m_run == -INFINITY) ? 0.f : exp2f((m_run - m_new) * c);
-      l_run *= alpha;
-#pragma unroll
-      for (int mt = 0; mt < D / 32; ++mt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[mt][r] *= alpha;
-      m_run = m_new;
-    }
-    const float mc = (m_run == -INFINITY) ? 0.f : m_run * c;
-    float lsum = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      s0[r] = __builtin_amdgcn_exp2f(fmaf(s0[r], c, -mc));
-      s1[r] = __builtin_amdgcn_exp2f(fmaf(s1[r], c, -mc));
-      lsum += s0[r] + s1[r];
-    }
-    l_run += lsum;
-
-    // ---- O^T += V^T P^T ----
-    bf16x8 pb[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const f32x16& sv = (ks < 2) ? s0 : s1;
-      const int base = 8 * (ks & 1);
-      u32x4 u;
-      u[0] = pack_bf16x2(sv[base + 0], sv[base + 1]);
-      u[1] = pack_bf16x2(sv[base + 2], sv[base + 3]);
-      u[2] = pack_bf16x2(sv[base + 4], sv[base + 5]);
-      u[3] = pack_bf16x2(sv[base + 6], sv[base + 7]);
-      pb[ks] = __builtin_bit_cast(bf16x8, u);
-    }
-    {
-      const bf16_t* va = &sm.Vt[buf][l32 * VP + 8 * hh];
-#pragma unroll
-      for (int mt = 0; mt < D / 32; ++mt)
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const bf16x8 a = *(const bf16x8*)(va + 32 * mt * VP + 16 * ks);
-          o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[ks], o[mt], 0, 0, 0);
-        }
-    }
-
-    if (it + 1 < ntiles) store_tile(buf ^ 1);
-    __syncthreads();
-  }
-
-  finish_rows<D, W>(p, w, o, m_run, l_run, vscale, cn, row, rvalid, q0, n, qh);
-}
-
-template <int D, int W, bool FP8, bool PAGED, bool MASKED, int SRC>
-__global__ __launch_bounds__(64 * W) void attn_kernel(const AttnParams p) {
-  __shared__ __attribute__((aligned(16))) Smem<D> sm;
-  const WorkItem w = p.work ? p.work[blockIdx.x] : implicit_work(p, blockIdx.x);
-  if ((w.mode & 0xff) == MODE_NOOP) return;
-  attn_body<D, W, FP8, PAGED, MASKED>(p, w, p.src[SRC], sm);
-}
-
-// ---------------------------------------------------------------------------
 // bf16 attention with direct global->LDS tile loads (gfx950).
 //
 // K and V tiles travel global -> LDS with global_load_lds_dwordx4 (each wave
@@ -615,44 +249,6 @@ struct DmaSmem {
   bf16_t ring[kStages][2][64 * D];  // [stage][K, V][key row * D]
   int pages[kMaxStagedPages];
 };
-
-// XOR swizzle of 16-byte chunks in a key row (row pitch 256 B for D = 128,
-// 128 B for D = 64): 16 consecutive rows map one chunk to 16 distinct banks.
-template <int D>
-__device__ __forceinline__ int chunk_swizzle(int row) {
-  return D == 128 ? (row & 15) : ((row >> 1) & 7);
-}
-
-// One global_load_lds_dwordx4: lane l copies 16 bytes from `src` to LDS byte
-// address lds_addr + 16*l (lds_addr wave-uniform, passed through M0).  Issued
-// as inline asm so that the compiler does not track these LDS writes: its own
-// tracking waits for every outstanding DMA (vmcnt(0)) before transposing LDS
-// reads, which would drain the whole prefetch ring each tile.  Completion is
-// enforced explicitly (wait_vmcnt + s_barrier).  M0 is saved and restored.
-__device__ __forceinline__ void dma16(const void* src, unsigned lds_addr) {
-  unsigned saved;
-  __asm__ volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %1\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %2, off\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(src)
-      : "memory");
-}
-
-__device__ __forceinline__ unsigned lds_address(const void* p) {
-  return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
-}
-
-// s_waitcnt with vmcnt <= N and no wait on the other counters (gfx9 encoding:
-// vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 
 template <int D, int W, bool PAGED, bool MASKED>
 __device__ __forceinline__ void attn_dma_body(const AttnParams& p, const WorkItem& w, const KvSource& S,
@@ -693,7 +289,7 @@ __device__ __forceinline__ void attn_dma_body(const AttnParams& p, const WorkIte
   const unsigned long long* mrow = nullptr;
   if constexpr (MASKED) {
     mask_mode = S.mask_mode;
-    const int kvlen_req = S.kv_len ? S.kv_len[w.req] : (p.work ? nq : p.imp.kv_len);
+    const int kvlen_req = S.kv_len ? S.kv_len[w.req] : p.imp.kv_len;
     causal_off = kvlen_req - nq;
     if (mask_mode == MASK_TREE && rvalid) {
       mrow = S.tree_mask + (long long)(q0 + n) * S.mask_words;
@@ -912,7 +508,7 @@ __device__ __forceinline__ void attn_dma_body(const AttnParams& p, const WorkIte
 template <int D, int W, bool PAGED, bool MASKED, int SRC>
 __global__ __launch_bounds__(64 * W) void attn_dma_kernel(const AttnParams p) {
   __shared__ __attribute__((aligned(16))) DmaSmem<D> sm;
-  const WorkItem w = p.work ? p.work[blockIdx.x] : implicit_work(p, blockIdx.x);
+  const WorkItem w = implicit_work(p, blockIdx.x);
   if ((w.mode & 0xff) == MODE_NOOP) return;
   attn_dma_body<D, W, PAGED, MASKED>(p, w, p.src[SRC], sm);
 }
@@ -1003,51 +599,20 @@ __global__ __launch_bounds__(256) void merge_state_kernel(const MergeStateArgs a
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
-template <int D, int W, bool FP8, bool PAGED, bool MASKED, int SRC>
-static hipError_t launch_attn_t(const AttnParams& p, int nblocks, hipStream_t s) {
-  hipLaunchKernelGGL((attn_kernel<D, W, FP8, PAGED, MASKED, SRC>), dim3(nblocks), dim3(64 * W), 0, s, p);
-  return hipGetLastError();
-}
-
-// Kernel variants: the shared-prefix level (unmasked; contiguous or paged,
-// bf16 or fp8), the suffix tree level (masked, contiguous, kSuffixWaves waves)
-// and the single-source drop-in (contiguous bf16, optionally causal).
-template <int D, int W, bool PAGED, bool MASKED, int SRC>
+template <int D, int W, bool MASKED>
 static hipError_t launch_dma_t(const AttnParams& p, int nblocks, hipStream_t s) {
-  hipLaunchKernelGGL((attn_dma_kernel<D, W, PAGED, MASKED, SRC>), dim3(nblocks), dim3(64 * W), 0, s, p);
+  hipLaunchKernelGGL((attn_dma_kernel<D, W, false, MASKED, 0>), dim3(nblocks), dim3(64 * W), 0, s, p);
   return hipGetLastError();
 }
 
-// Kernel variants: bf16 sources use the direct-to-LDS kernel — the shared
-// prefix level (unmasked; contiguous or paged), the suffix tree level
-// (masked, contiguous, kSuffixWaves waves) and the single-source drop-in
-// (contiguous, optionally causal); an fp8 prefix uses the register-staged
-// kernel, which converts e4m3fn to bf16 on its way into LDS.
+// Kernel variants of the single-source drop-ins: contiguous bf16 K/V,
+// unmasked or causal, 4- or 8-wave workgroups.
 template <int D>
 static hipError_t launch_attention_d(const AttnParams& p, int waves, int src, bool fp8, bool paged, bool masked,
                                      int nblocks, hipStream_t s) {
-  if (src == 1) {
-    if (waves == kSuffixWaves && masked && !fp8 && !paged)
-      return launch_dma_t<D, kSuffixWaves, false, true, 1>(p, nblocks, s);
-    return hipErrorInvalidValue;
-  }
-  if (masked) {
-    if (fp8 || paged) return hipErrorInvalidValue;
-    if (waves == 4) return launch_dma_t<D, 4, false, true, 0>(p, nblocks, s);
-    if (waves == 8) return launch_dma_t<D, 8, false, true, 0>(p, nblocks, s);
-    return hipErrorInvalidValue;
-  }
-  if (!fp8) {
-    if (waves == 4) return paged ? launch_dma_t<D, 4, true, false, 0>(p, nblocks, s)
-                                 : launch_dma_t<D, 4, false, false, 0>(p, nblocks, s);
-    if (waves == 8) return paged ? launch_dma_t<D, 8, true, false, 0>(p, nblocks, s)
-                                 : launch_dma_t<D, 8, false, false, 0>(p, nblocks, s);
-    return hipErrorInvalidValue;
-  }
-  if (waves == 4) return paged ? launch_attn_t<D, 4, true, true, false, 0>(p, nblocks, s)
-                               : launch_attn_t<D, 4, true, false, false, 0>(p, nblocks, s);
-  if (waves == 8) return paged ? launch_attn_t<D, 8, true, true, false, 0>(p, nblocks, s)
-                               : launch_attn_t<D, 8, true, false, false, 0>(p, nblocks, s);
+  if (src != 0 || fp8 || paged) return hipErrorInvalidValue;
+  if (waves == 4) return masked ? launch_dma_t<D, 4, true>(p, nblocks, s) : launch_dma_t<D, 4, false>(p, nblocks, s);
+  if (waves == 8) return masked ? launch_dma_t<D, 8, true>(p, nblocks, s) : launch_dma_t<D, 8, false>(p, nblocks, s);
   return hipErrorInvalidValue;
 }
 

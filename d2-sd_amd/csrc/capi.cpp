@@ -265,8 +265,9 @@ int d2sd_cascade_plan(const d2sd_cascade_plan_desc* desc, int32_t* host_plan, si
     return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: need num_reqs > 0, qo_indptr and prefix_len");
   if (desc->kv_dtype != D2SD_KV_BF16 && desc->kv_dtype != D2SD_KV_FP8_E4M3)
     return fail(D2SD_ERR_UNSUPPORTED, "cascade_plan: kv_dtype");
-  if (desc->waves_per_block != 0 && desc->waves_per_block != 4 && desc->waves_per_block != 8)
-    return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: waves_per_block must be 0, 4 or 8");
+  if (desc->waves_per_block != 0 && desc->waves_per_block != 2 && desc->waves_per_block != 4 &&
+      desc->waves_per_block != 8)
+    return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: waves_per_block must be 0, 2, 4 or 8");
   if (desc->qo_indptr[0] != 0) return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: qo_indptr[0] must be 0");
   for (int r = 0; r < desc->num_reqs; ++r) {
     if (desc->qo_indptr[r + 1] < desc->qo_indptr[r])
@@ -275,10 +276,20 @@ int d2sd_cascade_plan(const d2sd_cascade_plan_desc* desc, int32_t* host_plan, si
   }
   if (desc->page_size < 0 || (desc->page_size & (desc->page_size - 1)))
     return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: page_size must be 0 or a power of two");
-  d2sd::PlanInput in{};
+  if (desc->page_size > 0) {
+    if (!desc->page_indptr) return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: paged prefix needs page_indptr");
+    for (int r = 0; r < desc->num_reqs; ++r) {
+      const long long need = ((long long)desc->prefix_len[r] + desc->page_size - 1) / desc->page_size;
+      if (desc->page_indptr[r + 1] - desc->page_indptr[r] < need)
+        return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: page_indptr gives a request fewer pages than prefix_len needs");
+    }
+  }
+  d2sd::VerifyPlanInput in{};
   in.num_reqs = desc->num_reqs;
   in.qo_indptr = desc->qo_indptr;
   in.prefix_len = desc->prefix_len;
+  in.page_indptr = desc->page_indptr;
+  in.prefix_tok_indptr = desc->prefix_tok_indptr;
   in.num_qo_heads = desc->num_qo_heads;
   in.num_kv_heads = desc->num_kv_heads;
   in.head_dim = desc->head_dim;
@@ -287,17 +298,17 @@ int d2sd_cascade_plan(const d2sd_cascade_plan_desc* desc, int32_t* host_plan, si
   in.max_splits = desc->max_splits;
   in.waves = desc->waves_per_block;
   in.page_size = desc->page_size;
-  d2sd::PlanOutput out{};
-  d2sd::plan_cascade(in, out);
-  static_assert(sizeof(d2sd::WorkItem) == 8 * sizeof(int32_t), "WorkItem layout");
+  d2sd::VerifyPlanOutput out{};
+  d2sd::plan_verify(in, out);
+  static_assert(sizeof(d2sd::VerifyItem) == 16 * sizeof(int32_t), "VerifyItem layout");
+  static_assert(sizeof(d2sd::VerifyMerge) == 8 * sizeof(int32_t), "VerifyMerge layout");
   std::memset(info, 0, sizeof(*info));
-  info->num_prefix_work = (int)out.prefix_work.size();
-  info->num_suffix_work = (int)out.suffix_work.size();
-  info->prefix_waves = out.waves;
-  info->suffix_waves = out.suffix_waves;
-  info->prefix_rows = out.rows_per_tile;
+  info->num_items = (int)out.items.size();
+  info->num_merges = (int)out.merges.size();
+  info->waves_per_block = out.waves;
+  info->rows_per_tile = out.rows;
   info->num_slots = out.num_slots;
-  info->plan_ints = 8 * (info->num_prefix_work + info->num_suffix_work);
+  info->plan_ints = 16 * info->num_items + 8 * info->num_merges;
   info->workspace_bytes = out.workspace_bytes;
   info->max_splits_used = out.max_splits_used;
   info->num_reqs = desc->num_reqs;
@@ -310,19 +321,22 @@ int d2sd_cascade_plan(const d2sd_cascade_plan_desc* desc, int32_t* host_plan, si
     if (host_plan_ints < (size_t)info->plan_ints)
       return fail(D2SD_ERR_WORKSPACE, "cascade_plan: host_plan too small (need " +
                                           std::to_string(info->plan_ints) + " int32)");
-    std::memcpy(host_plan, out.prefix_work.data(), out.prefix_work.size() * sizeof(d2sd::WorkItem));
-    std::memcpy(host_plan + 8 * out.prefix_work.size(), out.suffix_work.data(),
-                out.suffix_work.size() * sizeof(d2sd::WorkItem));
+    std::memcpy(host_plan, out.items.data(), out.items.size() * sizeof(d2sd::VerifyItem));
+    std::memcpy(host_plan + 16 * out.items.size(), out.merges.data(),
+                out.merges.size() * sizeof(d2sd::VerifyMerge));
   }
   return D2SD_OK;
 }
 
-static int build_cascade_params(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* a,
-                                d2sd::AttnParams& p) {
+static int build_verify_params(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* a,
+                               d2sd::VerifyParams& p) {
   if (!info || !a) return fail(D2SD_ERR_INVALID_ARG, "cascade_run: null info/args");
   const int D = info->head_dim;
   if (int rc = check_heads(info->num_qo_heads, info->num_kv_heads, D)) return rc;
-  if (!a->plan || !a->qo_indptr || !a->q || !a->k_suffix || !a->v_suffix || !a->out || !a->prefix_len)
+  if ((info->waves_per_block != 2 && info->waves_per_block != 4 && info->waves_per_block != 8) ||
+      info->rows_per_tile != d2sd::verify_rows(info->waves_per_block))
+    return fail(D2SD_ERR_INVALID_ARG, "cascade_run: info does not come from d2sd_cascade_plan");
+  if (!a->plan || !a->q || !a->k_suffix || !a->v_suffix || !a->out)
     return fail(D2SD_ERR_INVALID_ARG, "cascade_run: null pointer");
   if (info->num_slots > 0 && (!a->workspace || a->workspace_bytes < info->workspace_bytes))
     return fail(D2SD_ERR_WORKSPACE, "cascade_run: workspace too small (need " +
@@ -331,100 +345,98 @@ static int build_cascade_params(const d2sd_cascade_plan_info* info, const d2sd_c
       !stride_ok(a->q_stride_n) || !stride_ok(a->q_stride_h) || !stride_ok(a->suffix_stride_n) ||
       !stride_ok(a->suffix_stride_h) || !stride_ok(a->o_stride_n) || !stride_ok(a->o_stride_h))
     return fail(D2SD_ERR_INVALID_ARG, "cascade_run: tensors must be 16-byte aligned with strides % 8 == 0");
+  if (info->workspace_bytes > 0 && !aligned16(a->workspace))
+    return fail(D2SD_ERR_INVALID_ARG, "cascade_run: workspace must be 16-byte aligned");
   const bool has_prefix = a->k_prefix != nullptr;
-  if (has_prefix) {
-    if (!a->v_prefix || !aligned16(a->k_prefix) || !aligned16(a->v_prefix) || !stride_ok(a->prefix_stride_tok) ||
-        !stride_ok(a->prefix_stride_head) || (a->page_size > 0 && !stride_ok(a->prefix_stride_page)))
-      return fail(D2SD_ERR_INVALID_ARG, "cascade_run: prefix K/V must be 16-byte aligned with strides % 8 == 0");
-    if (a->page_size > 0 && ((a->page_size & (a->page_size - 1)) || !a->page_table || !a->page_indptr))
-      return fail(D2SD_ERR_INVALID_ARG, "cascade_run: paged prefix needs a power-of-two page_size, page_table and page_indptr");
-    if (a->page_size != info->page_size)
-      return fail(D2SD_ERR_INVALID_ARG, "cascade_run: page_size differs from the planned one");
-  }
   if (info->max_splits_used > 0 && !has_prefix)
     return fail(D2SD_ERR_INVALID_ARG, "cascade_run: the plan has prefix keys but k_prefix is null");
+  if (has_prefix) {
+    const int esz = info->kv_dtype == D2SD_KV_FP8_E4M3 ? 1 : 2;
+    auto ok = [&](int64_t st) { return (st * esz) % 16 == 0; };
+    if (!a->v_prefix || !aligned16(a->k_prefix) || !aligned16(a->v_prefix) || !ok(a->prefix_stride_tok) ||
+        !ok(a->prefix_stride_head) || (info->page_size > 0 && !ok(a->prefix_stride_page)))
+      return fail(D2SD_ERR_INVALID_ARG, "cascade_run: prefix K/V must be 16-byte aligned with 16-byte strides");
+    if (a->page_size != info->page_size)
+      return fail(D2SD_ERR_INVALID_ARG, "cascade_run: page_size differs from the planned one");
+    if (info->page_size > 0 && !a->page_table)
+      return fail(D2SD_ERR_INVALID_ARG, "cascade_run: paged prefix needs page_table");
+  }
+  if (a->mask_mode != D2SD_MASK_NONE && a->mask_mode != D2SD_MASK_CAUSAL && a->mask_mode != D2SD_MASK_TREE)
+    return fail(D2SD_ERR_INVALID_ARG, "cascade_run: mask_mode");
   if (a->mask_mode == D2SD_MASK_TREE && (!a->tree_mask || a->mask_words <= 0))
     return fail(D2SD_ERR_INVALID_ARG, "cascade_run: tree mask needs tree_mask and mask_words");
-  if (info->kv_dtype == D2SD_KV_FP8_E4M3 && (!a->k_scale || !a->v_scale))
+  if (info->kv_dtype == D2SD_KV_FP8_E4M3 && has_prefix && (!a->k_scale || !a->v_scale))
     return fail(D2SD_ERR_INVALID_ARG, "cascade_run: fp8 prefix needs k_scale and v_scale");
+  if (!(a->sm_scale > 0.f) || !std::isfinite(a->sm_scale))
+    return fail(D2SD_ERR_INVALID_ARG, "cascade_run: bad sm_scale");
 
-  p = d2sd::AttnParams{};
+  p = d2sd::VerifyParams{};
   p.q = a->q;
   p.q_stride_n = a->q_stride_n;
   p.q_stride_h = a->q_stride_h;
-  p.qo_indptr = a->qo_indptr;
   p.o = a->out;
   p.o_stride_n = a->o_stride_n;
   p.o_stride_h = a->o_stride_h;
   p.lse = a->lse;
   p.lse_stride_n = a->lse_stride_n;
-  const long long rows = info->prefix_rows;
+  const long long rows = info->rows_per_tile;
   p.part_o = a->workspace;
   p.part_lse = a->workspace ? (float*)((char*)a->workspace + (long long)info->num_slots * rows * D * 2) : nullptr;
-  p.work = (const d2sd::WorkItem*)a->plan;
-  p.merge = nullptr;
-  p.prefix_rows = info->prefix_rows;
+  p.items = (const d2sd::VerifyItem*)a->plan;
+  p.merges = (const d2sd::VerifyMerge*)(a->plan + 16 * (long long)info->num_items);
   p.sinks = a->sinks;
-  d2sd::KvSource& pre = p.src[0];
+  p.tree_mask = (const unsigned long long*)a->tree_mask;
+  d2sd::VerifySource& pre = p.pre;
   pre.k = a->k_prefix;
   pre.v = a->v_prefix;
   pre.stride_tok = a->prefix_stride_tok;
   pre.stride_head = a->prefix_stride_head;
   pre.stride_page = a->prefix_stride_page;
-  pre.tok_indptr = a->prefix_tok_indptr;
-  pre.page_indptr = a->page_size > 0 ? a->page_indptr : nullptr;
-  pre.page_table = a->page_size > 0 ? a->page_table : nullptr;
-  pre.kv_len = a->prefix_len;
+  pre.page_table = info->page_size > 0 ? a->page_table : nullptr;
   pre.k_scale = a->k_scale;
   pre.v_scale = a->v_scale;
   int lg = 0;
-  while (a->page_size > 0 && (1 << lg) < a->page_size) ++lg;
+  while (info->page_size > 0 && (1 << lg) < info->page_size) ++lg;
   pre.log2_page = lg;
-  pre.mask_mode = d2sd::MASK_NONE;
-  pre.dtype = info->kv_dtype == D2SD_KV_FP8_E4M3 ? d2sd::KV_FP8 : d2sd::KV_BF16;
-  d2sd::KvSource& suf = p.src[1];
+  pre.fp8 = info->kv_dtype == D2SD_KV_FP8_E4M3;
+  d2sd::VerifySource& suf = p.suf;
   suf.k = a->k_suffix;
   suf.v = a->v_suffix;
   suf.stride_tok = a->suffix_stride_n;
   suf.stride_head = a->suffix_stride_h;
-  suf.tok_indptr = a->qo_indptr;
-  suf.kv_len = nullptr;  // suffix keys == the request's queries
-  suf.tree_mask = (const unsigned long long*)a->tree_mask;
-  suf.mask_mode = a->mask_mode;
-  suf.mask_words = a->mask_words;
-  suf.dtype = d2sd::KV_BF16;
   p.sm_scale = a->sm_scale;
   p.sm_scale_log2 = a->sm_scale * kLog2e;
-  p.num_kv_heads = info->num_kv_heads;
   p.group = info->num_qo_heads / info->num_kv_heads;
+  p.mask_mode = a->mask_mode;
+  p.mask_words = a->mask_words;
   p.lse_base2 = a->lse_base2;
-  p.num_merge = 0;
+  p.num_merges = info->num_merges;
   return D2SD_OK;
 }
 
-int d2sd_cascade_prefix(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* a, d2sd_stream_t stream) {
+int d2sd_cascade_attention(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* a,
+                           d2sd_stream_t stream) {
   g_last_error.clear();
-  d2sd::AttnParams p{};
-  if (int rc = build_cascade_params(info, a, p)) return rc;
-  const bool fp8 = info->kv_dtype == D2SD_KV_FP8_E4M3;
-  hipError_t e = d2sd::launch_attention(p, info->head_dim, info->prefix_waves, 0, fp8, info->page_size > 0,
-                                        false, info->num_prefix_work, (hipStream_t)stream);
-  return e == hipSuccess ? D2SD_OK : fail_hip(e, "cascade prefix launch");
+  d2sd::VerifyParams p{};
+  if (int rc = build_verify_params(info, a, p)) return rc;
+  hipError_t e = d2sd::launch_verify_attention(p, info->head_dim, info->waves_per_block, info->page_size > 0,
+                                               info->kv_dtype == D2SD_KV_FP8_E4M3, info->num_items,
+                                               (hipStream_t)stream);
+  return e == hipSuccess ? D2SD_OK : fail_hip(e, "cascade attention launch");
 }
 
-int d2sd_cascade_suffix(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* a, d2sd_stream_t stream) {
+int d2sd_cascade_merge(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* a, d2sd_stream_t stream) {
   g_last_error.clear();
-  d2sd::AttnParams p{};
-  if (int rc = build_cascade_params(info, a, p)) return rc;
-  p.work += info->num_prefix_work;
-  hipError_t e = d2sd::launch_attention(p, info->head_dim, info->suffix_waves, 1, false, false, true,
-                                        info->num_suffix_work, (hipStream_t)stream);
-  return e == hipSuccess ? D2SD_OK : fail_hip(e, "cascade suffix launch");
+  d2sd::VerifyParams p{};
+  if (int rc = build_verify_params(info, a, p)) return rc;
+  hipError_t e = d2sd::launch_verify_merge(p, info->head_dim, info->rows_per_tile, info->num_merges,
+                                           (hipStream_t)stream);
+  return e == hipSuccess ? D2SD_OK : fail_hip(e, "cascade merge launch");
 }
 
 int d2sd_cascade_run(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* a, d2sd_stream_t stream) {
-  if (int rc = d2sd_cascade_prefix(info, a, stream)) return rc;
-  return d2sd_cascade_suffix(info, a, stream);
+  if (int rc = d2sd_cascade_attention(info, a, stream)) return rc;
+  return d2sd_cascade_merge(info, a, stream);
 }
 
 }  // extern "C"

@@ -12,29 +12,20 @@ enum : int {
   MODE_FINAL = 1,    // only producer for its rows: write bf16 O and LSE directly
   MODE_INPLACE = 2,  // merge into the (O, LSE) already stored at the output
   MODE_NOOP = 3,     // padding item, exits immediately
-  MODE_MERGE_SLOTS = 4,  // merge (mode >> 8) prefix partials at `slot` with its own state
 };
 
 enum : int { MASK_NONE = 0, MASK_CAUSAL = 1, MASK_TREE = 2 };
 
 // Page ids one attention workgroup stages in LDS (its split's pages).
 constexpr int kMaxStagedPages = 1024;
-// Waves of the suffix (tree attention + merge) launch: 64-row blocks.
-constexpr int kSuffixWaves = 2;
 enum : int { KV_BF16 = 0, KV_FP8 = 1 };
 
-// One attention workgroup: rows [qtile*ROWS, (qtile+1)*ROWS) of the packed
-// (token, query-head) rows that read kv head `kvh` of request `req`, against
-// keys [kv_begin, kv_end) of key source `src`.  `mode` holds the epilogue in
-// its low 8 bits and, for MODE_MERGE_SLOTS, the partial count above them.
+// One attention workgroup of the single-source kernels: rows
+// [qtile*ROWS, (qtile+1)*ROWS) of the packed (token, query-head) rows that read
+// kv head `kvh` of request `req`, against keys [kv_begin, kv_end) of key
+// source `src`, with epilogue `mode`.
 struct WorkItem {
   int req, kvh, qtile, src, kv_begin, kv_end, slot, mode;
-};
-
-// One merge item: rows of tile (req, kvh, qtile), partial slots
-// [slot_begin, slot_begin + nslots), epilogue FINAL or INPLACE.
-struct MergeItem {
-  int req, kvh, qtile, slot_begin, nslots, mode, pad0, pad1;
 };
 
 // Where the keys/values of one level live.  Offsets are in elements.
@@ -58,10 +49,10 @@ struct KvSource {
   int dtype;               // KV_BF16 / KV_FP8
 };
 
-// Uniform work decomposition used when no explicit work list is given:
-// every request has qo_len queries and kv_len keys; items are ordered so that
-// all q-tiles reading one (request, kv head, split) key chunk land on the
-// same XCD (workgroups are dealt to the 8 XCDs round-robin).
+// Uniform work decomposition of the single-source kernels: every request
+// has qo_len queries and kv_len keys; items are ordered so that all q-tiles
+// reading one (request, kv head, split) key chunk land on the same XCD
+// (workgroups are dealt to the 8 XCDs round-robin).
 struct ImplicitWork {
   int num_reqs;
   int qtiles;
@@ -83,8 +74,6 @@ struct AttnParams {
   long long lse_stride_n, lse_stride_req;
   void* part_o;                  // bf16 [slot][ROWS * D], register image
   float* part_lse;               // [slot][ROWS]
-  const WorkItem* work;          // nullable => implicit
-  const MergeItem* merge;        // nullable => implicit
   const float* sinks;            // nullable, [Hq]
   KvSource src[2];
   ImplicitWork imp;
@@ -94,7 +83,72 @@ struct AttnParams {
   int group;                     // Hq / Hkv
   int lse_base2;
   int num_merge;
-  int prefix_rows;               // rows per partial slot (MODE_MERGE_SLOTS)
 };
+
+
+// ---------------------------------------------------------------------------
+// Cascade verify attention (verify_attention.hip): one attention launch whose
+// workgroups each own ROWS = 64 * W packed rows of one (request, kv head,
+// q-tile) group and either one key chunk of the shared prefix or the whole
+// suffix tree, then one merge launch.
+// ---------------------------------------------------------------------------
+enum : int { SRC_PREFIX = 0, SRC_SUFFIX = 1 };
+
+// 64 bytes; everything a workgroup needs is baked in by the planner so that
+// the kernel's first dependent load is the item itself.
+struct VerifyItem {
+  int req, kvh, qtile, src;
+  int kv_begin, kv_end;  // keys [kv_begin, kv_end) of the source
+  int slot;              // partial slot (MODE_PARTIAL)
+  int mode;              // MODE_PARTIAL / MODE_FINAL / MODE_NOOP
+  int q0, nq;            // the request's first query row and query count
+  int base;              // paged: page_table index of the request's page 0;
+                         // contiguous: token offset of the request's key 0
+  int causal_off;        // MASK_CAUSAL: key j visible to query i iff j <= i + causal_off
+  int pad[4];
+};
+
+// One group whose partial slots [slot0, slot0 + nslots) are merged.
+struct VerifyMerge {
+  int req, kvh, qtile, slot0, nslots, q0, nq, pad;
+};
+
+struct VerifySource {
+  const void* k;
+  const void* v;
+  long long stride_tok, stride_head, stride_page;  // elements
+  const int* page_table;   // nullable => contiguous
+  const float* k_scale;    // fp8 dequant scale per kv head (nullable => 1)
+  const float* v_scale;
+  int log2_page;
+  int fp8;
+};
+
+struct VerifyParams {
+  const void* q;
+  long long q_stride_n, q_stride_h;
+  void* o;
+  long long o_stride_n, o_stride_h;
+  float* lse;              // nullable
+  long long lse_stride_n;
+  void* part_o;            // bf16 [slot][ROWS * D], register image
+  float* part_lse;         // [slot][ROWS]
+  const VerifyItem* items;
+  const VerifyMerge* merges;
+  const float* sinks;      // nullable, [Hq]
+  const unsigned long long* tree_mask;  // [total_q][mask_words]
+  VerifySource pre, suf;
+  float sm_scale;
+  float sm_scale_log2;
+  int group;               // Hq / Hkv
+  int mask_mode;           // suffix level: MASK_NONE / MASK_CAUSAL / MASK_TREE
+  int mask_words;
+  int lse_base2;
+  int num_merges;
+  int pad;
+};
+
+// Splits per group are capped so that one merge batch holds all partials.
+constexpr int kMaxVerifySplits = 15;
 
 }  // namespace d2sd

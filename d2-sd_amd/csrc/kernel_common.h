@@ -1,0 +1,108 @@
+// Device helpers shared by the gfx950 attention kernels (attention.hip,
+// verify_attention.hip): vector types, bf16 packing, fp8 expansion, the
+// direct global->LDS copy and explicit vmcnt waits.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+namespace d2sd {
+
+typedef __bf16 bf16_t;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+// Lazy rescaling: the running max used for exponentiation may trail the true
+// row max by up to 2^kRescaleSlack before O and l are rescaled.
+constexpr float kRescaleSlack = 8.0f;
+// Tree-mask words held in registers per row (rows of up to 256 nodes).
+constexpr int kMaskRegWords = 4;
+
+__device__ __forceinline__ bf16x8 zero_bf16x8() {
+  u32x4 z = {0u, 0u, 0u, 0u};
+  return __builtin_bit_cast(bf16x8, z);
+}
+
+__device__ __forceinline__ unsigned pack_bf16x2(float a, float b) {
+  f32x2 v = {a, b};
+  return __builtin_bit_cast(unsigned, __builtin_convertvector(v, bf16x2));
+}
+
+__device__ __forceinline__ float bf16_lo(unsigned w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(unsigned w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Element offset, inside one partial slot, of the 4 values (mt, q4) that lane
+// `lane` of 32-row block `blk` holds: the accumulator register image, so that
+// every partial store / load is one contiguous 512-byte wave access.
+template <int D>
+__device__ __forceinline__ int image_offset(int blk, int mt, int q4, int lane) {
+  return ((blk * (D / 32) + mt) * 4 + q4) * 256 + 4 * lane;
+}
+
+// fp8 e4m3fn (OCP) -> bf16, exact.  Bytes b0..b3 of w -> 4 bf16 in a u32x2.
+// e4m3fn placed in the top of an fp16 gives value(fp16) * 2^8 == value(e4m3fn)
+// for normals and subnormals alike (exponent bias 15 vs 7); the 2^8 is folded
+// into the dequantisation scale by the caller.
+__device__ __forceinline__ u32x2 fp8x4_to_bf16x4(unsigned w) {
+  u32x2 r;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const unsigned b0 = (w >> (16 * h)) & 0xffu, b1 = (w >> (16 * h + 8)) & 0xffu;
+    const unsigned h0 = ((b0 & 0x80u) << 8) | ((b0 & 0x7fu) << 7);
+    const unsigned h1 = ((b1 & 0x80u) << 8) | ((b1 & 0x7fu) << 7);
+    const float f0 = (float)__builtin_bit_cast(_Float16, (unsigned short)h0);
+    const float f1 = (float)__builtin_bit_cast(_Float16, (unsigned short)h1);
+    // fp16 values with a 3-bit mantissa are exact in bf16: truncate.
+    r[h] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
+  }
+  return r;
+}
+
+// One global_load_lds_dwordx4: lane l copies 16 bytes from `src` to LDS byte
+// address lds_addr + 16*l (lds_addr wave-uniform, passed through M0).  Issued
+// as inline asm so that the compiler does not track these LDS writes: its own
+// tracking waits for every outstanding DMA (vmcnt(0)) before LDS reads, which
+// would drain the whole prefetch ring each tile.  Completion is enforced
+// explicitly (wait_vmcnt + s_barrier).  M0 is saved and restored.
+__device__ __forceinline__ void dma16(const void* src, unsigned lds_addr) {
+  unsigned saved;
+  __asm__ volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(src)
+      : "memory");
+}
+
+__device__ __forceinline__ unsigned lds_address(const void* p) {
+  return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+// s_waitcnt with vmcnt <= N and no wait on the other counters (gfx9 encoding:
+// vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// XOR swizzle of 16-byte chunks in a key row (row pitch 256 B for D = 128,
+// 128 B for D = 64): 16 consecutive rows map one chunk to 16 distinct banks.
+template <int D>
+__device__ __forceinline__ int chunk_swizzle(int row) {
+  return D == 128 ? (row & 15) : ((row >> 1) & 7);
+}
+
+}  // namespace d2sd

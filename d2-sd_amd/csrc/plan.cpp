@@ -1,4 +1,5 @@
-// Host-side work planning for cascade verify attention (plan()).
+// Host-side work planning for cascade verify attention (plan()) and the
+// single-source drop-in (single_prefill_with_kv_cache).
 //
 // Splits every request's visible prefix into key chunks (split-KV) so that the
 // attention launch fills the device, adds one suffix (tree) item per q-tile,
@@ -27,12 +28,20 @@ int blocks_per_cu(int waves) { return waves == 4 ? 2 : 1; }
 
 // Deal sets of work items to the 8 XCDs (largest first onto the least-loaded
 // XCD) and interleave them so that item k of XCD x lands at workgroup index
-// 8k + x; shorter XCD lists are padded with NOOP items.
-template <typename SetT>
-static void order_for_xcds(std::vector<SetT>& sets, std::vector<WorkItem>& out) {
-  std::stable_sort(sets.begin(), sets.end(), [](const SetT& a, const SetT& b) { return a.cost > b.cost; });
+// 8k + x (workgroups are dispatched to XCDs round-robin); shorter XCD lists are
+// padded with NOOP items.
+template <typename Item>
+struct ItemSet {
+  long long cost;
+  std::vector<Item> items;
+};
+
+template <typename Item>
+static void order_for_xcds(std::vector<ItemSet<Item>>& sets, std::vector<Item>& out) {
+  std::stable_sort(sets.begin(), sets.end(),
+                   [](const ItemSet<Item>& a, const ItemSet<Item>& b) { return a.cost > b.cost; });
   std::vector<long long> load(8, 0);
-  std::vector<std::vector<WorkItem>> lists(8);
+  std::vector<std::vector<Item>> lists(8);
   for (auto& set : sets) {
     const int x = (int)(std::min_element(load.begin(), load.end()) - load.begin());
     load[x] += set.cost;
@@ -45,7 +54,7 @@ static void order_for_xcds(std::vector<SetT>& sets, std::vector<WorkItem>& out) 
       if (k < lists[x].size()) {
         out.push_back(lists[x][k]);
       } else {
-        WorkItem w{};
+        Item w{};
         w.mode = MODE_NOOP;
         out.push_back(w);
       }
@@ -53,134 +62,154 @@ static void order_for_xcds(std::vector<SetT>& sets, std::vector<WorkItem>& out) 
   while (!out.empty() && out.back().mode == MODE_NOOP) out.pop_back();
 }
 
-int plan_cascade(const PlanInput& in, PlanOutput& out) {
-  out.prefix_work.clear();
-  out.suffix_work.clear();
+int verify_wgs_per_cu(int waves) { return waves == 8 ? 1 : 2; }
+int verify_rows(int waves) { return waves == 2 ? 128 : 32 * waves; }
+
+// Cascade verify plan.  Groups are (request, kv head, q-tile of ROWS packed
+// rows).  Each group gets S key chunks of its visible prefix (S partial
+// slots) plus one suffix item (slot S), merged by one merge item; a group
+// with no prefix keys has only its suffix item, which writes the output.
+// The chunk length is the smallest that keeps every item of the launch
+// resident at once (verify_wgs_per_cu per CU), capped so that S stays within
+// kMaxVerifySplits and a chunk's page ids fit the kernel's LDS staging.
+int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
+  out.items.clear();
+  out.merges.clear();
   const int Hkv = in.num_kv_heads;
   const int g = in.num_qo_heads / Hkv;
-  int max_rows = 0;
-  for (int r = 0; r < in.num_reqs; ++r) max_rows = std::max(max_rows, (in.qo_indptr[r + 1] - in.qo_indptr[r]) * g);
-  const int WA = in.waves ? in.waves : choose_waves(max_rows);
-  const int ROWS_A = 32 * WA;
-  const int WB = kSuffixWaves;  // divides WA, so a suffix block lies in one prefix tile
-  const int ROWS_B = 32 * WB;
-  const int num_cus = in.num_cus > 0 ? in.num_cus : 256;
-  const long long target = (long long)num_cus * blocks_per_cu(WA);
-
+  const int W = in.waves ? in.waves : 4;
+  const int ROWS = verify_rows(W);
   const int R = in.num_reqs;
-  std::vector<int> qtiles(R), ptiles(R), kv0(R), kv1(R), splits(R, 0), nq(R);
-  long long prefix_cost = 0;
+  const int num_cus = in.num_cus > 0 ? in.num_cus : 256;
+  const long long capacity = (long long)num_cus * verify_wgs_per_cu(W);
+  const int split_cap =
+      in.max_splits > 0 ? std::min(in.max_splits, kMaxVerifySplits) : kMaxVerifySplits;
+
+  std::vector<int> nq(R), qtiles(R), ptiles(R), stiles(R), kv0(R), kv1(R), splits(R, 0);
+  long long units = 0, groups = 0;
+  int max_ptiles = 1;
   for (int r = 0; r < R; ++r) {
     nq[r] = in.qo_indptr[r + 1] - in.qo_indptr[r];
-    qtiles[r] = (nq[r] * g + ROWS_A - 1) / ROWS_A;
+    qtiles[r] = (nq[r] * g + ROWS - 1) / ROWS;
     const int L = in.prefix_len[r];
     const int Leff = in.window_left >= 0 ? std::min(L, in.window_left) : L;
     kv0[r] = L - Leff;
     kv1[r] = L;
     ptiles[r] = nq[r] > 0 ? (Leff + 63) / 64 : 0;
-    prefix_cost += (long long)Hkv * qtiles[r] * ptiles[r];
+    stiles[r] = (nq[r] + 63) / 64;
+    max_ptiles = std::max(max_ptiles, ptiles[r]);
+    units += (long long)Hkv * qtiles[r] * (ptiles[r] + stiles[r]);
+    groups += (long long)Hkv * qtiles[r];
   }
-  // Key tiles per prefix split: the smallest chunk for which one wave of
-  // workgroups covers the prefix level, capped so that one split's page ids
-  // fit the kernel's LDS staging area.
-  int chunk = 1;
-  if (prefix_cost > 0) {
-    chunk = (int)std::max<long long>(1, (prefix_cost + target - 1) / target);
-    auto wgs = [&](int c) {
-      long long t = 0;
-      for (int r = 0; r < R; ++r) t += (long long)Hkv * qtiles[r] * ((ptiles[r] + c - 1) / c);
-      return t;
-    };
-    // once every request is a single split, more chunking cannot help
-    int max_ptiles = 1;
-    for (int r = 0; r < R; ++r) max_ptiles = std::max(max_ptiles, ptiles[r]);
-    while (chunk < max_ptiles && wgs(chunk) > target) ++chunk;
-    if (in.page_size > 0) {
-      const int max_chunk = std::max(1, ((kMaxStagedPages - 2) * in.page_size) / 64);
-      chunk = std::min(chunk, max_chunk);
-    }
+  auto wgs = [&](int c) {
+    long long t = 0;
+    for (int r = 0; r < R; ++r)
+      if (nq[r] > 0) t += (long long)Hkv * qtiles[r] * ((ptiles[r] + c - 1) / c + 1);
+    return t;
+  };
+  int chunk = (int)std::max<long long>(1, (units + capacity - 1) / std::max<long long>(capacity, 1));
+  while (chunk < max_ptiles && wgs(chunk) > capacity) ++chunk;
+  for (int r = 0; r < R; ++r) chunk = std::max(chunk, (ptiles[r] + split_cap - 1) / split_cap);
+  if (in.page_size > 0) {
+    const int max_chunk = std::max(1, ((kMaxStagedPages - 2) * in.page_size) / 64);
+    chunk = std::min(chunk, max_chunk);
   }
+  (void)groups;
 
-  // slot_begin per group (r, h, qt): S_r consecutive partial slots.
+  // consecutive slots per group: S prefix partials, then the suffix partial
   std::vector<int> grp0(R + 1, 0);
   for (int r = 0; r < R; ++r) grp0[r + 1] = grp0[r] + Hkv * qtiles[r];
-  std::vector<int> slot_begin(grp0[R], -1);
+  std::vector<int> slot0(grp0[R], -1);
   int slot = 0, max_splits_used = 0;
   for (int r = 0; r < R; ++r) {
-    int s = ptiles[r] == 0 ? 0 : (ptiles[r] + chunk - 1) / chunk;
-    if (in.max_splits > 0) s = std::min(s, in.max_splits);
-    splits[r] = s;
-    max_splits_used = std::max(max_splits_used, s);
+    const int S = ptiles[r] == 0 ? 0 : (ptiles[r] + chunk - 1) / chunk;
+    splits[r] = S;
+    max_splits_used = std::max(max_splits_used, S);
     for (int gi = grp0[r]; gi < grp0[r + 1]; ++gi) {
-      if (s > 0) slot_begin[gi] = slot;
-      slot += s;
+      if (S > 0) {
+        slot0[gi] = slot;
+        slot += S + 1;
+      }
     }
   }
 
-  // Sets of work items that read the same keys (placed on one XCD).
-  struct Set {
-    long long cost;
-    std::vector<WorkItem> items;
-  };
-  std::vector<Set> pre_sets, suf_sets;
+  std::vector<ItemSet<VerifyItem>> pre_sets, suf_sets;
   for (int r = 0; r < R; ++r) {
     if (nq[r] == 0) continue;
     const int S = splits[r];
+    const int q0 = in.qo_indptr[r];
+    const int pbase = in.page_size > 0 ? in.page_indptr[r] : (in.prefix_tok_indptr ? in.prefix_tok_indptr[r] : 0);
     for (int h = 0; h < Hkv; ++h) {
       for (int s = 0; s < S; ++s) {
         const int base = ptiles[r] / S, rem = ptiles[r] % S;
         const int t0 = s * base + std::min(s, rem);
         const int nt = base + (s < rem ? 1 : 0);
-        Set set;
+        ItemSet<VerifyItem> set;
         set.cost = (long long)nt * qtiles[r];
         for (int qt = 0; qt < qtiles[r]; ++qt) {
-          WorkItem w;
+          VerifyItem w{};
           w.req = r;
           w.kvh = h;
           w.qtile = qt;
-          w.src = 0;
+          w.src = SRC_PREFIX;
           w.kv_begin = kv0[r] + 64 * t0;
           w.kv_end = std::min(kv1[r], kv0[r] + 64 * (t0 + nt));
-          w.slot = slot_begin[grp0[r] + h * qtiles[r] + qt] + s;
+          w.slot = slot0[grp0[r] + h * qtiles[r] + qt] + s;
           w.mode = MODE_PARTIAL;
+          w.q0 = q0;
+          w.nq = nq[r];
+          w.base = pbase;
+          w.causal_off = 0;
           set.items.push_back(w);
         }
         pre_sets.push_back(std::move(set));
       }
-      const int nb = (nq[r] * g + ROWS_B - 1) / ROWS_B;
-      Set set;
-      set.cost = (long long)nb * ((nq[r] + 63) / 64);
-      for (int b = 0; b < nb; ++b) {
-        const int qt = (b * ROWS_B) / ROWS_A;
-        WorkItem w;
+      ItemSet<VerifyItem> set;
+      set.cost = (long long)stiles[r] * qtiles[r];
+      for (int qt = 0; qt < qtiles[r]; ++qt) {
+        const int gi = grp0[r] + h * qtiles[r] + qt;
+        VerifyItem w{};
         w.req = r;
         w.kvh = h;
-        w.qtile = b;
-        w.src = 1;
+        w.qtile = qt;
+        w.src = SRC_SUFFIX;
         w.kv_begin = 0;
         w.kv_end = nq[r];
-        if (S > 0) {
-          w.slot = slot_begin[grp0[r] + h * qtiles[r] + qt];
-          w.mode = MODE_MERGE_SLOTS | (S << 8);
-        } else {
-          w.slot = -1;
-          w.mode = MODE_FINAL;
-        }
+        w.slot = S > 0 ? slot0[gi] + S : -1;
+        w.mode = S > 0 ? MODE_PARTIAL : MODE_FINAL;
+        w.q0 = q0;
+        w.nq = nq[r];
+        w.base = q0;  // the request's suffix keys are rows q0.. of k/v_suffix
+        w.causal_off = 0;
         set.items.push_back(w);
+        if (S > 0) {
+          VerifyMerge m{};
+          m.req = r;
+          m.kvh = h;
+          m.qtile = qt;
+          m.slot0 = slot0[gi];
+          m.nslots = S + 1;
+          m.q0 = q0;
+          m.nq = nq[r];
+          out.merges.push_back(m);
+        }
       }
       suf_sets.push_back(std::move(set));
     }
   }
-  order_for_xcds(pre_sets, out.prefix_work);
-  order_for_xcds(suf_sets, out.suffix_work);
+  // prefix sets first (longer), suffix sets after them on the least-loaded XCDs
+  std::vector<ItemSet<VerifyItem>> sets;
+  sets.reserve(pre_sets.size() + suf_sets.size());
+  for (auto& s_ : pre_sets) sets.push_back(std::move(s_));
+  for (auto& s_ : suf_sets) sets.push_back(std::move(s_));
+  order_for_xcds(sets, out.items);
 
-  out.waves = WA;
-  out.suffix_waves = WB;
-  out.rows_per_tile = ROWS_A;
+  out.waves = W;
+  out.rows = ROWS;
   out.num_slots = slot;
   out.max_splits_used = max_splits_used;
   // bf16 partial O + fp32 LSE per (slot, row)
-  out.workspace_bytes = (size_t)slot * ROWS_A * ((size_t)in.head_dim * 2 + sizeof(float));
+  out.workspace_bytes = (size_t)slot * ROWS * ((size_t)in.head_dim * 2 + sizeof(float));
   return 0;
 }
 

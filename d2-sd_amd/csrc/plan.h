@@ -1,4 +1,4 @@
-// Host-side work planner interface (plan.cpp).
+// Host-side work planners (plan.cpp) and kernel launchers.
 #pragma once
 
 #include <hip/hip_runtime_api.h>
@@ -10,38 +10,49 @@
 
 namespace d2sd {
 
-struct PlanInput {
+// ---- cascade verify attention (verify_attention.hip) ----
+struct VerifyPlanInput {
   int num_reqs;
-  const int* qo_indptr;   // host [num_reqs + 1]
-  const int* prefix_len;  // host [num_reqs]
+  const int* qo_indptr;          // host [num_reqs + 1]
+  const int* prefix_len;         // host [num_reqs]
+  const int* page_indptr;        // host [num_reqs + 1] (paged prefix)
+  const int* prefix_tok_indptr;  // host [num_reqs] (contiguous prefix; nullable => 0)
   int num_qo_heads, num_kv_heads, head_dim;
   int window_left;
   int num_cus;
-  int max_splits;
-  int waves;      // 0: choose
-  int page_size;  // 0: contiguous prefix
+  int max_splits;  // 0: no limit beyond kMaxVerifySplits
+  int waves;       // 0: choose; else 2, 4 or 8
+  int page_size;   // 0: contiguous prefix
 };
 
-
-struct PlanOutput {
-  std::vector<WorkItem> prefix_work;  // prefix launch (split-KV partials)
-  std::vector<WorkItem> suffix_work;  // suffix launch (tree attention + merge)
+struct VerifyPlanOutput {
+  std::vector<VerifyItem> items;    // attention launch
+  std::vector<VerifyMerge> merges;  // merge launch
   int waves;
-  int suffix_waves;
-  int rows_per_tile;
+  int rows;                         // rows per workgroup tile (= per partial slot)
   int num_slots;
   int max_splits_used;
   size_t workspace_bytes;
 };
 
+int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out);
+// Workgroups of the attention launch resident per CU (LDS bound) and packed
+// rows per workgroup, by waves per workgroup (2: 64-row waves; 4, 8: 32-row
+// waves).
+int verify_wgs_per_cu(int waves);
+int verify_rows(int waves);
+
+hipError_t launch_verify_attention(const VerifyParams& p, int head_dim, int waves, bool paged, bool fp8, int nitems,
+                                   hipStream_t s);
+hipError_t launch_verify_merge(const VerifyParams& p, int head_dim, int rows, int nmerges, hipStream_t s);
+
+// ---- single-source drop-ins (attention.hip) ----
 int choose_waves(int rows_per_head_max);
 int blocks_per_cu(int waves);
-int plan_cascade(const PlanInput& in, PlanOutput& out);
 void plan_single(int qo_len, int kv_len, int num_qo_heads, int num_kv_heads, int head_dim,
                  int window_left, int num_cus, ImplicitWork& imp, int& waves, size_t& workspace_bytes);
 
-// attention.hip launchers
-// src: 0 = p.src[0] (prefix / single source), 1 = p.src[1] (suffix tree)
+// src: 0 = p.src[0] (single source), 1 = p.src[1]
 hipError_t launch_attention(const AttnParams& p, int head_dim, int waves, int src, bool fp8, bool paged,
                             bool masked, int nblocks, hipStream_t s);
 hipError_t launch_merge(const AttnParams& p, int head_dim, int rows_per_tile, int nitems, hipStream_t s);

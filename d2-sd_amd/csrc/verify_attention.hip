@@ -1,0 +1,757 @@
+// gfx950 (CDNA4) kernels of the cascade verify attention plan()/run() path:
+//
+//   verify_attn_kernel   one launch for both levels of
+//                        generation/verification.py:127-165 — workgroups
+//                        owning a key chunk of the shared prefix (split-KV,
+//                        contiguous or paged, bf16 or fp8 e4m3fn) and
+//                        workgroups owning the whole tree-masked suffix.
+//                        Each writes a normalised partial state (bf16 O in
+//                        its register image + fp32 LSE), or the final output
+//                        when it is its group's only producer.
+//   verify_merge_kernel  log-sum-exp merge of a group's partials
+//                        (flashinfer.merge_state_in_place semantics,
+//                        verification.py:163-165) and the GPT-OSS sink rescale
+//                        (verification.py:173-176), writing O and LSE.
+//
+// Rows.  The rows of one (request, kv head) are the packed (query n, query
+// head j) pairs, row = n*g + j (g = Hq / Hkv), so all query heads sharing a kv
+// head read each key/value element once per workgroup.  A workgroup owns
+// ROWS consecutive rows as 32-row MFMA blocks: either two waves of two blocks
+// (every K / V^T fragment read from LDS feeds two MFMAs; one wave per SIMD)
+// or four / eight waves of one block (two waves per SIMD, so that one wave's
+// softmax overlaps the other's MFMAs).
+//
+// Per 64-key tile a wave computes S^T = K . Q^T (A = K from LDS, B = its Q
+// rows held in registers for the whole loop): lane l holds the scores of query
+// row l%32 of each block for 32 keys, so softmax max / sum are in-lane plus one
+// exchange with lane l^32.  P^T is fed back as the B operand of
+// O^T += V^T . P^T straight from registers; the V^T A operand is read with
+// ds_read_b64_tr_b16 from the row-major V tile in the key order the P^T
+// registers hold.
+//
+// Key tiles reach LDS by global_load_lds_dwordx4 (bf16 sources) into a ring of
+// STAGES tiles, or, for an fp8 prefix, through registers where e4m3fn is
+// expanded to bf16 (V stored transposed with permuted key slots).
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "d2sd_internal.h"
+#include "kernel_common.h"
+
+namespace d2sd {
+
+template <int D, int STAGES>
+struct VerifySmem {
+  union {
+    bf16_t ring[STAGES][2][64 * D];  // direct-to-LDS tiles: [stage][K, V][key row * D], chunk-swizzled
+    struct {
+      bf16_t Ks[2][64 * (D + 8)];    // register-staged K tiles (row pitch D + 8)
+      bf16_t Vt[2][D * (64 + 8)];    // register-staged V^T tiles (row pitch 64 + 8)
+    } st;
+  };
+  int pages[kMaxStagedPages];        // page ids of the workgroup's key range
+};
+
+template <int D>
+__device__ __forceinline__ void store_out(const VerifyParams& p, int qrow, int qh, int hh,
+                                          const f32x16 (&o)[D / 32], float lse) {
+  bf16_t* orow = (bf16_t*)p.o + (long long)qrow * p.o_stride_n + (long long)qh * p.o_stride_h;
+  float sc = 1.f;
+  if (p.sinks) sc = (lse == -INFINITY) ? 0.f : 1.f / (1.f + __expf(p.sinks[qh] - lse));
+#pragma unroll
+  for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4)
+      *(u32x2*)(orow + 32 * mt + 8 * q4 + 4 * hh) =
+          (u32x2){pack_bf16x2(o[mt][4 * q4] * sc, o[mt][4 * q4 + 1] * sc),
+                  pack_bf16x2(o[mt][4 * q4 + 2] * sc, o[mt][4 * q4 + 3] * sc)};
+  if (p.lse && hh == 0) p.lse[(long long)qrow * p.lse_stride_n + qh] = p.lse_base2 ? lse * kLog2e : lse;
+}
+
+// Row value of the partner lane l ^ 32 (the other half of the wave), by
+// v_permlane32_swap: after swapping the upper half of `a` with the lower half
+// of `b` (both copies of x), lane l < 32 finds x[l + 32] in b and lane l >= 32
+// finds x[l - 32] in a.
+__device__ __forceinline__ float xor32(float x, int hh) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(hh ? r[0] : r[1]);
+}
+
+// One global_load_lds_dwordx4 with a wave-uniform base: lane l copies 16
+// bytes from sbase + voff (voff per lane) to LDS byte address lds_addr + 16*l.
+__device__ __forceinline__ void dma16s(const void* sbase, unsigned voff, unsigned lds_addr) {
+  unsigned saved;
+  __asm__ volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %2, %3\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds_addr), "v"(voff), "s"(sbase)
+      : "memory");
+}
+
+// One workgroup: rows [qtile*ROWS, +ROWS) of (req, kvh) against keys
+// [kv_begin, kv_end) of source S.  Each of the W waves owns RB 32-row
+// blocks (ROWS = 32*RB*W).
+//   PAGED  : S is a paged pool (the range's page ids are staged in LDS)
+//   MASKED : the suffix level (causal / tree / no mask; else only the
+//            key-range tail is masked)
+//   FP8    : S holds e4m3fn bytes, staged through registers
+template <int D, int W, int RB, int STAGES, bool PAGED, bool MASKED, bool FP8>
+__device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyItem& w, const VerifySource& S,
+                                            VerifySmem<D, STAGES>& sm) {
+  constexpr int ROWS = 32 * RB * W;
+  constexpr int NT = 64 * W;
+  constexpr int MT = D / 32;
+  constexpr int KS = D / 16;
+  constexpr int ESZ = FP8 ? 1 : 2;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31;
+  const int hh = lane >> 5;
+
+  const int g = p.group;
+  const int R = w.nq * g;
+  const int wrow0 = w.qtile * ROWS + wv * 32 * RB;
+  const bool live = wrow0 < R;  // wave-uniform: the wave owns at least one valid row
+  int n[RB], qh[RB];
+  bool rv[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int row = wrow0 + 32 * rb + l32;
+    rv[rb] = row < R;
+    n[rb] = rv[rb] ? row / g : 0;
+    qh[rb] = w.kvh * g + (rv[rb] ? row - n[rb] * g : 0);
+  }
+  const int kv_begin = w.kv_begin, kv_end = w.kv_end;
+  const int ntiles = kv_end > kv_begin ? (kv_end - kv_begin + 63) >> 6 : 0;
+
+  // ---- suffix masks: the rows' tree-mask words held in registers ----
+  int mask_mode = MASK_NONE;
+  unsigned long long mreg[RB][kMaskRegWords];
+  const unsigned long long* mrow[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    mrow[rb] = nullptr;
+#pragma unroll
+    for (int k = 0; k < kMaskRegWords; ++k) mreg[rb][k] = 0ull;
+  }
+  if constexpr (MASKED) {
+    mask_mode = p.mask_mode;
+    if (mask_mode == MASK_TREE) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+        if (rv[rb]) {
+          mrow[rb] = p.tree_mask + (long long)(w.q0 + n[rb]) * p.mask_words;
+#pragma unroll
+          for (int k = 0; k < kMaskRegWords; ++k) mreg[rb][k] = (k < p.mask_words) ? mrow[rb][k] : 0ull;
+        }
+    }
+  }
+  auto tile_word = [&](int rb, int wi) -> unsigned long long {
+    return wi == 0 ? mreg[rb][0] : wi == 1 ? mreg[rb][1] : wi == 2 ? mreg[rb][2] : wi == 3 ? mreg[rb][3]
+                                                                    : (mrow[rb] ? mrow[rb][wi] : 0ull);
+  };
+
+  // ---- source addressing (bytes; the kv head is folded into the bases) ----
+  const char* kbase = (const char*)S.k + (long long)w.kvh * S.stride_head * ESZ;
+  const char* vbase = (const char*)S.v + (long long)w.kvh * S.stride_head * ESZ;
+  const long long tok_b = S.stride_tok * ESZ;
+  const long long page_b = S.stride_page * ESZ;
+  const int log2p = S.log2_page;
+  const int pmask = (1 << log2p) - 1;
+  int pg_first = 0;
+  if constexpr (PAGED) {
+    if (ntiles > 0) {
+      pg_first = kv_begin >> log2p;
+      const int npg = ((kv_end - 1) >> log2p) - pg_first + 1;  // <= kMaxStagedPages (planner)
+      const int* pt = S.page_table + w.base + pg_first;
+      for (int i = tid; i < npg; i += NT) sm.pages[i] = pt[i];
+    }
+  } else {
+    const long long off = (long long)w.base * tok_b;
+    kbase += off;
+    vbase += off;
+  }
+
+  // ---- Q fragments (B operand of S^T = K Q^T): lane holds 8 consecutive
+  // head dims at offset 8*hh of every 16-wide k step, for row block rb ----
+  bf16x8 qf[RB][KS];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const bf16_t* qp = (const bf16_t*)p.q + (long long)(w.q0 + n[rb]) * p.q_stride_n +
+                       (long long)qh[rb] * p.q_stride_h + 8 * hh;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[rb][ks] = rv[rb] ? *(const bf16x8*)(qp + 16 * ks) : zero_bf16x8();
+  }
+
+  float kscale = 1.f, vscale = 1.f;
+  if constexpr (FP8) {
+    // e4m3fn bytes are expanded as value / 2^8 (see fp8x4_to_bf16x4)
+    kscale = (S.k_scale ? S.k_scale[w.kvh] : 1.f) * 256.f;
+    vscale = (S.v_scale ? S.v_scale[w.kvh] : 1.f) * 256.f;
+  }
+  const float c = p.sm_scale_log2 * kscale;  // raw score -> log2 domain
+  const float cn = p.sm_scale * kscale;      // raw score -> natural domain
+
+  // Complete the Q / mask / page-id loads here, visibly to the compiler:
+  // otherwise it keeps them pending into the tile loop and waits vmcnt(0)
+  // there, which would also drain the DMA ring.
+  wait_vmcnt<0>();
+  __syncthreads();  // page ids visible
+
+  auto tok_off = [&](int t) -> long long {
+    if constexpr (PAGED)
+      return (long long)sm.pages[(t >> log2p) - pg_first] * page_b + (long long)(t & pmask) * tok_b;
+    else
+      return (long long)t * tok_b;
+  };
+
+  f32x16 o[RB][MT];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[rb][mt][r] = 0.f;
+  float m_run[RB], l_run[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    m_run[rb] = -INFINITY;
+    l_run[rb] = 0.f;
+  }
+
+  // Whether any row of this wave sees a key of tile kb (suffix masks).
+  auto tile_visible = [&](int kb) -> bool {
+    if constexpr (MASKED) {
+      if (mask_mode == MASK_TREE) {
+        unsigned long long any = 0ull;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) any |= tile_word(rb, kb >> 6);
+        return __any(any != 0ull);
+      }
+      if (mask_mode == MASK_CAUSAL) {
+        bool any = false;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) any = any || (rv[rb] && kb <= n[rb] + w.causal_off);
+        return __any(any);
+      }
+    }
+    return true;
+  };
+
+  // One 64-key tile: QK^T, masking, online softmax, PV.  kfrag(kt, ks) is the
+  // A operand of keys 32kt..32kt+31, head dims 16ks.. (this lane's part);
+  // vfrag(mt, ks) the A operand of head dims 32mt.., keys 16ks.. in P^T order.
+  auto compute_tile = [&](int kb, auto&& kfrag, auto&& vfrag, auto masked_tile) {
+    f32x16 s[RB][2];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[rb][0][r] = 0.f;
+        s[rb][1][r] = 0.f;
+      }
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const bf16x8 a0 = kfrag(0, ks);
+      const bf16x8 a1 = kfrag(1, ks);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        s[rb][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[rb][ks], s[rb][0], 0, 0, 0);
+        s[rb][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[rb][ks], s[rb][1], 0, 0, 0);
+      }
+    }
+
+    // masking.  vis (bit kk = key kb + kk visible) per row block; register r
+    // of 32-key tile kt holds key 32*kt + 8*(r/4) + 4*hh + r%4, i.e. bit
+    // 8*(r/4) + r%4 of the row's 32-bit half kt shifted down by 4*hh.
+    if constexpr (decltype(masked_tile)::value) {
+      const int rem = kv_end - kb;  // > 0: tile it < ntiles
+      const unsigned long long tail = rem >= 64 ? ~0ull : ((1ull << rem) - 1ull);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        unsigned long long vis = tail;
+        if constexpr (MASKED) {
+          if (mask_mode == MASK_TREE) {
+            vis &= rv[rb] ? tile_word(rb, kb >> 6) : 0ull;
+          } else if (mask_mode == MASK_CAUSAL) {
+            const int lim = n[rb] + w.causal_off - kb;  // keys kk <= lim are visible
+            vis &= lim >= 63 ? ~0ull : (lim < 0 ? 0ull : ((2ull << lim) - 1ull));
+          }
+        }
+        const unsigned lo = (unsigned)vis >> (4 * hh);
+        const unsigned hi = (unsigned)(vis >> 32) >> (4 * hh);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int bit = 8 * (r >> 2) + (r & 3);
+          s[rb][0][r] = ((lo >> bit) & 1u) ? s[rb][0][r] : -INFINITY;
+          s[rb][1][r] = ((hi >> bit) & 1u) ? s[rb][1][r] : -INFINITY;
+        }
+      }
+    }
+
+    // online softmax (lane-local row, partner lane l^32); P^T packed to bf16
+    bf16x8 pb[RB][4];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      // row max: 16 three-input maxima over four independent chains
+      float m4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+#pragma unroll
+      for (int r = 0; r < 16; ++r) m4[r & 3] = fmaxf(fmaxf(m4[r & 3], s[rb][0][r]), s[rb][1][r]);
+      float mx = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
+      mx = fmaxf(mx, xor32(mx, hh));
+      const bool grow = (mx > m_run[rb]) && ((m_run[rb] == -INFINITY) || (mx - m_run[rb]) * c > kRescaleSlack);
+      if (__any(grow)) {
+        const float m_new = grow ? mx : m_run[rb];
+        const float alpha = (m_run[rb] == -INFINITY) ? 0.f : exp2f((m_run[rb] - m_new) * c);
+        l_run[rb] *= alpha;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[rb][mt][r] *= alpha;
+        m_run[rb] = m_new;
+      }
+      const float mc = (m_run[rb] == -INFINITY) ? 0.f : m_run[rb] * c;
+      float lsum = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[rb][0][r] = __builtin_amdgcn_exp2f(fmaf(s[rb][0][r], c, -mc));
+        s[rb][1][r] = __builtin_amdgcn_exp2f(fmaf(s[rb][1][r], c, -mc));
+        lsum += s[rb][0][r] + s[rb][1][r];
+      }
+      l_run[rb] += lsum;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const f32x16& sv = s[rb][ks >> 1];
+        const int base = 8 * (ks & 1);
+        u32x4 u;
+        u[0] = pack_bf16x2(sv[base + 0], sv[base + 1]);
+        u[1] = pack_bf16x2(sv[base + 2], sv[base + 3]);
+        u[2] = pack_bf16x2(sv[base + 4], sv[base + 5]);
+        u[3] = pack_bf16x2(sv[base + 6], sv[base + 7]);
+        pb[rb][ks] = __builtin_bit_cast(bf16x8, u);
+      }
+    }
+
+    // O^T += V^T P^T
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const bf16x8 a = vfrag(mt, ks);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          o[rb][mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[rb][ks], o[rb][mt], 0, 0, 0);
+      }
+  };
+
+  if constexpr (!FP8) {
+    // ================= direct global -> LDS ring (bf16 sources) =================
+    constexpr int CH = D / 8;      // 16-byte chunks per key row
+    constexpr int RPI = 64 / CH;   // key rows per 1 KB wave instruction
+    constexpr int IPT = 64 / RPI;  // instructions per 64-key tile (K or V)
+    constexpr int IPW = IPT / W;   // ... per wave
+    constexpr int LPT = 2 * IPW;   // DMA loads per tile per wave (K + V)
+    constexpr int STAGE_BYTES = 2 * 64 * D * 2;
+    static_assert(IPW >= 1 && IPT % W == 0, "tile/wave mismatch");
+    static_assert(STAGES >= 2 && STAGES <= 4, "ring depth");
+    static_assert((STAGES - 1) * LPT < 64, "vmcnt range");
+
+    const unsigned ring_lds = __builtin_amdgcn_readfirstlane(lds_address(&sm.ring[0][0][0]));
+    // Per-lane part of the source offset of DMA instruction i: key row
+    // lrow of its RPI-row group, stored chunk cs holding global chunk
+    // cs ^ swizzle(row).  Full tiles of an item whose key range starts on a
+    // 64-key boundary (and, paged, whose pages hold whole row groups) add a
+    // wave-uniform base per instruction: the row group's page and row.
+    const int lrow = lane / CH, cs = lane % CH;
+    const bool fast = (kv_begin & 63) == 0 && tok_b < (1ll << 26) && (!PAGED || (1 << log2p) >= RPI);
+    unsigned lane_off[IPW];
+#pragma unroll
+    for (int i = 0; i < IPW; ++i) {
+      const int r = (wv * IPW + i) * RPI + lrow;
+      lane_off[i] = (unsigned)(lrow * tok_b) + (unsigned)((cs ^ chunk_swizzle<D>(r)) * 16);
+    }
+
+    // DMA of tile `it` into ring stage it % STAGES.  Keys past kv_end (tail
+    // tile only) load the last valid key: finite data whose scores the tail
+    // mask removes.
+    auto issue = [&](int it) {
+      const int kb = kv_begin + it * 64;
+      const unsigned kst = ring_lds + (it % STAGES) * STAGE_BYTES;
+      const unsigned vst = kst + 64 * D * 2;
+      if (fast && kb + 64 <= kv_end) {
+#pragma unroll
+        for (int i = 0; i < IPW; ++i) {
+          const int inst = wv * IPW + i;
+          const int t0 = kb + inst * RPI;  // first key of the row group (uniform)
+          long long ub;
+          if constexpr (PAGED) {
+            const int pg = __builtin_amdgcn_readfirstlane(sm.pages[(t0 >> log2p) - pg_first]);
+            ub = (long long)pg * page_b + (long long)(t0 & pmask) * tok_b;
+          } else {
+            ub = (long long)t0 * tok_b;
+          }
+          dma16s(kbase + ub, lane_off[i], kst + inst * 1024);
+          dma16s(vbase + ub, lane_off[i], vst + inst * 1024);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < IPW; ++i) {
+          const int inst = wv * IPW + i;
+          const int r = inst * RPI + lrow;
+          const long long off = tok_off(min(kb + r, kv_end - 1)) + (cs ^ chunk_swizzle<D>(r)) * 16;
+          dma16(kbase + off, kst + inst * 1024);
+          dma16(vbase + off, vst + inst * 1024);
+        }
+      }
+    };
+
+    // LDS byte offsets (inside a stage) of this lane's fragments.  K: key row
+    // l32 (+32 for kt = 1), chunk (2ks + hh) ^ swizzle.  V^T for
+    // ds_read_b64_tr_b16: lane k of a 16-lane group G names key row
+    // 4*hh + k/4 (+8 for the second read, +16ks) and head dims
+    // 16*(G&1) + 4*(k&3) .. +3 of the 32-wide block mt.
+    unsigned koff[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) koff[ks] = (l32 * D + 8 * ((2 * ks + hh) ^ chunk_swizzle<D>(l32))) * 2;
+    const int k16 = lane & 15;
+    const int krow = 4 * hh + (k16 >> 2);
+    const int dsub = 16 * ((lane >> 4) & 1) + 4 * (k16 & 3);
+    unsigned voff0[MT], voff1[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int d = 32 * mt + dsub;
+      voff0[mt] = 64 * D * 2 + (krow * D + 8 * ((d >> 3) ^ chunk_swizzle<D>(krow)) + (d & 7)) * 2;
+      voff1[mt] = 64 * D * 2 + ((krow + 8) * D + 8 * ((d >> 3) ^ chunk_swizzle<D>(krow + 8)) + (d & 7)) * 2;
+    }
+    typedef __attribute__((address_space(3))) char lds_char;
+
+#pragma unroll
+    for (int t = 0; t < STAGES - 1; ++t)
+      if (t < ntiles) issue(t);
+
+    // One step of the ring: wait for tile `it`, refill the stage freed by
+    // tile it-1, compute tile `it` (masked or not, as the tag says).
+    auto step = [&](int it, auto masked_tile) {
+      // tile `it` has landed once at most min(STAGES-2, tiles issued after it)
+      // tiles of this wave's DMA are still outstanding; after the barrier every
+      // wave's share is visible and stage (it-1) % STAGES is free.
+      const int ahead = min(STAGES - 2, ntiles - 1 - it);
+      __asm__ volatile("" ::: "memory");
+      if (ahead >= 2) wait_vmcnt<2 * LPT>();
+      else if (ahead == 1) wait_vmcnt<LPT>();
+      else wait_vmcnt<0>();
+      __builtin_amdgcn_s_barrier();
+      __asm__ volatile("" ::: "memory");
+      if (it + STAGES - 1 < ntiles) issue(it + STAGES - 1);
+
+      const int kb = kv_begin + it * 64;
+      if (!live || !tile_visible(kb)) return;
+      const lds_char* st = (const lds_char*)(uintptr_t)(ring_lds + (it % STAGES) * STAGE_BYTES);
+      auto kfrag = [&](int kt, int ks) -> bf16x8 {
+        return *(const __attribute__((address_space(3))) bf16x8*)(st + koff[ks] + kt * 32 * D * 2);
+      };
+      auto vfrag = [&](int mt, int ks) -> bf16x8 {
+        typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(st + voff0[mt] + ks * 16 * D * 2));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(st + voff1[mt] + ks * 16 * D * 2));
+        const u32x2 ulo = __builtin_bit_cast(u32x2, lo), uhi = __builtin_bit_cast(u32x2, hi);
+        return __builtin_bit_cast(bf16x8, (u32x4){ulo[0], ulo[1], uhi[0], uhi[1]});
+      };
+      compute_tile(kb, kfrag, vfrag, masked_tile);
+    };
+
+    if constexpr (MASKED) {
+      for (int it = 0; it < ntiles; ++it) step(it, std::true_type{});
+    } else {
+      // full prefix tiles carry no mask code; the partial tail tile (if any)
+      // is peeled off the loop
+      const int nfull = (kv_end - kv_begin) >> 6;
+      for (int it = 0; it < nfull; ++it) step(it, std::false_type{});
+      if (nfull < ntiles) step(nfull, std::true_type{});
+    }
+  } else {
+    // ============ register-staged tiles (fp8 e4m3fn -> bf16 in LDS) ============
+    constexpr int KP = D + 8;          // K tile pitch (elements)
+    constexpr int VP = 64 + 8;         // V^T tile pitch (elements)
+    constexpr int KCH = D / 8;         // 8-element chunks per key row
+    constexpr int NK = 64 * KCH / NT;  // K chunks per thread == V keys per thread
+    constexpr int VKG = 64 / NK;       // V key groups per d-chunk
+    static_assert(NK == 1 || NK == 2 || NK == 4 || NK == 8, "tile/thread mismatch");
+    u32x2 kr[NK], vr[NK];  // 8 fp8 elements each
+
+    auto load_tile = [&](int kb) {
+#pragma unroll
+      for (int i = 0; i < NK; ++i) {
+        const int c_ = tid + i * NT;
+        const int t = min(kb + c_ / KCH, kv_end - 1);
+        kr[i] = *(const u32x2*)(kbase + tok_off(t) + (c_ % KCH) * 8);
+      }
+      const int kg = tid % VKG, dc = tid / VKG;
+#pragma unroll
+      for (int i = 0; i < NK; ++i) {
+        const int t = min(kb + kg * NK + i, kv_end - 1);
+        vr[i] = *(const u32x2*)(vbase + tok_off(t) + dc * 8);
+      }
+    };
+    auto to_bf16 = [](const u32x2& r) -> u32x4 {
+      const u32x2 lo = fp8x4_to_bf16x4(r[0]), hi = fp8x4_to_bf16x4(r[1]);
+      return (u32x4){lo[0], lo[1], hi[0], hi[1]};
+    };
+    // K row-major; V transposed with the keys of each 16-key group in the
+    // order a lane of half h holds them in the S^T accumulator: keys
+    // 4h+{0..3} and 4h+8+{0..3} at slots 8h..8h+7.
+    auto store_tile = [&](int buf) {
+#pragma unroll
+      for (int i = 0; i < NK; ++i) {
+        const int c_ = tid + i * NT;
+        *(u32x4*)(&sm.st.Ks[buf][(c_ / KCH) * KP + (c_ % KCH) * 8]) = to_bf16(kr[i]);
+      }
+      const int kg = tid % VKG, dc = tid / VKG;
+      u32x4 vv[NK];
+#pragma unroll
+      for (int i = 0; i < NK; ++i) vv[i] = to_bf16(vr[i]);
+      auto slot_of = [](int kk) { return (kk & ~15) + 8 * ((kk >> 2) & 1) + (kk & 3) + 4 * ((kk >> 3) & 1); };
+#pragma unroll
+      for (int dd = 0; dd < 8; ++dd) {
+        const int wi = dd >> 1;
+        const int sh = (dd & 1) * 16;
+        bf16_t* rowp = &sm.st.Vt[buf][(dc * 8 + dd) * VP];
+        if constexpr (NK >= 4) {
+#pragma unroll
+          for (int q = 0; q < NK / 4; ++q) {
+            const unsigned e0 = (vv[4 * q][wi] >> sh) & 0xffffu, e1 = (vv[4 * q + 1][wi] >> sh) & 0xffffu;
+            const unsigned e2 = (vv[4 * q + 2][wi] >> sh) & 0xffffu, e3 = (vv[4 * q + 3][wi] >> sh) & 0xffffu;
+            *(u32x2*)(rowp + slot_of(kg * NK + 4 * q)) = (u32x2){e0 | (e1 << 16), e2 | (e3 << 16)};
+          }
+        } else if constexpr (NK == 2) {
+          const unsigned e0 = (vv[0][wi] >> sh) & 0xffffu, e1 = (vv[1][wi] >> sh) & 0xffffu;
+          *(unsigned*)(rowp + slot_of(kg * 2)) = e0 | (e1 << 16);
+        } else {
+          *(unsigned short*)(rowp + slot_of(kg)) = (unsigned short)((vv[0][wi] >> sh) & 0xffffu);
+        }
+      }
+    };
+
+    if (ntiles > 0) {
+      load_tile(kv_begin);
+      store_tile(0);
+    }
+    __syncthreads();
+    auto step = [&](int it, auto masked_tile) {
+      const int buf = it & 1;
+      const int kb = kv_begin + it * 64;
+      if (it + 1 < ntiles) load_tile(kb + 64);
+      if (live) {
+        const bf16_t* ks_ = &sm.st.Ks[buf][0];
+        const bf16_t* vt_ = &sm.st.Vt[buf][0];
+        auto kfrag = [&](int kt, int ks) -> bf16x8 {
+          return *(const bf16x8*)(ks_ + (l32 + 32 * kt) * KP + 8 * hh + 16 * ks);
+        };
+        auto vfrag = [&](int mt, int ks) -> bf16x8 {
+          return *(const bf16x8*)(vt_ + (l32 + 32 * mt) * VP + 8 * hh + 16 * ks);
+        };
+        compute_tile(kb, kfrag, vfrag, masked_tile);
+      }
+      if (it + 1 < ntiles) store_tile(buf ^ 1);
+      __syncthreads();
+    };
+    const int nfull = (kv_end - kv_begin) >> 6;
+    for (int it = 0; it < nfull; ++it) step(it, std::false_type{});
+    if (nfull < ntiles) step(nfull, std::true_type{});
+  }
+
+  // ---- epilogue: normalise, then a partial slot or the final output ----
+  if (!live) return;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const float l_tot = l_run[rb] + xor32(l_run[rb], hh);
+    const bool nonempty = l_tot > 0.f;
+    const float inv = nonempty ? vscale / l_tot : 0.f;
+    const float lse = nonempty ? m_run[rb] * cn + logf(l_tot) : -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[rb][mt][r] *= inv;
+    if (w.mode == MODE_PARTIAL) {
+      const int blk = RB * wv + rb;
+      bf16_t* po = (bf16_t*)p.part_o + (long long)w.slot * ROWS * D;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4)
+          *(u32x2*)(po + image_offset<D>(blk, mt, q4, lane)) =
+              (u32x2){pack_bf16x2(o[rb][mt][4 * q4], o[rb][mt][4 * q4 + 1]),
+                      pack_bf16x2(o[rb][mt][4 * q4 + 2], o[rb][mt][4 * q4 + 3])};
+      if (hh == 0) p.part_lse[(long long)w.slot * ROWS + blk * 32 + l32] = lse;
+    } else if (rv[rb]) {
+      store_out<D>(p, w.q0 + n[rb], qh[rb], hh, o[rb], lse);
+    }
+  }
+}
+
+// Workgroup shapes (waves_per_block of the plan): 2 = two waves of 64 rows
+// (one wave per SIMD, up to 512 registers), 4 = four waves of 32 rows and
+// 8 = eight waves of 32 rows (two waves per SIMD, up to 256 registers).
+template <int WPB>
+struct Shape;
+template <>
+struct Shape<2> { static constexpr int W = 2, RB = 2, OCC = 1; };
+template <>
+struct Shape<4> { static constexpr int W = 4, RB = 1, OCC = 2; };
+template <>
+struct Shape<8> { static constexpr int W = 8, RB = 1, OCC = 2; };
+
+// The prefix level (paged or contiguous, bf16 or fp8) and the suffix level
+// (contiguous bf16, masked) share one launch; the item's src picks the body.
+template <int D, int WPB, int STAGES, bool PAGED, bool FP8>
+__global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(Shape<WPB>::OCC, Shape<WPB>::OCC)))
+void verify_attn_kernel(const VerifyParams p) {
+  constexpr int W = Shape<WPB>::W, RB = Shape<WPB>::RB;
+  __shared__ __attribute__((aligned(16))) VerifySmem<D, STAGES> sm;
+  const VerifyItem w = p.items[blockIdx.x];
+  if (w.mode == MODE_NOOP) return;
+  if (w.src == SRC_PREFIX)
+    verify_body<D, W, RB, STAGES, PAGED, false, FP8>(p, w, p.pre, sm);
+  else
+    verify_body<D, W, RB, STAGES, false, true, false>(p, w, p.suf, sm);
+}
+
+// ---------------------------------------------------------------------------
+// Merge: one wave per (group, 32-row block, 32-wide head-dim block); lane l
+// owns row l%32 and the 16 head dims 32mt + 8q4 + 4(l/32) + e.  All partial
+// loads of up to kMaxVerifySplits + 1 slots are in flight at once.
+// ---------------------------------------------------------------------------
+template <int D, int ROWS>
+__global__ __launch_bounds__(256) void verify_merge_kernel(const VerifyParams p) {
+  constexpr int BLK = ROWS / 32, MT = D / 32, B = kMaxVerifySplits + 1;
+  const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int item = gw / (BLK * MT);
+  if (item >= p.num_merges) return;
+  const int rem = gw - item * (BLK * MT);
+  const int blk = rem / MT, mt = rem - blk * MT;
+  const VerifyMerge m = p.merges[item];
+  const int lane = threadIdx.x & 63, l32 = lane & 31, hh = lane >> 5;
+  const int g = p.group;
+  const int row = m.qtile * ROWS + blk * 32 + l32;
+  if (row >= m.nq * g) return;
+  const int n = row / g, qh = m.kvh * g + (row - n * g);
+
+  float acc[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+  float mval = -INFINITY, wsum = 0.f;
+  const long long slot_elems = (long long)ROWS * D;
+  for (int s0 = 0; s0 < m.nslots; s0 += B) {
+    const int cnt = min(B, m.nslots - s0);
+    float ls[B];
+    u32x2 v[B][4];
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      ls[b] = -INFINITY;
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) v[b][q4] = (u32x2){0u, 0u};
+      if (b < cnt) {
+        const long long s = m.slot0 + s0 + b;
+        ls[b] = p.part_lse[s * ROWS + blk * 32 + l32];
+        const bf16_t* po = (const bf16_t*)p.part_o + s * slot_elems;
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) v[b][q4] = *(const u32x2*)(po + image_offset<D>(blk, mt, q4, lane));
+      }
+    }
+    float bm = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < B; ++b) bm = fmaxf(bm, ls[b]);
+    const float nm = fmaxf(mval, bm);
+    if (nm == -INFINITY) continue;  // nothing visible so far
+    const float f = (mval == -INFINITY) ? 0.f : __expf(mval - nm);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] *= f;
+    wsum *= f;
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const float wt = (ls[b] == -INFINITY) ? 0.f : __expf(ls[b] - nm);
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        acc[4 * q4] += wt * bf16_lo(v[b][q4][0]);
+        acc[4 * q4 + 1] += wt * bf16_hi(v[b][q4][0]);
+        acc[4 * q4 + 2] += wt * bf16_lo(v[b][q4][1]);
+        acc[4 * q4 + 3] += wt * bf16_hi(v[b][q4][1]);
+      }
+      wsum += wt;
+    }
+    mval = nm;
+  }
+  const bool nonempty = wsum > 0.f;
+  const float lse = nonempty ? mval + logf(wsum) : -INFINITY;
+  float sc = nonempty ? 1.f / wsum : 0.f;
+  if (p.sinks) sc *= nonempty ? 1.f / (1.f + __expf(p.sinks[qh] - lse)) : 0.f;
+  bf16_t* orow = (bf16_t*)p.o + (long long)(m.q0 + n) * p.o_stride_n + (long long)qh * p.o_stride_h;
+#pragma unroll
+  for (int q4 = 0; q4 < 4; ++q4)
+    *(u32x2*)(orow + 32 * mt + 8 * q4 + 4 * hh) =
+        (u32x2){pack_bf16x2(acc[4 * q4] * sc, acc[4 * q4 + 1] * sc),
+                pack_bf16x2(acc[4 * q4 + 2] * sc, acc[4 * q4 + 3] * sc)};
+  if (p.lse && mt == 0 && hh == 0)
+    p.lse[(long long)(m.q0 + n) * p.lse_stride_n + qh] = p.lse_base2 ? lse * kLog2e : lse;
+}
+
+// ---------------------------------------------------------------------------
+// Host launchers
+// ---------------------------------------------------------------------------
+// Ring depth: the LDS budget is 160 KB per CU, shared by the resident
+// workgroups (two for 128-row tiles, one for 256-row tiles).
+template <int D>
+constexpr int verify_stages(int wpb) {
+  return wpb == 8 ? 4 : (D == 128 ? 2 : 4);
+}
+
+template <int D, int WPB, bool PAGED, bool FP8>
+static hipError_t launch_verify_t(const VerifyParams& p, int nitems, hipStream_t s) {
+  constexpr int ST = verify_stages<D>(WPB);
+  hipLaunchKernelGGL((verify_attn_kernel<D, WPB, ST, PAGED, FP8>), dim3(nitems), dim3(64 * WPB), 0, s, p);
+  return hipGetLastError();
+}
+
+template <int D, int WPB>
+static hipError_t launch_verify_w(const VerifyParams& p, bool paged, bool fp8, int nitems, hipStream_t s) {
+  if (fp8) return paged ? launch_verify_t<D, WPB, true, true>(p, nitems, s) : launch_verify_t<D, WPB, false, true>(p, nitems, s);
+  return paged ? launch_verify_t<D, WPB, true, false>(p, nitems, s) : launch_verify_t<D, WPB, false, false>(p, nitems, s);
+}
+
+hipError_t launch_verify_attention(const VerifyParams& p, int head_dim, int waves, bool paged, bool fp8, int nitems,
+                                   hipStream_t s) {
+  if (nitems <= 0) return hipSuccess;
+  if (head_dim == 128) {
+    if (waves == 2) return launch_verify_w<128, 2>(p, paged, fp8, nitems, s);
+    if (waves == 4) return launch_verify_w<128, 4>(p, paged, fp8, nitems, s);
+    if (waves == 8) return launch_verify_w<128, 8>(p, paged, fp8, nitems, s);
+  } else if (head_dim == 64) {
+    if (waves == 2) return launch_verify_w<64, 2>(p, paged, fp8, nitems, s);
+    if (waves == 4) return launch_verify_w<64, 4>(p, paged, fp8, nitems, s);
+    if (waves == 8) return launch_verify_w<64, 8>(p, paged, fp8, nitems, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_verify_merge(const VerifyParams& p, int head_dim, int rows, int nmerges, hipStream_t s) {
+  if (nmerges <= 0) return hipSuccess;
+  const long long waves = (long long)nmerges * (rows / 32) * (head_dim / 32);
+  const unsigned blocks = (unsigned)((waves + 3) / 4);
+  if (head_dim == 128 && rows == 128) hipLaunchKernelGGL((verify_merge_kernel<128, 128>), dim3(blocks), dim3(256), 0, s, p);
+  else if (head_dim == 128 && rows == 256) hipLaunchKernelGGL((verify_merge_kernel<128, 256>), dim3(blocks), dim3(256), 0, s, p);
+  else if (head_dim == 64 && rows == 128) hipLaunchKernelGGL((verify_merge_kernel<64, 128>), dim3(blocks), dim3(256), 0, s, p);
+  else if (head_dim == 64 && rows == 256) hipLaunchKernelGGL((verify_merge_kernel<64, 256>), dim3(blocks), dim3(256), 0, s, p);
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+}  // namespace d2sd

@@ -21,12 +21,16 @@ LIB_PATH = PKG_DIR / "libd2sd.so"
 INCLUDE = ROOT.parent / "include"
 
 ARCH = "gfx950"
-SOURCES = ["attention.hip", "plan.cpp", "capi.cpp"]
+SOURCES = ["attention.hip", "verify_attention.hip", "plan.cpp", "capi.cpp"]
 
 COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function", f"-I{INCLUDE}", f"-I{CSRC}"]
 # Device code: never let the compiler emit packed-fp32 VALU forms.
 DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
           "-ffp-contract=fast"]
+# Per-source extras.  verify_attention.hip runs one wave per SIMD with up to
+# 512 registers; MFMA results in VGPRs (not AGPRs) keep the accumulators out
+# of per-tile AGPR<->VGPR copies.
+EXTRA = {"verify_attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 
 def hipcc() -> str:
@@ -41,7 +45,7 @@ def _compile(src: str) -> Path:
     obj = OBJ_DIR / (path.stem + ".o")
     cmd = [hipcc(), *COMMON]
     if path.suffix == ".hip":
-        cmd += DEVICE
+        cmd += DEVICE + EXTRA.get(src, [])
     else:
         cmd += ["-x", "c++", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include"]
     cmd += ["-c", str(path), "-o", str(obj)]

@@ -31,8 +31,8 @@ EXPORTED_SYMBOLS = (
     "d2sd_graph_destroy",
     "d2sd_cascade_plan",
     "d2sd_cascade_run",
-    "d2sd_cascade_prefix",
-    "d2sd_cascade_suffix",
+    "d2sd_cascade_attention",
+    "d2sd_cascade_merge",
 )
 
 
@@ -41,6 +41,8 @@ class PlanDesc(C.Structure):
         ("num_reqs", C.c_int),
         ("qo_indptr", C.POINTER(C.c_int32)),
         ("prefix_len", C.POINTER(C.c_int32)),
+        ("page_indptr", C.POINTER(C.c_int32)),
+        ("prefix_tok_indptr", C.POINTER(C.c_int32)),
         ("num_qo_heads", C.c_int),
         ("num_kv_heads", C.c_int),
         ("head_dim", C.c_int),
@@ -55,11 +57,10 @@ class PlanDesc(C.Structure):
 
 class PlanInfo(C.Structure):
     _fields_ = [
-        ("num_prefix_work", C.c_int),
-        ("num_suffix_work", C.c_int),
-        ("prefix_waves", C.c_int),
-        ("suffix_waves", C.c_int),
-        ("prefix_rows", C.c_int),
+        ("num_items", C.c_int),
+        ("num_merges", C.c_int),
+        ("waves_per_block", C.c_int),
+        ("rows_per_tile", C.c_int),
         ("num_slots", C.c_int),
         ("plan_ints", C.c_int),
         ("workspace_bytes", C.c_size_t),
@@ -76,7 +77,6 @@ class PlanInfo(C.Structure):
 class RunArgs(C.Structure):
     _fields_ = [
         ("plan", C.c_void_p),
-        ("qo_indptr", C.c_void_p),
         ("q", C.c_void_p),
         ("q_stride_n", C.c_int64),
         ("q_stride_h", C.c_int64),
@@ -93,10 +93,7 @@ class RunArgs(C.Structure):
         ("prefix_stride_head", C.c_int64),
         ("prefix_stride_page", C.c_int64),
         ("page_size", C.c_int),
-        ("page_indptr", C.c_void_p),
         ("page_table", C.c_void_p),
-        ("prefix_tok_indptr", C.c_void_p),
-        ("prefix_len", C.c_void_p),
         ("k_scale", C.c_void_p),
         ("v_scale", C.c_void_p),
         ("sinks", C.c_void_p),
@@ -110,6 +107,11 @@ class RunArgs(C.Structure):
         ("workspace", C.c_void_p),
         ("workspace_bytes", C.c_size_t),
     ]
+
+
+# int32 entries per attention item / merge item in the host plan
+PLAN_ITEM_INTS = 16
+PLAN_MERGE_INTS = 8
 
 
 def _load() -> C.CDLL:
@@ -144,7 +146,7 @@ def _load() -> C.CDLL:
     lib.d2sd_graph_destroy.argtypes = [vp]
     lib.d2sd_cascade_plan.restype = i32
     lib.d2sd_cascade_plan.argtypes = [C.POINTER(PlanDesc), C.POINTER(C.c_int32), sz, C.POINTER(PlanInfo)]
-    for name in ("d2sd_cascade_run", "d2sd_cascade_prefix", "d2sd_cascade_suffix"):
+    for name in ("d2sd_cascade_run", "d2sd_cascade_attention", "d2sd_cascade_merge"):
         fn = getattr(lib, name)
         fn.restype = i32
         fn.argtypes = [C.POINTER(PlanInfo), C.POINTER(RunArgs), vp]

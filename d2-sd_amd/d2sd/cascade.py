@@ -13,9 +13,9 @@ elementwise ops:
 
 with the queries of request r = its tree nodes q[qo_indptr[r]:qo_indptr[r+1]].
 plan() does all host work and device uploads; run() only launches kernels
-(two per call: split-KV attention over prefix chunks and suffix trees, then the
-merge), allocates nothing when `out`/`lse` are given, and can be captured into
-a HipGraph.
+(two per call: attention over prefix key chunks and suffix trees, writing
+partial states, then their merge), allocates nothing when `out`/`lse` are
+given, and can be captured into a HipGraph.
 """
 from __future__ import annotations
 
@@ -96,10 +96,22 @@ class CascadeVerifyAttention:
             raise TypeError("kv_dtype must be torch.bfloat16 or torch.float8_e4m3fn")
         fp8 = kv_dtype == torch.float8_e4m3fn
         dev = self.device
+        pi = None
+        if int(page_size) > 0:
+            if page_indptr is None or page_table is None:
+                raise ValueError("paged prefix needs page_indptr and page_table")
+            pi = _i32(page_indptr)
+            if pi.shape[0] != R + 1:
+                raise ValueError("page_indptr must have R + 1 entries")
+        pti = _i32(prefix_tok_indptr) if (prefix_tok_indptr is not None and int(page_size) == 0) else None
+        if pti is not None and pti.shape[0] != R:
+            raise ValueError("prefix_tok_indptr must have R entries")
         desc = _lib.PlanDesc()
         desc.num_reqs = R
         desc.qo_indptr = qo.ctypes.data_as(C.POINTER(C.c_int32))
         desc.prefix_len = pl.ctypes.data_as(C.POINTER(C.c_int32))
+        desc.page_indptr = pi.ctypes.data_as(C.POINTER(C.c_int32)) if pi is not None else None
+        desc.prefix_tok_indptr = pti.ctypes.data_as(C.POINTER(C.c_int32)) if pti is not None else None
         desc.num_qo_heads = num_qo_heads
         desc.num_kv_heads = num_kv_heads
         desc.head_dim = head_dim
@@ -119,8 +131,6 @@ class CascadeVerifyAttention:
         self.qo_indptr_host = qo
         self.prefix_len_host = pl
         self.plan_dev = torch.from_numpy(host).to(dev)
-        self.qo_indptr_dev = torch.from_numpy(qo).to(dev)
-        self.prefix_len_dev = torch.from_numpy(pl).to(dev)
         self.workspace = torch.empty(max(int(info.workspace_bytes), 16), dtype=torch.uint8, device=dev)
         self.mask_mode = _MASK_MODES[mask_mode]
         self.total_q = int(qo[-1])
@@ -139,25 +149,12 @@ class CascadeVerifyAttention:
             self.tree_mask_dev = None
         self.page_size = int(page_size)
         if self.page_size > 0:
-            if page_indptr is None or page_table is None:
-                raise ValueError("paged prefix needs page_indptr and page_table")
-            pi = _i32(page_indptr)
-            if pi.shape[0] != R + 1:
-                raise ValueError("page_indptr must have R + 1 entries")
-            need = (pl + self.page_size - 1) // self.page_size
-            if np.any(pi[1:] - pi[:-1] < need):
-                raise ValueError("page_indptr gives a request fewer pages than its prefix_len needs")
-            self.page_indptr_dev = torch.from_numpy(pi).to(dev)
             pt = page_table if isinstance(page_table, torch.Tensor) else torch.from_numpy(_i32(page_table))
             self.page_table_dev = pt.to(device=dev, dtype=torch.int32).contiguous()
             if self.page_table_dev.numel() < int(pi[-1]):
                 raise ValueError("page_table shorter than page_indptr[-1]")
-            self.prefix_tok_indptr_dev = None
         else:
-            self.page_indptr_dev = None
             self.page_table_dev = None
-            self.prefix_tok_indptr_dev = (torch.from_numpy(_i32(prefix_tok_indptr)).to(dev)
-                                          if prefix_tok_indptr is not None else None)
         self.kv_layout = kv_layout
         self.num_qo_heads, self.num_kv_heads, self.head_dim = num_qo_heads, num_kv_heads, head_dim
         self.sm_scale = float(sm_scale) if sm_scale is not None else head_dim ** -0.5
@@ -220,16 +217,16 @@ class CascadeVerifyAttention:
         planned.  Returns (out [total_q, Hq, D] bf16, lse [total_q, Hq] fp32)."""
         return self._launch("d2sd_cascade_run", q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse)
 
-    def run_prefix(self, q, k_suffix, v_suffix, k_prefix=None, v_prefix=None, out=None, lse=None):
-        """First half of run(): the shared-prefix launch alone (split-KV
-        partials in the plan's workspace).  run_suffix() with the same
-        arguments finishes the call."""
-        return self._launch("d2sd_cascade_prefix", q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse)
+    def run_attention(self, q, k_suffix, v_suffix, k_prefix=None, v_prefix=None, out=None, lse=None):
+        """First half of run(): the attention launch alone (prefix key chunks
+        and suffix trees; partial states in the plan's workspace).
+        run_merge() with the same arguments finishes the call."""
+        return self._launch("d2sd_cascade_attention", q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse)
 
-    def run_suffix(self, q, k_suffix, v_suffix, k_prefix=None, v_prefix=None, out=None, lse=None):
-        """Second half of run(): tree-masked suffix level + merge of the
-        workspace partials + sink, into out / lse."""
-        return self._launch("d2sd_cascade_suffix", q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse)
+    def run_merge(self, q, k_suffix, v_suffix, k_prefix=None, v_prefix=None, out=None, lse=None):
+        """Second half of run(): merge of the workspace partials + sink into
+        out / lse."""
+        return self._launch("d2sd_cascade_merge", q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse)
 
     def _launch(self, fn_name, q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse):
         if not self._planned:
@@ -251,7 +248,6 @@ class CascadeVerifyAttention:
             raise ValueError("lse must be float32 [total_q, Hq] with contiguous heads")
         a = _lib.RunArgs()
         a.plan = self.plan_dev.data_ptr()
-        a.qo_indptr = self.qo_indptr_dev.data_ptr()
         a.q = q.data_ptr()
         a.q_stride_n, a.q_stride_h = q.stride(0), q.stride(1)
         a.k_suffix, a.v_suffix = k_suffix.data_ptr(), v_suffix.data_ptr()
@@ -268,11 +264,7 @@ class CascadeVerifyAttention:
             a.k_prefix, a.v_prefix = k_prefix.data_ptr(), v_prefix.data_ptr()
             a.prefix_stride_tok, a.prefix_stride_head, a.prefix_stride_page = st, sh, sp
         a.page_size = self.page_size
-        a.page_indptr = self.page_indptr_dev.data_ptr() if self.page_indptr_dev is not None else None
         a.page_table = self.page_table_dev.data_ptr() if self.page_table_dev is not None else None
-        a.prefix_tok_indptr = (self.prefix_tok_indptr_dev.data_ptr()
-                               if self.prefix_tok_indptr_dev is not None else None)
-        a.prefix_len = self.prefix_len_dev.data_ptr()
         a.k_scale = self.k_scale.data_ptr() if self.k_scale is not None else None
         a.v_scale = self.v_scale.data_ptr() if self.v_scale is not None else None
         a.sinks = self.sinks.data_ptr() if self.sinks is not None else None

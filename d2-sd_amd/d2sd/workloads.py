@@ -270,3 +270,26 @@ def verify_bytes_flops(prob: VerifyProblem) -> tuple:
         nbytes += 2 * n * hkv * d * 2 + n * ((n + 63) // 64) * 8
         flops += 4 * hq * d * anc
     return nbytes, flops
+
+
+def attention_launch_bytes_flops(prob: VerifyProblem) -> tuple:
+    """Algorithmic bytes and flops of the attention launch of run() (per
+    layer): both levels' K/V once (prefix at the cache dtype, suffix bf16),
+    Q once, the page table and the tree mask; flops over visible (query,
+    key) pairs only.  O / LSE are written by the merge launch and partial
+    states are implementation traffic, so neither is counted here."""
+    hq, hkv, d = prob.num_qo_heads, prob.num_kv_heads, prob.head_dim
+    b_kv = 1 if prob.kv_dtype == torch.float8_e4m3fn else 2
+    nbytes = 0
+    flops = 0
+    for i, r in enumerate(prob.requests):
+        Leff = prob.visible_prefix(i)
+        n = r.n
+        anc = int(ancestor_mask(r.tree.parents).sum())
+        nbytes += 2 * Leff * hkv * d * b_kv + 2 * n * hkv * d * 2 + n * hq * d * 2 + n * ((n + 63) // 64) * 8
+        if prob.page_size > 0:
+            nbytes += 4 * ((r.prefix_len + prob.page_size - 1) // prob.page_size)
+        flops += 4 * hq * d * (n * Leff + anc)
+    if b_kv == 1:
+        nbytes += 2 * hkv * 4
+    return nbytes, flops

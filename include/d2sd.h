@@ -135,8 +135,9 @@ int d2sd_graph_destroy(void* graph_exec);
  * Suffix key j is visible to suffix query i of request r iff bit j of
  *   tree_mask[(qo_indptr[r] + i) * mask_words + j / 64]
  * is set (bit (j % 64), little-endian 64-bit words).  mask_mode may instead
- * be D2SD_MASK_CAUSAL (chain) or D2SD_MASK_NONE (all suffix keys visible,
- * the non-causal DTA-draft case of model/dflash.py:127-130).
+ * be D2SD_MASK_CAUSAL (chain: key j visible iff j <= i) or D2SD_MASK_NONE (all
+ * suffix keys visible, the non-causal DTA-draft case of
+ * model/dflash.py:127-130).
  *
  * The prefix is either contiguous (page_size == 0): key t of request r at
  *   k_prefix + (prefix_tok_indptr[r] + t)*prefix_stride_tok + h*prefix_stride_head
@@ -145,32 +146,42 @@ int d2sd_graph_destroy(void* graph_exec);
  *   k_prefix + page_table[page_indptr[r] + t/page_size]*prefix_stride_page
  *            + (t % page_size)*prefix_stride_tok + h*prefix_stride_head.
  * window_left >= 0 keeps the last window_left prefix keys (all queries).
+ *
+ * plan() bakes every per-request offset into a work list the caller uploads;
+ * run() is two launches — attention (prefix key chunks and suffix trees, each
+ * writing a partial state to the workspace, or the output directly when a
+ * request has no prefix) and merge (log-sum-exp merge + sink into out / lse).
+ * run() allocates nothing and never synchronises the host, so it may be
+ * captured into a hipGraph; the device plan, page_table contents and tensors
+ * may change between replays as long as the plan's shape does not.
  * ---------------------------------------------------------------------- */
 typedef struct {
   int num_reqs;
-  const int32_t* qo_indptr;  /* host, [num_reqs + 1] */
-  const int32_t* prefix_len; /* host, [num_reqs] */
+  const int32_t* qo_indptr;         /* host, [num_reqs + 1] */
+  const int32_t* prefix_len;        /* host, [num_reqs] */
+  const int32_t* page_indptr;       /* host, [num_reqs + 1]; required when page_size > 0 */
+  const int32_t* prefix_tok_indptr; /* host, [num_reqs]; contiguous prefix, nullable */
   int num_qo_heads;
   int num_kv_heads;
   int head_dim;
   int window_left;     /* -1: full prefix */
   int kv_dtype;        /* D2SD_KV_* of the prefix cache */
-  int page_size;       /* 0: contiguous prefix; else the run's page size */
+  int page_size;       /* 0: contiguous prefix; else the pool's page size */
   int num_cus;         /* 0: query the device */
-  int max_splits;      /* 0: no limit */
-  int waves_per_block; /* prefix launch: 0 = choose, else 4 or 8 */
+  int max_splits;      /* 0: default cap */
+  int waves_per_block; /* 0 = choose; 2 (64-row waves, 128-row tiles), 4 (32-row
+                          waves, 128-row tiles) or 8 (32-row waves, 256-row tiles) */
 } d2sd_cascade_plan_desc;
 
 typedef struct {
-  int num_prefix_work;  /* workgroups of the prefix launch */
-  int num_suffix_work;  /* workgroups of the suffix (tree + merge) launch */
-  int prefix_waves;     /* 4 or 8 */
-  int suffix_waves;     /* waves per suffix workgroup */
-  int prefix_rows;      /* 32 * prefix_waves: rows per partial slot */
-  int num_slots;        /* split-KV partial slots */
+  int num_items;        /* workgroups of the attention launch */
+  int num_merges;       /* groups merged by the merge launch */
+  int waves_per_block;
+  int rows_per_tile;    /* packed (query, head) rows per workgroup and partial slot */
+  int num_slots;        /* partial slots in the workspace */
   int plan_ints;        /* int32 entries written to host_plan */
-  size_t workspace_bytes; /* float workspace for partials */
-  int max_splits_used;  /* 0: no prefix work at all */
+  size_t workspace_bytes;
+  int max_splits_used;  /* prefix key chunks of the most-split request */
   int num_reqs;
   int num_qo_heads;
   int num_kv_heads;
@@ -187,7 +198,6 @@ int d2sd_cascade_plan(const d2sd_cascade_plan_desc* desc, int32_t* host_plan,
 
 typedef struct {
   const int32_t* plan;      /* device copy of the host plan */
-  const int32_t* qo_indptr; /* device, [num_reqs + 1] */
   const void* q;            /* [total_q, Hq, D] bf16 */
   int64_t q_stride_n, q_stride_h;
   const void* k_suffix;     /* [total_q, Hkv, D] bf16 */
@@ -196,14 +206,11 @@ typedef struct {
   int mask_mode;            /* D2SD_MASK_* for the suffix level */
   int mask_words;           /* 64-bit words per tree-mask row */
   const uint64_t* tree_mask;
-  const void* k_prefix;     /* bf16 or fp8 bytes */
+  const void* k_prefix;     /* bf16 or fp8 bytes; NULL when no request has a prefix */
   const void* v_prefix;
   int64_t prefix_stride_tok, prefix_stride_head, prefix_stride_page;
-  int page_size;            /* 0: contiguous */
-  const int32_t* page_indptr;       /* device, [num_reqs + 1] (paged) */
-  const int32_t* page_table;        /* device (paged) */
-  const int32_t* prefix_tok_indptr; /* device, [num_reqs] (contiguous; nullable) */
-  const int32_t* prefix_len;        /* device, [num_reqs] */
+  int page_size;            /* must equal the planned page size */
+  const int32_t* page_table;/* device (paged) */
   const float* k_scale;     /* fp8: [Hkv] */
   const float* v_scale;
   const float* sinks;       /* nullable, [Hq] */
@@ -213,21 +220,17 @@ typedef struct {
   int64_t lse_stride_n;
   float sm_scale;
   int lse_base2;
-  void* workspace;
+  void* workspace;          /* >= info.workspace_bytes */
   size_t workspace_bytes;
 } d2sd_cascade_run_args;
 
-/* run = prefix launch then suffix launch.  Both halves are also exported:
- * prefix (one launch) writes the split-KV partial states of the shared-prefix
- * level to the workspace; suffix (one launch) computes the tree-masked suffix
- * level and, in its epilogue, merges the prefix partials, applies the sink and
- * writes out / lse.  Between the two the workspace holds the partial state. */
+/* run = attention launch then merge launch; both halves are also exported. */
 int d2sd_cascade_run(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* args,
                      d2sd_stream_t stream);
-int d2sd_cascade_prefix(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* args,
-                        d2sd_stream_t stream);
-int d2sd_cascade_suffix(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* args,
-                        d2sd_stream_t stream);
+int d2sd_cascade_attention(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* args,
+                           d2sd_stream_t stream);
+int d2sd_cascade_merge(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* args,
+                       d2sd_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -246,7 +246,7 @@ def test_cascade_config5_subset():
     (0, [16, 4, 9], -1, 0),        # empty prefix: suffix level alone
     (1, [1], -1, 0),               # single key, single node
     (65, [40, 1, 39], -1, 4),      # N > 64 nodes (two mask words), L % 64 == 1
-    (130, [30, 0, 17], 100, 8),    # forest (p=0), window inside the prefix
+    (130, [30, 0, 17], 100, 2),    # forest (p=0), window inside the prefix
     (50, [20, 5], 500, 0),         # window longer than the prefix
 ])
 def test_cascade_edges(L, shared, window, waves):

@@ -35,13 +35,20 @@ def test_version_and_error_strings():
     assert _lib.lib.d2sd_last_error() is not None
 
 
-def _plan(qo, pl, hq=32, hkv=8, d=128, window=-1, num_cus=256, waves=0, max_splits=0, page_size=16):
+def _plan(qo, pl, hq=32, hkv=8, d=128, window=-1, num_cus=256, waves=0, max_splits=0, page_size=16,
+          page_indptr=None, tok_indptr=None):
     desc = _lib.PlanDesc()
     qo = np.asarray(qo, dtype=np.int32)
     pl = np.asarray(pl, dtype=np.int32)
+    if page_size and page_indptr is None:
+        page_indptr = np.concatenate([[0], np.cumsum((pl + page_size - 1) // page_size)])
+    pi = np.asarray(page_indptr, dtype=np.int32) if page_indptr is not None else None
+    ti = np.asarray(tok_indptr, dtype=np.int32) if tok_indptr is not None else None
     desc.num_reqs = len(pl)
     desc.qo_indptr = qo.ctypes.data_as(C.POINTER(C.c_int32))
     desc.prefix_len = pl.ctypes.data_as(C.POINTER(C.c_int32))
+    desc.page_indptr = pi.ctypes.data_as(C.POINTER(C.c_int32)) if pi is not None else None
+    desc.prefix_tok_indptr = ti.ctypes.data_as(C.POINTER(C.c_int32)) if ti is not None else None
     desc.num_qo_heads, desc.num_kv_heads, desc.head_dim = hq, hkv, d
     desc.window_left = window
     desc.kv_dtype = 0
@@ -50,103 +57,124 @@ def _plan(qo, pl, hq=32, hkv=8, d=128, window=-1, num_cus=256, waves=0, max_spli
     desc.max_splits = max_splits
     desc.waves_per_block = waves
     info = _lib.PlanInfo()
-    assert _lib.lib.d2sd_cascade_plan(C.byref(desc), None, 0, C.byref(info)) == 0
+    assert _lib.lib.d2sd_cascade_plan(C.byref(desc), None, 0, C.byref(info)) == 0, _lib.lib.d2sd_last_error()
     host = np.zeros(max(info.plan_ints, 8), dtype=np.int32)
     rc = _lib.lib.d2sd_cascade_plan(C.byref(desc), host.ctypes.data_as(C.POINTER(C.c_int32)), host.size,
                                     C.byref(info))
     assert rc == 0, _lib.lib.d2sd_last_error()
-    npre, nsuf = info.num_prefix_work, info.num_suffix_work
-    pre = host[: 8 * npre].reshape(-1, 8)
-    suf = host[8 * npre: 8 * (npre + nsuf)].reshape(-1, 8)
-    return info, pre, suf
+    ni, nm = info.num_items, info.num_merges
+    items = host[: 16 * ni].reshape(-1, 16)
+    merges = host[16 * ni: 16 * ni + 8 * nm].reshape(-1, 8)
+    return info, items, merges
 
 
-MODE_PARTIAL, MODE_FINAL, MODE_NOOP, MODE_MERGE = 0, 1, 3, 4
+MODE_PARTIAL, MODE_FINAL, MODE_NOOP = 0, 1, 3
+SRC_PREFIX, SRC_SUFFIX = 0, 1
+# VerifyItem fields
+REQ, KVH, QT, SRC, KB, KE, SLOT, MODE, Q0, NQ, BASE, COFF = range(12)
 
 
-@pytest.mark.parametrize("qo,pl,window,page,hq", [
-    ([0, 128], [4096], -1, 16, 32),
-    ([256 * i for i in range(33)], [8192] * 32, -1, 16, 64),   # more tile groups than CUs
-    ([0, 256], [8192], -1, 16, 64),
-    ([0, 150], [4096], -1, 16, 32),
-    ([0, 41], [1024], -1, 0, 32),
-    ([0, 256], [8192], 128, 16, 32),
-    ([0, 64, 100, 164], [8192, 20000, 0], -1, 16, 32),
-    ([0, 30], [0], -1, 0, 32),
-    ([0, 150, 300], [777, 33], 500, 1, 32),
-    ([64 * i for i in range(33)], [8192] * 32, -1, 16, 32),
+@pytest.mark.parametrize("qo,pl,window,page,hq,waves", [
+    ([0, 128], [4096], -1, 16, 32, 0),
+    ([256 * i for i in range(33)], [8192] * 32, -1, 16, 64, 0),   # more groups than CUs
+    ([0, 256], [8192], -1, 16, 64, 4),
+    ([0, 150], [4096], -1, 16, 32, 0),
+    ([0, 41], [1024], -1, 0, 32, 0),
+    ([0, 256], [8192], 128, 16, 32, 2),
+    ([0, 150], [4096], -1, 16, 32, 8),
+    ([0, 64, 100, 164], [8192, 20000, 0], -1, 16, 32, 0),
+    ([0, 30], [0], -1, 0, 32, 0),
+    ([0, 150, 300], [777, 33], 500, 1, 32, 4),
+    ([64 * i for i in range(33)], [8192] * 32, -1, 16, 32, 0),
+    ([0, 0, 40], [100, 5000], -1, 16, 32, 0),                       # a request with no queries
 ])
-def test_plan_partitions_work(qo, pl, window, page, hq):
+def test_plan_partitions_work(qo, pl, window, page, hq, waves):
+    """Every (request, kv head, q-tile) group: prefix items partition its
+    visible prefix on 64-key tile boundaries into consecutive slots, one suffix
+    item covers its nodes, and one merge item reads exactly those slots; a
+    group without prefix keys has a FINAL suffix item and no merge."""
     hkv = 8
     g = hq // hkv
-    info, pre, suf = _plan(qo, pl, hq, hkv, 128, window, page_size=page)
-    rows = info.prefix_rows
-    assert info.prefix_waves in (4, 8) and rows == 32 * info.prefix_waves
-    srows = 32 * info.suffix_waves
-    assert rows % srows == 0
-    for lst in (pre, suf):
-        assert lst.shape[0] == 0 or lst[-1, 7] != MODE_NOOP
-    cover, slots = {}, {}
-    for req, kvh, qt, src, kb, ke, slot, mode in pre[pre[:, 7] != MODE_NOOP].tolist():
-        assert src == 0 and mode == MODE_PARTIAL
-        cover.setdefault((req, kvh, qt), []).append((kb, ke, slot))
-    all_slots = [c[2] for v in cover.values() for c in v]
+    page_indptr = None
+    if page:
+        page_indptr = np.concatenate([[0], np.cumsum((np.asarray(pl) + page - 1) // page)])
+    info, items, merges = _plan(qo, pl, hq, hkv, 128, window, page_size=page, waves=waves,
+                                page_indptr=page_indptr)
+    rows = info.rows_per_tile
+    assert info.waves_per_block in (2, 4, 8)
+    assert rows == {2: 128, 4: 128, 8: 256}[info.waves_per_block]
+    assert items.shape[0] == 0 or items[-1, MODE] != MODE_NOOP
+    live = items[items[:, MODE] != MODE_NOOP]
+    assert len(live) <= 256 * (1 if info.waves_per_block == 8 else 2) or len(qo) > 30
+    pre, suf = {}, {}
+    for it in live.tolist():
+        key = (it[REQ], it[KVH], it[QT])
+        r = it[REQ]
+        assert it[Q0] == qo[r] and it[NQ] == qo[r + 1] - qo[r]
+        if it[SRC] == SRC_PREFIX:
+            assert it[MODE] == MODE_PARTIAL
+            assert it[BASE] == (page_indptr[r] if page else 0)
+            pre.setdefault(key, []).append((it[KB], it[KE], it[SLOT]))
+        else:
+            assert it[SRC] == SRC_SUFFIX and key not in suf
+            assert (it[KB], it[KE], it[BASE]) == (0, qo[r + 1] - qo[r], qo[r])
+            suf[key] = (it[SLOT], it[MODE])
+    all_slots = [c[2] for v in pre.values() for c in v] + [v[0] for v in suf.values() if v[1] == MODE_PARTIAL]
     assert len(all_slots) == len(set(all_slots)) == info.num_slots
-    blocks = {}
-    for req, kvh, qt, src, kb, ke, slot, mode in suf[suf[:, 7] != MODE_NOOP].tolist():
-        assert src == 1
-        blocks.setdefault((req, kvh), []).append((qt, kb, ke, slot, mode))
+    assert sorted(all_slots) == list(range(info.num_slots))
+    mg = {(m[0], m[1], m[2]): (m[3], m[4], m[5], m[6]) for m in merges.tolist()}
+    assert len(mg) == len(merges)
     for r in range(len(pl)):
         n = qo[r + 1] - qo[r]
         L = pl[r]
         Leff = min(L, window) if window >= 0 else L
         for h in range(hkv):
-            qtiles = (n * g + rows - 1) // rows
-            for qt in range(qtiles):
-                ch = sorted(cover.get((r, h, qt), []))
+            for qt in range((n * g + rows - 1) // rows):
+                key = (r, h, qt)
+                assert key in suf
+                ch = sorted(pre.get(key, []))
                 if Leff == 0:
-                    assert ch == []
+                    assert ch == [] and suf[key] == (-1, MODE_FINAL) and key not in mg
                     continue
-                # chunks partition [L - Leff, L) on 64-key tile boundaries
                 assert ch[0][0] == L - Leff and ch[-1][1] == L
                 for (a, b, _), (c, _, _) in zip(ch[:-1], ch[1:]):
                     assert b == c and (b - ch[0][0]) % 64 == 0
-                # the group's slots are consecutive in key order
-                assert [c[2] for c in ch] == list(range(ch[0][2], ch[0][2] + len(ch)))
+                s0 = ch[0][2]
+                assert [c[2] for c in ch] == list(range(s0, s0 + len(ch)))
+                assert suf[key] == (s0 + len(ch), MODE_PARTIAL)
+                assert mg[key] == (s0, len(ch) + 1, qo[r], n)
+                assert len(ch) <= 15
                 if page:
                     for a, b, _ in ch:
                         assert (b - 1) // page - a // page + 1 <= 1024
-            nb = (n * g + srows - 1) // srows
-            bl = sorted(blocks.get((r, h), []))
-            assert [b[0] for b in bl] == list(range(nb))
-            for b, kb, ke, slot, mode in bl:
-                assert (kb, ke) == (0, n)
-                ch = sorted(cover.get((r, h, (b * srows) // rows), []))
-                if ch:
-                    assert mode & 0xff == MODE_MERGE and mode >> 8 == len(ch) and slot == ch[0][2]
-                else:
-                    assert mode == MODE_FINAL and slot == -1
     assert info.workspace_bytes == info.num_slots * rows * (128 * 2 + 4)
 
 
-def test_plan_prefix_fits_one_wave_of_workgroups():
-    info, pre, _ = _plan([0, 150], [4096])
-    live = (pre[:, 7] != MODE_NOOP).sum()
-    assert info.prefix_waves == 8 and live <= 256
-    info, pre, _ = _plan([0, 41], [1024])
-    assert (pre[:, 7] != MODE_NOOP).sum() <= 256 * (2 if info.prefix_waves == 4 else 1)
+def test_plan_fills_the_device_once():
+    info, items, _ = _plan([0, 150], [4096])
+    live = (items[:, MODE] != MODE_NOOP).sum()
+    assert info.waves_per_block == 4 and 256 < live <= 512
+    info, items, _ = _plan([0, 41], [1024], page_size=0)
+    assert (items[:, MODE] != MODE_NOOP).sum() <= 512
+
+
+def test_plan_contiguous_token_offsets():
+    _, items, _ = _plan([0, 10, 30], [100, 200], page_size=0, tok_indptr=[0, 100])
+    for it in items[items[:, MODE] != MODE_NOOP].tolist():
+        if it[SRC] == SRC_PREFIX:
+            assert it[BASE] == [0, 100][it[REQ]]
 
 
 def test_plan_xcd_grouping():
     """Items reading the same keys sit on one XCD (work index % 8)."""
-    info, pre, suf = _plan([0, 150, 200], [4096, 3000])
-    for lst, key in ((pre, lambda w: (w[0], w[1], w[4])), (suf, lambda w: (w[0], w[1]))):
-        xcd = {}
-        for i, w in enumerate(lst.tolist()):
-            if w[7] == MODE_NOOP:
-                continue
-            xcd.setdefault(key(w), set()).add(i % 8)
-        assert all(len(s) == 1 for s in xcd.values())
+    info, items, _ = _plan([0, 150, 200], [4096, 3000])
+    xcd = {}
+    for i, w in enumerate(items.tolist()):
+        if w[MODE] == MODE_NOOP:
+            continue
+        key = (w[SRC], w[REQ], w[KVH], w[KB])
+        xcd.setdefault(key, set()).add(i % 8)
+    assert all(len(s) == 1 for s in xcd.values())
 
 
 def test_plan_rejects_bad_input():
@@ -161,6 +189,15 @@ def test_plan_rejects_bad_input():
     assert _lib.lib.d2sd_cascade_plan(C.byref(desc), None, 0, C.byref(info)) == 2
     assert b"head_dim" in _lib.lib.d2sd_last_error()
     desc.head_dim, desc.num_qo_heads = 128, 30
+    assert _lib.lib.d2sd_cascade_plan(C.byref(desc), None, 0, C.byref(info)) == 1
+    desc.num_qo_heads = 32
+    desc.page_size = 16                     # paged without page_indptr
+    assert _lib.lib.d2sd_cascade_plan(C.byref(desc), None, 0, C.byref(info)) == 1
+    assert b"page_indptr" in _lib.lib.d2sd_last_error()
+    pi = np.asarray([0, 3], dtype=np.int32)  # 3 pages < ceil(100 / 16)
+    desc.page_indptr = pi.ctypes.data_as(C.POINTER(C.c_int32))
+    assert _lib.lib.d2sd_cascade_plan(C.byref(desc), None, 0, C.byref(info)) == 1
+    desc.page_size, desc.waves_per_block = 0, 6
     assert _lib.lib.d2sd_cascade_plan(C.byref(desc), None, 0, C.byref(info)) == 1
 
 
