@@ -11,6 +11,16 @@ pool (604 MB in total, beyond the 256 MB Infinity Cache).  The 36 layer calls
 replayed.
 
 Prints ONE JSON line.  value = microseconds per layer-call (lower is better).
+
+HBM traffic of the attention launch (roofline.traffic) comes from two
+rocprofv3 counter runs over this same workload:
+
+    python bench.py --measure-traffic     # writes profiles/verify_attn_cfg2_traffic.txt
+
+which starts `rocprofv3 --pmc FETCH_SIZE` and then `--pmc WRITE_SIZE` as child
+processes on `bench.py --traffic-workload` (the 36 attention launches plus a
+plain 256 MiB device copy of known size).  Each counter is scaled by
+known_bytes / counter for the copy kernel.  A default run reads that file.
 """
 from __future__ import annotations
 
@@ -28,6 +38,8 @@ for _p in (ROOT, ROOT / "d2-sd_amd"):
         sys.path.insert(0, str(_p))
 
 METRIC = "cascade-verify attn µs/layer + HBM GB/s (% roofline), Qwen3-8B shape, 1 GPU"
+TRAFFIC_FILE = ROOT / "profiles" / "verify_attn_cfg2_traffic.txt"
+COPY_BYTES = 256 << 20
 HBM_PEAK_GBPS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
@@ -96,6 +108,112 @@ def cpu_baseline(mp, reps: int, torch) -> dict:
             "queries_per_s": prob.total_q / (us * 1e-6), "cpu_model": cpu_model()}
 
 
+def traffic_workload(args) -> int:
+    """The workload the counter runs profile: one plain device copy of
+    COPY_BYTES (calibration) then the attention launch of every layer, each
+    repeated a few times."""
+    import torch
+    import d2sd
+    from d2sd import workloads as wl
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    src = torch.ones(COPY_BYTES, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    prob = wl.config2(args.seed, layers=args.layers)
+    mp = wl.materialize(prob, dev)
+    attn = d2sd.CascadeVerifyAttention(dev)
+    wl.plan_for(attn, mp)
+    T, hq, d = prob.total_q, prob.num_qo_heads, prob.head_dim
+    o = torch.empty(T, hq, d, dtype=torch.bfloat16, device=dev)
+    lse = torch.empty(T, hq, dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+        for lt in mp.layers:
+            attn.run_attention(lt.q, lt.k_suffix, lt.v_suffix, lt.k_prefix, lt.v_prefix, out=o, lse=lse)
+        torch.cuda.synchronize()
+    print("traffic workload done", flush=True)
+    return 0
+
+
+def _counter_means(csv_path: Path, counter: str) -> dict:
+    import csv
+    sums, counts = {}, {}
+    with open(csv_path) as f:
+        for row in csv.DictReader(f):
+            if row["Counter_Name"] != counter:
+                continue
+            name = row["Kernel_Name"]
+            key = "attention" if "verify_attn_kernel" in name else ("copy" if "copyBuffer" in name else None)
+            if key is None:
+                continue
+            sums[key] = sums.get(key, 0.0) + float(row["Counter_Value"])
+            counts[key] = counts.get(key, 0) + 1
+    return {k: sums[k] / counts[k] for k in sums}
+
+
+def measure_traffic(args) -> int:
+    """Two counter runs (FETCH_SIZE, WRITE_SIZE) of the traffic workload as
+    child processes; writes TRAFFIC_FILE."""
+    import subprocess
+    import tempfile
+    res = {}
+    with tempfile.TemporaryDirectory(dir=os.environ.get("TMPDIR", "/tmp")) as tmp:
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            outdir = Path(tmp) / counter
+            cmd = ["rocprofv3", "--pmc", counter, "--kernel-include-regex", "verify_attn_kernel|copyBuffer",
+                   "-d", str(outdir), "-o", "run", "--output-format", "csv", "--",
+                   sys.executable, str(Path(__file__).resolve()), "--traffic-workload",
+                   "--layers", str(args.layers), "--seed", str(args.seed)]
+            log("running " + " ".join(cmd))
+            r = subprocess.run(cmd, timeout=300, capture_output=True, text=True)
+            if r.returncode != 0:
+                print(r.stdout[-2000:], r.stderr[-2000:], file=sys.stderr)
+                return r.returncode
+            files = list(outdir.rglob("*counter_collection.csv"))
+            if not files:
+                print("no counter_collection.csv from rocprofv3", file=sys.stderr)
+                return 1
+            res[counter] = _counter_means(files[0], counter)
+    # FETCH_SIZE / WRITE_SIZE are in KiB per dispatch; the copy kernel reads
+    # and writes COPY_BYTES each
+    fetch_scale = COPY_BYTES / (res["FETCH_SIZE"]["copy"] * 1024.0)
+    write_scale = COPY_BYTES / (res["WRITE_SIZE"]["copy"] * 1024.0)
+    fetch_b = res["FETCH_SIZE"]["attention"] * 1024.0 * fetch_scale
+    write_b = res["WRITE_SIZE"]["attention"] * 1024.0 * write_scale
+    lines = [
+        "# HBM traffic of the cascade verify attention launch, config 2 (Qwen3-8B, L=4096 paged, 36 layers)",
+        f"# command: python bench.py --measure-traffic --layers {args.layers} --seed {args.seed}",
+        "#   = rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) --kernel-include-regex 'verify_attn_kernel|copyBuffer'",
+        "#     --output-format csv -- python bench.py --traffic-workload",
+        f"copy_kernel_bytes: {COPY_BYTES}",
+        f"copy_FETCH_SIZE_KiB: {res['FETCH_SIZE']['copy']:.1f}",
+        f"copy_WRITE_SIZE_KiB: {res['WRITE_SIZE']['copy']:.1f}",
+        f"fetch_scale: {fetch_scale:.4f}",
+        f"write_scale: {write_scale:.4f}",
+        f"attention_FETCH_SIZE_KiB_per_dispatch: {res['FETCH_SIZE']['attention']:.1f}",
+        f"attention_WRITE_SIZE_KiB_per_dispatch: {res['WRITE_SIZE']['attention']:.1f}",
+        f"attention_fetch_bytes_per_launch: {fetch_b:.0f}",
+        f"attention_write_bytes_per_launch: {write_b:.0f}",
+        f"traffic_bytes_per_launch: {fetch_b + write_b:.0f}",
+    ]
+    TRAFFIC_FILE.parent.mkdir(exist_ok=True)
+    TRAFFIC_FILE.write_text("\n".join(lines) + "\n")
+    print("\n".join(lines))
+    return 0
+
+
+def read_traffic():
+    """traffic_bytes_per_launch from TRAFFIC_FILE, or None."""
+    try:
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -106,7 +224,14 @@ def main() -> int:
     ap.add_argument("--cpu-reps", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=50)
+    ap.add_argument("--measure-traffic", action="store_true",
+                    help="run the two rocprofv3 counter passes and write the traffic summary")
+    ap.add_argument("--traffic-workload", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.traffic_workload:
+        return traffic_workload(args)
+    if args.measure_traffic:
+        return measure_traffic(args)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: every path here runs on a single MI355X "
               "(multi-GPU sharding is a design note, not a measured configuration).", file=sys.stderr)
@@ -186,7 +311,7 @@ def main() -> int:
         achieved = ab / (attn_us * 1e-6) / 1e9
         roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": achieved / HBM_PEAK_GBPS}
-    roof["traffic"] = None
+    roof["traffic"] = read_traffic()
     roof["kernel"] = "d2sd::verify_attn_kernel<128, %d, ...> (prefix chunks + suffix trees)" % info.waves_per_block
     roof["kernel_us"] = attn_us
     roof["algorithmic_bytes"] = ab
