@@ -108,9 +108,10 @@ struct VerifyItem {
   int pad[4];
 };
 
-// One group whose partial slots [slot0, slot0 + nslots) are merged.
+// One 32-row block `blk` of a group whose partial slots
+// [slot0, slot0 + nslots) are merged (nslots == 0: padding, no work).
 struct VerifyMerge {
-  int req, kvh, qtile, slot0, nslots, q0, nq, pad;
+  int req, kvh, qtile, slot0, nslots, q0, nq, blk;
 };
 
 struct VerifySource {

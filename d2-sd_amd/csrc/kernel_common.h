@@ -68,22 +68,32 @@ __device__ __forceinline__ u32x2 fp8x4_to_bf16x4(unsigned w) {
 }
 
 // One global_load_lds_dwordx4: lane l copies 16 bytes from `src` to LDS byte
-// address lds_addr + 16*l (lds_addr wave-uniform, passed through M0).  Issued
-// as inline asm so that the compiler does not track these LDS writes: its own
-// tracking waits for every outstanding DMA (vmcnt(0)) before LDS reads, which
-// would drain the whole prefetch ring each tile.  Completion is enforced
-// explicitly (wait_vmcnt + s_barrier).  M0 is saved and restored.
+// address lds_addr + 16*l (lds_addr wave-uniform, passed through M0, which the
+// statement declares clobbered).  Issued as inline asm so that the compiler
+// does not track these LDS writes: its own tracking waits for every
+// outstanding DMA (vmcnt(0)) before LDS reads, which would drain the whole
+// prefetch ring each tile.  Completion is enforced explicitly (wait_vmcnt +
+// s_barrier).
 __device__ __forceinline__ void dma16(const void* src, unsigned lds_addr) {
-  unsigned saved;
   __asm__ volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %1\n\t"
+      "s_mov_b32 m0, %0\n\t"
       "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %2, off\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
+      "global_load_lds_dwordx4 %1, off"
+      :
       : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(src)
-      : "memory");
+      : "memory", "m0");
+}
+
+// The same with a wave-uniform base: lane l copies 16 bytes from
+// sbase + voff (voff per lane).
+__device__ __forceinline__ void dma16s(const void* sbase, unsigned voff, unsigned lds_addr) {
+  __asm__ volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %2"
+      :
+      : "s"(lds_addr), "v"(voff), "s"(sbase)
+      : "memory", "m0");
 }
 
 __device__ __forceinline__ unsigned lds_address(const void* p) {

@@ -36,16 +36,20 @@ struct ItemSet {
   std::vector<Item> items;
 };
 
+// Returns, per input set (input order), the XCD it was dealt to.
 template <typename Item>
-static void order_for_xcds(std::vector<ItemSet<Item>>& sets, std::vector<Item>& out) {
-  std::stable_sort(sets.begin(), sets.end(),
-                   [](const ItemSet<Item>& a, const ItemSet<Item>& b) { return a.cost > b.cost; });
+static std::vector<int> order_for_xcds(std::vector<ItemSet<Item>>& sets, std::vector<Item>& out) {
+  std::vector<int> idx(sets.size());
+  for (size_t i = 0; i < idx.size(); ++i) idx[i] = (int)i;
+  std::stable_sort(idx.begin(), idx.end(), [&](int a, int b) { return sets[a].cost > sets[b].cost; });
   std::vector<long long> load(8, 0);
   std::vector<std::vector<Item>> lists(8);
-  for (auto& set : sets) {
+  std::vector<int> xcd_of(sets.size(), 0);
+  for (int i : idx) {
     const int x = (int)(std::min_element(load.begin(), load.end()) - load.begin());
-    load[x] += set.cost;
-    lists[x].insert(lists[x].end(), set.items.begin(), set.items.end());
+    load[x] += sets[i].cost;
+    xcd_of[i] = x;
+    lists[x].insert(lists[x].end(), sets[i].items.begin(), sets[i].items.end());
   }
   size_t maxlen = 0;
   for (auto& l : lists) maxlen = std::max(maxlen, l.size());
@@ -60,6 +64,24 @@ static void order_for_xcds(std::vector<ItemSet<Item>>& sets, std::vector<Item>& 
       }
     }
   while (!out.empty() && out.back().mode == MODE_NOOP) out.pop_back();
+  return xcd_of;
+}
+
+// Interleave per-XCD merge lists: merge workgroup 8k + x runs on XCD x.
+static void interleave_merges(std::vector<std::vector<VerifyMerge>>& lists, std::vector<VerifyMerge>& out) {
+  size_t maxlen = 0;
+  for (auto& l : lists) maxlen = std::max(maxlen, l.size());
+  for (size_t k = 0; k < maxlen; ++k)
+    for (int x = 0; x < 8; ++x) {
+      if (k < lists[x].size()) {
+        out.push_back(lists[x][k]);
+      } else {
+        VerifyMerge m{};
+        m.nslots = 0;  // padding: no work
+        out.push_back(m);
+      }
+    }
+  while (!out.empty() && out.back().nslots == 0) out.pop_back();
 }
 
 int verify_wgs_per_cu(int waves) { return waves == 8 ? 1 : 2; }
@@ -111,7 +133,7 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
   while (chunk < max_ptiles && wgs(chunk) > capacity) ++chunk;
   for (int r = 0; r < R; ++r) chunk = std::max(chunk, (ptiles[r] + split_cap - 1) / split_cap);
   if (in.page_size > 0) {
-    const int max_chunk = std::max(1, ((kMaxStagedPages - 2) * in.page_size) / 64);
+    const int max_chunk = std::max(1, ((kMaxStagedPages - 8) * in.page_size) / 64);
     chunk = std::min(chunk, max_chunk);
   }
   (void)groups;
@@ -133,17 +155,27 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
     }
   }
 
-  std::vector<ItemSet<VerifyItem>> pre_sets, suf_sets;
+  // One set per (request, kv head): all its q-tiles, key chunks and suffix
+  // items run on one XCD, so the head's K/V and Q come from HBM once and its
+  // partial states stay in that XCD's L2.  With fewer such sets than XCDs,
+  // each key chunk (with all q-tiles reading it) is a set of its own.
+  long long nheads_sets = 0;
+  for (int r = 0; r < R; ++r) nheads_sets += nq[r] > 0 ? Hkv : 0;
+  const bool per_head = nheads_sets >= 8;
+  std::vector<ItemSet<VerifyItem>> sets;
+  std::vector<std::vector<VerifyMerge>> set_merges;
   for (int r = 0; r < R; ++r) {
     if (nq[r] == 0) continue;
     const int S = splits[r];
     const int q0 = in.qo_indptr[r];
     const int pbase = in.page_size > 0 ? in.page_indptr[r] : (in.prefix_tok_indptr ? in.prefix_tok_indptr[r] : 0);
     for (int h = 0; h < Hkv; ++h) {
-      for (int s = 0; s < S; ++s) {
+      ItemSet<VerifyItem> head_set;
+      head_set.cost = 0;
+      for (int s_ = 0; s_ < S; ++s_) {
         const int base = ptiles[r] / S, rem = ptiles[r] % S;
-        const int t0 = s * base + std::min(s, rem);
-        const int nt = base + (s < rem ? 1 : 0);
+        const int t0 = s_ * base + std::min(s_, rem);
+        const int nt = base + (s_ < rem ? 1 : 0);
         ItemSet<VerifyItem> set;
         set.cost = (long long)nt * qtiles[r];
         for (int qt = 0; qt < qtiles[r]; ++qt) {
@@ -154,7 +186,7 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
           w.src = SRC_PREFIX;
           w.kv_begin = kv0[r] + 64 * t0;
           w.kv_end = std::min(kv1[r], kv0[r] + 64 * (t0 + nt));
-          w.slot = slot0[grp0[r] + h * qtiles[r] + qt] + s;
+          w.slot = slot0[grp0[r] + h * qtiles[r] + qt] + s_;
           w.mode = MODE_PARTIAL;
           w.q0 = q0;
           w.nq = nq[r];
@@ -162,10 +194,17 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
           w.causal_off = 0;
           set.items.push_back(w);
         }
-        pre_sets.push_back(std::move(set));
+        if (per_head) {
+          head_set.cost += set.cost;
+          head_set.items.insert(head_set.items.end(), set.items.begin(), set.items.end());
+        } else {
+          sets.push_back(std::move(set));
+          set_merges.emplace_back();
+        }
       }
       ItemSet<VerifyItem> set;
       set.cost = (long long)stiles[r] * qtiles[r];
+      std::vector<VerifyMerge> merges;
       for (int qt = 0; qt < qtiles[r]; ++qt) {
         const int gi = grp0[r] + h * qtiles[r] + qt;
         VerifyItem w{};
@@ -183,26 +222,37 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
         w.causal_off = 0;
         set.items.push_back(w);
         if (S > 0) {
-          VerifyMerge m{};
-          m.req = r;
-          m.kvh = h;
-          m.qtile = qt;
-          m.slot0 = slot0[gi];
-          m.nslots = S + 1;
-          m.q0 = q0;
-          m.nq = nq[r];
-          out.merges.push_back(m);
+          // one merge workgroup per 32-row block holding valid rows
+          for (int blk = 0; blk < ROWS / 32 && qt * ROWS + blk * 32 < nq[r] * g; ++blk) {
+            VerifyMerge m{};
+            m.req = r;
+            m.kvh = h;
+            m.qtile = qt;
+            m.slot0 = slot0[gi];
+            m.nslots = S + 1;
+            m.q0 = q0;
+            m.nq = nq[r];
+            m.blk = blk;
+            merges.push_back(m);
+          }
         }
       }
-      suf_sets.push_back(std::move(set));
+      if (per_head) {
+        head_set.cost += set.cost;
+        head_set.items.insert(head_set.items.end(), set.items.begin(), set.items.end());
+        sets.push_back(std::move(head_set));
+        set_merges.push_back(std::move(merges));
+      } else {
+        sets.push_back(std::move(set));
+        set_merges.push_back(std::move(merges));
+      }
     }
   }
-  // prefix sets first (longer), suffix sets after them on the least-loaded XCDs
-  std::vector<ItemSet<VerifyItem>> sets;
-  sets.reserve(pre_sets.size() + suf_sets.size());
-  for (auto& s_ : pre_sets) sets.push_back(std::move(s_));
-  for (auto& s_ : suf_sets) sets.push_back(std::move(s_));
-  order_for_xcds(sets, out.items);
+  const std::vector<int> xcd = order_for_xcds(sets, out.items);
+  std::vector<std::vector<VerifyMerge>> mlists(8);
+  for (size_t i = 0; i < set_merges.size(); ++i)
+    mlists[xcd[i]].insert(mlists[xcd[i]].end(), set_merges[i].begin(), set_merges[i].end());
+  interleave_merges(mlists, out.merges);
 
   out.waves = W;
   out.rows = ROWS;

@@ -80,21 +80,6 @@ __device__ __forceinline__ float xor32(float x, int hh) {
   return __uint_as_float(hh ? r[0] : r[1]);
 }
 
-// One global_load_lds_dwordx4 with a wave-uniform base: lane l copies 16
-// bytes from sbase + voff (voff per lane) to LDS byte address lds_addr + 16*l.
-__device__ __forceinline__ void dma16s(const void* sbase, unsigned voff, unsigned lds_addr) {
-  unsigned saved;
-  __asm__ volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %1\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %2, %3\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "s"(lds_addr), "v"(voff), "s"(sbase)
-      : "memory");
-}
-
 // One workgroup: rows [qtile*ROWS, +ROWS) of (req, kvh) against keys
 // [kv_begin, kv_end) of source S.  Each of the W waves owns RB 32-row
 // blocks (ROWS = 32*RB*W).
@@ -167,6 +152,17 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
   const long long page_b = S.stride_page * ESZ;
   const int log2p = S.log2_page;
   const int pmask = (1 << log2p) - 1;
+  // ---- Q fragments (B operand of S^T = K Q^T): lane holds 8 consecutive
+  // head dims at offset 8*hh of every 16-wide k step, for row block rb ----
+  bf16x8 qf[RB][KS];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const bf16_t* qp = (const bf16_t*)p.q + (long long)(w.q0 + n[rb]) * p.q_stride_n +
+                       (long long)qh[rb] * p.q_stride_h + 8 * hh;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[rb][ks] = rv[rb] ? *(const bf16x8*)(qp + 16 * ks) : zero_bf16x8();
+  }
+
   int pg_first = 0;
   if constexpr (PAGED) {
     if (ntiles > 0) {
@@ -179,17 +175,6 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
     const long long off = (long long)w.base * tok_b;
     kbase += off;
     vbase += off;
-  }
-
-  // ---- Q fragments (B operand of S^T = K Q^T): lane holds 8 consecutive
-  // head dims at offset 8*hh of every 16-wide k step, for row block rb ----
-  bf16x8 qf[RB][KS];
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-    const bf16_t* qp = (const bf16_t*)p.q + (long long)(w.q0 + n[rb]) * p.q_stride_n +
-                       (long long)qh[rb] * p.q_stride_h + 8 * hh;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qf[rb][ks] = rv[rb] ? *(const bf16x8*)(qp + 16 * ks) : zero_bf16x8();
   }
 
   float kscale = 1.f, vscale = 1.f;
@@ -341,11 +326,11 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
       }
     }
 
-    // O^T += V^T P^T
+    // O^T += V^T P^T: consecutive MFMAs update different accumulators
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
+      for (int mt = 0; mt < MT; ++mt) {
         const bf16x8 a = vfrag(mt, ks);
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
@@ -371,34 +356,55 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
     // cs ^ swizzle(row).  Full tiles of an item whose key range starts on a
     // 64-key boundary (and, paged, whose pages hold whole row groups) add a
     // wave-uniform base per instruction: the row group's page and row.
+    // A wave's instructions cover WROWS consecutive key rows of a tile; on the
+    // fast path (paged) they lie in at most two pages, and the in-page row of
+    // every instruction is a per-lane constant.
+    constexpr int WROWS = IPW * RPI;
     const int lrow = lane / CH, cs = lane % CH;
-    const bool fast = (kv_begin & 63) == 0 && tok_b < (1ll << 26) && (!PAGED || (1 << log2p) >= RPI);
+    const int P = 1 << log2p;
+    const bool fast = (kv_begin & 63) == 0 && tok_b < (1ll << 26) &&
+                      (!PAGED || (P >= RPI && P <= 64 && 2 * P >= WROWS));
     unsigned lane_off[IPW];
 #pragma unroll
     for (int i = 0; i < IPW; ++i) {
-      const int r = (wv * IPW + i) * RPI + lrow;
-      lane_off[i] = (unsigned)(lrow * tok_b) + (unsigned)((cs ^ chunk_swizzle<D>(r)) * 16);
+      const int r0 = (wv * IPW + i) * RPI;  // first row of the instruction in the tile
+      const int row_in_src = PAGED ? (r0 & pmask) : r0;
+      lane_off[i] = (unsigned)((row_in_src + lrow) * tok_b) + (unsigned)((cs ^ chunk_swizzle<D>(r0 + lrow)) * 16);
     }
+    // Page ids of the (at most two) pages of this wave's rows of tile `it`,
+    // read from the staged list one step before the tile is issued.
+    auto wave_pages = [&](int it) -> int2 {
+      int2 r = {0, 0};
+      if constexpr (PAGED) {
+        const int kb = kv_begin + it * 64;
+        const int s0 = min(((kb + wv * WROWS) >> log2p) - pg_first, kMaxStagedPages - 1);
+        const int s1 = min(((kb + wv * WROWS + WROWS - 1) >> log2p) - pg_first, kMaxStagedPages - 1);
+        r.x = sm.pages[max(s0, 0)];
+        r.y = sm.pages[max(s1, 0)];
+      }
+      return r;
+    };
 
     // DMA of tile `it` into ring stage it % STAGES.  Keys past kv_end (tail
     // tile only) load the last valid key: finite data whose scores the tail
     // mask removes.
-    auto issue = [&](int it) {
+    auto issue = [&](int it, int2 pg) {
       const int kb = kv_begin + it * 64;
       const unsigned kst = ring_lds + (it % STAGES) * STAGE_BYTES;
       const unsigned vst = kst + 64 * D * 2;
       if (fast && kb + 64 <= kv_end) {
+        long long o0, o1;
+        if constexpr (PAGED) {
+          o0 = (long long)__builtin_amdgcn_readfirstlane(pg.x) * page_b;
+          o1 = (long long)__builtin_amdgcn_readfirstlane(pg.y) * page_b;
+        } else {
+          o0 = o1 = (long long)kb * tok_b;
+        }
 #pragma unroll
         for (int i = 0; i < IPW; ++i) {
           const int inst = wv * IPW + i;
-          const int t0 = kb + inst * RPI;  // first key of the row group (uniform)
-          long long ub;
-          if constexpr (PAGED) {
-            const int pg = __builtin_amdgcn_readfirstlane(sm.pages[(t0 >> log2p) - pg_first]);
-            ub = (long long)pg * page_b + (long long)(t0 & pmask) * tok_b;
-          } else {
-            ub = (long long)t0 * tok_b;
-          }
+          const bool second = PAGED && (((inst * RPI) >> log2p) != ((wv * WROWS) >> log2p));
+          const long long ub = second ? o1 : o0;
           dma16s(kbase + ub, lane_off[i], kst + inst * 1024);
           dma16s(vbase + ub, lane_off[i], vst + inst * 1024);
         }
@@ -436,7 +442,8 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
 
 #pragma unroll
     for (int t = 0; t < STAGES - 1; ++t)
-      if (t < ntiles) issue(t);
+      if (t < ntiles) issue(t, wave_pages(t));
+    int2 pnext = wave_pages(STAGES - 1);
 
     // One step of the ring: wait for tile `it`, refill the stage freed by
     // tile it-1, compute tile `it` (masked or not, as the tag says).
@@ -451,7 +458,8 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
       else wait_vmcnt<0>();
       __builtin_amdgcn_s_barrier();
       __asm__ volatile("" ::: "memory");
-      if (it + STAGES - 1 < ntiles) issue(it + STAGES - 1);
+      if (it + STAGES - 1 < ntiles) issue(it + STAGES - 1, pnext);
+      pnext = wave_pages(it + STAGES);
 
       const int kb = kv_begin + it * 64;
       if (!live || !tile_visible(kb)) return;
@@ -626,19 +634,18 @@ void verify_attn_kernel(const VerifyParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Merge: one wave per (group, 32-row block, 32-wide head-dim block); lane l
-// owns row l%32 and the 16 head dims 32mt + 8q4 + 4(l/32) + e.  All partial
+// Merge: one workgroup per (group, 32-row block), placed on the XCD whose L2
+// holds the group's partials; wave mt owns the 32-wide head-dim block mt and
+// lane l owns row l%32 and head dims 32mt + 8q4 + 4(l/32) + e.  All partial
 // loads of up to kMaxVerifySplits + 1 slots are in flight at once.
 // ---------------------------------------------------------------------------
 template <int D, int ROWS>
-__global__ __launch_bounds__(256) void verify_merge_kernel(const VerifyParams p) {
-  constexpr int BLK = ROWS / 32, MT = D / 32, B = kMaxVerifySplits + 1;
-  const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int item = gw / (BLK * MT);
-  if (item >= p.num_merges) return;
-  const int rem = gw - item * (BLK * MT);
-  const int blk = rem / MT, mt = rem - blk * MT;
-  const VerifyMerge m = p.merges[item];
+__global__ __launch_bounds__(64 * (D / 32)) void verify_merge_kernel(const VerifyParams p) {
+  constexpr int B = kMaxVerifySplits + 1;
+  const VerifyMerge m = p.merges[blockIdx.x];
+  if (m.nslots == 0) return;  // padding
+  const int blk = m.blk;
+  const int mt = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63, l32 = lane & 31, hh = lane >> 5;
   const int g = p.group;
   const int row = m.qtile * ROWS + blk * 32 + l32;
@@ -744,12 +751,11 @@ hipError_t launch_verify_attention(const VerifyParams& p, int head_dim, int wave
 
 hipError_t launch_verify_merge(const VerifyParams& p, int head_dim, int rows, int nmerges, hipStream_t s) {
   if (nmerges <= 0) return hipSuccess;
-  const long long waves = (long long)nmerges * (rows / 32) * (head_dim / 32);
-  const unsigned blocks = (unsigned)((waves + 3) / 4);
-  if (head_dim == 128 && rows == 128) hipLaunchKernelGGL((verify_merge_kernel<128, 128>), dim3(blocks), dim3(256), 0, s, p);
-  else if (head_dim == 128 && rows == 256) hipLaunchKernelGGL((verify_merge_kernel<128, 256>), dim3(blocks), dim3(256), 0, s, p);
-  else if (head_dim == 64 && rows == 128) hipLaunchKernelGGL((verify_merge_kernel<64, 128>), dim3(blocks), dim3(256), 0, s, p);
-  else if (head_dim == 64 && rows == 256) hipLaunchKernelGGL((verify_merge_kernel<64, 256>), dim3(blocks), dim3(256), 0, s, p);
+  const dim3 grid((unsigned)nmerges), block(2 * head_dim);  // one wave per 32 head dims
+  if (head_dim == 128 && rows == 128) hipLaunchKernelGGL((verify_merge_kernel<128, 128>), grid, block, 0, s, p);
+  else if (head_dim == 128 && rows == 256) hipLaunchKernelGGL((verify_merge_kernel<128, 256>), grid, block, 0, s, p);
+  else if (head_dim == 64 && rows == 128) hipLaunchKernelGGL((verify_merge_kernel<64, 128>), grid, block, 0, s, p);
+  else if (head_dim == 64 && rows == 256) hipLaunchKernelGGL((verify_merge_kernel<64, 256>), grid, block, 0, s, p);
   else return hipErrorInvalidValue;
   return hipGetLastError();
 }

@@ -122,8 +122,22 @@ def test_plan_partitions_work(qo, pl, window, page, hq, waves):
     all_slots = [c[2] for v in pre.values() for c in v] + [v[0] for v in suf.values() if v[1] == MODE_PARTIAL]
     assert len(all_slots) == len(set(all_slots)) == info.num_slots
     assert sorted(all_slots) == list(range(info.num_slots))
-    mg = {(m[0], m[1], m[2]): (m[3], m[4], m[5], m[6]) for m in merges.tolist()}
-    assert len(mg) == len(merges)
+    mg = {}
+    for i, m in enumerate(merges.tolist()):
+        if m[4] == 0:          # padding
+            continue
+        key = (m[0], m[1], m[2])
+        assert m[7] not in mg.setdefault(key, {})
+        mg[key][m[7]] = (m[3], m[4], m[5], m[6], i % 8)
+    # every item of a group runs on one XCD (workgroup index % 8) and so do
+    # its merge workgroups, when there are at least 8 (request, kv head) pairs
+    xcd_of = {}
+    for i, it in enumerate(items.tolist()):
+        if it[MODE] != MODE_NOOP:
+            xcd_of.setdefault((it[REQ], it[KVH], it[QT]), set()).add(i % 8)
+    heads = sum(hkv for r in range(len(pl)) if qo[r + 1] > qo[r])
+    if heads >= 8:
+        assert all(len(v) == 1 for v in xcd_of.values())
     for r in range(len(pl)):
         n = qo[r + 1] - qo[r]
         L = pl[r]
@@ -142,7 +156,12 @@ def test_plan_partitions_work(qo, pl, window, page, hq, waves):
                 s0 = ch[0][2]
                 assert [c[2] for c in ch] == list(range(s0, s0 + len(ch)))
                 assert suf[key] == (s0 + len(ch), MODE_PARTIAL)
-                assert mg[key] == (s0, len(ch) + 1, qo[r], n)
+                blks = [b for b in range(rows // 32) if qt * rows + b * 32 < n * g]
+                assert sorted(mg[key]) == blks
+                for b in blks:
+                    assert mg[key][b][:4] == (s0, len(ch) + 1, qo[r], n)
+                    if heads >= 8:
+                        assert {mg[key][b][4]} == xcd_of[key]
                 assert len(ch) <= 15
                 if page:
                     for a, b, _ in ch:
@@ -166,15 +185,19 @@ def test_plan_contiguous_token_offsets():
 
 
 def test_plan_xcd_grouping():
-    """Items reading the same keys sit on one XCD (work index % 8)."""
-    info, items, _ = _plan([0, 150, 200], [4096, 3000])
-    xcd = {}
-    for i, w in enumerate(items.tolist()):
-        if w[MODE] == MODE_NOOP:
-            continue
-        key = (w[SRC], w[REQ], w[KVH], w[KB])
-        xcd.setdefault(key, set()).add(i % 8)
-    assert all(len(s) == 1 for s in xcd.values())
+    """Items reading the same keys sit on one XCD (work index % 8): with at
+    least 8 (request, kv head) pairs, everything of one pair; otherwise every
+    key chunk with all the q-tiles that read it."""
+    for qo, pl, hkv, key_fn in (([0, 150, 200], [4096, 3000], 8, lambda w: (w[REQ], w[KVH])),
+                                ([0, 150], [4096], 4, lambda w: (w[SRC], w[REQ], w[KVH], w[KB]))):
+        info, items, _ = _plan(qo, pl, hq=8 * hkv, hkv=hkv)
+        xcd = {}
+        for i, w in enumerate(items.tolist()):
+            if w[MODE] == MODE_NOOP:
+                continue
+            xcd.setdefault(key_fn(w), set()).add(i % 8)
+        assert all(len(s) == 1 for s in xcd.values())
+        assert len({x for s in xcd.values() for x in s}) == 8   # all XCDs used
 
 
 def test_plan_rejects_bad_input():
