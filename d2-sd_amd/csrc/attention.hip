@@ -285,7 +285,7 @@ __device__ __forceinline__ void attn_dma_body(const AttnParams& p, const WorkIte
   const int ntiles = (kv_end - kv_begin + 63) >> 6;
 
   int mask_mode = MASK_NONE, causal_off = 0;
-  unsigned long long mreg[kMaskRegWords] = {0ull, 0ull, 0ull, 0ull};
+  unsigned long long mreg[kMaskRegWords] = {};
   const unsigned long long* mrow = nullptr;
   if constexpr (MASKED) {
     mask_mode = S.mask_mode;
@@ -415,8 +415,9 @@ __device__ __forceinline__ void attn_dma_body(const AttnParams& p, const WorkIte
       if constexpr (MASKED) {
         if (mask_mode == MASK_TREE) {
           const int wi = kb >> 6;
-          mw = wi == 0 ? mreg[0] : wi == 1 ? mreg[1] : wi == 2 ? mreg[2] : wi == 3 ? mreg[3]
-                                                                                  : (mrow ? mrow[wi] : 0ull);
+          mw = (wi >= kMaskRegWords && mrow) ? mrow[wi] : 0ull;
+#pragma unroll
+          for (int k = 0; k < kMaskRegWords; ++k) mw = (wi == k) ? mreg[k] : mw;
           if (!rvalid) mw = 0ull;
         }
       }

@@ -7,7 +7,20 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 namespace d2sd {
+
+// f(std::integral_constant<int, 0>{}), ..., f(std::integral_constant<int, N-1>{})
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 typedef __bf16 bf16_t;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -24,8 +37,9 @@ constexpr float kLn2 = 0.6931471805599453f;
 // Lazy rescaling: the running max used for exponentiation may trail the true
 // row max by up to 2^kRescaleSlack before O and l are rescaled.
 constexpr float kRescaleSlack = 8.0f;
-// Tree-mask words held in registers per row (rows of up to 256 nodes).
-constexpr int kMaskRegWords = 4;
+// Tree-mask words held in registers per row (rows of up to 128 nodes); later
+// words are read from the (cached) mask row when their tile comes up.
+constexpr int kMaskRegWords = 2;
 
 __device__ __forceinline__ bf16x8 zero_bf16x8() {
   u32x4 z = {0u, 0u, 0u, 0u};
@@ -109,10 +123,21 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 // XOR swizzle of 16-byte chunks in a key row (row pitch 256 B for D = 128,
-// 128 B for D = 64): 16 consecutive rows map one chunk to 16 distinct banks.
+// 128 B for D = 64), chosen so that both LDS read patterns of a tile are free
+// of bank conflicts (LDS serves 256 bytes per pass):
+//  * K fragments, ds_read_b128: 16 lanes read one logical chunk of 16
+//    consecutive rows -> the swizzle is a bijection over any 16 aligned rows
+//    (for D = 64, over the 8 rows of each parity, which share a 256-byte line
+//    pair position);
+//  * V^T fragments, ds_read_b64_tr_b16: 32 lanes read 4 consecutive logical
+//    chunks (4m .. 4m+3) of 4 consecutive rows 4a .. 4a+3 -> those rows'
+//    swizzles differ in the bits above the low two (bits 2-3 for D = 128,
+//    bit 2 between rows of equal parity for D = 64).
+// The plain `chunk ^ row` swizzle satisfies only the first and leaves the
+// transposed reads 4-way conflicted (measured: 63 vs 185 B/clk per CU).
 template <int D>
 __device__ __forceinline__ int chunk_swizzle(int row) {
-  return D == 128 ? (row & 15) : ((row >> 1) & 7);
+  return D == 128 ? (((row & 3) << 2) | ((row >> 2) & 3)) : ((((row >> 1) & 1) << 2) | ((row >> 2) & 3));
 }
 
 }  // namespace d2sd

@@ -141,8 +141,10 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
     }
   }
   auto tile_word = [&](int rb, int wi) -> unsigned long long {
-    return wi == 0 ? mreg[rb][0] : wi == 1 ? mreg[rb][1] : wi == 2 ? mreg[rb][2] : wi == 3 ? mreg[rb][3]
-                                                                    : (mrow[rb] ? mrow[rb][wi] : 0ull);
+    unsigned long long m = (wi >= kMaskRegWords && mrow[rb]) ? mrow[rb][wi] : 0ull;
+#pragma unroll
+    for (int k = 0; k < kMaskRegWords; ++k) m = (wi == k) ? mreg[rb][k] : m;
+    return m;
   };
 
   // ---- source addressing (bytes; the kv head is folded into the bases) ----
@@ -185,6 +187,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
   }
   const float c = p.sm_scale_log2 * kscale;  // raw score -> log2 domain
   const float cn = p.sm_scale * kscale;      // raw score -> natural domain
+  const float slack_raw = c > 0.f ? kRescaleSlack / c : 0.f;  // kRescaleSlack in raw-score units
 
   // Complete the Q / mask / page-id loads here, visibly to the compiler:
   // otherwise it keeps them pending into the tile loop and waits vmcnt(0)
@@ -238,20 +241,14 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
   auto compute_tile = [&](int kb, auto&& kfrag, auto&& vfrag, auto masked_tile) {
     f32x16 s[RB][2];
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s[rb][0][r] = 0.f;
-        s[rb][1][r] = 0.f;
-      }
-#pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const bf16x8 a0 = kfrag(0, ks);
       const bf16x8 a1 = kfrag(1, ks);
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
-        s[rb][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[rb][ks], s[rb][0], 0, 0, 0);
-        s[rb][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[rb][ks], s[rb][1], 0, 0, 0);
+        // the first step starts from a zero accumulator (inline constant)
+        s[rb][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[rb][ks], ks == 0 ? f32x16{} : s[rb][0], 0, 0, 0);
+        s[rb][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[rb][ks], ks == 0 ? f32x16{} : s[rb][1], 0, 0, 0);
       }
     }
 
@@ -283,36 +280,42 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
       }
     }
 
-    // online softmax (lane-local row, partner lane l^32); P^T packed to bf16
+    // online softmax (lane-local row, partner lane l^32); P^T packed to bf16.
+    // The running max m_run lags the true row max by up to kRescaleSlack
+    // (log2 units) before O and l are rescaled, so the rescale branch is rare.
+    // The row sum l adds the fp32 probabilities: a sum of the bf16-rounded P
+    // would be off by up to 2^-9 relative for rows that see only a few keys
+    // (tree rows near the root), beyond the LSE tolerance.
     bf16x8 pb[RB][4];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
-      // row max: 16 three-input maxima over four independent chains
-      float m4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+      // row max: three-input maxima over four independent chains
+      float m4[4] = {s[rb][0][0], s[rb][0][1], s[rb][0][2], s[rb][0][3]};
 #pragma unroll
-      for (int r = 0; r < 16; ++r) m4[r & 3] = fmaxf(fmaxf(m4[r & 3], s[rb][0][r]), s[rb][1][r]);
+      for (int r = 4; r < 16; ++r) m4[r & 3] = fmaxf(m4[r & 3], s[rb][0][r]);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) m4[r & 3] = fmaxf(m4[r & 3], s[rb][1][r]);
       float mx = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
       mx = fmaxf(mx, xor32(mx, hh));
-      const bool grow = (mx > m_run[rb]) && ((m_run[rb] == -INFINITY) || (mx - m_run[rb]) * c > kRescaleSlack);
-      if (__any(grow)) {
-        const float m_new = grow ? mx : m_run[rb];
-        const float alpha = (m_run[rb] == -INFINITY) ? 0.f : exp2f((m_run[rb] - m_new) * c);
+      // grow iff mx exceeds m_run by more than the slack (always when m_run is
+      // -inf and mx finite; never when the row sees nothing yet)
+      if (__any(mx > m_run[rb] + slack_raw)) {
+        const float m_new = fmaxf(m_run[rb], mx);
+        const float alpha = (m_run[rb] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((m_run[rb] - m_new) * c);
         l_run[rb] *= alpha;
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) o[rb][mt][r] *= alpha;
+        for (int mt = 0; mt < MT; ++mt) o[rb][mt] *= alpha;
         m_run[rb] = m_new;
       }
       const float mc = (m_run[rb] == -INFINITY) ? 0.f : m_run[rb] * c;
-      float lsum = 0.f;
+      float ls[4] = {0.f, 0.f, 0.f, 0.f};  // four independent add chains
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         s[rb][0][r] = __builtin_amdgcn_exp2f(fmaf(s[rb][0][r], c, -mc));
         s[rb][1][r] = __builtin_amdgcn_exp2f(fmaf(s[rb][1][r], c, -mc));
-        lsum += s[rb][0][r] + s[rb][1][r];
+        ls[r & 3] += s[rb][0][r] + s[rb][1][r];
       }
-      l_run[rb] += lsum;
+      l_run[rb] += (ls[0] + ls[1]) + (ls[2] + ls[3]);
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const f32x16& sv = s[rb][ks >> 1];
@@ -353,17 +356,17 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
     const unsigned ring_lds = __builtin_amdgcn_readfirstlane(lds_address(&sm.ring[0][0][0]));
     // Per-lane part of the source offset of DMA instruction i: key row
     // lrow of its RPI-row group, stored chunk cs holding global chunk
-    // cs ^ swizzle(row).  Full tiles of an item whose key range starts on a
-    // 64-key boundary (and, paged, whose pages hold whole row groups) add a
-    // wave-uniform base per instruction: the row group's page and row.
-    // A wave's instructions cover WROWS consecutive key rows of a tile; on the
-    // fast path (paged) they lie in at most two pages, and the in-page row of
-    // every instruction is a per-lane constant.
+    // cs ^ swizzle(row).  A wave's instructions cover WROWS consecutive key
+    // rows of a tile.  Fast path: full tiles of an item whose key range starts
+    // on a 64-key boundary and, paged, whose pages hold 16..64 keys, at least
+    // WROWS: the wave's rows then lie in one page at a fixed in-page row, so
+    // one wave-uniform base per tile (page id * page bytes, a 32 x 32 -> 64-bit
+    // scalar multiply) plus this per-lane constant addresses every DMA.
     constexpr int WROWS = IPW * RPI;
     const int lrow = lane / CH, cs = lane % CH;
     const int P = 1 << log2p;
     const bool fast = (kv_begin & 63) == 0 && tok_b < (1ll << 26) &&
-                      (!PAGED || (P >= RPI && P <= 64 && 2 * P >= WROWS));
+                      (!PAGED || (P >= WROWS && P <= 64 && page_b < (1ll << 32)));
     unsigned lane_off[IPW];
 #pragma unroll
     for (int i = 0; i < IPW; ++i) {
@@ -371,42 +374,36 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
       const int row_in_src = PAGED ? (r0 & pmask) : r0;
       lane_off[i] = (unsigned)((row_in_src + lrow) * tok_b) + (unsigned)((cs ^ chunk_swizzle<D>(r0 + lrow)) * 16);
     }
-    // Page ids of the (at most two) pages of this wave's rows of tile `it`,
-    // read from the staged list one step before the tile is issued.
-    auto wave_pages = [&](int it) -> int2 {
-      int2 r = {0, 0};
+    // Page id of this wave's rows of tile `it` (fast path), read from the
+    // staged list one step before the tile is issued.
+    auto wave_page = [&](int it) -> int {
       if constexpr (PAGED) {
-        const int kb = kv_begin + it * 64;
-        const int s0 = min(((kb + wv * WROWS) >> log2p) - pg_first, kMaxStagedPages - 1);
-        const int s1 = min(((kb + wv * WROWS + WROWS - 1) >> log2p) - pg_first, kMaxStagedPages - 1);
-        r.x = sm.pages[max(s0, 0)];
-        r.y = sm.pages[max(s1, 0)];
+        const int s0 = min(((kv_begin + it * 64 + wv * WROWS) >> log2p) - pg_first, kMaxStagedPages - 1);
+        return sm.pages[max(s0, 0)];
       }
-      return r;
+      return 0;
     };
 
     // DMA of tile `it` into ring stage it % STAGES.  Keys past kv_end (tail
     // tile only) load the last valid key: finite data whose scores the tail
     // mask removes.
-    auto issue = [&](int it, int2 pg) {
+    auto issue = [&](int it, int pg) {
       const int kb = kv_begin + it * 64;
       const unsigned kst = ring_lds + (it % STAGES) * STAGE_BYTES;
       const unsigned vst = kst + 64 * D * 2;
       if (fast && kb + 64 <= kv_end) {
-        long long o0, o1;
-        if constexpr (PAGED) {
-          o0 = (long long)__builtin_amdgcn_readfirstlane(pg.x) * page_b;
-          o1 = (long long)__builtin_amdgcn_readfirstlane(pg.y) * page_b;
-        } else {
-          o0 = o1 = (long long)kb * tok_b;
-        }
+        unsigned long long ub;
+        if constexpr (PAGED)
+          ub = (unsigned long long)(unsigned)__builtin_amdgcn_readfirstlane(pg) * (unsigned)page_b;
+        else
+          ub = (unsigned long long)(unsigned)kb * (unsigned)tok_b;
+        const char* kb_ = kbase + ub;
+        const char* vb_ = vbase + ub;
 #pragma unroll
         for (int i = 0; i < IPW; ++i) {
           const int inst = wv * IPW + i;
-          const bool second = PAGED && (((inst * RPI) >> log2p) != ((wv * WROWS) >> log2p));
-          const long long ub = second ? o1 : o0;
-          dma16s(kbase + ub, lane_off[i], kst + inst * 1024);
-          dma16s(vbase + ub, lane_off[i], vst + inst * 1024);
+          dma16s(kb_, lane_off[i], kst + inst * 1024);
+          dma16s(vb_, lane_off[i], vst + inst * 1024);
         }
       } else {
 #pragma unroll
@@ -420,11 +417,11 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
       }
     };
 
-    // LDS byte offsets (inside a stage) of this lane's fragments.  K: key row
-    // l32 (+32 for kt = 1), chunk (2ks + hh) ^ swizzle.  V^T for
-    // ds_read_b64_tr_b16: lane k of a 16-lane group G names key row
-    // 4*hh + k/4 (+8 for the second read, +16ks) and head dims
-    // 16*(G&1) + 4*(k&3) .. +3 of the 32-wide block mt.
+    // LDS byte offsets (inside a stage) of this lane's fragments; the
+    // key-row / head-dim steps are immediate offsets.  K: key row l32 (+32 for
+    // kt = 1), chunk (2ks + hh) ^ swizzle.  V^T for ds_read_b64_tr_b16: lane k
+    // of a 16-lane group G names key row 4*hh + k/4 (+8 for the second read,
+    // +16ks) and head dims 16*(G&1) + 4*(k&3) .. +3 of the 32-wide block mt.
     unsigned koff[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) koff[ks] = (l32 * D + 8 * ((2 * ks + hh) ^ chunk_swizzle<D>(l32))) * 2;
@@ -442,8 +439,8 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
 
 #pragma unroll
     for (int t = 0; t < STAGES - 1; ++t)
-      if (t < ntiles) issue(t, wave_pages(t));
-    int2 pnext = wave_pages(STAGES - 1);
+      if (t < ntiles) issue(t, wave_page(t));
+    int pnext = wave_page(STAGES - 1);
 
     // One step of the ring: wait for tile `it`, refill the stage freed by
     // tile it-1, compute tile `it` (masked or not, as the tag says).
@@ -459,7 +456,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
       __builtin_amdgcn_s_barrier();
       __asm__ volatile("" ::: "memory");
       if (it + STAGES - 1 < ntiles) issue(it + STAGES - 1, pnext);
-      pnext = wave_pages(it + STAGES);
+      pnext = wave_page(it + STAGES);
 
       const int kb = kv_begin + it * 64;
       if (!live || !tile_visible(kb)) return;
@@ -469,23 +466,21 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
       };
       auto vfrag = [&](int mt, int ks) -> bf16x8 {
         typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(st + voff0[mt] + ks * 16 * D * 2));
-        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(st + voff1[mt] + ks * 16 * D * 2));
+        const lds_char* p0 = st + voff0[mt] + ks * 16 * D * 2;
+        const lds_char* p1 = st + voff1[mt] + ks * 16 * D * 2;
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p0);
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p1);
         const u32x2 ulo = __builtin_bit_cast(u32x2, lo), uhi = __builtin_bit_cast(u32x2, hi);
         return __builtin_bit_cast(bf16x8, (u32x4){ulo[0], ulo[1], uhi[0], uhi[1]});
       };
       compute_tile(kb, kfrag, vfrag, masked_tile);
     };
-
-    if constexpr (MASKED) {
-      for (int it = 0; it < ntiles; ++it) step(it, std::true_type{});
-    } else {
-      // full prefix tiles carry no mask code; the partial tail tile (if any)
-      // is peeled off the loop
-      const int nfull = (kv_end - kv_begin) >> 6;
-      for (int it = 0; it < nfull; ++it) step(it, std::false_type{});
-      if (nfull < ntiles) step(nfull, std::true_type{});
-    }
+    // Full tiles carry no mask code (prefix level); the suffix level masks
+    // every tile; the partial tail tile (if any) is peeled off the loop.
+    using full_tag = std::integral_constant<bool, MASKED>;
+    const int nfull = MASKED ? ntiles : (kv_end - kv_begin) >> 6;
+    for (int it = 0; it < nfull; ++it) step(it, full_tag{});
+    if (nfull < ntiles) step(nfull, std::true_type{});
   } else {
     // ============ register-staged tiles (fp8 e4m3fn -> bf16 in LDS) ============
     constexpr int KP = D + 8;          // K tile pitch (elements)
