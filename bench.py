@@ -269,13 +269,16 @@ def main() -> int:
     with g_attn.capture():
         for i in range(len(mp.layers)):
             layer_call(i, attn.run_attention)
-    g_merge = d2sd.HipGraph()
-    with g_merge.capture():
-        for i in range(len(mp.layers)):
-            layer_call(i, attn.run_merge)
+    fused = bool(info.merge_in_attention)
+    g_merge = None
+    if not fused:
+        g_merge = d2sd.HipGraph()
+        with g_merge.capture():
+            for i in range(len(mp.layers)):
+                layer_call(i, attn.run_merge)
     log(f"plan: attention {info.num_items} workgroups x {info.waves_per_block} waves "
         f"({info.rows_per_tile} rows each), {info.max_splits_used} prefix splits, {info.num_slots} partial "
-        f"slots, {info.num_merges} merge groups")
+        f"slots, " + ("merged by each group's last producer" if fused else f"{info.num_merges} merge groups"))
 
     for _ in range(args.warmup):
         step.replay()
@@ -294,7 +297,7 @@ def main() -> int:
 
     # per-kernel averages (graphs of the 36 launches of one kernel)
     attn_us = time_graph(g_attn, args.kernel_reps, torch) * 1000.0 / len(mp.layers)
-    merge_us = time_graph(g_merge, args.kernel_reps, torch) * 1000.0 / len(mp.layers)
+    merge_us = time_graph(g_merge, args.kernel_reps, torch) * 1000.0 / len(mp.layers) if g_merge else 0.0
     log(f"attention kernel {attn_us:.3f} us/launch, merge kernel {merge_us:.3f} us/launch")
 
     vb, vf = wl.verify_bytes_flops(prob)

@@ -298,6 +298,7 @@ int d2sd_cascade_plan(const d2sd_cascade_plan_desc* desc, int32_t* host_plan, si
   in.max_splits = desc->max_splits;
   in.waves = desc->waves_per_block;
   in.page_size = desc->page_size;
+  in.separate_merge = desc->separate_merge != 0;
   d2sd::VerifyPlanOutput out{};
   d2sd::plan_verify(in, out);
   static_assert(sizeof(d2sd::VerifyItem) == 16 * sizeof(int32_t), "VerifyItem layout");
@@ -317,6 +318,9 @@ int d2sd_cascade_plan(const d2sd_cascade_plan_desc* desc, int32_t* host_plan, si
   info->head_dim = desc->head_dim;
   info->kv_dtype = desc->kv_dtype;
   info->page_size = desc->page_size;
+  info->num_groups = out.num_groups;
+  info->merge_in_attention = out.merge_in_attention ? 1 : 0;
+  info->counters_offset = out.counters_offset;
   if (host_plan) {
     if (host_plan_ints < (size_t)info->plan_ints)
       return fail(D2SD_ERR_WORKSPACE, "cascade_plan: host_plan too small (need " +
@@ -384,6 +388,7 @@ static int build_verify_params(const d2sd_cascade_plan_info* info, const d2sd_ca
   p.part_lse = a->workspace ? (float*)((char*)a->workspace + (long long)info->num_slots * rows * D * 2) : nullptr;
   p.items = (const d2sd::VerifyItem*)a->plan;
   p.merges = (const d2sd::VerifyMerge*)(a->plan + 16 * (long long)info->num_items);
+  p.counters = info->merge_in_attention ? (int*)((char*)a->workspace + info->counters_offset) : nullptr;
   p.sinks = a->sinks;
   p.tree_mask = (const unsigned long long*)a->tree_mask;
   d2sd::VerifySource& pre = p.pre;
@@ -429,6 +434,7 @@ int d2sd_cascade_merge(const d2sd_cascade_plan_info* info, const d2sd_cascade_ru
   g_last_error.clear();
   d2sd::VerifyParams p{};
   if (int rc = build_verify_params(info, a, p)) return rc;
+  if (info->merge_in_attention) return D2SD_OK;  // the attention launch merged
   hipError_t e = d2sd::launch_verify_merge(p, info->head_dim, info->rows_per_tile, info->num_merges,
                                            (hipStream_t)stream);
   return e == hipSuccess ? D2SD_OK : fail_hip(e, "cascade merge launch");

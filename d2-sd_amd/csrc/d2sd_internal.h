@@ -105,7 +105,9 @@ struct VerifyItem {
   int base;              // paged: page_table index of the request's page 0;
                          // contiguous: token offset of the request's key 0
   int causal_off;        // MASK_CAUSAL: key j visible to query i iff j <= i + causal_off
-  int pad[4];
+  int group;             // MODE_PARTIAL: completion counter of the item's (request, kv head, q-tile)
+  int slot0, nprod;      // ... whose nprod partial slots are [slot0, slot0 + nprod)
+  int pad;
 };
 
 // One 32-row block `blk` of a group whose partial slots
@@ -136,6 +138,7 @@ struct VerifyParams {
   float* part_lse;         // [slot][ROWS]
   const VerifyItem* items;
   const VerifyMerge* merges;
+  int* counters;           // [groups] zero between launches; null: partials are merged by verify_merge_kernel
   const float* sinks;      // nullable, [Hq]
   const unsigned long long* tree_mask;  // [total_q][mask_words]
   VerifySource pre, suf;

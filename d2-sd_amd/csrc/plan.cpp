@@ -188,6 +188,9 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
           w.kv_end = std::min(kv1[r], kv0[r] + 64 * (t0 + nt));
           w.slot = slot0[grp0[r] + h * qtiles[r] + qt] + s_;
           w.mode = MODE_PARTIAL;
+          w.group = grp0[r] + h * qtiles[r] + qt;
+          w.slot0 = slot0[w.group];
+          w.nprod = S + 1;
           w.q0 = q0;
           w.nq = nq[r];
           w.base = pbase;
@@ -216,6 +219,9 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
         w.kv_end = nq[r];
         w.slot = S > 0 ? slot0[gi] + S : -1;
         w.mode = S > 0 ? MODE_PARTIAL : MODE_FINAL;
+        w.group = gi;
+        w.slot0 = S > 0 ? slot0[gi] : -1;
+        w.nprod = S + 1;
         w.q0 = q0;
         w.nq = nq[r];
         w.base = q0;  // the request's suffix keys are rows q0.. of k/v_suffix
@@ -258,8 +264,15 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
   out.rows = ROWS;
   out.num_slots = slot;
   out.max_splits_used = max_splits_used;
-  // bf16 partial O + fp32 LSE per (slot, row)
-  out.workspace_bytes = (size_t)slot * ROWS * ((size_t)in.head_dim * 2 + sizeof(float));
+  out.num_groups = grp0[R];
+  out.merge_in_attention = !in.separate_merge && slot > 0;
+  if (out.merge_in_attention) out.merges.clear();
+  // bf16 partial O + fp32 LSE per (slot, row), then one int32 completion
+  // counter per group (16-byte aligned)
+  const size_t part_bytes = (size_t)slot * ROWS * ((size_t)in.head_dim * 2 + sizeof(float));
+  out.counters_offset = (part_bytes + 15) & ~(size_t)15;
+  out.workspace_bytes = out.merge_in_attention ? out.counters_offset + (size_t)out.num_groups * sizeof(int)
+                                               : part_bytes;
   return 0;
 }
 

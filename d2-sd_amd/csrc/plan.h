@@ -23,6 +23,7 @@ struct VerifyPlanInput {
   int max_splits;  // 0: no limit beyond kMaxVerifySplits
   int waves;       // 0: choose; else 2, 4 or 8
   int page_size;   // 0: contiguous prefix
+  bool separate_merge;  // partials merged by the merge launch, not by each group's last producer
 };
 
 struct VerifyPlanOutput {
@@ -32,6 +33,9 @@ struct VerifyPlanOutput {
   int rows;                         // rows per workgroup tile (= per partial slot)
   int num_slots;
   int max_splits_used;
+  int num_groups;                   // (request, kv head, q-tile) groups with split prefixes
+  bool merge_in_attention;
+  size_t counters_offset;           // workspace byte offset of the int32 completion counters
   size_t workspace_bytes;
 };
 

@@ -53,7 +53,12 @@ struct VerifySmem {
     } st;
   };
   int pages[kMaxStagedPages];        // page ids of the workgroup's key range
+  int last;                          // this workgroup is its group's last producer
 };
+
+// Partial slots merged per batch by a group's last producer (all loads of a
+// batch are in flight together).
+constexpr int kMergeBatch = 4;
 
 template <int D>
 __device__ __forceinline__ void store_out(const VerifyParams& p, int qrow, int qh, int hh,
@@ -573,31 +578,107 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
   }
 
   // ---- epilogue: normalise, then a partial slot or the final output ----
+  float lse_r[RB];
+  if (live) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const float l_tot = l_run[rb] + xor32(l_run[rb], hh);
+      const bool nonempty = l_tot > 0.f;
+      const float inv = nonempty ? vscale / l_tot : 0.f;
+      lse_r[rb] = nonempty ? m_run[rb] * cn + logf(l_tot) : -INFINITY;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) o[rb][mt] *= inv;
+      if (w.mode == MODE_PARTIAL) {
+        const int blk = RB * wv + rb;
+        bf16_t* po = (bf16_t*)p.part_o + (long long)w.slot * ROWS * D;
+        float* pl = p.part_lse + (long long)w.slot * ROWS + blk * 32 + l32;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) {
+            const u32x2 val = {pack_bf16x2(o[rb][mt][4 * q4], o[rb][mt][4 * q4 + 1]),
+                               pack_bf16x2(o[rb][mt][4 * q4 + 2], o[rb][mt][4 * q4 + 3])};
+            u32x2* dst = (u32x2*)(po + image_offset<D>(blk, mt, q4, lane));
+            if (p.counters) store_agent(dst, val);
+            else *dst = val;
+          }
+        if (hh == 0) {
+          if (p.counters) store_agent(pl, lse_r[rb]);
+          else *pl = lse_r[rb];
+        }
+      } else if (rv[rb]) {
+        store_out<D>(p, w.q0 + n[rb], qh[rb], hh, o[rb], lse_r[rb]);
+      }
+    }
+  }
+  if (w.mode != MODE_PARTIAL || !p.counters) return;
+
+  // ---- merge in the group's last producer (no waiting: whoever completes
+  // the count does the merge; flashinfer.merge_state_in_place semantics,
+  // generation/verification.py:163-165, and the sink of :173-176) ----
+  wait_vmcnt<0>();  // this wave's partial stores are complete (device-visible)
+  __syncthreads();
+  if (tid == 0)
+    sm.last = __hip_atomic_fetch_add(&p.counters[w.group], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+              w.nprod - 1;
+  __syncthreads();
+  if (!sm.last) return;
+  if (tid == 0) p.counters[w.group] = 0;  // ready for the next launch
   if (!live) return;
+  const long long slot_elems = (long long)ROWS * D;
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
-    const float l_tot = l_run[rb] + xor32(l_run[rb], hh);
-    const bool nonempty = l_tot > 0.f;
-    const float inv = nonempty ? vscale / l_tot : 0.f;
-    const float lse = nonempty ? m_run[rb] * cn + logf(l_tot) : -INFINITY;
+    const int blk = RB * wv + rb;
+    // every slot, this workgroup's own included, in slot order from the
+    // workspace: the result does not depend on which producer came last
+    float mval = -INFINITY, wsum = 0.f;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int mt = 0; mt < MT; ++mt) o[rb][mt] = f32x16{};
+    for (int s0 = 0; s0 < w.nprod; s0 += kMergeBatch) {
+      float ls[kMergeBatch];
+      u32x2 v[kMergeBatch][MT][4];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[rb][mt][r] *= inv;
-    if (w.mode == MODE_PARTIAL) {
-      const int blk = RB * wv + rb;
-      bf16_t* po = (bf16_t*)p.part_o + (long long)w.slot * ROWS * D;
+      for (int b = 0; b < kMergeBatch; ++b) {
+        const int slot = w.slot0 + s0 + b;
+        const bool use = s0 + b < w.nprod;
+        ls[b] = use ? load_agent(p.part_lse + (long long)slot * ROWS + blk * 32 + l32) : -INFINITY;
+        const bf16_t* po = (const bf16_t*)p.part_o + (long long)slot * slot_elems;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4)
-          *(u32x2*)(po + image_offset<D>(blk, mt, q4, lane)) =
-              (u32x2){pack_bf16x2(o[rb][mt][4 * q4], o[rb][mt][4 * q4 + 1]),
-                      pack_bf16x2(o[rb][mt][4 * q4 + 2], o[rb][mt][4 * q4 + 3])};
-      if (hh == 0) p.part_lse[(long long)w.slot * ROWS + blk * 32 + l32] = lse;
-    } else if (rv[rb]) {
-      store_out<D>(p, w.q0 + n[rb], qh[rb], hh, o[rb], lse);
+          for (int q4 = 0; q4 < 4; ++q4)
+            v[b][mt][q4] = use ? load_agent((const u32x2*)(po + image_offset<D>(blk, mt, q4, lane))) : (u32x2){0u, 0u};
+      }
+      float bm = -INFINITY;
+#pragma unroll
+      for (int b = 0; b < kMergeBatch; ++b) bm = fmaxf(bm, ls[b]);
+      const float nm = fmaxf(mval, bm);
+      if (nm == -INFINITY) continue;  // nothing visible so far
+      const float f = mval == -INFINITY ? 0.f : __expf(mval - nm);  // 1 when the max holds
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) o[rb][mt] *= f;
+      wsum *= f;
+#pragma unroll
+      for (int b = 0; b < kMergeBatch; ++b) {
+        const float wt = ls[b] == -INFINITY ? 0.f : __expf(ls[b] - nm);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) {
+            o[rb][mt][4 * q4] += wt * bf16_lo(v[b][mt][q4][0]);
+            o[rb][mt][4 * q4 + 1] += wt * bf16_hi(v[b][mt][q4][0]);
+            o[rb][mt][4 * q4 + 2] += wt * bf16_lo(v[b][mt][q4][1]);
+            o[rb][mt][4 * q4 + 3] += wt * bf16_hi(v[b][mt][q4][1]);
+          }
+        wsum += wt;
+      }
+      mval = nm;
     }
+    const bool nonempty = wsum > 0.f;
+    const float inv = nonempty ? 1.f / wsum : 0.f;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) o[rb][mt] *= inv;
+    if (rv[rb]) store_out<D>(p, w.q0 + n[rb], qh[rb], hh, o[rb], nonempty ? mval + logf(wsum) : -INFINITY);
   }
 }
 

@@ -52,6 +52,7 @@ class PlanDesc(C.Structure):
         ("num_cus", C.c_int),
         ("max_splits", C.c_int),
         ("waves_per_block", C.c_int),
+        ("separate_merge", C.c_int),
     ]
 
 
@@ -71,6 +72,9 @@ class PlanInfo(C.Structure):
         ("head_dim", C.c_int),
         ("kv_dtype", C.c_int),
         ("page_size", C.c_int),
+        ("num_groups", C.c_int),
+        ("merge_in_attention", C.c_int),
+        ("counters_offset", C.c_size_t),
     ]
 
 

@@ -67,6 +67,7 @@ class CascadeVerifyAttention:
         max_splits: int = 0,
         waves_per_block: int = 0,
         num_cus: int = 0,
+        separate_merge: bool = True,
     ) -> "CascadeVerifyAttention":
         """Plan one verify call.
 
@@ -121,6 +122,7 @@ class CascadeVerifyAttention:
         desc.num_cus = num_cus
         desc.max_splits = max_splits
         desc.waves_per_block = waves_per_block
+        desc.separate_merge = 1 if separate_merge else 0
         info = _lib.PlanInfo()
         check(lib.d2sd_cascade_plan(C.byref(desc), None, 0, C.byref(info)), "cascade_plan (size)")
         host = np.zeros(max(info.plan_ints, 8), dtype=np.int32)
@@ -131,7 +133,9 @@ class CascadeVerifyAttention:
         self.qo_indptr_host = qo
         self.prefix_len_host = pl
         self.plan_dev = torch.from_numpy(host).to(dev)
-        self.workspace = torch.empty(max(int(info.workspace_bytes), 16), dtype=torch.uint8, device=dev)
+        # zero-filled once: the groups' completion counters at its end start at
+        # 0, and every run leaves them at 0
+        self.workspace = torch.zeros(max(int(info.workspace_bytes), 16), dtype=torch.uint8, device=dev)
         self.mask_mode = _MASK_MODES[mask_mode]
         self.total_q = int(qo[-1])
         if self.mask_mode == _lib.D2SD_MASK_TREE:

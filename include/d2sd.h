@@ -171,6 +171,9 @@ typedef struct {
   int max_splits;      /* 0: default cap */
   int waves_per_block; /* 0 = choose; 2 (64-row waves, 128-row tiles), 4 (32-row
                           waves, 128-row tiles) or 8 (32-row waves, 256-row tiles) */
+  int separate_merge;  /* 1: the merge launch merges the partial states; 0: the
+                          last workgroup to finish a (request, kv head, q-tile)
+                          merges them inside the attention launch */
 } d2sd_cascade_plan_desc;
 
 typedef struct {
@@ -188,6 +191,10 @@ typedef struct {
   int head_dim;
   int kv_dtype;
   int page_size;
+  int num_groups;         /* (request, kv head, q-tile) groups with split prefixes */
+  int merge_in_attention; /* 1: run() is the attention launch alone */
+  size_t counters_offset; /* byte offset of the groups' completion counters in the
+                             workspace (merge_in_attention) */
 } d2sd_cascade_plan_info;
 
 /* Fills host_plan (capacity host_plan_ints int32) with the work list; the

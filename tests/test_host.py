@@ -36,7 +36,7 @@ def test_version_and_error_strings():
 
 
 def _plan(qo, pl, hq=32, hkv=8, d=128, window=-1, num_cus=256, waves=0, max_splits=0, page_size=16,
-          page_indptr=None, tok_indptr=None):
+          page_indptr=None, tok_indptr=None, separate_merge=True):
     desc = _lib.PlanDesc()
     qo = np.asarray(qo, dtype=np.int32)
     pl = np.asarray(pl, dtype=np.int32)
@@ -56,6 +56,7 @@ def _plan(qo, pl, hq=32, hkv=8, d=128, window=-1, num_cus=256, waves=0, max_spli
     desc.num_cus = num_cus
     desc.max_splits = max_splits
     desc.waves_per_block = waves
+    desc.separate_merge = 1 if separate_merge else 0
     info = _lib.PlanInfo()
     assert _lib.lib.d2sd_cascade_plan(C.byref(desc), None, 0, C.byref(info)) == 0, _lib.lib.d2sd_last_error()
     host = np.zeros(max(info.plan_ints, 8), dtype=np.int32)
@@ -71,7 +72,7 @@ def _plan(qo, pl, hq=32, hkv=8, d=128, window=-1, num_cus=256, waves=0, max_spli
 MODE_PARTIAL, MODE_FINAL, MODE_NOOP = 0, 1, 3
 SRC_PREFIX, SRC_SUFFIX = 0, 1
 # VerifyItem fields
-REQ, KVH, QT, SRC, KB, KE, SLOT, MODE, Q0, NQ, BASE, COFF = range(12)
+REQ, KVH, QT, SRC, KB, KE, SLOT, MODE, Q0, NQ, BASE, COFF, GROUP, SLOT0, NPROD = range(15)
 
 
 @pytest.mark.parametrize("qo,pl,window,page,hq,waves", [
@@ -88,18 +89,30 @@ REQ, KVH, QT, SRC, KB, KE, SLOT, MODE, Q0, NQ, BASE, COFF = range(12)
     ([64 * i for i in range(33)], [8192] * 32, -1, 16, 32, 0),
     ([0, 0, 40], [100, 5000], -1, 16, 32, 0),                       # a request with no queries
 ])
-def test_plan_partitions_work(qo, pl, window, page, hq, waves):
+@pytest.mark.parametrize("separate_merge", [True, False])
+def test_plan_partitions_work(qo, pl, window, page, hq, waves, separate_merge):
     """Every (request, kv head, q-tile) group: prefix items partition its
     visible prefix on 64-key tile boundaries into consecutive slots, one suffix
-    item covers its nodes, and one merge item reads exactly those slots; a
-    group without prefix keys has a FINAL suffix item and no merge."""
+    item covers its nodes, and the group's slots are merged exactly once: by
+    one merge item per 32-row block (separate merge) or by whichever of the
+    group's producers completes its counter (every producer names the same
+    counter, first slot and producer count); a group without prefix keys has a
+    FINAL suffix item and no merge."""
     hkv = 8
     g = hq // hkv
     page_indptr = None
     if page:
         page_indptr = np.concatenate([[0], np.cumsum((np.asarray(pl) + page - 1) // page)])
     info, items, merges = _plan(qo, pl, hq, hkv, 128, window, page_size=page, waves=waves,
-                                page_indptr=page_indptr)
+                                page_indptr=page_indptr, separate_merge=separate_merge)
+    fused = bool(info.merge_in_attention)
+    assert fused == (not separate_merge and info.num_slots > 0)
+    part_bytes = info.num_slots * info.rows_per_tile * (128 * 2 + 4)
+    if fused:
+        assert info.num_merges == 0 and info.counters_offset >= part_bytes and info.counters_offset % 16 == 0
+        assert info.workspace_bytes == info.counters_offset + 4 * info.num_groups
+    else:
+        assert info.workspace_bytes == part_bytes
     rows = info.rows_per_tile
     assert info.waves_per_block in (2, 4, 8)
     assert rows == {2: 128, 4: 128, 8: 256}[info.waves_per_block]
@@ -138,6 +151,7 @@ def test_plan_partitions_work(qo, pl, window, page, hq, waves):
     heads = sum(hkv for r in range(len(pl)) if qo[r + 1] > qo[r])
     if heads >= 8:
         assert all(len(v) == 1 for v in xcd_of.values())
+    groups_seen = set()
     for r in range(len(pl)):
         n = qo[r + 1] - qo[r]
         L = pl[r]
@@ -156,17 +170,24 @@ def test_plan_partitions_work(qo, pl, window, page, hq, waves):
                 s0 = ch[0][2]
                 assert [c[2] for c in ch] == list(range(s0, s0 + len(ch)))
                 assert suf[key] == (s0 + len(ch), MODE_PARTIAL)
-                blks = [b for b in range(rows // 32) if qt * rows + b * 32 < n * g]
-                assert sorted(mg[key]) == blks
-                for b in blks:
-                    assert mg[key][b][:4] == (s0, len(ch) + 1, qo[r], n)
-                    if heads >= 8:
-                        assert {mg[key][b][4]} == xcd_of[key]
+                if fused:
+                    grp = {(it[GROUP], it[SLOT0], it[NPROD]) for it in live.tolist()
+                           if (it[REQ], it[KVH], it[QT]) == key}
+                    assert len(grp) == 1 and next(iter(grp))[1:] == (s0, len(ch) + 1)
+                    gid = next(iter(grp))[0]
+                    assert 0 <= gid < info.num_groups and gid not in groups_seen
+                    groups_seen.add(gid)
+                else:
+                    blks = [b for b in range(rows // 32) if qt * rows + b * 32 < n * g]
+                    assert sorted(mg[key]) == blks
+                    for b in blks:
+                        assert mg[key][b][:4] == (s0, len(ch) + 1, qo[r], n)
+                        if heads >= 8:
+                            assert {mg[key][b][4]} == xcd_of[key]
                 assert len(ch) <= 15
                 if page:
                     for a, b, _ in ch:
                         assert (b - 1) // page - a // page + 1 <= 1024
-    assert info.workspace_bytes == info.num_slots * rows * (128 * 2 + 4)
 
 
 def test_plan_fills_the_device_once():
