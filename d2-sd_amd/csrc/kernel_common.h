@@ -99,14 +99,21 @@ __device__ __forceinline__ void dma16(const void* src, unsigned lds_addr) {
 }
 
 // The same with a wave-uniform base: lane l copies 16 bytes from
-// sbase + voff (voff per lane).
+// sbase + voff (voff per lane).  sbase and lds_addr must be wave-uniform;
+// they are moved to scalar registers here (free when the compiler already
+// holds them there).
 __device__ __forceinline__ void dma16s(const void* sbase, unsigned voff, unsigned lds_addr) {
+  // (readfirstlane returns int: widen through unsigned, never sign-extend)
+  const unsigned long long b = (unsigned long long)sbase;
+  const unsigned hi = (unsigned)__builtin_amdgcn_readfirstlane((unsigned)(b >> 32));
+  const unsigned lo = (unsigned)__builtin_amdgcn_readfirstlane((unsigned)b);
+  const unsigned long long sb = ((unsigned long long)hi << 32) | (unsigned long long)lo;
   __asm__ volatile(
       "s_mov_b32 m0, %0\n\t"
       "s_nop 0\n\t"
       "global_load_lds_dwordx4 %1, %2"
       :
-      : "s"(lds_addr), "v"(voff), "s"(sbase)
+      : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voff), "s"((const void*)sb)
       : "memory", "m0");
 }
 
