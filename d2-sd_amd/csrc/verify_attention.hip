@@ -29,9 +29,10 @@
 // ds_read_b64_tr_b16 from the row-major V tile in the key order the P^T
 // registers hold.
 //
-// Key tiles reach LDS by global_load_lds_dwordx4 (bf16 sources) into a ring of
-// STAGES tiles, or, for an fp8 prefix, through registers where e4m3fn is
-// expanded to bf16 (V stored transposed with permuted key slots).
+// Key tiles reach LDS by global_load_lds_dwordx4 (bf16 sources) into separate
+// K and V rings (K tiles issued one step further ahead than V, since S = K.Q^T
+// comes first in a tile), or, for an fp8 prefix, through registers where
+// e4m3fn is expanded to bf16 (V stored transposed with permuted key slots).
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -43,18 +44,53 @@
 
 namespace d2sd {
 
-template <int D, int STAGES>
+// Direct-to-LDS rings of one workgroup: KST K tiles and VST = KST - 1 V tiles
+// (64 keys x D, chunk-swizzled rows), so that K tiles are issued two steps
+// ahead and V tiles one; NPG staged page ids (0: page ids come from scalar
+// loads of the page table).  Sized to the LDS share of a workgroup: 160 KB
+// per CU, two workgroups per CU for 4-wave tiles, one for 8-wave tiles.
+template <int D, int WPB>
+struct RingCfg;
+template <>
+struct RingCfg<128, 2> { static constexpr int KST = 3, VST = 2, NPG = 0; };  // 80 KB
+template <>
+struct RingCfg<128, 4> { static constexpr int KST = 3, VST = 2, NPG = 0; };  // 80 KB
+template <>
+struct RingCfg<128, 8> { static constexpr int KST = 4, VST = 3, NPG = kMaxStagedPages; };  // 116 KB
+template <>
+struct RingCfg<64, 2> { static constexpr int KST = 5, VST = 4, NPG = kMaxStagedPages; };  // 76 KB
+template <>
+struct RingCfg<64, 4> { static constexpr int KST = 5, VST = 4, NPG = kMaxStagedPages; };  // 76 KB
+template <>
+struct RingCfg<64, 8> { static constexpr int KST = 6, VST = 5, NPG = kMaxStagedPages; };  // 92 KB
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Wzero-length-array"
+template <int D, int KST, int VST, int NPG>
 struct VerifySmem {
   union {
-    bf16_t ring[STAGES][2][64 * D];  // direct-to-LDS tiles: [stage][K, V][key row * D], chunk-swizzled
     struct {
-      bf16_t Ks[2][64 * (D + 8)];    // register-staged K tiles (row pitch D + 8)
-      bf16_t Vt[2][D * (64 + 8)];    // register-staged V^T tiles (row pitch 64 + 8)
+      bf16_t k[KST][64 * D];           // direct-to-LDS K tiles
+      bf16_t v[VST][64 * D];           // direct-to-LDS V tiles
+      int pages[NPG];                  // page ids of the workgroup's key range
+    } ring;
+    struct {
+      bf16_t Ks[2][64 * (D + 8)];      // register-staged K tiles (row pitch D + 8)
+      bf16_t Vt[2][D * (64 + 8)];      // register-staged V^T tiles (row pitch 64 + 8)
+      int pages[kMaxStagedPages];
     } st;
+    int last;                          // after the tile loop: this workgroup is its group's last producer
   };
-  int pages[kMaxStagedPages];        // page ids of the workgroup's key range
-  int last;                          // this workgroup is its group's last producer
 };
+#pragma clang diagnostic pop
+
+// vmcnt <= k * UNIT for a wave-uniform k in [0, MAXK]
+template <int UNIT, int MAXK>
+__device__ __forceinline__ void wait_vmcnt_units(int k) {
+  static_for<MAXK + 1>([&](auto i) {
+    if (k == (int)decltype(i)::value) wait_vmcnt<decltype(i)::value * UNIT>();
+  });
+}
 
 // Partial slots merged per batch by a group's last producer (all loads of a
 // batch are in flight together).
@@ -92,9 +128,9 @@ __device__ __forceinline__ float xor32(float x, int hh) {
 //   MASKED : the suffix level (causal / tree / no mask; else only the
 //            key-range tail is masked)
 //   FP8    : S holds e4m3fn bytes, staged through registers
-template <int D, int W, int RB, int STAGES, bool PAGED, bool MASKED, bool FP8>
+template <int D, int W, int RB, int KST, int VST, int NPG, bool PAGED, bool MASKED, bool FP8>
 __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyItem& w, const VerifySource& S,
-                                            VerifySmem<D, STAGES>& sm) {
+                                            VerifySmem<D, KST, VST, NPG>& sm) {
   constexpr int ROWS = 32 * RB * W;
   constexpr int NT = 64 * W;
   constexpr int MT = D / 32;
@@ -159,6 +195,27 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
   const long long page_b = S.stride_page * ESZ;
   const int log2p = S.log2_page;
   const int pmask = (1 << log2p) - 1;
+  // ---- page ids of the key range: loaded first, so that staging them (and
+  // issuing the first key tiles) waits for these loads only, not for Q ----
+  constexpr int PPT = (kMaxStagedPages + NT - 1) / NT;  // page ids per thread
+  // page ids staged in LDS (else read from the page table by scalar loads)
+  constexpr bool STAGED = PAGED && (FP8 || NPG > 0);
+  int* const pages = FP8 ? sm.st.pages : sm.ring.pages;
+  int pg_first = 0, npg = 0;
+  int pgv[PPT];
+  if constexpr (STAGED) {
+    if (ntiles > 0) {
+      pg_first = kv_begin >> log2p;
+      npg = ((kv_end - 1) >> log2p) - pg_first + 1;  // <= kMaxStagedPages (planner)
+      const int* pt = S.page_table + w.base + pg_first;
+      // unconditional (index clamped into the range) so that the wait before
+      // the LDS stores below counts exactly the loads issued after these
+#pragma unroll
+      for (int j = 0; j < PPT; ++j) pgv[j] = pt[min(tid + j * NT, npg - 1)];
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
   // ---- Q fragments (B operand of S^T = K Q^T): lane holds 8 consecutive
   // head dims at offset 8*hh of every 16-wide k step, for row block rb ----
   bf16x8 qf[RB][KS];
@@ -167,17 +224,18 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
     const bf16_t* qp = (const bf16_t*)p.q + (long long)(w.q0 + n[rb]) * p.q_stride_n +
                        (long long)qh[rb] * p.q_stride_h + 8 * hh;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qf[rb][ks] = rv[rb] ? *(const bf16x8*)(qp + 16 * ks) : zero_bf16x8();
+    // unconditional: rows past the group's end read a valid row (node 0);
+    // their results are never stored or merged
+    for (int ks = 0; ks < KS; ++ks) qf[rb][ks] = *(const bf16x8*)(qp + 16 * ks);
   }
+  __builtin_amdgcn_sched_barrier(0);
 
-  int pg_first = 0;
-  if constexpr (PAGED) {
-    if (ntiles > 0) {
-      pg_first = kv_begin >> log2p;
-      const int npg = ((kv_end - 1) >> log2p) - pg_first + 1;  // <= kMaxStagedPages (planner)
-      const int* pt = S.page_table + w.base + pg_first;
-      for (int i = tid; i < npg; i += NT) sm.pages[i] = pt[i];
-    }
+  if constexpr (STAGED) {
+#pragma unroll
+    for (int j = 0; j < PPT; ++j)
+      if (tid + j * NT < npg) pages[tid + j * NT] = pgv[j];
+  } else if constexpr (PAGED) {
+    if (ntiles > 0) pg_first = kv_begin >> log2p;
   } else {
     const long long off = (long long)w.base * tok_b;
     kbase += off;
@@ -194,15 +252,13 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
   const float cn = p.sm_scale * kscale;      // raw score -> natural domain
   const float slack_raw = c > 0.f ? kRescaleSlack / c : 0.f;  // kRescaleSlack in raw-score units
 
-  // Complete the Q / mask / page-id loads here, visibly to the compiler:
-  // otherwise it keeps them pending into the tile loop and waits vmcnt(0)
-  // there, which would also drain the DMA ring.
-  wait_vmcnt<0>();
-  __syncthreads();  // page ids visible
+  __syncthreads();  // page ids visible (each thread's stores waited for its page-id loads only)
 
   auto tok_off = [&](int t) -> long long {
-    if constexpr (PAGED)
-      return (long long)sm.pages[(t >> log2p) - pg_first] * page_b + (long long)(t & pmask) * tok_b;
+    if constexpr (STAGED)
+      return (long long)pages[(t >> log2p) - pg_first] * page_b + (long long)(t & pmask) * tok_b;
+    else if constexpr (PAGED)
+      return (long long)S.page_table[w.base + (t >> log2p)] * page_b + (long long)(t & pmask) * tok_b;
     else
       return (long long)t * tok_b;
   };
@@ -347,18 +403,20 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
   };
 
   if constexpr (!FP8) {
-    // ================= direct global -> LDS ring (bf16 sources) =================
+    // ================= direct global -> LDS rings (bf16 sources) =================
     constexpr int CH = D / 8;      // 16-byte chunks per key row
     constexpr int RPI = 64 / CH;   // key rows per 1 KB wave instruction
     constexpr int IPT = 64 / RPI;  // instructions per 64-key tile (K or V)
     constexpr int IPW = IPT / W;   // ... per wave
-    constexpr int LPT = 2 * IPW;   // DMA loads per tile per wave (K + V)
-    constexpr int STAGE_BYTES = 2 * 64 * D * 2;
+    constexpr int TB = 64 * D * 2; // bytes of one K or V tile
     static_assert(IPW >= 1 && IPT % W == 0, "tile/wave mismatch");
-    static_assert(STAGES >= 2 && STAGES <= 4, "ring depth");
-    static_assert((STAGES - 1) * LPT < 64, "vmcnt range");
+    static_assert(KST == VST + 1 && VST >= 2, "ring depths");
+    // loads that may still be outstanding when tile `it` has landed (below)
+    constexpr int MAXK = 1 + (VST - 2) + (VST - 2);
+    static_assert(MAXK * IPW < 64, "vmcnt range");
 
-    const unsigned ring_lds = __builtin_amdgcn_readfirstlane(lds_address(&sm.ring[0][0][0]));
+    const unsigned kring = __builtin_amdgcn_readfirstlane(lds_address(&sm.ring.k[0][0]));
+    const unsigned vring = __builtin_amdgcn_readfirstlane(lds_address(&sm.ring.v[0][0]));
     // Per-lane part of the source offset of DMA instruction i: key row
     // lrow of its RPI-row group, stored chunk cs holding global chunk
     // cs ^ swizzle(row).  A wave's instructions cover WROWS consecutive key
@@ -379,50 +437,50 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
       const int row_in_src = PAGED ? (r0 & pmask) : r0;
       lane_off[i] = (unsigned)((row_in_src + lrow) * tok_b) + (unsigned)((cs ^ chunk_swizzle<D>(r0 + lrow)) * 16);
     }
-    // Page id of this wave's rows of tile `it` (fast path), read from the
-    // staged list one step before the tile is issued.
+    // Page id of this wave's rows of tile `it` (fast path; tiles past the
+    // range clamp to its last page), fetched one step before it is needed:
+    // from the staged list, or by a scalar load of the page table.
+    const int last_page = ntiles > 0 ? (kv_end - 1) >> log2p : 0;
     auto wave_page = [&](int it) -> int {
       if constexpr (PAGED) {
-        const int s0 = min(((kv_begin + it * 64 + wv * WROWS) >> log2p) - pg_first, kMaxStagedPages - 1);
-        return sm.pages[max(s0, 0)];
+        const int pi = min((kv_begin + it * 64 + wv * WROWS) >> log2p, last_page);
+        if constexpr (STAGED) {
+          return pages[min(max(pi - pg_first, 0), kMaxStagedPages - 1)];
+        } else {
+          typedef const __attribute__((address_space(4))) int const_int;
+          return ntiles > 0 ? ((const_int*)S.page_table)[w.base + pi] : 0;
+        }
       }
       return 0;
     };
 
-    // DMA of tile `it` into ring stage it % STAGES.  Keys past kv_end (tail
+    // DMA of K (or V) of tile `it` into its ring slot.  Keys past kv_end (tail
     // tile only) load the last valid key: finite data whose scores the tail
     // mask removes.
-    auto issue = [&](int it, int pg) {
+    auto issue = [&](int it, int pg, const char* base, unsigned slot_lds) {
       const int kb = kv_begin + it * 64;
-      const unsigned kst = ring_lds + (it % STAGES) * STAGE_BYTES;
-      const unsigned vst = kst + 64 * D * 2;
       if (fast && kb + 64 <= kv_end) {
         unsigned long long ub;
         if constexpr (PAGED)
           ub = (unsigned long long)(unsigned)__builtin_amdgcn_readfirstlane(pg) * (unsigned)page_b;
         else
           ub = (unsigned long long)(unsigned)kb * (unsigned)tok_b;
-        const char* kb_ = kbase + ub;
-        const char* vb_ = vbase + ub;
+        const char* b_ = base + ub;
 #pragma unroll
-        for (int i = 0; i < IPW; ++i) {
-          const int inst = wv * IPW + i;
-          dma16s(kb_, lane_off[i], kst + inst * 1024);
-          dma16s(vb_, lane_off[i], vst + inst * 1024);
-        }
+        for (int i = 0; i < IPW; ++i) dma16s(b_, lane_off[i], slot_lds + (wv * IPW + i) * 1024);
       } else {
 #pragma unroll
         for (int i = 0; i < IPW; ++i) {
           const int inst = wv * IPW + i;
           const int r = inst * RPI + lrow;
-          const long long off = tok_off(min(kb + r, kv_end - 1)) + (cs ^ chunk_swizzle<D>(r)) * 16;
-          dma16(kbase + off, kst + inst * 1024);
-          dma16(vbase + off, vst + inst * 1024);
+          dma16(base + tok_off(min(kb + r, kv_end - 1)) + (cs ^ chunk_swizzle<D>(r)) * 16, slot_lds + inst * 1024);
         }
       }
     };
+    auto issue_k = [&](int it, int pg) { issue(it, pg, kbase, kring + (it % KST) * TB); };
+    auto issue_v = [&](int it, int pg) { issue(it, pg, vbase, vring + (it % VST) * TB); };
 
-    // LDS byte offsets (inside a stage) of this lane's fragments; the
+    // LDS byte offsets (inside a tile) of this lane's fragments; the
     // key-row / head-dim steps are immediate offsets.  K: key row l32 (+32 for
     // kt = 1), chunk (2ks + hh) ^ swizzle.  V^T for ds_read_b64_tr_b16: lane k
     // of a 16-lane group G names key row 4*hh + k/4 (+8 for the second read,
@@ -437,42 +495,55 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int d = 32 * mt + dsub;
-      voff0[mt] = 64 * D * 2 + (krow * D + 8 * ((d >> 3) ^ chunk_swizzle<D>(krow)) + (d & 7)) * 2;
-      voff1[mt] = 64 * D * 2 + ((krow + 8) * D + 8 * ((d >> 3) ^ chunk_swizzle<D>(krow + 8)) + (d & 7)) * 2;
+      voff0[mt] = (krow * D + 8 * ((d >> 3) ^ chunk_swizzle<D>(krow)) + (d & 7)) * 2;
+      voff1[mt] = ((krow + 8) * D + 8 * ((d >> 3) ^ chunk_swizzle<D>(krow + 8)) + (d & 7)) * 2;
     }
     typedef __attribute__((address_space(3))) char lds_char;
 
-#pragma unroll
-    for (int t = 0; t < STAGES - 1; ++t)
-      if (t < ntiles) issue(t, wave_page(t));
-    int pnext = wave_page(STAGES - 1);
+    // Issue order: step s issues V(s + VST - 1) then K(s + KST - 1); the
+    // prologue plays steps -(KST - 1) .. -1.
+    static_for<KST - 1>([&](auto j) {
+      constexpr int st = decltype(j)::value - (KST - 1);
+      if (st + VST - 1 >= 0 && st + VST - 1 < ntiles) issue_v(st + VST - 1, wave_page(st + VST - 1));
+      if (st + KST - 1 < ntiles) issue_k(st + KST - 1, wave_page(st + KST - 1));
+    });
+    int pk_next = wave_page(KST - 1), pv_next = wave_page(VST - 1);
+    // Complete the Q / mask loads (and the first key tiles, in flight
+    // meanwhile) here, visibly to the compiler: otherwise it keeps them
+    // pending into the tile loop and waits vmcnt(0) there, which would also
+    // drain the DMA rings.
+    wait_vmcnt<0>();
 
-    // One step of the ring: wait for tile `it`, refill the stage freed by
-    // tile it-1, compute tile `it` (masked or not, as the tag says).
+    // One step: wait for tile `it`, refill the K and V slots freed by tile
+    // it-1, compute tile `it` (masked or not, as the tag says).
     auto step = [&](int it, auto masked_tile) {
-      // tile `it` has landed once at most min(STAGES-2, tiles issued after it)
-      // tiles of this wave's DMA are still outstanding; after the barrier every
-      // wave's share is visible and stage (it-1) % STAGES is free.
-      const int ahead = min(STAGES - 2, ntiles - 1 - it);
+      // K(it) was issued before V(it); once V(it) has landed, the only loads
+      // of this wave still outstanding are those issued after it: K(it + 1)
+      // in the same step and the V and K tiles of the VST - 2 later steps
+      // (those tiles that exist).  After the barrier every wave's share is
+      // visible and the slots of tile it-1 are free.
+      const int r = ntiles - 1 - it;
+      const int kout = min(r, 1) + min(r, VST - 2) + max(0, min(r, VST - 1) - 1);
       __asm__ volatile("" ::: "memory");
-      if (ahead >= 2) wait_vmcnt<2 * LPT>();
-      else if (ahead == 1) wait_vmcnt<LPT>();
-      else wait_vmcnt<0>();
+      wait_vmcnt_units<IPW, MAXK>(kout);
       __builtin_amdgcn_s_barrier();
       __asm__ volatile("" ::: "memory");
-      if (it + STAGES - 1 < ntiles) issue(it + STAGES - 1, pnext);
-      pnext = wave_page(it + STAGES);
+      if (it + VST - 1 < ntiles) issue_v(it + VST - 1, pv_next);
+      if (it + KST - 1 < ntiles) issue_k(it + KST - 1, pk_next);
+      pv_next = wave_page(it + VST);
+      pk_next = wave_page(it + KST);
 
       const int kb = kv_begin + it * 64;
       if (!live || !tile_visible(kb)) return;
-      const lds_char* st = (const lds_char*)(uintptr_t)(ring_lds + (it % STAGES) * STAGE_BYTES);
+      const lds_char* kst = (const lds_char*)(uintptr_t)(kring + (it % KST) * TB);
+      const lds_char* vst = (const lds_char*)(uintptr_t)(vring + (it % VST) * TB);
       auto kfrag = [&](int kt, int ks) -> bf16x8 {
-        return *(const __attribute__((address_space(3))) bf16x8*)(st + koff[ks] + kt * 32 * D * 2);
+        return *(const __attribute__((address_space(3))) bf16x8*)(kst + koff[ks] + kt * 32 * D * 2);
       };
       auto vfrag = [&](int mt, int ks) -> bf16x8 {
         typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-        const lds_char* p0 = st + voff0[mt] + ks * 16 * D * 2;
-        const lds_char* p1 = st + voff1[mt] + ks * 16 * D * 2;
+        const lds_char* p0 = vst + voff0[mt] + ks * 16 * D * 2;
+        const lds_char* p1 = vst + voff1[mt] + ks * 16 * D * 2;
         const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p0);
         const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p1);
         const u32x2 ulo = __builtin_bit_cast(u32x2, lo), uhi = __builtin_bit_cast(u32x2, hi);
@@ -488,6 +559,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
     if (nfull < ntiles) step(nfull, std::true_type{});
   } else {
     // ============ register-staged tiles (fp8 e4m3fn -> bf16 in LDS) ============
+    wait_vmcnt<0>();  // Q / mask loads complete, visibly to the compiler (see above)
     constexpr int KP = D + 8;          // K tile pitch (elements)
     constexpr int VP = 64 + 8;         // V^T tile pitch (elements)
     constexpr int KCH = D / 8;         // 8-element chunks per key row
@@ -696,17 +768,18 @@ struct Shape<8> { static constexpr int W = 8, RB = 1, OCC = 2; };
 
 // The prefix level (paged or contiguous, bf16 or fp8) and the suffix level
 // (contiguous bf16, masked) share one launch; the item's src picks the body.
-template <int D, int WPB, int STAGES, bool PAGED, bool FP8>
+template <int D, int WPB, bool PAGED, bool FP8>
 __global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(Shape<WPB>::OCC, Shape<WPB>::OCC)))
 void verify_attn_kernel(const VerifyParams p) {
   constexpr int W = Shape<WPB>::W, RB = Shape<WPB>::RB;
-  __shared__ __attribute__((aligned(16))) VerifySmem<D, STAGES> sm;
+  using R = RingCfg<D, WPB>;
+  __shared__ __attribute__((aligned(16))) VerifySmem<D, R::KST, R::VST, R::NPG> sm;
   const VerifyItem w = p.items[blockIdx.x];
   if (w.mode == MODE_NOOP) return;
   if (w.src == SRC_PREFIX)
-    verify_body<D, W, RB, STAGES, PAGED, false, FP8>(p, w, p.pre, sm);
+    verify_body<D, W, RB, R::KST, R::VST, R::NPG, PAGED, false, FP8>(p, w, p.pre, sm);
   else
-    verify_body<D, W, RB, STAGES, false, true, false>(p, w, p.suf, sm);
+    verify_body<D, W, RB, R::KST, R::VST, R::NPG, false, true, false>(p, w, p.suf, sm);
 }
 
 // ---------------------------------------------------------------------------
@@ -790,17 +863,9 @@ __global__ __launch_bounds__(64 * (D / 32)) void verify_merge_kernel(const Verif
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
-// Ring depth: the LDS budget is 160 KB per CU, shared by the resident
-// workgroups (two for 128-row tiles, one for 256-row tiles).
-template <int D>
-constexpr int verify_stages(int wpb) {
-  return wpb == 8 ? 4 : (D == 128 ? 2 : 4);
-}
-
 template <int D, int WPB, bool PAGED, bool FP8>
 static hipError_t launch_verify_t(const VerifyParams& p, int nitems, hipStream_t s) {
-  constexpr int ST = verify_stages<D>(WPB);
-  hipLaunchKernelGGL((verify_attn_kernel<D, WPB, ST, PAGED, FP8>), dim3(nitems), dim3(64 * WPB), 0, s, p);
+  hipLaunchKernelGGL((verify_attn_kernel<D, WPB, PAGED, FP8>), dim3(nitems), dim3(64 * WPB), 0, s, p);
   return hipGetLastError();
 }
 
