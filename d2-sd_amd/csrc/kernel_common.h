@@ -87,12 +87,14 @@ __device__ __forceinline__ u32x2 fp8x4_to_bf16x4(unsigned w) {
 // does not track these LDS writes: its own tracking waits for every
 // outstanding DMA (vmcnt(0)) before LDS reads, which would drain the whole
 // prefetch ring each tile.  Completion is enforced explicitly (wait_vmcnt +
-// s_barrier).
+// s_barrier).  The loads are non-temporal (nt): a key / value tile is read by
+// the workgroups of one launch at about the same time and never again, so it
+// should not displace the partial states that the merge reads back from L2.
 __device__ __forceinline__ void dma16(const void* src, unsigned lds_addr) {
   __asm__ volatile(
       "s_mov_b32 m0, %0\n\t"
       "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, off"
+      "global_load_lds_dwordx4 %1, off nt"
       :
       : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(src)
       : "memory", "m0");
@@ -111,7 +113,7 @@ __device__ __forceinline__ void dma16s(const void* sbase, unsigned voff, unsigne
   __asm__ volatile(
       "s_mov_b32 m0, %0\n\t"
       "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, %2"
+      "global_load_lds_dwordx4 %1, %2 nt"
       :
       : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voff), "s"((const void*)sb)
       : "memory", "m0");

@@ -296,26 +296,25 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
     return true;
   };
 
-  // One 64-key tile: QK^T, masking, online softmax, PV.  kfrag(kt, ks) is the
-  // A operand of keys 32kt..32kt+31, head dims 16ks.. (this lane's part);
-  // vfrag(mt, ks) the A operand of head dims 32mt.., keys 16ks.. in P^T order.
-  auto compute_tile = [&](int kb, auto&& kfrag, auto&& vfrag, auto masked_tile) {
-    f32x16 s[RB][2];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const bf16x8 a0 = kfrag(0, ks);
-      const bf16x8 a1 = kfrag(1, ks);
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        // the first step starts from a zero accumulator (inline constant)
-        s[rb][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[rb][ks], ks == 0 ? f32x16{} : s[rb][0], 0, 0, 0);
-        s[rb][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[rb][ks], ks == 0 ? f32x16{} : s[rb][1], 0, 0, 0);
-      }
-    }
+  // Pieces of one 64-key tile.  kfrag(kt, ks) is the A operand of keys
+  // 32kt..32kt+31, head dims 16ks.. (this lane's part); vfrag(mt, ks) the A
+  // operand of head dims 32mt.., keys 16ks.. in P^T order.
 
-    // masking.  vis (bit kk = key kb + kk visible) per row block; register r
-    // of 32-key tile kt holds key 32*kt + 8*(r/4) + 4*hh + r%4, i.e. bit
-    // 8*(r/4) + r%4 of the row's 32-bit half kt shifted down by 4*hh.
+  // S^T += K Q^T over head dims 16ks..16ks+15 (ks == 0 starts from zero)
+  auto qk_ks = [&](f32x16 (&s)[RB][2], auto&& kfrag, int ks) {
+    const bf16x8 a0 = kfrag(0, ks);
+    const bf16x8 a1 = kfrag(1, ks);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      s[rb][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[rb][ks], ks == 0 ? f32x16{} : s[rb][0], 0, 0, 0);
+      s[rb][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[rb][ks], ks == 0 ? f32x16{} : s[rb][1], 0, 0, 0);
+    }
+  };
+
+  // masking.  vis (bit kk = key kb + kk visible) per row block; register r
+  // of 32-key tile kt holds key 32*kt + 8*(r/4) + 4*hh + r%4, i.e. bit
+  // 8*(r/4) + r%4 of the row's 32-bit half kt shifted down by 4*hh.
+  auto mask_scores = [&](f32x16 (&s)[RB][2], int kb, auto masked_tile) {
     if constexpr (decltype(masked_tile)::value) {
       const int rem = kv_end - kb;  // > 0: tile it < ntiles
       const unsigned long long tail = rem >= 64 ? ~0ull : ((1ull << rem) - 1ull);
@@ -340,14 +339,13 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
         }
       }
     }
+  };
 
-    // online softmax (lane-local row, partner lane l^32); P^T packed to bf16.
-    // The running max m_run lags the true row max by up to kRescaleSlack
-    // (log2 units) before O and l are rescaled, so the rescale branch is rare.
-    // The row sum l adds the fp32 probabilities: a sum of the bf16-rounded P
-    // would be off by up to 2^-9 relative for rows that see only a few keys
-    // (tree rows near the root), beyond the LSE tolerance.
-    bf16x8 pb[RB][4];
+  // Online softmax (lane-local row, partner lane l^32).  The running max
+  // m_run lags the true row max by up to kRescaleSlack (log2 units) before O
+  // and l are rescaled, so the rescale branch is rare.  mc = m_run * c is
+  // the exponent offset of the tile's probabilities.
+  auto max_rescale = [&](const f32x16 (&s)[RB][2], float (&mc)[RB]) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       // row max: three-input maxima over four independent chains
@@ -368,38 +366,102 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
         for (int mt = 0; mt < MT; ++mt) o[rb][mt] *= alpha;
         m_run[rb] = m_new;
       }
-      const float mc = (m_run[rb] == -INFINITY) ? 0.f : m_run[rb] * c;
+      mc[rb] = (m_run[rb] == -INFINITY) ? 0.f : m_run[rb] * c;
+    }
+  };
+
+  // P^T (bf16) of keys 16j..16j+15 of row block rb.  The row sum adds the
+  // fp32 probabilities: a sum of the bf16-rounded P would be off by up to
+  // 2^-9 relative for rows that see only a few keys (tree rows near the
+  // root), beyond the LSE tolerance.
+  auto p_chunk = [&](const f32x16 (&s)[RB][2], int rb, int j, float mc_, float (&ls)[4]) -> bf16x8 {
+    const f32x16& sv = s[rb][j >> 1];
+    const int base = 8 * (j & 1);
+    float pv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      pv[i] = __builtin_amdgcn_exp2f(fmaf(sv[base + i], c, -mc_));
+      ls[i & 3] += pv[i];
+    }
+    u32x4 u;
+    u[0] = pack_bf16x2(pv[0], pv[1]);
+    u[1] = pack_bf16x2(pv[2], pv[3]);
+    u[2] = pack_bf16x2(pv[4], pv[5]);
+    u[3] = pack_bf16x2(pv[6], pv[7]);
+    return __builtin_bit_cast(bf16x8, u);
+  };
+
+  // O^T += V^T P^T over keys 16j..16j+15: consecutive MFMAs update
+  // different accumulators
+  auto pv_chunk = [&](auto&& vfrag, const bf16x8 (&pb)[RB][4], int j) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const bf16x8 a = vfrag(mt, j);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+        o[rb][mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[rb][j], o[rb][mt], 0, 0, 0);
+    }
+  };
+
+  // The remaining softmax and PV of a tile whose scores s are final.
+  auto finish_tile = [&](const f32x16 (&s)[RB][2], auto&& vfrag) {
+    float mc[RB];
+    max_rescale(s, mc);
+    bf16x8 pb[RB][4];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
       float ls[4] = {0.f, 0.f, 0.f, 0.f};  // four independent add chains
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s[rb][0][r] = __builtin_amdgcn_exp2f(fmaf(s[rb][0][r], c, -mc));
-        s[rb][1][r] = __builtin_amdgcn_exp2f(fmaf(s[rb][1][r], c, -mc));
-        ls[r & 3] += s[rb][0][r] + s[rb][1][r];
-      }
+      for (int j = 0; j < 4; ++j) pb[rb][j] = p_chunk(s, rb, j, mc[rb], ls);
       l_run[rb] += (ls[0] + ls[1]) + (ls[2] + ls[3]);
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const f32x16& sv = s[rb][ks >> 1];
-        const int base = 8 * (ks & 1);
-        u32x4 u;
-        u[0] = pack_bf16x2(sv[base + 0], sv[base + 1]);
-        u[1] = pack_bf16x2(sv[base + 2], sv[base + 3]);
-        u[2] = pack_bf16x2(sv[base + 4], sv[base + 5]);
-        u[3] = pack_bf16x2(sv[base + 6], sv[base + 7]);
-        pb[rb][ks] = __builtin_bit_cast(bf16x8, u);
-      }
     }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pv_chunk(vfrag, pb, j);
+  };
 
-    // O^T += V^T P^T: consecutive MFMAs update different accumulators
+  // One whole 64-key tile: QK^T, masking, online softmax, PV.
+  auto compute_tile = [&](int kb, auto&& kfrag, auto&& vfrag, auto masked_tile) {
+    f32x16 s[RB][2];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
+    for (int ks = 0; ks < KS; ++ks) qk_ks(s, kfrag, ks);
+    mask_scores(s, kb, masked_tile);
+    finish_tile(s, vfrag);
+  };
+
+  // Software-pipelined tile step (unmasked prefix tiles): the softmax and PV
+  // of the current tile (scores sc) interleaved with QK^T of the next tile
+  // (kfrag_n), which becomes sc.  MFMA and VALU work of one wave then
+  // overlap: the QK^T MFMAs are independent of the softmax.  The 16-key P
+  // chunk j is converted while PV of chunk j-1 runs.
+  auto pipelined_tile = [&](f32x16 (&sc)[RB][2], auto&& kfrag_n, auto&& vfrag) {
+    constexpr int Q1 = KS / 4;  // QK^T k-steps beside the row max
+    f32x16 sn[RB][2];
+    static_for<Q1>([&](auto ks) { qk_ks(sn, kfrag_n, decltype(ks)::value); });
+    float mc[RB];
+    max_rescale(sc, mc);
+    float ls[RB][4];
+    bf16x8 pb[RB][4];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const bf16x8 a = vfrag(mt, ks);
+    for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb)
-          o[rb][mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[rb][ks], o[rb][mt], 0, 0, 0);
-      }
+      for (int i = 0; i < 4; ++i) ls[rb][i] = 0.f;
+    }
+    // QK^T k-steps [Q1 + (j (KS - Q1)) / 4, Q1 + ((j + 1)(KS - Q1)) / 4) go with chunk j
+    static_for<4>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) pb[rb][j] = p_chunk(sc, rb, j, mc[rb], ls[rb]);
+      if constexpr (j > 0) pv_chunk(vfrag, pb, j - 1);
+      constexpr int k0 = Q1 + (j * (KS - Q1)) / 4, k1 = Q1 + ((j + 1) * (KS - Q1)) / 4;
+      static_for<k1 - k0>([&](auto kk) { qk_ks(sn, kfrag_n, k0 + decltype(kk)::value); });
+    });
+    pv_chunk(vfrag, pb, 3);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      l_run[rb] += (ls[rb][0] + ls[rb][1]) + (ls[rb][2] + ls[rb][3]);
+      sc[rb][0] = sn[rb][0];
+      sc[rb][1] = sn[rb][1];
+    }
   };
 
   if constexpr (!FP8) {
@@ -500,47 +562,16 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
     }
     typedef __attribute__((address_space(3))) char lds_char;
 
-    // Issue order: step s issues V(s + VST - 1) then K(s + KST - 1); the
-    // prologue plays steps -(KST - 1) .. -1.
-    static_for<KST - 1>([&](auto j) {
-      constexpr int st = decltype(j)::value - (KST - 1);
-      if (st + VST - 1 >= 0 && st + VST - 1 < ntiles) issue_v(st + VST - 1, wave_page(st + VST - 1));
-      if (st + KST - 1 < ntiles) issue_k(st + KST - 1, wave_page(st + KST - 1));
-    });
-    int pk_next = wave_page(KST - 1), pv_next = wave_page(VST - 1);
-    // Complete the Q / mask loads (and the first key tiles, in flight
-    // meanwhile) here, visibly to the compiler: otherwise it keeps them
-    // pending into the tile loop and waits vmcnt(0) there, which would also
-    // drain the DMA rings.
-    wait_vmcnt<0>();
-
-    // One step: wait for tile `it`, refill the K and V slots freed by tile
-    // it-1, compute tile `it` (masked or not, as the tag says).
-    auto step = [&](int it, auto masked_tile) {
-      // K(it) was issued before V(it); once V(it) has landed, the only loads
-      // of this wave still outstanding are those issued after it: K(it + 1)
-      // in the same step and the V and K tiles of the VST - 2 later steps
-      // (those tiles that exist).  After the barrier every wave's share is
-      // visible and the slots of tile it-1 are free.
-      const int r = ntiles - 1 - it;
-      const int kout = min(r, 1) + min(r, VST - 2) + max(0, min(r, VST - 1) - 1);
-      __asm__ volatile("" ::: "memory");
-      wait_vmcnt_units<IPW, MAXK>(kout);
-      __builtin_amdgcn_s_barrier();
-      __asm__ volatile("" ::: "memory");
-      if (it + VST - 1 < ntiles) issue_v(it + VST - 1, pv_next);
-      if (it + KST - 1 < ntiles) issue_k(it + KST - 1, pk_next);
-      pv_next = wave_page(it + VST);
-      pk_next = wave_page(it + KST);
-
-      const int kb = kv_begin + it * 64;
-      if (!live || !tile_visible(kb)) return;
+    // Fragment readers of the ring slots holding K(it) / V(it).
+    auto kfrag_at = [&](int it) {
       const lds_char* kst = (const lds_char*)(uintptr_t)(kring + (it % KST) * TB);
-      const lds_char* vst = (const lds_char*)(uintptr_t)(vring + (it % VST) * TB);
-      auto kfrag = [&](int kt, int ks) -> bf16x8 {
+      return [&, kst](int kt, int ks) -> bf16x8 {
         return *(const __attribute__((address_space(3))) bf16x8*)(kst + koff[ks] + kt * 32 * D * 2);
       };
-      auto vfrag = [&](int mt, int ks) -> bf16x8 {
+    };
+    auto vfrag_at = [&](int it) {
+      const lds_char* vst = (const lds_char*)(uintptr_t)(vring + (it % VST) * TB);
+      return [&, vst](int mt, int ks) -> bf16x8 {
         typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
         const lds_char* p0 = vst + voff0[mt] + ks * 16 * D * 2;
         const lds_char* p1 = vst + voff1[mt] + ks * 16 * D * 2;
@@ -549,14 +580,100 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
         const u32x2 ulo = __builtin_bit_cast(u32x2, lo), uhi = __builtin_bit_cast(u32x2, hi);
         return __builtin_bit_cast(bf16x8, (u32x4){ulo[0], ulo[1], uhi[0], uhi[1]});
       };
-      compute_tile(kb, kfrag, vfrag, masked_tile);
     };
-    // Full tiles carry no mask code (prefix level); the suffix level masks
-    // every tile; the partial tail tile (if any) is peeled off the loop.
-    using full_tag = std::integral_constant<bool, MASKED>;
-    const int nfull = MASKED ? ntiles : (kv_end - kv_begin) >> 6;
-    for (int it = 0; it < nfull; ++it) step(it, full_tag{});
-    if (nfull < ntiles) step(nfull, std::true_type{});
+
+    if constexpr (!MASKED) {
+      // ---- prefix level: software-pipelined tiles ----
+      // K(j) is read one step before V(j) (QK^T of tile j runs under the
+      // softmax of tile j-1).  Issue order: K(0), K(1), then step s issues
+      // V(s + VST - 1) and K(s + KST); the prologue plays steps
+      // -(VST - 1) .. -1.  Slots: K(j) in j % KST, V(j) in j % VST; step s
+      // refills the slots of K(s) (read in step s-1) and V(s-1).
+      if (0 < ntiles) issue_k(0, wave_page(0));
+      if (1 < ntiles) issue_k(1, wave_page(1));
+      static_for<VST - 1>([&](auto j) {
+        constexpr int st = decltype(j)::value - (VST - 1);
+        if (st + VST - 1 < ntiles) issue_v(st + VST - 1, wave_page(st + VST - 1));
+        if (st + KST < ntiles) issue_k(st + KST, wave_page(st + KST));
+      });
+      int pv_next = wave_page(VST - 1), pk_next = wave_page(KST);
+      // Complete the Q loads and the first tiles here, visibly to the
+      // compiler: otherwise it keeps the Q loads pending into the tile loop
+      // and waits vmcnt(0) there, which would also drain the DMA rings.
+      wait_vmcnt<0>();
+      __builtin_amdgcn_s_barrier();
+      f32x16 sc[RB][2];
+      if (live && ntiles > 0) {
+        auto kf = kfrag_at(0);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) qk_ks(sc, kf, ks);
+      }
+      // Step s: wait until V(s) and K(s + 1) have landed.  V(s) was issued
+      // after K(s + 1); the loads issued after V(s) may stay outstanding:
+      // K(s + 2) and the V / K pairs of the VST - 2 following steps (those
+      // tiles that exist).  The barrier makes every wave's share visible and
+      // frees the slots of K(s) and V(s - 1).
+      auto pstep_wait = [&](int it) {
+        const int r = ntiles - 1 - it;
+        const int kout = (r >= 2 ? 1 : 0) + min(r, VST - 2) + max(0, min(VST - 2, r - 2));
+        __asm__ volatile("" ::: "memory");
+        wait_vmcnt_units<IPW, MAXK>(kout);
+        __builtin_amdgcn_s_barrier();
+        __asm__ volatile("" ::: "memory");
+        if (it + VST - 1 < ntiles) issue_v(it + VST - 1, pv_next);
+        if (it + KST < ntiles) issue_k(it + KST, pk_next);
+        pv_next = wave_page(it + VST);
+        pk_next = wave_page(it + KST + 1);
+      };
+      for (int it = 0; it + 1 < ntiles; ++it) {
+        pstep_wait(it);
+        if (live) pipelined_tile(sc, kfrag_at(it + 1), vfrag_at(it));
+      }
+      if (ntiles > 0) {
+        // last tile: keys past kv_end (a partial tile) are masked
+        pstep_wait(ntiles - 1);
+        if (live) {
+          mask_scores(sc, kv_begin + (ntiles - 1) * 64, std::true_type{});
+          finish_tile(sc, vfrag_at(ntiles - 1));
+        }
+      }
+    } else {
+      // ---- suffix level: masked tiles, skipped where no row sees a key ----
+      // Issue order: step s issues V(s + VST - 1) then K(s + KST - 1); the
+      // prologue plays steps -(KST - 1) .. -1.
+      static_for<KST - 1>([&](auto j) {
+        constexpr int st = decltype(j)::value - (KST - 1);
+        if (st + VST - 1 >= 0 && st + VST - 1 < ntiles) issue_v(st + VST - 1, wave_page(st + VST - 1));
+        if (st + KST - 1 < ntiles) issue_k(st + KST - 1, wave_page(st + KST - 1));
+      });
+      int pk_next = wave_page(KST - 1), pv_next = wave_page(VST - 1);
+      wait_vmcnt<0>();  // Q / mask loads and the first tiles (see above)
+
+      // One step: wait for tile `it`, refill the K and V slots freed by tile
+      // it-1, compute tile `it`.
+      auto step = [&](int it) {
+        // K(it) was issued before V(it); once V(it) has landed, the only loads
+        // of this wave still outstanding are those issued after it: K(it + 1)
+        // in the same step and the V and K tiles of the VST - 2 later steps
+        // (those tiles that exist).  After the barrier every wave's share is
+        // visible and the slots of tile it-1 are free.
+        const int r = ntiles - 1 - it;
+        const int kout = min(r, 1) + min(r, VST - 2) + max(0, min(r, VST - 1) - 1);
+        __asm__ volatile("" ::: "memory");
+        wait_vmcnt_units<IPW, MAXK>(kout);
+        __builtin_amdgcn_s_barrier();
+        __asm__ volatile("" ::: "memory");
+        if (it + VST - 1 < ntiles) issue_v(it + VST - 1, pv_next);
+        if (it + KST - 1 < ntiles) issue_k(it + KST - 1, pk_next);
+        pv_next = wave_page(it + VST);
+        pk_next = wave_page(it + KST);
+
+        const int kb = kv_begin + it * 64;
+        if (!live || !tile_visible(kb)) return;
+        compute_tile(kb, kfrag_at(it), vfrag_at(it), std::true_type{});
+      };
+      for (int it = 0; it < ntiles; ++it) step(it);
+    }
   } else {
     // ============ register-staged tiles (fp8 e4m3fn -> bf16 in LDS) ============
     wait_vmcnt<0>();  // Q / mask loads complete, visibly to the compiler (see above)
@@ -775,6 +892,15 @@ void verify_attn_kernel(const VerifyParams p) {
   using R = RingCfg<D, WPB>;
   __shared__ __attribute__((aligned(16))) VerifySmem<D, R::KST, R::VST, R::NPG> sm;
   const VerifyItem w = p.items[blockIdx.x];
+  // Load the whole item and the prefix-level arguments in one round of
+  // scalar loads (the compiler would otherwise fetch the fields used after
+  // the mode test in later rounds): the Q loads and the first page ids
+  // depend on both.
+  __asm__ volatile("" ::"s"(w.kvh), "s"(w.qtile), "s"(w.kv_begin), "s"(w.kv_end), "s"(w.slot), "s"(w.q0), "s"(w.nq),
+                   "s"(w.base), "s"(w.src));
+  __asm__ volatile("" ::"s"(p.q), "s"(p.q_stride_n), "s"(p.q_stride_h), "s"(p.pre.k), "s"(p.pre.v),
+                   "s"(p.pre.page_table), "s"(p.pre.stride_tok), "s"(p.pre.stride_head), "s"(p.pre.stride_page),
+                   "s"(p.pre.log2_page), "s"(p.group), "s"(p.sm_scale_log2));
   if (w.mode == MODE_NOOP) return;
   if (w.src == SRC_PREFIX)
     verify_body<D, W, RB, R::KST, R::VST, R::NPG, PAGED, false, FP8>(p, w, p.pre, sm);
