@@ -122,7 +122,7 @@ def traffic_workload(args) -> int:
     prob = wl.config2(args.seed, layers=args.layers)
     mp = wl.materialize(prob, dev)
     attn = d2sd.CascadeVerifyAttention(dev)
-    wl.plan_for(attn, mp)
+    wl.plan_for(attn, mp, merge_mode=args.merge_mode)
     T, hq, d = prob.total_q, prob.num_qo_heads, prob.head_dim
     o = torch.empty(T, hq, d, dtype=torch.bfloat16, device=dev)
     lse = torch.empty(T, hq, dtype=torch.float32, device=dev)
@@ -164,7 +164,7 @@ def measure_traffic(args) -> int:
             cmd = ["rocprofv3", "--pmc", counter, "--kernel-include-regex", "verify_attn_kernel|copyBuffer",
                    "-d", str(outdir), "-o", "run", "--output-format", "csv", "--",
                    sys.executable, str(Path(__file__).resolve()), "--traffic-workload",
-                   "--layers", str(args.layers), "--seed", str(args.seed)]
+                   "--layers", str(args.layers), "--seed", str(args.seed), "--merge-mode", args.merge_mode]
             log("running " + " ".join(cmd))
             r = subprocess.run(cmd, timeout=300, capture_output=True, text=True)
             if r.returncode != 0:
@@ -224,6 +224,8 @@ def main() -> int:
     ap.add_argument("--cpu-reps", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=50)
+    ap.add_argument("--merge-mode", default="launch", choices=["launch", "last_producer"],
+                    help="where split partial states are merged (plan merge_mode)")
     ap.add_argument("--measure-traffic", action="store_true",
                     help="run the two rocprofv3 counter passes and write the traffic summary")
     ap.add_argument("--traffic-workload", action="store_true", help=argparse.SUPPRESS)
@@ -247,7 +249,7 @@ def main() -> int:
     log(f"materialising {prob.name}: N={prob.total_q} nodes, {args.layers} layers")
     mp = wl.materialize(prob, dev)
     attn = d2sd.CascadeVerifyAttention(dev)
-    wl.plan_for(attn, mp)
+    wl.plan_for(attn, mp, merge_mode=args.merge_mode)
     info = attn.info
     T, hq, d = prob.total_q, prob.num_qo_heads, prob.head_dim
     outs = [(torch.empty(T, hq, d, dtype=torch.bfloat16, device=dev),
@@ -278,7 +280,8 @@ def main() -> int:
                 layer_call(i, attn.run_merge)
     log(f"plan: attention {info.num_items} workgroups x {info.waves_per_block} waves "
         f"({info.rows_per_tile} rows each), {info.max_splits_used} prefix splits, {info.num_slots} partial "
-        f"slots, " + ("merged by each group's last producer" if fused else f"{info.num_merges} merge groups"))
+        f"slots, " + (f"merged inside the attention launch (mode {info.merge_mode})" if fused
+                       else f"{info.num_merges} merge groups"))
 
     for _ in range(args.warmup):
         step.replay()

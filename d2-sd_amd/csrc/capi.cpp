@@ -298,7 +298,9 @@ int d2sd_cascade_plan(const d2sd_cascade_plan_desc* desc, int32_t* host_plan, si
   in.max_splits = desc->max_splits;
   in.waves = desc->waves_per_block;
   in.page_size = desc->page_size;
-  in.separate_merge = desc->separate_merge != 0;
+  if (desc->merge_mode != D2SD_MERGE_LAUNCH && desc->merge_mode != D2SD_MERGE_LAST_PRODUCER)
+    return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: merge_mode must be one of D2SD_MERGE_*");
+  in.merge_mode = desc->merge_mode;
   d2sd::VerifyPlanOutput out{};
   d2sd::plan_verify(in, out);
   static_assert(sizeof(d2sd::VerifyItem) == 16 * sizeof(int32_t), "VerifyItem layout");
@@ -321,6 +323,7 @@ int d2sd_cascade_plan(const d2sd_cascade_plan_desc* desc, int32_t* host_plan, si
   info->num_groups = out.num_groups;
   info->merge_in_attention = out.merge_in_attention ? 1 : 0;
   info->counters_offset = out.counters_offset;
+  info->merge_mode = out.merge_mode;
   if (host_plan) {
     if (host_plan_ints < (size_t)info->plan_ints)
       return fail(D2SD_ERR_WORKSPACE, "cascade_plan: host_plan too small (need " +
@@ -388,7 +391,8 @@ static int build_verify_params(const d2sd_cascade_plan_info* info, const d2sd_ca
   p.part_lse = a->workspace ? (float*)((char*)a->workspace + (long long)info->num_slots * rows * D * 2) : nullptr;
   p.items = (const d2sd::VerifyItem*)a->plan;
   p.merges = (const d2sd::VerifyMerge*)(a->plan + 16 * (long long)info->num_items);
-  p.counters = info->merge_in_attention ? (int*)((char*)a->workspace + info->counters_offset) : nullptr;
+  if (info->merge_in_attention) p.counters = (int*)((char*)a->workspace + info->counters_offset);
+  p.merge_mode = info->merge_mode;
   p.sinks = a->sinks;
   p.tree_mask = (const unsigned long long*)a->tree_mask;
   d2sd::VerifySource& pre = p.pre;

@@ -14,6 +14,12 @@ enum : int {
   MODE_NOOP = 3,     // padding item, exits immediately
 };
 
+// Where a cascade plan merges the partial states of a split group.
+enum : int {
+  MERGE_LAUNCH = 0,         // a separate merge launch
+  MERGE_LAST_PRODUCER = 1,  // the group's last producer, inside the attention launch
+};
+
 enum : int { MASK_NONE = 0, MASK_CAUSAL = 1, MASK_TREE = 2 };
 
 // Page ids one attention workgroup stages in LDS (its split's pages).
@@ -138,7 +144,7 @@ struct VerifyParams {
   float* part_lse;         // [slot][ROWS]
   const VerifyItem* items;
   const VerifyMerge* merges;
-  int* counters;           // [groups] zero between launches; null: partials are merged by verify_merge_kernel
+  int* counters;           // [groups] producer arrivals, zero between launches (MERGE_LAST_PRODUCER)
   const float* sinks;      // nullable, [Hq]
   const unsigned long long* tree_mask;  // [total_q][mask_words]
   VerifySource pre, suf;
@@ -149,7 +155,7 @@ struct VerifyParams {
   int mask_words;
   int lse_base2;
   int num_merges;
-  int pad;
+  int merge_mode;          // MERGE_*
 };
 
 // Splits per group are capped so that one merge batch holds all partials.

@@ -68,7 +68,7 @@ static std::vector<int> order_for_xcds(std::vector<ItemSet<Item>>& sets, std::ve
 }
 
 // Interleave per-XCD merge lists: merge workgroup 8k + x runs on XCD x.
-static void interleave_merges(std::vector<std::vector<VerifyMerge>>& lists, std::vector<VerifyMerge>& out) {
+static void interleave_merges(const std::vector<std::vector<VerifyMerge>>& lists, std::vector<VerifyMerge>& out) {
   size_t maxlen = 0;
   for (auto& l : lists) maxlen = std::max(maxlen, l.size());
   for (size_t k = 0; k < maxlen; ++k)
@@ -265,10 +265,11 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
   out.num_slots = slot;
   out.max_splits_used = max_splits_used;
   out.num_groups = grp0[R];
-  out.merge_in_attention = !in.separate_merge && slot > 0;
+  out.merge_mode = slot > 0 ? in.merge_mode : MERGE_LAUNCH;
+  out.merge_in_attention = out.merge_mode != MERGE_LAUNCH;
   if (out.merge_in_attention) out.merges.clear();
-  // bf16 partial O + fp32 LSE per (slot, row), then one int32 completion
-  // counter per group (16-byte aligned)
+  // bf16 partial O + fp32 LSE per (slot, row), then the int32 counters
+  // (16-byte aligned)
   const size_t part_bytes = (size_t)slot * ROWS * ((size_t)in.head_dim * 2 + sizeof(float));
   out.counters_offset = (part_bytes + 15) & ~(size_t)15;
   out.workspace_bytes = out.merge_in_attention ? out.counters_offset + (size_t)out.num_groups * sizeof(int)

@@ -23,7 +23,7 @@ struct VerifyPlanInput {
   int max_splits;  // 0: no limit beyond kMaxVerifySplits
   int waves;       // 0: choose; else 2, 4 or 8
   int page_size;   // 0: contiguous prefix
-  bool separate_merge;  // partials merged by the merge launch, not by each group's last producer
+  int merge_mode;  // MERGE_*
 };
 
 struct VerifyPlanOutput {
@@ -34,8 +34,10 @@ struct VerifyPlanOutput {
   int num_slots;
   int max_splits_used;
   int num_groups;                   // (request, kv head, q-tile) groups with split prefixes
-  bool merge_in_attention;
-  size_t counters_offset;           // workspace byte offset of the int32 completion counters
+  int merge_mode;                   // MERGE_* in effect (MERGE_LAUNCH when nothing is split)
+  bool merge_in_attention;          // merge_mode != MERGE_LAUNCH
+  size_t counters_offset;           // workspace byte offset of the int32 counters: the producer
+                                    // arrivals of each group
   size_t workspace_bytes;
 };
 

@@ -804,7 +804,10 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
 
   // ---- merge in the group's last producer (no waiting: whoever completes
   // the count does the merge; flashinfer.merge_state_in_place semantics,
-  // generation/verification.py:163-165, and the sink of :173-176) ----
+  // generation/verification.py:163-165, and the sink of :173-176).  The
+  // partial states are exchanged through device-scope stores and loads; all
+  // workgroups of a group run on one XCD (the planner's placement), whose L2
+  // they share. ----
   wait_vmcnt<0>();  // this wave's partial stores are complete (device-visible)
   __syncthreads();
   if (tid == 0)
@@ -812,7 +815,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
               w.nprod - 1;
   __syncthreads();
   if (!sm.last) return;
-  if (tid == 0) p.counters[w.group] = 0;  // ready for the next launch
+  if (tid == 0) __hip_atomic_exchange(&p.counters[w.group], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next launch
   if (!live) return;
   const long long slot_elems = (long long)ROWS * D;
 #pragma unroll
@@ -909,31 +912,31 @@ void verify_attn_kernel(const VerifyParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Merge: one workgroup per (group, 32-row block), placed on the XCD whose L2
-// holds the group's partials; wave mt owns the 32-wide head-dim block mt and
-// lane l owns row l%32 and head dims 32mt + 8q4 + 4(l/32) + e.  All partial
-// loads of up to kMaxVerifySplits + 1 slots are in flight at once.
+// Merge of one 32-row block `blk` of a group, head dims [32 mt, 32 mt + 32):
+// the log-sum-exp merge of partial slots [slot0, slot0 + nslots)
+// (flashinfer.merge_state_in_place semantics, generation/verification.py:
+// 163-165) and the GPT-OSS sink (verification.py:173-176), written to O and
+// LSE.  Lane l owns row l%32 and head dims 32mt + 8q4 + 4(l/32) + e; all
+// partial loads (up to kMaxVerifySplits + 1 slots) are in flight at once.
+// COHERENT: the partials were written inside this launch (device-scope loads).
 // ---------------------------------------------------------------------------
-template <int D, int ROWS>
-__global__ __launch_bounds__(64 * (D / 32)) void verify_merge_kernel(const VerifyParams p) {
+template <int D, int ROWS, bool COHERENT>
+__device__ __forceinline__ void merge_rows(const VerifyParams& p, int slot0, int nslots, int blk, int mt,
+                                           int lane, int q0, int nq, int kvh, int qtile) {
   constexpr int B = kMaxVerifySplits + 1;
-  const VerifyMerge m = p.merges[blockIdx.x];
-  if (m.nslots == 0) return;  // padding
-  const int blk = m.blk;
-  const int mt = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63, l32 = lane & 31, hh = lane >> 5;
+  const int l32 = lane & 31, hh = lane >> 5;
   const int g = p.group;
-  const int row = m.qtile * ROWS + blk * 32 + l32;
-  if (row >= m.nq * g) return;
-  const int n = row / g, qh = m.kvh * g + (row - n * g);
+  const int row = qtile * ROWS + blk * 32 + l32;
+  if (row >= nq * g) return;
+  const int n = row / g, qh = kvh * g + (row - n * g);
 
   float acc[16];
 #pragma unroll
   for (int e = 0; e < 16; ++e) acc[e] = 0.f;
   float mval = -INFINITY, wsum = 0.f;
   const long long slot_elems = (long long)ROWS * D;
-  for (int s0 = 0; s0 < m.nslots; s0 += B) {
-    const int cnt = min(B, m.nslots - s0);
+  for (int s0 = 0; s0 < nslots; s0 += B) {
+    const int cnt = min(B, nslots - s0);
     float ls[B];
     u32x2 v[B][4];
 #pragma unroll
@@ -942,11 +945,15 @@ __global__ __launch_bounds__(64 * (D / 32)) void verify_merge_kernel(const Verif
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) v[b][q4] = (u32x2){0u, 0u};
       if (b < cnt) {
-        const long long s = m.slot0 + s0 + b;
-        ls[b] = p.part_lse[s * ROWS + blk * 32 + l32];
+        const long long s = slot0 + s0 + b;
+        const float* pl = p.part_lse + s * ROWS + blk * 32 + l32;
+        ls[b] = COHERENT ? load_agent(pl) : *pl;
         const bf16_t* po = (const bf16_t*)p.part_o + s * slot_elems;
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) v[b][q4] = *(const u32x2*)(po + image_offset<D>(blk, mt, q4, lane));
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const u32x2* src = (const u32x2*)(po + image_offset<D>(blk, mt, q4, lane));
+          v[b][q4] = COHERENT ? load_agent(src) : *src;
+        }
       }
     }
     float bm = -INFINITY;
@@ -976,14 +983,24 @@ __global__ __launch_bounds__(64 * (D / 32)) void verify_merge_kernel(const Verif
   const float lse = nonempty ? mval + logf(wsum) : -INFINITY;
   float sc = nonempty ? 1.f / wsum : 0.f;
   if (p.sinks) sc *= nonempty ? 1.f / (1.f + __expf(p.sinks[qh] - lse)) : 0.f;
-  bf16_t* orow = (bf16_t*)p.o + (long long)(m.q0 + n) * p.o_stride_n + (long long)qh * p.o_stride_h;
+  bf16_t* orow = (bf16_t*)p.o + (long long)(q0 + n) * p.o_stride_n + (long long)qh * p.o_stride_h;
 #pragma unroll
   for (int q4 = 0; q4 < 4; ++q4)
     *(u32x2*)(orow + 32 * mt + 8 * q4 + 4 * hh) =
         (u32x2){pack_bf16x2(acc[4 * q4] * sc, acc[4 * q4 + 1] * sc),
                 pack_bf16x2(acc[4 * q4 + 2] * sc, acc[4 * q4 + 3] * sc)};
   if (p.lse && mt == 0 && hh == 0)
-    p.lse[(long long)(m.q0 + n) * p.lse_stride_n + qh] = p.lse_base2 ? lse * kLog2e : lse;
+    p.lse[(long long)(q0 + n) * p.lse_stride_n + qh] = p.lse_base2 ? lse * kLog2e : lse;
+}
+
+// Merge launch: one workgroup per (group, 32-row block), placed on the XCD
+// whose L2 holds the group's partials; wave mt owns head-dim block mt.
+template <int D, int ROWS>
+__global__ __launch_bounds__(64 * (D / 32)) void verify_merge_kernel(const VerifyParams p) {
+  const VerifyMerge m = p.merges[blockIdx.x];
+  if (m.nslots == 0) return;  // padding
+  merge_rows<D, ROWS, false>(p, m.slot0, m.nslots, m.blk, threadIdx.x >> 6, threadIdx.x & 63, m.q0, m.nq, m.kvh,
+                             m.qtile);
 }
 
 // ---------------------------------------------------------------------------

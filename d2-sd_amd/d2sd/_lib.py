@@ -16,6 +16,8 @@ D2SD_KV_FP8_E4M3 = 1
 D2SD_MASK_NONE = 0
 D2SD_MASK_CAUSAL = 1
 D2SD_MASK_TREE = 2
+D2SD_MERGE_LAUNCH = 0
+D2SD_MERGE_LAST_PRODUCER = 1
 
 # Every symbol include/d2sd.h declares.
 EXPORTED_SYMBOLS = (
@@ -52,7 +54,7 @@ class PlanDesc(C.Structure):
         ("num_cus", C.c_int),
         ("max_splits", C.c_int),
         ("waves_per_block", C.c_int),
-        ("separate_merge", C.c_int),
+        ("merge_mode", C.c_int),
     ]
 
 
@@ -75,6 +77,7 @@ class PlanInfo(C.Structure):
         ("num_groups", C.c_int),
         ("merge_in_attention", C.c_int),
         ("counters_offset", C.c_size_t),
+        ("merge_mode", C.c_int),
     ]
 
 

@@ -30,6 +30,11 @@ from ._lib import check, lib
 from .tree import pack_tree_masks
 
 _MASK_MODES = {"none": _lib.D2SD_MASK_NONE, "causal": _lib.D2SD_MASK_CAUSAL, "tree": _lib.D2SD_MASK_TREE}
+# where the partial states of a split (request, kv head, q-tile) group are merged
+_MERGE_MODES = {
+    "launch": _lib.D2SD_MERGE_LAUNCH,  # a second (merge) launch
+    "last_producer": _lib.D2SD_MERGE_LAST_PRODUCER,  # the group's last producer, same launch
+}
 
 
 def _i32(x) -> np.ndarray:
@@ -67,7 +72,7 @@ class CascadeVerifyAttention:
         max_splits: int = 0,
         waves_per_block: int = 0,
         num_cus: int = 0,
-        separate_merge: bool = True,
+        merge_mode: str = "launch",
     ) -> "CascadeVerifyAttention":
         """Plan one verify call.
 
@@ -83,12 +88,17 @@ class CascadeVerifyAttention:
         window_left >= 0 keeps the last window_left prefix keys for all queries
         (verification.py:133-135).  sinks [Hq] fp32 applies O *= sigmoid(lse - sink).
         kv_dtype torch.float8_e4m3fn takes per-kv-head fp32 k_scale / v_scale.
+        merge_mode: "launch" (a second launch merges the split partial states) or
+        "last_producer" (each group's last producer workgroup merges them inside
+        the attention launch).
         """
         qo = _i32(qo_indptr)
         pl = _i32(prefix_len)
         R = int(pl.shape[0])
         if qo.shape[0] != R + 1:
             raise ValueError("qo_indptr must have len(prefix_len) + 1 entries")
+        if merge_mode not in _MERGE_MODES:
+            raise ValueError(f"merge_mode must be one of {sorted(_MERGE_MODES)}")
         if mask_mode not in _MASK_MODES:
             raise ValueError(f"mask_mode must be one of {sorted(_MASK_MODES)}")
         if kv_layout not in ("HND", "NHD"):
@@ -122,7 +132,7 @@ class CascadeVerifyAttention:
         desc.num_cus = num_cus
         desc.max_splits = max_splits
         desc.waves_per_block = waves_per_block
-        desc.separate_merge = 1 if separate_merge else 0
+        desc.merge_mode = _MERGE_MODES[merge_mode]
         info = _lib.PlanInfo()
         check(lib.d2sd_cascade_plan(C.byref(desc), None, 0, C.byref(info)), "cascade_plan (size)")
         host = np.zeros(max(info.plan_ints, 8), dtype=np.int32)
@@ -133,8 +143,8 @@ class CascadeVerifyAttention:
         self.qo_indptr_host = qo
         self.prefix_len_host = pl
         self.plan_dev = torch.from_numpy(host).to(dev)
-        # zero-filled once: the groups' completion counters at its end start at
-        # 0, and every run leaves them at 0
+        # zero-filled once: the counters at its end start at 0, and every run
+        # leaves them at 0
         self.workspace = torch.zeros(max(int(info.workspace_bytes), 16), dtype=torch.uint8, device=dev)
         self.mask_mode = _MASK_MODES[mask_mode]
         self.total_q = int(qo[-1])

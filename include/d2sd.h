@@ -46,6 +46,12 @@ typedef struct ihipStream_t* d2sd_stream_t; /* == hipStream_t */
 #define D2SD_MASK_CAUSAL 1 /* key j visible to query i iff j <= i + (kv_len - qo_len) */
 #define D2SD_MASK_TREE 2   /* ancestor bitmask, see d2sd_cascade_run_args */
 
+/* Where a cascade plan merges the partial states of a split group */
+#define D2SD_MERGE_LAUNCH 0        /* a second (merge) launch */
+#define D2SD_MERGE_LAST_PRODUCER 1 /* the group's last producer, inside the attention launch
+                                      (needs a group's workgroups on one XCD: the planner's
+                                      placement, with workgroups dealt to XCDs round-robin) */
+
 /* Message for the last failed call on this thread ("" if none). */
 const char* d2sd_last_error(void);
 /* Library version string. */
@@ -148,9 +154,11 @@ int d2sd_graph_destroy(void* graph_exec);
  * window_left >= 0 keeps the last window_left prefix keys (all queries).
  *
  * plan() bakes every per-request offset into a work list the caller uploads;
- * run() is two launches — attention (prefix key chunks and suffix trees, each
+ * run() is the attention launch (prefix key chunks and suffix trees, each
  * writing a partial state to the workspace, or the output directly when a
- * request has no prefix) and merge (log-sum-exp merge + sink into out / lse).
+ * request has no prefix) and, with D2SD_MERGE_LAUNCH, a merge launch
+ * (log-sum-exp merge + sink into out / lse); the other merge modes merge
+ * inside the attention launch.
  * run() allocates nothing and never synchronises the host, so it may be
  * captured into a hipGraph; the device plan, page_table contents and tensors
  * may change between replays as long as the plan's shape does not.
@@ -171,9 +179,8 @@ typedef struct {
   int max_splits;      /* 0: default cap */
   int waves_per_block; /* 0 = choose; 2 (64-row waves, 128-row tiles), 4 (32-row
                           waves, 128-row tiles) or 8 (32-row waves, 256-row tiles) */
-  int separate_merge;  /* 1: the merge launch merges the partial states; 0: the
-                          last workgroup to finish a (request, kv head, q-tile)
-                          merges them inside the attention launch */
+  int merge_mode;      /* D2SD_MERGE_*: where the partial states of a split
+                          (request, kv head, q-tile) group are merged */
 } d2sd_cascade_plan_desc;
 
 typedef struct {
@@ -193,8 +200,10 @@ typedef struct {
   int page_size;
   int num_groups;         /* (request, kv head, q-tile) groups with split prefixes */
   int merge_in_attention; /* 1: run() is the attention launch alone */
-  size_t counters_offset; /* byte offset of the groups' completion counters in the
-                             workspace (merge_in_attention) */
+  size_t counters_offset; /* byte offset of the groups' int32 completion counters
+                             in the workspace (merge_in_attention); zero before
+                             the first run(), and left zero by every run() */
+  int merge_mode;         /* the plan's D2SD_MERGE_* */
 } d2sd_cascade_plan_info;
 
 /* Fills host_plan (capacity host_plan_ints int32) with the work list; the

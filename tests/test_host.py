@@ -36,7 +36,7 @@ def test_version_and_error_strings():
 
 
 def _plan(qo, pl, hq=32, hkv=8, d=128, window=-1, num_cus=256, waves=0, max_splits=0, page_size=16,
-          page_indptr=None, tok_indptr=None, separate_merge=True):
+          page_indptr=None, tok_indptr=None, merge_mode=0):
     desc = _lib.PlanDesc()
     qo = np.asarray(qo, dtype=np.int32)
     pl = np.asarray(pl, dtype=np.int32)
@@ -56,7 +56,7 @@ def _plan(qo, pl, hq=32, hkv=8, d=128, window=-1, num_cus=256, waves=0, max_spli
     desc.num_cus = num_cus
     desc.max_splits = max_splits
     desc.waves_per_block = waves
-    desc.separate_merge = 1 if separate_merge else 0
+    desc.merge_mode = merge_mode
     info = _lib.PlanInfo()
     assert _lib.lib.d2sd_cascade_plan(C.byref(desc), None, 0, C.byref(info)) == 0, _lib.lib.d2sd_last_error()
     host = np.zeros(max(info.plan_ints, 8), dtype=np.int32)
@@ -71,6 +71,7 @@ def _plan(qo, pl, hq=32, hkv=8, d=128, window=-1, num_cus=256, waves=0, max_spli
 
 MODE_PARTIAL, MODE_FINAL, MODE_NOOP = 0, 1, 3
 SRC_PREFIX, SRC_SUFFIX = 0, 1
+MERGE_LAUNCH, MERGE_LAST_PRODUCER = 0, 1
 # VerifyItem fields
 REQ, KVH, QT, SRC, KB, KE, SLOT, MODE, Q0, NQ, BASE, COFF, GROUP, SLOT0, NPROD = range(15)
 
@@ -89,8 +90,8 @@ REQ, KVH, QT, SRC, KB, KE, SLOT, MODE, Q0, NQ, BASE, COFF, GROUP, SLOT0, NPROD =
     ([64 * i for i in range(33)], [8192] * 32, -1, 16, 32, 0),
     ([0, 0, 40], [100, 5000], -1, 16, 32, 0),                       # a request with no queries
 ])
-@pytest.mark.parametrize("separate_merge", [True, False])
-def test_plan_partitions_work(qo, pl, window, page, hq, waves, separate_merge):
+@pytest.mark.parametrize("merge_mode", [MERGE_LAUNCH, MERGE_LAST_PRODUCER])
+def test_plan_partitions_work(qo, pl, window, page, hq, waves, merge_mode):
     """Every (request, kv head, q-tile) group: prefix items partition its
     visible prefix on 64-key tile boundaries into consecutive slots, one suffix
     item covers its nodes, and the group's slots are merged exactly once: by
@@ -104,9 +105,10 @@ def test_plan_partitions_work(qo, pl, window, page, hq, waves, separate_merge):
     if page:
         page_indptr = np.concatenate([[0], np.cumsum((np.asarray(pl) + page - 1) // page)])
     info, items, merges = _plan(qo, pl, hq, hkv, 128, window, page_size=page, waves=waves,
-                                page_indptr=page_indptr, separate_merge=separate_merge)
+                                page_indptr=page_indptr, merge_mode=merge_mode)
     fused = bool(info.merge_in_attention)
-    assert fused == (not separate_merge and info.num_slots > 0)
+    assert fused == (merge_mode != MERGE_LAUNCH and info.num_slots > 0)
+    assert info.merge_mode == (merge_mode if info.num_slots > 0 else MERGE_LAUNCH)
     part_bytes = info.num_slots * info.rows_per_tile * (128 * 2 + 4)
     if fused:
         assert info.num_merges == 0 and info.counters_offset >= part_bytes and info.counters_offset % 16 == 0
