@@ -993,14 +993,18 @@ __device__ __forceinline__ void merge_rows(const VerifyParams& p, int slot0, int
     p.lse[(long long)(q0 + n) * p.lse_stride_n + qh] = p.lse_base2 ? lse * kLog2e : lse;
 }
 
-// Merge launch: one workgroup per (group, 32-row block), placed on the XCD
-// whose L2 holds the group's partials; wave mt owns head-dim block mt.
+// Merge launch: one single-wave workgroup per (group, 32-row block, 32-wide
+// head-dim block mt), so that the partial loads spread over every CU.
+// Workgroup b handles merge b % nm8 and block b / nm8 (nm8 = merges rounded
+// up to a multiple of 8), which keeps merge m on XCD m % 8, the XCD of its
+// partials.
 template <int D, int ROWS>
-__global__ __launch_bounds__(64 * (D / 32)) void verify_merge_kernel(const VerifyParams p) {
-  const VerifyMerge m = p.merges[blockIdx.x];
+__global__ __launch_bounds__(64) void verify_merge_kernel(const VerifyParams p, int nm8) {
+  const int mi = blockIdx.x % nm8, mt = blockIdx.x / nm8;
+  if (mi >= p.num_merges) return;
+  const VerifyMerge m = p.merges[mi];
   if (m.nslots == 0) return;  // padding
-  merge_rows<D, ROWS, false>(p, m.slot0, m.nslots, m.blk, threadIdx.x >> 6, threadIdx.x & 63, m.q0, m.nq, m.kvh,
-                             m.qtile);
+  merge_rows<D, ROWS, false>(p, m.slot0, m.nslots, m.blk, mt, threadIdx.x, m.q0, m.nq, m.kvh, m.qtile);
 }
 
 // ---------------------------------------------------------------------------
@@ -1035,11 +1039,13 @@ hipError_t launch_verify_attention(const VerifyParams& p, int head_dim, int wave
 
 hipError_t launch_verify_merge(const VerifyParams& p, int head_dim, int rows, int nmerges, hipStream_t s) {
   if (nmerges <= 0) return hipSuccess;
-  const dim3 grid((unsigned)nmerges), block(2 * head_dim);  // one wave per 32 head dims
-  if (head_dim == 128 && rows == 128) hipLaunchKernelGGL((verify_merge_kernel<128, 128>), grid, block, 0, s, p);
-  else if (head_dim == 128 && rows == 256) hipLaunchKernelGGL((verify_merge_kernel<128, 256>), grid, block, 0, s, p);
-  else if (head_dim == 64 && rows == 128) hipLaunchKernelGGL((verify_merge_kernel<64, 128>), grid, block, 0, s, p);
-  else if (head_dim == 64 && rows == 256) hipLaunchKernelGGL((verify_merge_kernel<64, 256>), grid, block, 0, s, p);
+  if (p.num_merges != nmerges) return hipErrorInvalidValue;
+  const int nm8 = (nmerges + 7) & ~7;
+  const dim3 grid((unsigned)(nm8 * (head_dim / 32))), block(64);
+  if (head_dim == 128 && rows == 128) hipLaunchKernelGGL((verify_merge_kernel<128, 128>), grid, block, 0, s, p, nm8);
+  else if (head_dim == 128 && rows == 256) hipLaunchKernelGGL((verify_merge_kernel<128, 256>), grid, block, 0, s, p, nm8);
+  else if (head_dim == 64 && rows == 128) hipLaunchKernelGGL((verify_merge_kernel<64, 128>), grid, block, 0, s, p, nm8);
+  else if (head_dim == 64 && rows == 256) hipLaunchKernelGGL((verify_merge_kernel<64, 256>), grid, block, 0, s, p, nm8);
   else return hipErrorInvalidValue;
   return hipGetLastError();
 }
