@@ -994,15 +994,20 @@ __device__ __forceinline__ void merge_rows(const VerifyParams& p, int slot0, int
 }
 
 // Merge launch: one single-wave workgroup per (group, 32-row block, 32-wide
-// head-dim block mt), so that the partial loads spread over every CU.
-// Workgroup b handles merge b % nm8 and block b / nm8 (nm8 = merges rounded
-// up to a multiple of 8), which keeps merge m on XCD m % 8, the XCD of its
+// head-dim block mt), so that the partial loads spread over every CU.  The
+// grid is (merges rounded up to a multiple of 8) x (D / 32): workgroup (m, mt)
+// has linear index m + nm8 * mt, so merge m stays on XCD m % 8, the XCD of its
 // partials.
 template <int D, int ROWS>
-__global__ __launch_bounds__(64) void verify_merge_kernel(const VerifyParams p, int nm8) {
-  const int mi = blockIdx.x % nm8, mt = blockIdx.x / nm8;
+__global__ __launch_bounds__(64) void verify_merge_kernel(const VerifyParams p) {
+  const int mi = blockIdx.x, mt = blockIdx.y;
+  // the arguments in one round of scalar loads, then the whole record in one
+  __asm__ volatile("" ::"s"(p.merges), "s"(p.num_merges), "s"(p.part_o), "s"(p.part_lse), "s"(p.o),
+                   "s"(p.o_stride_n), "s"(p.o_stride_h), "s"(p.lse), "s"(p.lse_stride_n), "s"(p.group),
+                   "s"(p.sinks), "s"(p.lse_base2));
   if (mi >= p.num_merges) return;
   const VerifyMerge m = p.merges[mi];
+  __asm__ volatile("" ::"s"(m.kvh), "s"(m.qtile), "s"(m.slot0), "s"(m.nslots), "s"(m.q0), "s"(m.nq), "s"(m.blk));
   if (m.nslots == 0) return;  // padding
   merge_rows<D, ROWS, false>(p, m.slot0, m.nslots, m.blk, mt, threadIdx.x, m.q0, m.nq, m.kvh, m.qtile);
 }
@@ -1041,11 +1046,11 @@ hipError_t launch_verify_merge(const VerifyParams& p, int head_dim, int rows, in
   if (nmerges <= 0) return hipSuccess;
   if (p.num_merges != nmerges) return hipErrorInvalidValue;
   const int nm8 = (nmerges + 7) & ~7;
-  const dim3 grid((unsigned)(nm8 * (head_dim / 32))), block(64);
-  if (head_dim == 128 && rows == 128) hipLaunchKernelGGL((verify_merge_kernel<128, 128>), grid, block, 0, s, p, nm8);
-  else if (head_dim == 128 && rows == 256) hipLaunchKernelGGL((verify_merge_kernel<128, 256>), grid, block, 0, s, p, nm8);
-  else if (head_dim == 64 && rows == 128) hipLaunchKernelGGL((verify_merge_kernel<64, 128>), grid, block, 0, s, p, nm8);
-  else if (head_dim == 64 && rows == 256) hipLaunchKernelGGL((verify_merge_kernel<64, 256>), grid, block, 0, s, p, nm8);
+  const dim3 grid((unsigned)nm8, (unsigned)(head_dim / 32)), block(64);
+  if (head_dim == 128 && rows == 128) hipLaunchKernelGGL((verify_merge_kernel<128, 128>), grid, block, 0, s, p);
+  else if (head_dim == 128 && rows == 256) hipLaunchKernelGGL((verify_merge_kernel<128, 256>), grid, block, 0, s, p);
+  else if (head_dim == 64 && rows == 128) hipLaunchKernelGGL((verify_merge_kernel<64, 128>), grid, block, 0, s, p);
+  else if (head_dim == 64 && rows == 256) hipLaunchKernelGGL((verify_merge_kernel<64, 256>), grid, block, 0, s, p);
   else return hipErrorInvalidValue;
   return hipGetLastError();
 }
