@@ -203,6 +203,74 @@ def measure_traffic(args) -> int:
     return 0
 
 
+def measure_commit(args) -> int:
+    """Accepted-branch KV commit (d2sd.PagedKVCommit, generation/d3_generator.py:
+    227-232) at Qwen3-8B shape: 36 layers, prefix 4096 paged at 16, the first
+    acceptance_length tokens of row 1 of the d3 verify tree.  Beside it, the
+    reference's own form on the same GPU: per layer torch.cat of the
+    [1, Hkv, L, D] cache with the accepted window (keys and values), which
+    copies the whole cache.  Prints one JSON line."""
+    import numpy as np
+    import torch
+    import d2sd
+    from d2sd import tree as dtree
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    layers, P, hkv, d, L, acc = args.layers, 16, 8, 128, 4096, args.accepted
+    tr = dtree.d3_verify_tree(np.random.default_rng(args.seed).uniform(size=15))
+    rows = tr.num_nodes
+    acc = min(acc, tr.node_index.shape[1])
+    nodes = torch.as_tensor(tr.node_index[1][:acc], dtype=torch.int32, device=dev)
+    pages = (L + acc + P - 1) // P
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    kp = [torch.randn(pages + 8, hkv, P, d, generator=g, device=dev, dtype=torch.bfloat16) for _ in range(layers)]
+    vp = [torch.randn(pages + 8, hkv, P, d, generator=g, device=dev, dtype=torch.bfloat16) for _ in range(layers)]
+    kn = [torch.randn(rows, hkv, d, generator=g, device=dev, dtype=torch.bfloat16) for _ in range(layers)]
+    vn = [torch.randn(rows, hkv, d, generator=g, device=dev, dtype=torch.bfloat16) for _ in range(layers)]
+    table = torch.randperm(pages + 8, generator=g, device=dev)[:pages].to(torch.int32)
+    commit = d2sd.PagedKVCommit(kp, vp, kn, vn)
+    commit.commit(table, L, nodes)
+    torch.cuda.synchronize()
+    # many commits in one graph, so that the host's graph launches do not
+    # pace the GPU (a single-kernel graph replays slower than its kernel runs)
+    per_graph = 32
+    gc = d2sd.HipGraph()
+    with gc.capture():
+        for _ in range(per_graph):
+            commit.commit(table, L, nodes)
+    us = time_graph(gc, max(3, args.kernel_reps // 4), torch) * 1e3 / per_graph
+    # reference form: DynamicCache layer tensors [1, Hkv, L, D], grown by torch.cat
+    kc = [torch.randn(1, hkv, L, d, generator=g, device=dev, dtype=torch.bfloat16) for _ in range(layers)]
+    vc = [torch.randn(1, hkv, L, d, generator=g, device=dev, dtype=torch.bfloat16) for _ in range(layers)]
+    kw = [torch.randn(1, hkv, acc, d, generator=g, device=dev, dtype=torch.bfloat16) for _ in range(layers)]
+    vw = [torch.randn(1, hkv, acc, d, generator=g, device=dev, dtype=torch.bfloat16) for _ in range(layers)]
+    for _ in range(3):
+        out = [(torch.cat([kc[i], kw[i]], dim=2), torch.cat([vc[i], vw[i]], dim=2)) for i in range(layers)]
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = max(5, args.kernel_reps // 5)
+    e0.record()
+    for _ in range(reps):
+        out = [(torch.cat([kc[i], kw[i]], dim=2), torch.cat([vc[i], vw[i]], dim=2)) for i in range(layers)]
+    e1.record()
+    torch.cuda.synchronize()
+    ref_us = e0.elapsed_time(e1) / reps * 1e3
+    del out
+    moved = 2 * layers * acc * hkv * d * 2 * 2  # K and V rows, read + written
+    print(json.dumps({
+        "metric": "accepted-branch KV commit µs/step (36 layers, Qwen3-8B shape)",
+        "value": us, "unit": "us", "higher_is_better": False, "accepted_tokens": acc,
+        "bytes_moved": moved, "achieved_gbps": moved / (us * 1e-6) / 1e9,
+        "hbm_frac": moved / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS,
+        "reference_torch_cat_us": ref_us,
+        "reference_torch_cat_bytes": 2 * layers * 2 * (2 * L + acc) * hkv * d,
+        "speedup_vs_reference": ref_us / us,
+        "config": {"workload": "config 2 verify step commit", "layers": layers, "prefix": L, "page_size": P},
+    }))
+    return 0
+
+
 def read_traffic():
     """traffic_bytes_per_launch from TRAFFIC_FILE, or None."""
     try:
@@ -229,7 +297,12 @@ def main() -> int:
     ap.add_argument("--measure-traffic", action="store_true",
                     help="run the two rocprofv3 counter passes and write the traffic summary")
     ap.add_argument("--traffic-workload", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--commit", action="store_true",
+                    help="time the accepted-branch KV commit instead (one JSON line)")
+    ap.add_argument("--accepted", type=int, default=20, help="accepted tokens per step for --commit")
     args = ap.parse_args()
+    if args.commit:
+        return measure_commit(args)
     if args.traffic_workload:
         return traffic_workload(args)
     if args.measure_traffic:

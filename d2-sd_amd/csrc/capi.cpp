@@ -449,4 +449,54 @@ int d2sd_cascade_run(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_
   return d2sd_cascade_merge(info, a, stream);
 }
 
+// Accepted-branch KV commit (replaces generation/d3_generator.py:227-232).
+int d2sd_paged_kv_append(const d2sd_kv_append_args* a, d2sd_stream_t stream) {
+  g_last_error.clear();
+  if (!a) return fail(D2SD_ERR_INVALID_ARG, "paged_kv_append: null args");
+  if (a->num_accepted < 0 || a->num_layers < 0 || a->prefix_len < 0)
+    return fail(D2SD_ERR_INVALID_ARG, "paged_kv_append: negative count");
+  if (a->num_accepted == 0 || a->num_layers == 0) return D2SD_OK;
+  if (a->num_kv_heads <= 0 || a->head_dim <= 0 || a->head_dim % 8 != 0)
+    return fail(D2SD_ERR_INVALID_ARG, "paged_kv_append: head_dim must be a positive multiple of 8");
+  if (a->page_size <= 0 || (a->page_size & (a->page_size - 1)) != 0)
+    return fail(D2SD_ERR_INVALID_ARG, "paged_kv_append: page_size must be a power of two");
+  if (a->num_rows <= 0 || a->pool_pages <= 0)
+    return fail(D2SD_ERR_INVALID_ARG, "paged_kv_append: num_rows and pool_pages must be positive");
+  if (!a->node_ids || !a->page_table || !a->k_new || !a->v_new || !a->k_pool || !a->v_pool)
+    return fail(D2SD_ERR_INVALID_ARG, "paged_kv_append: null pointer");
+  const int64_t strides[5] = {a->new_stride_n, a->new_stride_h, a->pool_stride_page, a->pool_stride_head,
+                              a->pool_stride_tok};
+  for (int64_t st : strides)
+    if (st <= 0 || st % 8 != 0)
+      return fail(D2SD_ERR_INVALID_ARG, "paged_kv_append: strides must be positive multiples of 8 elements");
+  if ((int64_t)a->prefix_len + a->num_accepted > (int64_t)INT32_MAX)
+    return fail(D2SD_ERR_INVALID_ARG, "paged_kv_append: cache position overflows int32");
+  if (((int64_t)a->prefix_len + a->num_accepted + a->page_size - 1) / a->page_size > (int64_t)a->page_table_len)
+    return fail(D2SD_ERR_INVALID_ARG, "paged_kv_append: page_table does not cover prefix_len + num_accepted");
+  d2sd::KvAppendParams p{};
+  p.node_ids = a->node_ids;
+  p.page_table = a->page_table;
+  p.k_new = a->k_new;
+  p.v_new = a->v_new;
+  p.k_pool = a->k_pool;
+  p.v_pool = a->v_pool;
+  p.new_stride_n = a->new_stride_n;
+  p.new_stride_h = a->new_stride_h;
+  p.pool_stride_page = a->pool_stride_page;
+  p.pool_stride_head = a->pool_stride_head;
+  p.pool_stride_tok = a->pool_stride_tok;
+  p.num_layers = a->num_layers;
+  p.num_kv_heads = a->num_kv_heads;
+  p.head_dim = a->head_dim;
+  int lg = 0;
+  while ((1 << lg) < a->page_size) ++lg;
+  p.log2_page = lg;
+  p.prefix_len = a->prefix_len;
+  p.num_accepted = a->num_accepted;
+  p.num_rows = a->num_rows;
+  p.pool_pages = a->pool_pages;
+  hipError_t e = d2sd::launch_kv_append(p, (hipStream_t)stream);
+  return e == hipSuccess ? D2SD_OK : fail_hip(e, "paged_kv_append launch");
+}
+
 }  // extern "C"

@@ -161,4 +161,23 @@ struct VerifyParams {
 // Splits per group are capped so that one merge batch holds all partials.
 constexpr int kMaxVerifySplits = 15;
 
+// ---------------------------------------------------------------------------
+// Accepted-branch KV commit (kv_append.hip).
+// ---------------------------------------------------------------------------
+struct KvAppendParams {
+  const int* node_ids;     // [num_accepted] rows of k_new / v_new, in cache order
+  const int* page_table;   // the request's pages
+  const uint64_t* k_new;   // [num_layers] addresses of bf16 [rows, Hkv, D]
+  const uint64_t* v_new;
+  const uint64_t* k_pool;  // [num_layers] addresses of the bf16 page pools
+  const uint64_t* v_pool;
+  long long new_stride_n, new_stride_h;                          // elements
+  long long pool_stride_page, pool_stride_head, pool_stride_tok;  // elements
+  int num_layers, num_kv_heads, head_dim;
+  int log2_page;
+  int prefix_len, num_accepted;
+  int num_rows;    // rows of k_new / v_new (node ids outside are skipped)
+  int pool_pages;  // pages of each pool (page ids outside are skipped)
+};
+
 }  // namespace d2sd

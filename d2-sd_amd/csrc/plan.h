@@ -52,6 +52,9 @@ hipError_t launch_verify_attention(const VerifyParams& p, int head_dim, int wave
                                    hipStream_t s);
 hipError_t launch_verify_merge(const VerifyParams& p, int head_dim, int rows, int nmerges, hipStream_t s);
 
+// ---- accepted-branch KV commit (kv_append.hip) ----
+hipError_t launch_kv_append(const KvAppendParams& p, hipStream_t s);
+
 // ---- single-source drop-ins (attention.hip) ----
 int choose_waves(int rows_per_head_max);
 int blocks_per_cu(int waves);

@@ -35,6 +35,7 @@ EXPORTED_SYMBOLS = (
     "d2sd_cascade_run",
     "d2sd_cascade_attention",
     "d2sd_cascade_merge",
+    "d2sd_paged_kv_append",
 )
 
 
@@ -116,6 +117,31 @@ class RunArgs(C.Structure):
     ]
 
 
+class KvAppendArgs(C.Structure):
+    _fields_ = [
+        ("num_layers", C.c_int),
+        ("num_kv_heads", C.c_int),
+        ("head_dim", C.c_int),
+        ("page_size", C.c_int),
+        ("prefix_len", C.c_int),
+        ("num_accepted", C.c_int),
+        ("num_rows", C.c_int),
+        ("pool_pages", C.c_int),
+        ("page_table_len", C.c_int),
+        ("node_ids", C.c_void_p),
+        ("page_table", C.c_void_p),
+        ("k_new", C.c_void_p),
+        ("v_new", C.c_void_p),
+        ("k_pool", C.c_void_p),
+        ("v_pool", C.c_void_p),
+        ("new_stride_n", C.c_int64),
+        ("new_stride_h", C.c_int64),
+        ("pool_stride_page", C.c_int64),
+        ("pool_stride_head", C.c_int64),
+        ("pool_stride_tok", C.c_int64),
+    ]
+
+
 # int32 entries per attention item / merge item in the host plan
 PLAN_ITEM_INTS = 16
 PLAN_MERGE_INTS = 8
@@ -157,6 +183,8 @@ def _load() -> C.CDLL:
         fn = getattr(lib, name)
         fn.restype = i32
         fn.argtypes = [C.POINTER(PlanInfo), C.POINTER(RunArgs), vp]
+    lib.d2sd_paged_kv_append.restype = i32
+    lib.d2sd_paged_kv_append.argtypes = [C.POINTER(KvAppendArgs), vp]
     return lib
 
 

@@ -1,0 +1,103 @@
+"""Accepted-branch KV commit into the paged prefix cache (libd2sd.so).
+
+Replaces the cache growth of generation/d3_generator.py:227-232, which per
+layer and step does
+
+    k_win = new_kv[layer][0][valid_block:valid_block + 1, :, :acceptance_length, :]
+    layer.keys = torch.cat([layer.keys, k_win], dim=2)      (values alike)
+
+i.e. copies the whole cache.  Here the accepted branch's tokens (their tree
+node rows of each layer's suffix K/V, in order) are written in place into the
+pages that follow the prefix, for all layers in one launch; the prefix stays
+put, so page tables and hipGraphs stay valid across steps.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import Sequence
+
+import torch
+
+from . import _lib
+from ._lib import check, lib
+
+
+def _layout_strides(pool: torch.Tensor, kv_layout: str):
+    # [pages, Hkv, P, D] ("HND") or [pages, P, Hkv, D] ("NHD"), head_dim contiguous
+    if kv_layout == "HND":
+        return pool.stride(0), pool.stride(1), pool.stride(2), pool.shape[2], pool.shape[1]
+    if kv_layout == "NHD":
+        return pool.stride(0), pool.stride(2), pool.stride(1), pool.shape[1], pool.shape[2]
+    raise ValueError("kv_layout must be 'HND' or 'NHD'")
+
+
+class PagedKVCommit:
+    """Commits accepted tree nodes of every layer into paged K/V pools.
+
+    k_pools / v_pools: per layer a bf16 page pool ([pages, Hkv, P, D] for
+    kv_layout "HND", [pages, P, Hkv, D] for "NHD"); k_new / v_new: per layer the
+    step's suffix K/V, bf16 [rows, Hkv, D] (the tree nodes, as passed to
+    CascadeVerifyAttention.run).  All layers share shapes and strides.  The
+    per-layer addresses are kept in device arrays built here once, so that
+    commit() allocates nothing and may be captured into a hipGraph (the
+    tensors must stay alive and in place).
+    """
+
+    def __init__(self, k_pools: Sequence[torch.Tensor], v_pools: Sequence[torch.Tensor],
+                 k_new: Sequence[torch.Tensor], v_new: Sequence[torch.Tensor], kv_layout: str = "HND"):
+        n = len(k_pools)
+        if not (n == len(v_pools) == len(k_new) == len(v_new)) or n == 0:
+            raise ValueError("one k/v pool and one k/v new tensor per layer are required")
+        ref_pool, ref_new = k_pools[0], k_new[0]
+        for t in list(k_pools) + list(v_pools):
+            if t.dtype != torch.bfloat16 or t.shape != ref_pool.shape or t.stride() != ref_pool.stride():
+                raise ValueError("pools must be bf16 with one shape and stride for all layers")
+            if t.stride(-1) != 1 or t.device != ref_pool.device:
+                raise ValueError("pools must have a contiguous head_dim on one device")
+        for t in list(k_new) + list(v_new):
+            if t.dtype != torch.bfloat16 or t.shape != ref_new.shape or t.stride() != ref_new.stride():
+                raise ValueError("k_new / v_new must be bf16 with one shape and stride for all layers")
+            if t.dim() != 3 or t.stride(-1) != 1 or t.device != ref_pool.device:
+                raise ValueError("k_new / v_new must be [rows, Hkv, D] with a contiguous head_dim")
+        sp, sh, st, page_size, hkv = _layout_strides(ref_pool, kv_layout)
+        if ref_new.shape[1] != hkv or ref_new.shape[2] != ref_pool.shape[-1]:
+            raise ValueError("k_new / v_new heads and head_dim must match the pools")
+        dev = ref_pool.device
+        as_addr = lambda ts: torch.tensor([t.data_ptr() for t in ts], dtype=torch.int64, device=dev)
+        self._addr = [as_addr(k_new), as_addr(v_new), as_addr(k_pools), as_addr(v_pools)]
+        self._keep = (list(k_pools), list(v_pools), list(k_new), list(v_new))
+        a = _lib.KvAppendArgs()
+        a.num_layers = n
+        a.num_kv_heads = hkv
+        a.head_dim = ref_pool.shape[-1]
+        a.page_size = page_size
+        a.num_rows = ref_new.shape[0]
+        a.pool_pages = ref_pool.shape[0]
+        a.k_new, a.v_new, a.k_pool, a.v_pool = (t.data_ptr() for t in self._addr)
+        a.new_stride_n, a.new_stride_h = ref_new.stride(0), ref_new.stride(1)
+        a.pool_stride_page, a.pool_stride_head, a.pool_stride_tok = sp, sh, st
+        self._args = a
+        self.page_size = page_size
+
+    def commit(self, page_table: torch.Tensor, prefix_len: int, node_ids: torch.Tensor,
+               num_accepted: int | None = None) -> None:
+        """Writes rows node_ids[:num_accepted] of every layer's k_new / v_new to
+        cache positions prefix_len .. prefix_len + num_accepted - 1 of the
+        request whose pages are page_table (device int32, covering them)."""
+        if page_table.dtype != torch.int32 or node_ids.dtype != torch.int32:
+            raise TypeError("page_table and node_ids must be int32")
+        if not (page_table.is_contiguous() and node_ids.is_contiguous()):
+            raise ValueError("page_table and node_ids must be contiguous")
+        n = int(node_ids.numel() if num_accepted is None else num_accepted)
+        if n < 0 or n > node_ids.numel():
+            raise ValueError("num_accepted out of range")
+        if (int(prefix_len) + n + self.page_size - 1) // self.page_size > page_table.numel():
+            raise ValueError("page_table does not cover prefix_len + num_accepted tokens")
+        a = self._args
+        a.prefix_len = int(prefix_len)
+        a.num_accepted = n
+        a.node_ids = node_ids.data_ptr()
+        a.page_table = page_table.data_ptr()
+        a.page_table_len = page_table.numel()
+        check(lib.d2sd_paged_kv_append(C.byref(a), C.c_void_p(torch.cuda.current_stream().cuda_stream)),
+              "paged_kv_append")

@@ -248,6 +248,43 @@ int d2sd_cascade_attention(const d2sd_cascade_plan_info* info, const d2sd_cascad
 int d2sd_cascade_merge(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* args,
                        d2sd_stream_t stream);
 
+/* ----------------------------------------------------------------------
+ * Accepted-branch KV commit into the paged prefix cache.
+ * Replaces generation/d3_generator.py:227-232: per layer
+ *   layer.keys = torch.cat([layer.keys, k_win], dim=2)   (values alike),
+ * k_win = the accepted row's first acceptance_length new keys, which copies
+ * the whole cache every step.  Here token i of the accepted branch (row
+ * node_ids[i] of every layer's k_new / v_new) is written to cache position
+ * prefix_len + i: page page_table[(prefix_len + i) / page_size], slot
+ * (prefix_len + i) % page_size, for all layers in one launch.  The page
+ * table must already hold the pages for prefix_len + num_accepted tokens.
+ * Node ids outside [0, num_rows) and page ids outside [0, pool_pages) are
+ * skipped (nothing written).  bf16 pools only; strides in elements must be
+ * multiples of 8 and every address 16-byte aligned.  No allocation, no host
+ * synchronisation (capturable).
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  int num_layers;
+  int num_kv_heads;
+  int head_dim;              /* multiple of 8 */
+  int page_size;             /* power of two */
+  int prefix_len;            /* tokens already cached */
+  int num_accepted;          /* tokens appended */
+  int num_rows;              /* rows of each k_new / v_new */
+  int pool_pages;            /* pages of each pool */
+  int page_table_len;        /* entries of page_table; must cover prefix_len + num_accepted */
+  const int32_t* node_ids;   /* device [num_accepted] */
+  const int32_t* page_table; /* device, the request's pages */
+  const uint64_t* k_new;     /* device [num_layers]: addresses of bf16 [rows, Hkv, D] */
+  const uint64_t* v_new;
+  const uint64_t* k_pool;    /* device [num_layers]: addresses of the bf16 page pools */
+  const uint64_t* v_pool;
+  int64_t new_stride_n, new_stride_h;                         /* elements */
+  int64_t pool_stride_page, pool_stride_head, pool_stride_tok; /* elements */
+} d2sd_kv_append_args;
+
+int d2sd_paged_kv_append(const d2sd_kv_append_args* args, d2sd_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

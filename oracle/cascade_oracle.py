@@ -16,6 +16,7 @@ It restates the reference's verify-attention algorithm on the CPU in float64
   verification.py:173-176 (GPT-OSS sink)           sink_rescale_ref
   verification.py:127-176 as a whole (row layout)  cascade_verify_rows_ref
   the same over unique tree nodes, single pass     cascade_tree_ref
+  d3_generator.py:227-232 (accepted-branch commit) commit_accepted_ref
 
 FlashInfer itself (flashinfer-python>=0.2.0, requirements.txt:13) is not
 vendored in the reference and not installed here.  Its published algorithm for
@@ -229,8 +230,29 @@ def gather_paged(pool: Tensor, page_table: List[int], length: int, layout: str =
     return flat[:length]
 
 
+def commit_accepted_ref(pool: Tensor, page_table: List[int], prefix_len: int, new: Tensor,
+                        node_ids: List[int], layout: str = "HND") -> Tensor:
+    """Accepted-branch commit (generation/d3_generator.py:227-232): the cache
+    grows by the accepted row's tokens, here the tree nodes node_ids of `new`
+    ([rows, Hkv, D]) in order, at positions prefix_len .. prefix_len + n - 1 of
+    the paged pool.  Returns a new pool; nodes outside [0, rows) are skipped
+    (nothing written), as by the kernel."""
+    out = pool.clone()
+    P = pool.shape[2] if layout == "HND" else pool.shape[1]
+    for i, node in enumerate(node_ids):
+        if not 0 <= node < new.shape[0]:
+            continue
+        t = prefix_len + i
+        page, slot = page_table[t // P], t % P
+        if layout == "HND":
+            out[page, :, slot, :] = new[node]
+        else:
+            out[page, slot, :, :] = new[node]
+    return out
+
+
 __all__ = [
     "attention_ref", "attention_sdpa_ref", "causal_mask", "single_prefill_ref", "merge_state_ref",
     "sink_rescale_ref", "window_prefix_ref", "cascade_verify_rows_ref", "cascade_tree_ref",
-    "ancestor_mask_from_rows", "fp8_dequant_ref", "gather_paged",
+    "ancestor_mask_from_rows", "fp8_dequant_ref", "gather_paged", "commit_accepted_ref",
 ]

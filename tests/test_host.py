@@ -265,3 +265,30 @@ def test_python_surface_rejects_cpu_tensors():
         d2sd.single_prefill_with_kv_cache(q, k, k, causal=True, return_lse=True)
     with pytest.raises(ValueError, match="device"):
         d2sd.merge_state_in_place(q, torch.zeros(4, 32), q.clone(), torch.zeros(4, 32))
+
+
+def _kv_args(**kw):
+    a = _lib.KvAppendArgs()
+    base = dict(num_layers=2, num_kv_heads=8, head_dim=128, page_size=16, prefix_len=100, num_accepted=5,
+                num_rows=40, pool_pages=64, page_table_len=8, node_ids=8, page_table=8, k_new=8, v_new=8,
+                k_pool=8, v_pool=8, new_stride_n=1024, new_stride_h=128, pool_stride_page=16384,
+                pool_stride_head=2048, pool_stride_tok=128)
+    base.update(kw)
+    for k, v in base.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("bad", [dict(page_size=12), dict(head_dim=100), dict(num_rows=0), dict(k_pool=None),
+                                 dict(new_stride_h=100), dict(prefix_len=-1), dict(page_table_len=6),
+                                 dict(pool_stride_tok=0)])
+def test_kv_append_rejects_bad_arguments(bad):
+    """Argument checks of d2sd_paged_kv_append happen before any GPU work."""
+    rc = _lib.lib.d2sd_paged_kv_append(C.byref(_kv_args(**bad)), None)
+    assert rc == 1, _lib.lib.d2sd_last_error()            # D2SD_ERR_INVALID_ARG
+    assert _lib.lib.d2sd_last_error().startswith(b"paged_kv_append")
+
+
+def test_kv_append_with_nothing_to_append_launches_nothing():
+    assert _lib.lib.d2sd_paged_kv_append(C.byref(_kv_args(num_accepted=0)), None) == 0
+    assert _lib.lib.d2sd_paged_kv_append(C.byref(_kv_args(num_layers=0)), None) == 0

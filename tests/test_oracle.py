@@ -310,3 +310,49 @@ def test_pack_mask_bits():
     assert p.shape == (2, 2)
     assert int(p[0, 0]) == (1 | (1 << 5) | (1 << 63)) and int(p[0, 1]) == 0
     assert int(p[1, 0]) == 0 and int(p[1, 1]) == (1 | (1 << 5))
+
+
+# ---- accepted-branch commit (generation/d3_generator.py:227-232) ----
+
+def _cat_form(pool, table, L, new, nodes, layout):
+    """The reference's own operation: cache = torch.cat([cache, k_win], dim=2)
+    on the contiguous view."""
+    return torch.cat([orc.gather_paged(pool, table, L, layout), new[torch.as_tensor(nodes, dtype=torch.long)]], 0)
+
+
+@pytest.mark.parametrize("layout", ["HND", "NHD"])
+@pytest.mark.parametrize("L,n,P", [(0, 5, 4), (3, 2, 2), (7, 9, 4), (16, 16, 16), (31, 1, 16)])
+def test_commit_equals_cat_and_touches_only_new_slots(layout, L, n, P):
+    g = torch.Generator().manual_seed(L * 131 + n)
+    hkv, d, rows = 2, 8, 12
+    pages_needed = (L + n + P - 1) // P
+    pool_pages = pages_needed + 3
+    shape = (pool_pages, hkv, P, d) if layout == "HND" else (pool_pages, P, hkv, d)
+    pool = torch.randn(shape, generator=g)
+    table = torch.randperm(pool_pages, generator=g)[:pages_needed].tolist()
+    new = torch.randn(rows, hkv, d, generator=g)
+    nodes = torch.randint(0, rows, (n,), generator=g).tolist()
+    out = orc.commit_accepted_ref(pool, table, L, new, nodes, layout)
+    assert torch.equal(orc.gather_paged(out, table, L + n, layout), _cat_form(pool, table, L, new, nodes, layout))
+    # nothing else changed: the old prefix, other pages, slots past the end
+    written = torch.zeros(shape[:3] if layout == "HND" else shape[:2], dtype=torch.bool)
+    for i in range(n):
+        t = L + i
+        if layout == "HND":
+            written[table[t // P], :, t % P] = True
+        else:
+            written[table[t // P], t % P] = True
+    keep = ~written
+    assert torch.equal(out[keep], pool[keep])
+
+
+def test_commit_known_answer_and_skipped_nodes():
+    # P = 2, prefix of 3 tokens: new tokens go to page table[1] slot 1, then table[2] slot 0
+    pool = torch.zeros(4, 1, 2, 1)                       # HND, Hkv 1, D 1
+    new = torch.tensor([[[10.]], [[20.]], [[30.]]])
+    out = orc.commit_accepted_ref(pool, [3, 1, 0], 3, new, [2, 0], "HND")
+    assert out[1, 0, 1, 0] == 30. and out[0, 0, 0, 0] == 10.
+    assert out.sum() == 40.
+    # a node id outside [0, rows) writes nothing (positions still advance)
+    out = orc.commit_accepted_ref(pool, [3, 1, 0], 3, new, [-1, 1], "HND")
+    assert out[1, 0, 1, 0] == 0. and out[0, 0, 0, 0] == 20. and out.sum() == 20.
