@@ -390,3 +390,33 @@ def test_hipgraph_replays_match_eager():
         for (o, l), (eo, el) in zip(outs, eager):
             assert torch.equal(o, eo) and torch.equal(l, el), f"replay {rep}"
         _ = (torch.randn(1000, device=DEV) * 2).sum().item()   # eager work between replays
+
+
+# ------------------------------------------- DTA draft reuse (model/dflash.py:92-133)
+def test_dta_draft_cascade_through_plan_run():
+    """The DTA draft's cascade (model/dflash.py:96-133; runner built with
+    causal=False, benchmark.py:46-55): every row's queries see the shared
+    [cache | context] keys and, non-causally, their own row's noise keys.  Over
+    the tree-level API this is one plan: the shared keys are the contiguous
+    prefix ([Hkv, L, D], the DynamicCache layout), the rows' noise tokens are
+    the suffix nodes, and the node mask is block-diagonal all-ones (each row a
+    fully visible group).  Matches the reference's row flow in the oracle."""
+    gen = torch.Generator().manual_seed(21)
+    bsz, q_len, hq, hkv, d, cache_len, ctx_len = 4, 16, 32, 8, 128, 700, 24
+    L = cache_len + ctx_len
+    q = bf16_randn(gen, bsz, q_len, hq, d)
+    kn, vn = bf16_randn(gen, bsz, q_len, hkv, d), bf16_randn(gen, bsz, q_len, hkv, d)
+    k_shared, v_shared = bf16_randn(gen, L, hkv, d), bf16_randn(gen, L, hkv, d)   # cat([cache, context])
+    o_ref, lse_ref = orc.cascade_verify_rows_ref(q, kn, vn, k_shared, v_shared, d ** -0.5, -1, None, causal=False)
+    n = bsz * q_len
+    mask = np.zeros((n, n), dtype=bool)
+    for b in range(bsz):
+        mask[b * q_len:(b + 1) * q_len, b * q_len:(b + 1) * q_len] = True
+    attn = d2sd.CascadeVerifyAttention(DEV)
+    attn.plan([0, n], [L], hq, hkv, d, tree_masks=[mask], page_size=0, kv_layout="HND")
+    kp = k_shared.transpose(0, 1).contiguous().to(DEV)      # [Hkv, L, D]
+    vp = v_shared.transpose(0, 1).contiguous().to(DEV)
+    o, lse = attn.run(q.reshape(n, hq, d).to(DEV), kn.reshape(n, hkv, d).to(DEV), vn.reshape(n, hkv, d).to(DEV),
+                      kp, vp)
+    torch.cuda.synchronize()
+    check_close(o.view(bsz, q_len, hq, d), o_ref, lse.view(bsz, q_len, hq), lse_ref, "dta draft")
