@@ -271,6 +271,80 @@ def measure_commit(args) -> int:
     return 0
 
 
+def measure_accept(args) -> int:
+    """Greedy acceptance walk (d2sd.GreedyAccept, generation/d3_generator.py:
+    204-225 at temperature 0) at Qwen3-8B shape: the d3 verify tree's unique
+    nodes' logits [N, 151936] bf16, drafts following the target for a few
+    positions.  Beside it, the reference's own loop on the same GPU tensors
+    (host-driven: nonzero(), argmax, sum() per accepted token).  One JSON line."""
+    import numpy as np
+    import torch
+    import d2sd
+    from d2sd import tree as dtree
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    vocab = 151936
+    tr = dtree.d3_verify_tree(np.random.default_rng(args.seed).uniform(size=15))
+    N, lb = tr.num_nodes, tr.node_index.shape[1]
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    logits = torch.randn(N, vocab, generator=g, device=dev, dtype=torch.bfloat16)
+    node_index = torch.as_tensor(tr.node_index, dtype=torch.int32, device=dev)
+    am = logits.argmax(-1)
+    drafts = torch.randint(0, vocab, tuple(node_index.shape), generator=g, device=dev)
+    keep = [9, 14, 3, 20, 1]
+    for r in range(node_index.shape[0]):
+        for pos in range(1, keep[r]):
+            drafts[r, pos] = am[node_index[r, pos - 1]]
+    acc = d2sd.GreedyAccept(N, vocab, lb, dev)
+    acc(logits, node_index, drafts)
+    torch.cuda.synchronize()
+    per_graph = 32
+    ga = d2sd.HipGraph()
+    with ga.capture():
+        for _ in range(per_graph):
+            acc(logits, node_index, drafts)
+    us = time_graph(ga, max(3, args.kernel_reps // 4), torch) * 1e3 / per_graph
+    n = int(acc.result[0])
+    # the reference loop (d3_generator.py:204-225), rows' logits gathered once
+    out_logits = logits[node_index.long()]
+    def ref_loop():
+        valid_blocks = torch.ones(out_logits.shape[0], device=dev)
+        acceptance_length = 0
+        accept = []
+        while True:
+            valid_block = (valid_blocks > 0).nonzero(as_tuple=True)[0][0]
+            tok = torch.argmax(out_logits[valid_block, acceptance_length, :].unsqueeze(0), dim=-1)
+            acceptance_length += 1
+            accept.append(tok)
+            if acceptance_length == lb:
+                break
+            valid_blocks = torch.where(drafts[:, acceptance_length] == tok, valid_blocks, 0)
+            if valid_blocks.sum() == 0.:
+                break
+        return acceptance_length
+    for _ in range(3):
+        n_ref = ref_loop()
+    torch.cuda.synchronize()
+    reps = 20
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        n_ref = ref_loop()
+    torch.cuda.synchronize()
+    ref_us = (time.perf_counter() - t0) / reps * 1e6
+    moved = N * vocab * 2
+    print(json.dumps({
+        "metric": "greedy acceptance walk µs/step (d3 tree, Qwen3 vocab)",
+        "value": us, "unit": "us", "higher_is_better": False, "nodes": N, "vocab": vocab,
+        "acceptance_length": n, "reference_acceptance_length": n_ref,
+        "bytes_read": moved, "achieved_gbps": moved / (us * 1e-6) / 1e9,
+        "hbm_frac": moved / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS,
+        "reference_host_loop_us": ref_us, "speedup_vs_reference": ref_us / us,
+        "config": {"workload": "config 2 verify step acceptance", "rows": int(node_index.shape[0]), "row_len": lb},
+    }))
+    return 0
+
+
 def read_traffic():
     """traffic_bytes_per_launch from TRAFFIC_FILE, or None."""
     try:
@@ -300,9 +374,13 @@ def main() -> int:
     ap.add_argument("--commit", action="store_true",
                     help="time the accepted-branch KV commit instead (one JSON line)")
     ap.add_argument("--accepted", type=int, default=20, help="accepted tokens per step for --commit")
+    ap.add_argument("--accept", action="store_true",
+                    help="time the greedy acceptance walk instead (one JSON line)")
     args = ap.parse_args()
     if args.commit:
         return measure_commit(args)
+    if args.accept:
+        return measure_accept(args)
     if args.traffic_workload:
         return traffic_workload(args)
     if args.measure_traffic:

@@ -449,6 +449,52 @@ int d2sd_cascade_run(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_
   return d2sd_cascade_merge(info, a, stream);
 }
 
+// Greedy acceptance walk (replaces generation/d3_generator.py:204-225 at temperature 0).
+size_t d2sd_greedy_accept_workspace_size(int num_nodes, int vocab) {
+  if (num_nodes <= 0 || vocab <= 0) return 0;
+  int chunks = 1, chunk_len = 8;
+  d2sd::greedy_accept_chunks(num_nodes, vocab, chunks, chunk_len);
+  return (size_t)num_nodes * chunks * sizeof(unsigned long long);
+}
+
+int d2sd_greedy_accept(const d2sd_greedy_accept_args* a, d2sd_stream_t stream) {
+  g_last_error.clear();
+  if (!a) return fail(D2SD_ERR_INVALID_ARG, "greedy_accept: null args");
+  if (a->num_rows < 1 || a->num_rows > 64)
+    return fail(D2SD_ERR_INVALID_ARG, "greedy_accept: num_rows must be in [1, 64]");
+  if (a->row_len < 1 || a->num_nodes < 1 || a->vocab < 1)
+    return fail(D2SD_ERR_INVALID_ARG, "greedy_accept: row_len, num_nodes and vocab must be positive");
+  if (a->num_nodes > d2sd::kAcceptMaxNodes || a->num_rows * a->row_len > d2sd::kAcceptMaxCells)
+    return fail(D2SD_ERR_UNSUPPORTED, "greedy_accept: at most 4096 nodes and 2048 row positions");
+  if (a->logits_dtype != D2SD_DTYPE_BF16 && a->logits_dtype != D2SD_DTYPE_F32)
+    return fail(D2SD_ERR_INVALID_ARG, "greedy_accept: logits_dtype must be D2SD_DTYPE_BF16 or D2SD_DTYPE_F32");
+  if (a->logits_stride < a->vocab)
+    return fail(D2SD_ERR_INVALID_ARG, "greedy_accept: logits_stride must be >= vocab");
+  if (!a->logits || !a->node_index || !a->draft_ids || !a->accept_ids || !a->accept_nodes || !a->result ||
+      !a->workspace)
+    return fail(D2SD_ERR_INVALID_ARG, "greedy_accept: null pointer");
+  if (a->workspace_bytes < d2sd_greedy_accept_workspace_size(a->num_nodes, a->vocab))
+    return fail(D2SD_ERR_WORKSPACE, "greedy_accept: workspace too small (need " +
+                                        std::to_string(d2sd_greedy_accept_workspace_size(a->num_nodes, a->vocab)) +
+                                        " bytes)");
+  d2sd::AcceptParams p{};
+  p.logits = a->logits;
+  p.logits_stride = a->logits_stride;
+  p.node_index = a->node_index;
+  p.draft_ids = (const long long*)a->draft_ids;
+  p.accept_ids = (long long*)a->accept_ids;
+  p.accept_nodes = a->accept_nodes;
+  p.result = a->result;
+  p.keys = (unsigned long long*)a->workspace;
+  p.num_rows = a->num_rows;
+  p.row_len = a->row_len;
+  p.num_nodes = a->num_nodes;
+  p.vocab = a->vocab;
+  d2sd::greedy_accept_chunks(a->num_nodes, a->vocab, p.chunks, p.chunk_len);
+  hipError_t e = d2sd::launch_greedy_accept(p, a->logits_dtype == D2SD_DTYPE_BF16, (hipStream_t)stream);
+  return e == hipSuccess ? D2SD_OK : fail_hip(e, "greedy_accept launch");
+}
+
 // Accepted-branch KV commit (replaces generation/d3_generator.py:227-232).
 int d2sd_paged_kv_append(const d2sd_kv_append_args* a, d2sd_stream_t stream) {
   g_last_error.clear();
@@ -495,6 +541,7 @@ int d2sd_paged_kv_append(const d2sd_kv_append_args* a, d2sd_stream_t stream) {
   p.num_accepted = a->num_accepted;
   p.num_rows = a->num_rows;
   p.pool_pages = a->pool_pages;
+  p.num_accepted_dev = a->num_accepted_dev;
   hipError_t e = d2sd::launch_kv_append(p, (hipStream_t)stream);
   return e == hipSuccess ? D2SD_OK : fail_hip(e, "paged_kv_append launch");
 }

@@ -178,6 +178,25 @@ struct KvAppendParams {
   int prefix_len, num_accepted;
   int num_rows;    // rows of k_new / v_new (node ids outside are skipped)
   int pool_pages;  // pages of each pool (page ids outside are skipped)
+  const int* num_accepted_dev;  // nullable: the count is read here (clamped to [0, num_accepted])
+};
+
+// ---------------------------------------------------------------------------
+// Greedy acceptance walk (accept.hip).
+// ---------------------------------------------------------------------------
+constexpr int kAcceptMaxNodes = 4096;  // logits rows of one walk
+constexpr int kAcceptMaxCells = 2048;  // candidate rows x positions
+struct AcceptParams {
+  const void* logits;             // [num_nodes, vocab] bf16 or fp32, row stride logits_stride
+  long long logits_stride;        // elements
+  const int* node_index;          // [num_rows, row_len]
+  const long long* draft_ids;     // [num_rows, row_len]
+  long long* accept_ids;          // out [row_len]
+  int* accept_nodes;              // out [row_len]
+  int* result;                    // out [2]: acceptance length, final valid row
+  unsigned long long* keys;       // workspace [num_nodes, chunks]
+  int num_rows, row_len, num_nodes, vocab;
+  int chunks, chunk_len;          // vocabulary chunks per node (chunk_len a multiple of 8)
 };
 
 }  // namespace d2sd

@@ -21,6 +21,7 @@ namespace d2sd {
 
 __global__ __launch_bounds__(256) void kv_append_kernel(const KvAppendParams p) {
   const int i = blockIdx.x, layer = blockIdx.y;
+  if (p.num_accepted_dev && i >= min(max(*p.num_accepted_dev, 0), p.num_accepted)) return;
   const int node = p.node_ids[i];
   if (node < 0 || node >= p.num_rows) return;  // not a row of k_new / v_new: nothing written
   const int t = p.prefix_len + i;              // cache position of the token

@@ -55,6 +55,11 @@ hipError_t launch_verify_merge(const VerifyParams& p, int head_dim, int rows, in
 // ---- accepted-branch KV commit (kv_append.hip) ----
 hipError_t launch_kv_append(const KvAppendParams& p, hipStream_t s);
 
+// ---- greedy acceptance walk (accept.hip) ----
+hipError_t launch_greedy_accept(const AcceptParams& p, bool bf16, hipStream_t s);
+// vocabulary chunks per node of the argmax pass
+void greedy_accept_chunks(int num_nodes, int vocab, int& chunks, int& chunk_len);
+
 // ---- single-source drop-ins (attention.hip) ----
 int choose_waves(int rows_per_head_max);
 int blocks_per_cu(int waves);

@@ -18,6 +18,8 @@ D2SD_MASK_CAUSAL = 1
 D2SD_MASK_TREE = 2
 D2SD_MERGE_LAUNCH = 0
 D2SD_MERGE_LAST_PRODUCER = 1
+D2SD_DTYPE_BF16 = 0
+D2SD_DTYPE_F32 = 1
 
 # Every symbol include/d2sd.h declares.
 EXPORTED_SYMBOLS = (
@@ -36,6 +38,8 @@ EXPORTED_SYMBOLS = (
     "d2sd_cascade_attention",
     "d2sd_cascade_merge",
     "d2sd_paged_kv_append",
+    "d2sd_greedy_accept_workspace_size",
+    "d2sd_greedy_accept",
 )
 
 
@@ -139,6 +143,26 @@ class KvAppendArgs(C.Structure):
         ("pool_stride_page", C.c_int64),
         ("pool_stride_head", C.c_int64),
         ("pool_stride_tok", C.c_int64),
+        ("num_accepted_dev", C.c_void_p),
+    ]
+
+
+class AcceptArgs(C.Structure):
+    _fields_ = [
+        ("num_rows", C.c_int),
+        ("row_len", C.c_int),
+        ("num_nodes", C.c_int),
+        ("vocab", C.c_int),
+        ("logits_dtype", C.c_int),
+        ("logits", C.c_void_p),
+        ("logits_stride", C.c_int64),
+        ("node_index", C.c_void_p),
+        ("draft_ids", C.c_void_p),
+        ("accept_ids", C.c_void_p),
+        ("accept_nodes", C.c_void_p),
+        ("result", C.c_void_p),
+        ("workspace", C.c_void_p),
+        ("workspace_bytes", C.c_size_t),
     ]
 
 
@@ -185,6 +209,10 @@ def _load() -> C.CDLL:
         fn.argtypes = [C.POINTER(PlanInfo), C.POINTER(RunArgs), vp]
     lib.d2sd_paged_kv_append.restype = i32
     lib.d2sd_paged_kv_append.argtypes = [C.POINTER(KvAppendArgs), vp]
+    lib.d2sd_greedy_accept_workspace_size.restype = sz
+    lib.d2sd_greedy_accept_workspace_size.argtypes = [i32, i32]
+    lib.d2sd_greedy_accept.restype = i32
+    lib.d2sd_greedy_accept.argtypes = [C.POINTER(AcceptArgs), vp]
     return lib
 
 

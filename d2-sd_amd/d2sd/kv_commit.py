@@ -80,10 +80,12 @@ class PagedKVCommit:
         self.page_size = page_size
 
     def commit(self, page_table: torch.Tensor, prefix_len: int, node_ids: torch.Tensor,
-               num_accepted: int | None = None) -> None:
+               num_accepted: int | None = None, num_accepted_dev: torch.Tensor | None = None) -> None:
         """Writes rows node_ids[:num_accepted] of every layer's k_new / v_new to
         cache positions prefix_len .. prefix_len + num_accepted - 1 of the
-        request whose pages are page_table (device int32, covering them)."""
+        request whose pages are page_table (device int32, covering them).
+        num_accepted_dev (device int32, e.g. GreedyAccept's result) makes the
+        kernel read the count from the device, capped at num_accepted."""
         if page_table.dtype != torch.int32 or node_ids.dtype != torch.int32:
             raise TypeError("page_table and node_ids must be int32")
         if not (page_table.is_contiguous() and node_ids.is_contiguous()):
@@ -99,5 +101,11 @@ class PagedKVCommit:
         a.node_ids = node_ids.data_ptr()
         a.page_table = page_table.data_ptr()
         a.page_table_len = page_table.numel()
+        if num_accepted_dev is not None:
+            if num_accepted_dev.dtype != torch.int32 or num_accepted_dev.device != page_table.device:
+                raise TypeError("num_accepted_dev must be a device int32 tensor")
+            a.num_accepted_dev = num_accepted_dev.data_ptr()
+        else:
+            a.num_accepted_dev = None
         check(lib.d2sd_paged_kv_append(C.byref(a), C.c_void_p(torch.cuda.current_stream().cuda_stream)),
               "paged_kv_append")

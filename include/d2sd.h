@@ -281,9 +281,48 @@ typedef struct {
   const uint64_t* v_pool;
   int64_t new_stride_n, new_stride_h;                         /* elements */
   int64_t pool_stride_page, pool_stride_head, pool_stride_tok; /* elements */
+  const int32_t* num_accepted_dev; /* nullable: device count read by the kernel
+                                      (e.g. d2sd_greedy_accept's result[0]),
+                                      clamped to [0, num_accepted] */
 } d2sd_kv_append_args;
 
 int d2sd_paged_kv_append(const d2sd_kv_append_args* args, d2sd_stream_t stream);
+
+/* ----------------------------------------------------------------------
+ * Greedy acceptance walk of the verify tree, on the device.
+ * Replaces generation/d3_generator.py:204-225 at temperature 0 (greedy
+ * sampling is torch.argmax, model/utils.py:28-33, first index on ties):
+ * with every row valid, step a takes the first valid row vb, accepts the
+ * argmax of the logits of its node node_index[vb][a], and keeps the rows
+ * whose draft token at position a + 1 equals it; the walk ends when no row
+ * is valid or after row_len tokens.  Writes accept_ids[0..n) (token ids),
+ * accept_nodes[0..n) (their nodes, the rows of the step's suffix K/V that
+ * the KV commit appends), result[0] = n (acceptance_length) and result[1] =
+ * the final valid row (valid_block).  Logits of every node are read once
+ * (HBM bound); no host synchronisation.  A node id outside [0, num_nodes)
+ * ends the walk.  Logits must be NaN-free.
+ * ---------------------------------------------------------------------- */
+#define D2SD_DTYPE_BF16 0
+#define D2SD_DTYPE_F32 1
+typedef struct {
+  int num_rows;               /* candidate rows (bsz), <= 64 */
+  int row_len;                /* positions per row (block_size_2); num_rows * row_len <= 2048 */
+  int num_nodes;              /* rows of logits, <= 4096 */
+  int vocab;
+  int logits_dtype;           /* D2SD_DTYPE_* */
+  const void* logits;         /* device [num_nodes, vocab], row stride logits_stride elements */
+  int64_t logits_stride;
+  const int32_t* node_index;  /* device [num_rows, row_len] */
+  const int64_t* draft_ids;   /* device [num_rows, row_len]: the rows' draft tokens (block_output_ids) */
+  int64_t* accept_ids;        /* device out [row_len] */
+  int32_t* accept_nodes;      /* device out [row_len] */
+  int32_t* result;            /* device out [2]: acceptance_length, valid_block */
+  void* workspace;            /* device, d2sd_greedy_accept_workspace_size bytes */
+  size_t workspace_bytes;
+} d2sd_greedy_accept_args;
+
+size_t d2sd_greedy_accept_workspace_size(int num_nodes, int vocab);
+int d2sd_greedy_accept(const d2sd_greedy_accept_args* args, d2sd_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -17,6 +17,7 @@ It restates the reference's verify-attention algorithm on the CPU in float64
   verification.py:127-176 as a whole (row layout)  cascade_verify_rows_ref
   the same over unique tree nodes, single pass     cascade_tree_ref
   d3_generator.py:227-232 (accepted-branch commit) commit_accepted_ref
+  d3_generator.py:204-225 (greedy acceptance walk) greedy_accept_ref
 
 FlashInfer itself (flashinfer-python>=0.2.0, requirements.txt:13) is not
 vendored in the reference and not installed here.  Its published algorithm for
@@ -251,8 +252,40 @@ def commit_accepted_ref(pool: Tensor, page_table: List[int], prefix_len: int, ne
     return out
 
 
+def greedy_accept_ref(node_logits: Tensor, node_index, draft_ids) -> Tuple[List[int], List[int], int, int]:
+    """The acceptance loop of generation/d3_generator.py:204-225 at temperature
+    0 (sample() is torch.argmax, model/utils.py:28-33), literally, on the rows'
+    logits output_logits[row, pos] = node_logits[node_index[row][pos]] and the
+    rows' draft tokens block_output_ids = draft_ids.  Returns (accept_ids,
+    accepted nodes, acceptance_length, valid_block)."""
+    node_index = torch.as_tensor(node_index, dtype=torch.long)
+    block_output_ids = torch.as_tensor(draft_ids, dtype=torch.long)
+    bsz, block_size_2 = node_index.shape
+    output_logits = node_logits[node_index]                  # [bsz, Lb, V]
+    valid_blocks = torch.ones(bsz)
+    acceptance_length = 0
+    accept_ids: List[int] = []
+    nodes: List[int] = []
+    while True:
+        valid_block = int((valid_blocks > 0).nonzero(as_tuple=True)[0][0])
+        logit = output_logits[valid_block, acceptance_length, :]
+        sampled_token = int(torch.argmax(logit))
+        nodes.append(int(node_index[valid_block, acceptance_length]))
+        acceptance_length += 1
+        accept_ids.append(sampled_token)
+        if acceptance_length == block_size_2:
+            break
+        next_tokens = block_output_ids[:, acceptance_length]
+        valid_mask = next_tokens == sampled_token
+        valid_blocks = torch.where(valid_mask, valid_blocks, torch.zeros_like(valid_blocks))
+        if valid_blocks.sum() == 0.:
+            break
+    return accept_ids, nodes, acceptance_length, valid_block
+
+
 __all__ = [
     "attention_ref", "attention_sdpa_ref", "causal_mask", "single_prefill_ref", "merge_state_ref",
     "sink_rescale_ref", "window_prefix_ref", "cascade_verify_rows_ref", "cascade_tree_ref",
     "ancestor_mask_from_rows", "fp8_dequant_ref", "gather_paged", "commit_accepted_ref",
+    "greedy_accept_ref",
 ]

@@ -292,3 +292,28 @@ def test_kv_append_rejects_bad_arguments(bad):
 def test_kv_append_with_nothing_to_append_launches_nothing():
     assert _lib.lib.d2sd_paged_kv_append(C.byref(_kv_args(num_accepted=0)), None) == 0
     assert _lib.lib.d2sd_paged_kv_append(C.byref(_kv_args(num_layers=0)), None) == 0
+
+
+@pytest.mark.parametrize("nodes,vocab", [(150, 151936), (1, 7), (1, 151936), (4000, 32000)])
+def test_greedy_accept_workspace_covers_the_chunks(nodes, vocab):
+    ws = _lib.lib.d2sd_greedy_accept_workspace_size(nodes, vocab)
+    assert ws % (8 * nodes) == 0
+    chunks = ws // (8 * nodes)
+    assert 1 <= chunks and chunks * 1024 <= max(vocab + 1023, 1024) + 8 * chunks
+
+
+def test_greedy_accept_rejects_bad_arguments():
+    a = _lib.AcceptArgs()
+    a.num_rows, a.row_len, a.num_nodes, a.vocab, a.logits_dtype = 5, 32, 150, 1000, 0
+    a.logits_stride = 1000
+    for f in ("logits", "node_index", "draft_ids", "accept_ids", "accept_nodes", "result", "workspace"):
+        setattr(a, f, 8)
+    a.workspace_bytes = 1 << 30
+    for field, bad in (("num_rows", 65), ("logits_dtype", 7), ("logits_stride", 999), ("workspace", None)):
+        old = getattr(a, field)
+        setattr(a, field, bad)
+        assert _lib.lib.d2sd_greedy_accept(C.byref(a), None) == 1
+        assert _lib.lib.d2sd_last_error().startswith(b"greedy_accept")
+        setattr(a, field, old)
+    a.workspace_bytes = 8
+    assert _lib.lib.d2sd_greedy_accept(C.byref(a), None) == 3   # D2SD_ERR_WORKSPACE

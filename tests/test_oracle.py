@@ -356,3 +356,42 @@ def test_commit_known_answer_and_skipped_nodes():
     # a node id outside [0, rows) writes nothing (positions still advance)
     out = orc.commit_accepted_ref(pool, [3, 1, 0], 3, new, [-1, 1], "HND")
     assert out[1, 0, 1, 0] == 0. and out[0, 0, 0, 0] == 20. and out.sum() == 20.
+
+
+# ---- greedy acceptance walk (generation/d3_generator.py:204-225) ----
+
+def _chain_logits(tokens_per_node, vocab=11):
+    """Logits whose argmax at node j is tokens_per_node[j]."""
+    lg = torch.zeros(len(tokens_per_node), vocab)
+    for j, t in enumerate(tokens_per_node):
+        lg[j, t] = 1.0
+    return lg
+
+
+def test_accept_full_agreement_accepts_every_position():
+    # one chain of 4 nodes; the draft row follows the target's argmax
+    lg = _chain_logits([5, 6, 7, 8])
+    ids, nodes, n, vb = orc.greedy_accept_ref(lg, [[0, 1, 2, 3]], [[9, 5, 6, 7]])
+    assert (ids, nodes, n, vb) == ([5, 6, 7, 8], [0, 1, 2, 3], 4, 0)
+
+
+def test_accept_switches_to_the_first_matching_row():
+    # rows share node 0; row 0 drafts token 3 at position 1 (rejected), row 1
+    # drafts 4 (accepted: argmax of node 0); then row 1's node 2 gives 2, and
+    # its draft at position 2 is 7 (rejected) -> length 2, valid_block 1
+    lg = _chain_logits([4, 9, 2])
+    ids, nodes, n, vb = orc.greedy_accept_ref(lg, [[0, 1, 1], [0, 2, 2]], [[0, 3, 0], [0, 4, 7]])
+    assert (ids, nodes, n, vb) == ([4, 2], [0, 2], 2, 1)
+
+
+def test_accept_first_position_always_accepted():
+    lg = _chain_logits([1, 2])
+    ids, nodes, n, vb = orc.greedy_accept_ref(lg, [[0, 1]], [[0, 5]])
+    assert (ids, n, vb) == ([1], 1, 0)
+
+
+def test_accept_argmax_ties_take_the_first_index():
+    lg = torch.zeros(1, 8)
+    lg[0, 3] = lg[0, 6] = 2.0
+    ids, _, n, _ = orc.greedy_accept_ref(lg, [[0]], [[0]])
+    assert ids == [3] and n == 1
