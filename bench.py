@@ -345,6 +345,73 @@ def measure_accept(args) -> int:
     return 0
 
 
+def measure_qk_rope(args) -> int:
+    """QK RMSNorm + RoPE (d2sd.qk_norm_rope, generation/verification.py:113-123)
+    for the 36 layers of a Qwen3-8B verify step over the d3 tree's nodes, in
+    one graph; beside it the reference's form on the same GPU (transformers
+    Qwen3RMSNorm for q / k, the transposes, rotate_half RoPE).  One JSON line."""
+    import numpy as np
+    import torch
+    import d2sd
+    from d2sd import tree as dtree
+    from transformers.models.qwen3 import modeling_qwen3 as mq
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    layers, hq, hkv, d = args.layers, 32, 8, 128
+    T = dtree.d3_verify_tree(np.random.default_rng(args.seed).uniform(size=15)).num_nodes
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    qkv = [torch.randn(T, hq + 2 * hkv, d, generator=g, device=dev, dtype=torch.bfloat16) for _ in range(layers)]
+    wq = [(torch.rand(d, generator=g, device=dev) + 0.5).to(torch.bfloat16) for _ in range(layers)]
+    wk = [(torch.rand(d, generator=g, device=dev) + 0.5).to(torch.bfloat16) for _ in range(layers)]
+    pos = torch.arange(T, device=dev) + 4096
+    inv = 1.0 / (1e6 ** (torch.arange(0, d, 2, device=dev).float() / d))
+    ang = pos[:, None].float() * inv[None]
+    emb = torch.cat([ang, ang], -1)
+    cos, sin = emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16)
+    def ours():
+        for l in range(layers):
+            d2sd.qk_norm_rope(qkv[l][:, :hq], qkv[l][:, hq:hq + hkv], wq[l], wk[l], cos, sin, 1e-6)
+    ours()
+    torch.cuda.synchronize()
+    gr = d2sd.HipGraph()
+    with gr.capture():
+        ours()
+    us = time_graph(gr, max(5, args.kernel_reps), torch) * 1e3
+    qn, kn = mq.Qwen3RMSNorm(d, eps=1e-6).to(dev, torch.bfloat16), mq.Qwen3RMSNorm(d, eps=1e-6).to(dev, torch.bfloat16)
+    def reference():
+        outs = []
+        for l in range(layers):
+            q = qkv[l][None, :, :hq]                           # [1, T, Hq, D] as q.view(bsz, seq, H, D)
+            k = qkv[l][None, :, hq:hq + hkv]
+            q, k = qn(q).transpose(1, 2), kn(k).transpose(1, 2)
+            q, k = mq.apply_rotary_pos_emb(q, k, cos[None], sin[None])
+            outs.append((q.transpose(1, 2).contiguous(), k.transpose(1, 2).contiguous()))
+        return outs
+    with torch.no_grad():
+        for _ in range(3):
+            reference()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 20
+        e0.record()
+        for _ in range(reps):
+            reference()
+        e1.record()
+        torch.cuda.synchronize()
+    ref_us = e0.elapsed_time(e1) / reps * 1e3
+    moved = layers * (2 * T * (hq + hkv) * d * 2 + 2 * T * d * 2)
+    print(json.dumps({
+        "metric": "QK RMSNorm + RoPE µs/step (36 layers, Qwen3-8B shape, d3 tree nodes)",
+        "value": us, "unit": "us", "higher_is_better": False, "tokens": T,
+        "bytes_moved": moved, "achieved_gbps": moved / (us * 1e-6) / 1e9,
+        "hbm_frac": moved / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS,
+        "reference_torch_us": ref_us, "speedup_vs_reference": ref_us / us,
+        "config": {"workload": "config 2 verify step QK norm + RoPE", "layers": layers},
+    }))
+    return 0
+
+
 def read_traffic():
     """traffic_bytes_per_launch from TRAFFIC_FILE, or None."""
     try:
@@ -376,11 +443,15 @@ def main() -> int:
     ap.add_argument("--accepted", type=int, default=20, help="accepted tokens per step for --commit")
     ap.add_argument("--accept", action="store_true",
                     help="time the greedy acceptance walk instead (one JSON line)")
+    ap.add_argument("--qk-rope", action="store_true",
+                    help="time the fused QK RMSNorm + RoPE instead (one JSON line)")
     args = ap.parse_args()
     if args.commit:
         return measure_commit(args)
     if args.accept:
         return measure_accept(args)
+    if args.qk_rope:
+        return measure_qk_rope(args)
     if args.traffic_workload:
         return traffic_workload(args)
     if args.measure_traffic:

@@ -449,6 +449,41 @@ int d2sd_cascade_run(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_
   return d2sd_cascade_merge(info, a, stream);
 }
 
+// QK RMSNorm + RoPE (replaces generation/verification.py:113-123).
+int d2sd_qk_norm_rope(const d2sd_qk_norm_rope_args* a, d2sd_stream_t stream) {
+  g_last_error.clear();
+  if (!a) return fail(D2SD_ERR_INVALID_ARG, "qk_norm_rope: null args");
+  if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256)
+    return fail(D2SD_ERR_UNSUPPORTED, "qk_norm_rope: head_dim must be 64, 128 or 256");
+  if (a->num_tokens < 0 || a->num_qo_heads < 0 || a->num_kv_heads < 0)
+    return fail(D2SD_ERR_INVALID_ARG, "qk_norm_rope: negative count");
+  if ((a->num_qo_heads > 0 && !a->q) || (a->num_kv_heads > 0 && !a->k))
+    return fail(D2SD_ERR_INVALID_ARG, "qk_norm_rope: null q or k");
+  if ((a->cos == nullptr) != (a->sin == nullptr))
+    return fail(D2SD_ERR_INVALID_ARG, "qk_norm_rope: cos and sin go together");
+  if (!(a->eps >= 0.f)) return fail(D2SD_ERR_INVALID_ARG, "qk_norm_rope: eps must be >= 0");
+  d2sd::QkRopeParams p{};
+  p.q = a->q;
+  p.k = a->k;
+  p.q_stride_n = a->q_stride_n;
+  p.q_stride_h = a->q_stride_h;
+  p.k_stride_n = a->k_stride_n;
+  p.k_stride_h = a->k_stride_h;
+  p.q_norm = a->q_norm;
+  p.k_norm = a->k_norm;
+  p.cos = a->cos;
+  p.sin = a->sin;
+  p.cs_stride = a->cs_stride;
+  p.eps = a->eps;
+  p.num_tokens = a->num_tokens;
+  p.num_qo_heads = a->num_qo_heads;
+  p.num_kv_heads = a->num_kv_heads;
+  p.head_dim = a->head_dim;
+  p.half_cos = a->half_cos ? 1 : 0;
+  hipError_t e = d2sd::launch_qk_norm_rope(p, (hipStream_t)stream);
+  return e == hipSuccess ? D2SD_OK : fail_hip(e, "qk_norm_rope launch");
+}
+
 // Greedy acceptance walk (replaces generation/d3_generator.py:204-225 at temperature 0).
 size_t d2sd_greedy_accept_workspace_size(int num_nodes, int vocab) {
   if (num_nodes <= 0 || vocab <= 0) return 0;

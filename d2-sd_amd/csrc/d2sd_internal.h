@@ -184,6 +184,23 @@ struct KvAppendParams {
 // ---------------------------------------------------------------------------
 // Greedy acceptance walk (accept.hip).
 // ---------------------------------------------------------------------------
+// ---------------------------------------------------------------------------
+// QK RMSNorm + RoPE (qk_rope.hip).
+// ---------------------------------------------------------------------------
+struct QkRopeParams {
+  void* q;                  // bf16 [tokens, Hq, D], head_dim contiguous (in place)
+  void* k;                  // bf16 [tokens, Hkv, D]
+  long long q_stride_n, q_stride_h, k_stride_n, k_stride_h;  // elements
+  const void* q_norm;       // bf16 [D] RMSNorm weights (nullable: no norm)
+  const void* k_norm;
+  const void* cos;          // bf16 [tokens, D or D/2] (nullable: no rotation)
+  const void* sin;
+  long long cs_stride;      // elements between tokens of cos / sin
+  float eps;
+  int num_tokens, num_qo_heads, num_kv_heads, head_dim;
+  int half_cos;             // cos / sin hold D/2 columns
+};
+
 constexpr int kAcceptMaxNodes = 4096;  // logits rows of one walk
 constexpr int kAcceptMaxCells = 2048;  // candidate rows x positions
 struct AcceptParams {

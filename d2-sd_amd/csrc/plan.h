@@ -55,6 +55,9 @@ hipError_t launch_verify_merge(const VerifyParams& p, int head_dim, int rows, in
 // ---- accepted-branch KV commit (kv_append.hip) ----
 hipError_t launch_kv_append(const KvAppendParams& p, hipStream_t s);
 
+// ---- QK RMSNorm + RoPE (qk_rope.hip) ----
+hipError_t launch_qk_norm_rope(const QkRopeParams& p, hipStream_t s);
+
 // ---- greedy acceptance walk (accept.hip) ----
 hipError_t launch_greedy_accept(const AcceptParams& p, bool bf16, hipStream_t s);
 // vocabulary chunks per node of the argmax pass

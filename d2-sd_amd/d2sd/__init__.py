@@ -11,7 +11,8 @@ All device work runs hand-written HIP kernels in libd2sd.so (C ABI:
 include/d2sd.h); importing raises if the library has not been built.
 """
 from ._lib import LIB_PATH, version
-from .ops import local_attention_merge, merge_state, merge_state_in_place, single_prefill_with_kv_cache
+from .ops import (local_attention_merge, merge_state, merge_state_in_place, qk_norm_rope,
+                  single_prefill_with_kv_cache)
 from .graph import HipGraph
 from .cascade_graph import CascadeGraphRunner
 from .cascade import CascadeVerifyAttention
@@ -21,6 +22,6 @@ from . import tree
 
 __all__ = [
     "LIB_PATH", "version", "single_prefill_with_kv_cache", "merge_state_in_place", "merge_state",
-    "local_attention_merge", "HipGraph", "CascadeGraphRunner", "CascadeVerifyAttention", "PagedKVCommit", "GreedyAccept",
+    "local_attention_merge", "qk_norm_rope", "HipGraph", "CascadeGraphRunner", "CascadeVerifyAttention", "PagedKVCommit", "GreedyAccept",
     "tree",
 ]

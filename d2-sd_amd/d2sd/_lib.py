@@ -40,6 +40,7 @@ EXPORTED_SYMBOLS = (
     "d2sd_paged_kv_append",
     "d2sd_greedy_accept_workspace_size",
     "d2sd_greedy_accept",
+    "d2sd_qk_norm_rope",
 )
 
 
@@ -147,6 +148,28 @@ class KvAppendArgs(C.Structure):
     ]
 
 
+class QkRopeArgs(C.Structure):
+    _fields_ = [
+        ("q", C.c_void_p),
+        ("k", C.c_void_p),
+        ("q_stride_n", C.c_int64),
+        ("q_stride_h", C.c_int64),
+        ("k_stride_n", C.c_int64),
+        ("k_stride_h", C.c_int64),
+        ("q_norm", C.c_void_p),
+        ("k_norm", C.c_void_p),
+        ("cos", C.c_void_p),
+        ("sin", C.c_void_p),
+        ("cs_stride", C.c_int64),
+        ("eps", C.c_float),
+        ("num_tokens", C.c_int),
+        ("num_qo_heads", C.c_int),
+        ("num_kv_heads", C.c_int),
+        ("head_dim", C.c_int),
+        ("half_cos", C.c_int),
+    ]
+
+
 class AcceptArgs(C.Structure):
     _fields_ = [
         ("num_rows", C.c_int),
@@ -213,6 +236,8 @@ def _load() -> C.CDLL:
     lib.d2sd_greedy_accept_workspace_size.argtypes = [i32, i32]
     lib.d2sd_greedy_accept.restype = i32
     lib.d2sd_greedy_accept.argtypes = [C.POINTER(AcceptArgs), vp]
+    lib.d2sd_qk_norm_rope.restype = i32
+    lib.d2sd_qk_norm_rope.argtypes = [C.POINTER(QkRopeArgs), vp]
     return lib
 
 

@@ -181,3 +181,45 @@ def local_attention_merge(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out
 
 __all__ = ["single_prefill_with_kv_cache", "merge_state_in_place", "merge_state", "local_attention_merge"]
 _ = _lib
+
+
+def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, q_norm: Optional[torch.Tensor] = None,
+                 k_norm: Optional[torch.Tensor] = None, cos: Optional[torch.Tensor] = None,
+                 sin: Optional[torch.Tensor] = None, eps: float = 1e-6) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Per-head RMSNorm (weights q_norm / k_norm, bf16 [D]) then rotary
+    embedding (cos / sin bf16 [tokens, D], or [tokens, D/2] for the GPT-OSS
+    form), in place on q [tokens, Hq, D] and k [tokens, Hkv, D] (bf16).
+    Replaces generation/verification.py:113-123 (q_norm / k_norm, transposes,
+    _apply_rotary_pos_emb_qwen3 / _gpt_oss) with the same bf16 rounding
+    steps; returns (q, k)."""
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16:
+        raise TypeError("q and k must be bf16")
+    if q.dim() != 3 or k.dim() != 3 or q.shape[0] != k.shape[0] or q.shape[2] != k.shape[2]:
+        raise ValueError("q [tokens, Hq, D] and k [tokens, Hkv, D] with one token count and head_dim")
+    if q.stride(2) != 1 or k.stride(2) != 1:
+        raise ValueError("head_dim must be contiguous")
+    d = q.shape[2]
+    a = _lib.QkRopeArgs()
+    a.q, a.k = q.data_ptr(), k.data_ptr()
+    a.q_stride_n, a.q_stride_h = q.stride(0), q.stride(1)
+    a.k_stride_n, a.k_stride_h = k.stride(0), k.stride(1)
+    for name, w in (("q_norm", q_norm), ("k_norm", k_norm)):
+        if w is not None:
+            if w.dtype != torch.bfloat16 or w.numel() != d or not w.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous bf16 [head_dim] weight")
+            setattr(a, name, w.data_ptr())
+    if (cos is None) != (sin is None):
+        raise ValueError("cos and sin go together")
+    if cos is not None:
+        if cos.dtype != torch.bfloat16 or sin.dtype != torch.bfloat16 or cos.shape != sin.shape:
+            raise ValueError("cos / sin must be bf16 of one shape")
+        if cos.dim() != 2 or cos.shape[0] != q.shape[0] or cos.shape[1] not in (d, d // 2):
+            raise ValueError("cos / sin must be [tokens, head_dim] or [tokens, head_dim / 2]")
+        if cos.stride(1) != 1 or sin.stride() != cos.stride():
+            raise ValueError("cos / sin rows must be contiguous with one stride")
+        a.cos, a.sin, a.cs_stride = cos.data_ptr(), sin.data_ptr(), cos.stride(0)
+        a.half_cos = 1 if cos.shape[1] == d // 2 else 0
+    a.eps = float(eps)
+    a.num_tokens, a.num_qo_heads, a.num_kv_heads, a.head_dim = q.shape[0], q.shape[1], k.shape[1], d
+    check(lib.d2sd_qk_norm_rope(C.byref(a), _stream()), "qk_norm_rope")
+    return q, k

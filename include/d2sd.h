@@ -289,6 +289,38 @@ typedef struct {
 int d2sd_paged_kv_append(const d2sd_kv_append_args* args, d2sd_stream_t stream);
 
 /* ----------------------------------------------------------------------
+ * Per-head RMSNorm of the new queries and keys, then rotary embedding, in
+ * place, one launch.  Replaces generation/verification.py:113-123 (Qwen3:
+ * attn.q_norm / k_norm + _apply_rotary_pos_emb_qwen3; GPT-OSS: RoPE only)
+ * and its transposes: q [tokens, Hq, D] and k [tokens, Hkv, D] stay
+ * token-major (the layout d2sd_cascade_run reads).  Numerics follow the
+ * reference's bf16 ops step for step:
+ *   y = bf16(w * bf16(x / sqrt(mean(x^2) + eps)))      (when w is given)
+ *   out = bf16(bf16(y * cos) + bf16(rotate_half(y) * sin))  (when cos is given)
+ * cos / sin: bf16 [tokens, D] (Qwen3, halves equal) or [tokens, D / 2]
+ * (GPT-OSS; half_cos = 1), the rotary table at each token's position.
+ * head_dim 64, 128 or 256, contiguous.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  void* q;
+  void* k;
+  int64_t q_stride_n, q_stride_h, k_stride_n, k_stride_h; /* elements */
+  const void* q_norm;   /* bf16 [D] or NULL (no norm) */
+  const void* k_norm;
+  const void* cos;      /* bf16 or NULL (no rotation) */
+  const void* sin;
+  int64_t cs_stride;    /* elements between tokens of cos / sin */
+  float eps;
+  int num_tokens;
+  int num_qo_heads;
+  int num_kv_heads;
+  int head_dim;
+  int half_cos;
+} d2sd_qk_norm_rope_args;
+
+int d2sd_qk_norm_rope(const d2sd_qk_norm_rope_args* args, d2sd_stream_t stream);
+
+/* ----------------------------------------------------------------------
  * Greedy acceptance walk of the verify tree, on the device.
  * Replaces generation/d3_generator.py:204-225 at temperature 0 (greedy
  * sampling is torch.argmax, model/utils.py:28-33, first index on ties):

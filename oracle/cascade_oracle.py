@@ -18,6 +18,7 @@ It restates the reference's verify-attention algorithm on the CPU in float64
   the same over unique tree nodes, single pass     cascade_tree_ref
   d3_generator.py:227-232 (accepted-branch commit) commit_accepted_ref
   d3_generator.py:204-225 (greedy acceptance walk) greedy_accept_ref
+  verification.py:113-123 (QK RMSNorm + RoPE)       qk_norm_rope_ref
 
 FlashInfer itself (flashinfer-python>=0.2.0, requirements.txt:13) is not
 vendored in the reference and not installed here.  Its published algorithm for
@@ -252,6 +253,31 @@ def commit_accepted_ref(pool: Tensor, page_table: List[int], prefix_len: int, ne
     return out
 
 
+def qk_norm_rope_ref(x: Tensor, weight: Optional[Tensor], cos: Optional[Tensor], sin: Optional[Tensor],
+                     eps: float = 1e-6) -> Tensor:
+    """generation/verification.py:113-123 on x [tokens, heads, D] (bf16): the
+    per-head RMSNorm of transformers' Qwen3RMSNorm (fp32 statistics, result
+    cast to bf16, times the bf16 weight) when weight is given, then the
+    rotate_half RoPE of _apply_rotary_pos_emb_qwen3 (cos / sin [tokens, D]) or
+    the split-half form of _apply_rotary_pos_emb_gpt_oss (cos / sin
+    [tokens, D/2]), as bf16 tensor ops."""
+    y = x
+    if weight is not None:
+        h = x.to(torch.float32)
+        var = h.pow(2).mean(-1, keepdim=True)
+        h = h * torch.rsqrt(var + eps)
+        y = weight * h.to(x.dtype)
+    if cos is None:
+        return y
+    c, s_ = cos.unsqueeze(1), sin.unsqueeze(1)
+    if cos.shape[-1] == x.shape[-1]:
+        half = x.shape[-1] // 2
+        rot = torch.cat((-y[..., half:], y[..., :half]), dim=-1)
+        return (y * c) + (rot * s_)
+    first, second = torch.chunk(y, 2, dim=-1)
+    return torch.cat([first * c - second * s_, second * c + first * s_], dim=-1)
+
+
 def greedy_accept_ref(node_logits: Tensor, node_index, draft_ids) -> Tuple[List[int], List[int], int, int]:
     """The acceptance loop of generation/d3_generator.py:204-225 at temperature
     0 (sample() is torch.argmax, model/utils.py:28-33), literally, on the rows'
@@ -287,5 +313,5 @@ __all__ = [
     "attention_ref", "attention_sdpa_ref", "causal_mask", "single_prefill_ref", "merge_state_ref",
     "sink_rescale_ref", "window_prefix_ref", "cascade_verify_rows_ref", "cascade_tree_ref",
     "ancestor_mask_from_rows", "fp8_dequant_ref", "gather_paged", "commit_accepted_ref",
-    "greedy_accept_ref",
+    "greedy_accept_ref", "qk_norm_rope_ref",
 ]

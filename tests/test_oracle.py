@@ -395,3 +395,39 @@ def test_accept_argmax_ties_take_the_first_index():
     lg[0, 3] = lg[0, 6] = 2.0
     ids, _, n, _ = orc.greedy_accept_ref(lg, [[0]], [[0]])
     assert ids == [3] and n == 1
+
+
+# ---- QK RMSNorm + RoPE (generation/verification.py:113-123) ----
+
+def test_qk_norm_rope_ref_matches_transformers_qwen3():
+    """The restatement equals the installed transformers Qwen3 routines (the
+    library the reference calls: Qwen3RMSNorm, rotate_half RoPE)."""
+    from transformers.models.qwen3 import modeling_qwen3 as mq
+    g = torch.Generator().manual_seed(0)
+    T, H, D = 7, 4, 128
+    x = (torch.randn(T, H, D, generator=g) * 3).to(torch.bfloat16)
+    norm = mq.Qwen3RMSNorm(D, eps=1e-6).to(torch.bfloat16)
+    with torch.no_grad():
+        norm.weight.copy_((torch.rand(D, generator=g) + 0.5).to(torch.bfloat16))
+    pos = torch.arange(T) + 4000
+    inv = 1.0 / (1e6 ** (torch.arange(0, D, 2).float() / D))
+    ang = pos[:, None].float() * inv[None]
+    emb = torch.cat([ang, ang], -1)
+    cos, sin = emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16)
+    with torch.no_grad():
+        y = norm(x)                                                   # [T, H, D]
+        q_hf, _ = mq.apply_rotary_pos_emb(y.transpose(0, 1)[None], y.transpose(0, 1)[None], cos[None], sin[None])
+    ref = orc.qk_norm_rope_ref(x, norm.weight.detach(), cos, sin, 1e-6)
+    assert torch.equal(ref, q_hf[0].transpose(0, 1))
+
+
+def test_qk_norm_rope_ref_gpt_oss_form_equals_rotate_half_form():
+    """The GPT-OSS split-half RoPE with D/2 columns equals the rotate_half
+    form with the halves duplicated (both restated from verification.py:21-42)."""
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(5, 3, 64, generator=g).to(torch.bfloat16)
+    c = torch.randn(5, 32, generator=g).to(torch.bfloat16)
+    s = torch.randn(5, 32, generator=g).to(torch.bfloat16)
+    a = orc.qk_norm_rope_ref(x, None, c, s)
+    b = orc.qk_norm_rope_ref(x, None, torch.cat([c, c], -1), torch.cat([s, s], -1))
+    assert torch.equal(a, b)
