@@ -392,7 +392,6 @@ static int build_verify_params(const d2sd_cascade_plan_info* info, const d2sd_ca
   p.items = (const d2sd::VerifyItem*)a->plan;
   p.merges = (const d2sd::VerifyMerge*)(a->plan + 16 * (long long)info->num_items);
   if (info->merge_in_attention) p.counters = (int*)((char*)a->workspace + info->counters_offset);
-  p.merge_mode = info->merge_mode;
   p.sinks = a->sinks;
   p.tree_mask = (const unsigned long long*)a->tree_mask;
   d2sd::VerifySource& pre = p.pre;

@@ -155,7 +155,7 @@ struct VerifyParams {
   int mask_words;
   int lse_base2;
   int num_merges;
-  int merge_mode;          // MERGE_*
+  int pad;
 };
 
 // Splits per group are capped so that one merge batch holds all partials.
