@@ -48,9 +48,21 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const QkRopeParams p)
                 (long long)(is_k ? h - p.num_qo_heads : h) * (is_k ? p.k_stride_h : p.q_stride_h);
   const uint16_t* w = (const uint16_t*)(is_k ? p.k_norm : p.q_norm);
 
-  float y[E];
+  // every load up front, in one round (absent weights / tables read x as a
+  // stand-in, never used)
+  const uint16_t* cs = p.cos ? (const uint16_t*)p.cos + (long long)t * p.cs_stride : x;
+  const uint16_t* sn = p.cos ? (const uint16_t*)p.sin + (long long)t * p.cs_stride : x;
+  const uint16_t* wp = w ? w : x;
+  float y[E], wv[E], cv[E], sv[E];
 #pragma unroll
-  for (int j = 0; j < E; ++j) y[j] = bf(x[lane + 64 * j]);
+  for (int j = 0; j < E; ++j) {
+    const int d = lane + 64 * j;
+    const int dc = p.cos && p.half_cos ? (d & (D / 2 - 1)) : d;
+    y[j] = bf(x[d]);
+    wv[j] = bf(wp[d]);
+    cv[j] = bf(cs[dc]);
+    sv[j] = bf(sn[dc]);
+  }
   if (w) {
     float ss = 0.f;
 #pragma unroll
@@ -59,11 +71,9 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const QkRopeParams p)
     for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
     const float r = 1.0f / sqrtf(ss / (float)D + p.eps);
 #pragma unroll
-    for (int j = 0; j < E; ++j) y[j] = bf(to_bf(bf(w[lane + 64 * j]) * bf(to_bf(y[j] * r))));
+    for (int j = 0; j < E; ++j) y[j] = bf(to_bf(wv[j] * bf(to_bf(y[j] * r))));
   }
   if (p.cos) {
-    const uint16_t* cs = (const uint16_t*)p.cos + (long long)t * p.cs_stride;
-    const uint16_t* sn = (const uint16_t*)p.sin + (long long)t * p.cs_stride;
     float rot[E];
     if constexpr (D == 64) {
       const float other = __shfl_xor(y[0], 32);
@@ -75,10 +85,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const QkRopeParams p)
     float out[E];
 #pragma unroll
     for (int j = 0; j < E; ++j) {
-      const int d = lane + 64 * j;
-      const int dc = p.half_cos ? (d & (D / 2 - 1)) : d;
-      const float a = bf(to_bf(y[j] * bf(cs[dc])));
-      const float b = bf(to_bf(rot[j] * bf(sn[dc])));
+      const float a = bf(to_bf(y[j] * cv[j]));
+      const float b = bf(to_bf(rot[j] * sv[j]));
       out[j] = a + b;
     }
 #pragma unroll
