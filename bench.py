@@ -412,6 +412,79 @@ def measure_qk_rope(args) -> int:
     return 0
 
 
+# the other workloads of the verify path (parity cases of the tests), each
+# timed as a hipGraph of `layers` calls over distinct KV pools
+OTHER_WORKLOADS = {
+    "config1": lambda wl, seed: (wl.config1(seed), 64),      # 4.2 MB of KV per call: 64 pools pass the MALL
+    "config3": lambda wl, seed: (wl.config3(seed), 2),       # ~670 MB of KV per call
+    "config4_full": lambda wl, seed: (wl.config4(seed), 12),
+    "config4_sliding": lambda wl, seed: (wl.config4(seed, sliding=True), 12),
+    "config5": lambda wl, seed: (wl.config5(seed), 2),       # ~540 MB of fp8 KV per call
+}
+
+
+def measure_workload(args) -> int:
+    """One JSON line per named workload: µs per verify-attention call (attention
+    + merge launch), and the attention launch alone against its roofline
+    (HBM or MFMA, whichever bounds its algorithmic bytes / flops)."""
+    import torch
+    import d2sd
+    from d2sd import workloads as wl
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    for name in args.workload.split(","):
+        prob, nl = OTHER_WORKLOADS[name](wl, args.seed)
+        log(f"materialising {prob.name} ({nl} KV pools)")
+        mp = wl.materialize(prob, dev, layers=nl)
+        attn = d2sd.CascadeVerifyAttention(dev)
+        wl.plan_for(attn, mp, merge_mode=args.merge_mode)
+        info = attn.info
+        T, hq, d = prob.total_q, prob.num_qo_heads, prob.head_dim
+        outs = [(torch.empty(T, hq, d, dtype=torch.bfloat16, device=dev),
+                 torch.empty(T, hq, dtype=torch.float32, device=dev)) for _ in mp.layers]
+
+        def calls(fn):
+            for lt, (o, l) in zip(mp.layers, outs):
+                fn(lt.q, lt.k_suffix, lt.v_suffix, lt.k_prefix, lt.v_prefix, out=o, lse=l)
+
+        calls(attn.run)
+        torch.cuda.synchronize()
+        graphs = {}
+        for key, fn in (("call", attn.run), ("attention", attn.run_attention)):
+            graphs[key] = d2sd.HipGraph()
+            with graphs[key].capture():
+                calls(fn)
+        for _ in range(3):
+            graphs["call"].replay()
+        reps = max(5, args.kernel_reps // 2)
+        call_us = time_graph(graphs["call"], reps, torch) * 1e3 / nl
+        attn_us = time_graph(graphs["attention"], reps, torch) * 1e3 / nl
+        ab, af = wl.attention_launch_bytes_flops(prob)
+        vb, vf = wl.verify_bytes_flops(prob)
+        t_hbm, t_mfma = ab / (HBM_PEAK_GBPS * 1e9), af / (MFMA_BF16_PEAK_TFLOPS * 1e12)
+        bound = "mfma" if t_mfma > t_hbm else "hbm"
+        hbm = ab / (attn_us * 1e-6) / 1e9
+        tfl = af / (attn_us * 1e-6) / 1e12
+        print(json.dumps({
+            "workload": prob.name, "value": call_us, "unit": "us/call", "higher_is_better": False,
+            "queries": T, "requests": len(prob.requests), "kv_pools": nl,
+            "dtype": "fp8_e4m3fn kv / bf16" if prob.kv_dtype == torch.float8_e4m3fn else "bf16",
+            "attention_us": attn_us, "merge_us": call_us - attn_us,
+            "attention_bytes": ab, "attention_flops": af, "bound": bound,
+            "hbm_gbps": hbm, "hbm_frac": hbm / HBM_PEAK_GBPS,
+            "mfma_tflops": tfl, "mfma_frac": tfl / MFMA_BF16_PEAK_TFLOPS,
+            "roofline_floor_us": max(t_hbm, t_mfma) * 1e6,
+            "frac": max(t_hbm, t_mfma) / (attn_us * 1e-6),
+            "call_bytes": vb, "call_flops": vf, "queries_per_s": T / (call_us * 1e-6),
+            "plan": {"workgroups": info.num_items, "waves": info.waves_per_block,
+                     "splits": info.max_splits_used, "merges": info.num_merges},
+        }), flush=True)
+        del graphs, mp, attn, outs
+        torch.cuda.empty_cache()
+    return 0
+
+
 def read_traffic():
     """traffic_bytes_per_launch from TRAFFIC_FILE, or None."""
     try:
@@ -443,6 +516,9 @@ def main() -> int:
     ap.add_argument("--accepted", type=int, default=20, help="accepted tokens per step for --commit")
     ap.add_argument("--accept", action="store_true",
                     help="time the greedy acceptance walk instead (one JSON line)")
+    ap.add_argument("--workload", default=None,
+                    help="comma-separated: " + ", ".join(OTHER_WORKLOADS) + " (one JSON line each instead of "
+                         "the verify-step line)")
     ap.add_argument("--qk-rope", action="store_true",
                     help="time the fused QK RMSNorm + RoPE instead (one JSON line)")
     args = ap.parse_args()
@@ -452,6 +528,8 @@ def main() -> int:
         return measure_accept(args)
     if args.qk_rope:
         return measure_qk_rope(args)
+    if args.workload:
+        return measure_workload(args)
     if args.traffic_workload:
         return traffic_workload(args)
     if args.measure_traffic:
