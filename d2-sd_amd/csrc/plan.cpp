@@ -87,6 +87,28 @@ static void interleave_merges(const std::vector<std::vector<VerifyMerge>>& lists
 int verify_wgs_per_cu(int waves) { return waves == 8 ? 1 : 2; }
 int verify_rows(int waves) { return waves == 2 ? 128 : 32 * waves; }
 
+// Waves per workgroup when the caller leaves it to the planner: 4 (128-row
+// q-tiles, two workgroups per CU) by default; 8 (256-row q-tiles, one per CU)
+// when the 4-wave plan already has at least one q-tile group per workgroup
+// slot, so that the prefix would not be split anyway, and some kv head packs
+// more than 128 rows: each K/V tile staged in LDS then feeds twice the rows
+// (measured: Qwen3-32B shape, 32 requests x 8192 keys, 4565 queries: 1790
+// vs 2125 us per attention launch).  Where the prefix must be split to fill
+// the device the finer 4-wave tiles balance better.
+int verify_auto_waves(const VerifyPlanInput& in, int num_cus) {
+  const int Hkv = in.num_kv_heads;
+  const int g = in.num_qo_heads / Hkv;
+  long long groups = 0;
+  int max_rows = 0;
+  for (int r = 0; r < in.num_reqs; ++r) {
+    const int nq = in.qo_indptr[r + 1] - in.qo_indptr[r];
+    if (nq <= 0 || in.prefix_len[r] <= 0) continue;
+    max_rows = std::max(max_rows, nq * g);
+    groups += (long long)Hkv * ((nq * g + verify_rows(4) - 1) / verify_rows(4));
+  }
+  return max_rows > verify_rows(4) && groups >= (long long)num_cus * verify_wgs_per_cu(4) ? 8 : 4;
+}
+
 // Cascade verify plan.  Groups are (request, kv head, q-tile of ROWS packed
 // rows).  Each group gets S key chunks of its visible prefix (S partial
 // slots) plus one suffix item (slot S), merged by one merge item; a group
@@ -99,10 +121,10 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
   out.merges.clear();
   const int Hkv = in.num_kv_heads;
   const int g = in.num_qo_heads / Hkv;
-  const int W = in.waves ? in.waves : 4;
-  const int ROWS = verify_rows(W);
   const int R = in.num_reqs;
   const int num_cus = in.num_cus > 0 ? in.num_cus : 256;
+  const int W = in.waves ? in.waves : verify_auto_waves(in, num_cus);
+  const int ROWS = verify_rows(W);
   const long long capacity = (long long)num_cus * verify_wgs_per_cu(W);
   const int split_cap =
       in.max_splits > 0 ? std::min(in.max_splits, kMaxVerifySplits) : kMaxVerifySplits;

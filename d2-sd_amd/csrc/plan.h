@@ -47,6 +47,7 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out);
 // waves).
 int verify_wgs_per_cu(int waves);
 int verify_rows(int waves);
+int verify_auto_waves(const VerifyPlanInput& in, int num_cus);
 
 hipError_t launch_verify_attention(const VerifyParams& p, int head_dim, int waves, bool paged, bool fp8, int nitems,
                                    hipStream_t s);

@@ -192,6 +192,22 @@ def test_plan_partitions_work(qo, pl, window, page, hq, waves, merge_mode):
                         assert (b - 1) // page - a // page + 1 <= 1024
 
 
+def test_plan_chooses_waves():
+    """waves_per_block 0: 8-wave (256-row) tiles once the 4-wave plan has a
+    q-tile group per workgroup slot and a kv head packs > 128 rows (many
+    large requests), else 4 waves."""
+    qo = [143 * i for i in range(33)]                    # 32 requests x 143 nodes, 64/8 heads
+    info, _, _ = _plan(qo, [8192] * 32, hq=64, hkv=8)
+    assert info.waves_per_block == 8 and info.rows_per_tile == 256
+    info, _, _ = _plan([0, 150], [4096])                 # one request: the prefix is split, 4 waves
+    assert info.waves_per_block == 4
+    qo = [30 * i for i in range(33)]                     # many requests, 120 rows per kv head
+    info, _, _ = _plan(qo, [8192] * 32, hq=32, hkv=8)
+    assert info.waves_per_block == 4
+    info, _, _ = _plan([143 * i for i in range(33)], [8192] * 32, hq=64, hkv=8, waves=4)
+    assert info.waves_per_block == 4                     # an explicit choice stands
+
+
 def test_plan_fills_the_device_once():
     info, items, _ = _plan([0, 150], [4096])
     live = (items[:, MODE] != MODE_NOOP).sum()
