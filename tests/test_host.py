@@ -333,3 +333,23 @@ def test_greedy_accept_rejects_bad_arguments():
         setattr(a, field, old)
     a.workspace_bytes = 8
     assert _lib.lib.d2sd_greedy_accept(C.byref(a), None) == 3   # D2SD_ERR_WORKSPACE
+
+
+def test_bench_workloads_build_and_plan():
+    """Every `bench.py --workload` name builds its problem, whose sizes the
+    planner accepts (host work only: the plan is computed, nothing runs)."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("bench", Path(__file__).resolve().parents[1] / "bench.py")
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    from d2sd import workloads as wl
+    for name, make in bench.OTHER_WORKLOADS.items():
+        prob, pools = make(wl, 0)
+        assert pools >= 1 and prob.total_q > 0, name
+        qo = np.asarray(prob.qo_indptr)
+        page = prob.page_size
+        pl = np.asarray(prob.prefix_lens)
+        page_indptr = np.concatenate([[0], np.cumsum((pl + page - 1) // page)]) if page else None
+        info, items, _ = _plan(qo.tolist(), pl.tolist(), prob.num_qo_heads, prob.num_kv_heads, prob.head_dim,
+                               prob.window_left, page_size=page, page_indptr=page_indptr)
+        assert info.num_items > 0 and info.waves_per_block in (4, 8), name
