@@ -456,6 +456,9 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
       static_for<k1 - k0>([&](auto kk) { qk_ks(sn, kfrag_n, k0 + decltype(kk)::value); });
     });
     pv_chunk(vfrag, pb, 3);
+    // the scheduler's MFMA / LDS-read interleave for this region (measured
+    // 0.5% faster at one request of 4096 keys, 3% at eight of 8K-32K)
+    __builtin_amdgcn_iglp_opt(0);
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       l_run[rb] += (ls[rb][0] + ls[rb][1]) + (ls[rb][2] + ls[rb][3]);
