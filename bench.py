@@ -21,6 +21,11 @@ which starts `rocprofv3 --pmc FETCH_SIZE` and then `--pmc WRITE_SIZE` as child
 processes on `bench.py --traffic-workload` (the 36 attention launches plus a
 plain 256 MiB device copy of known size).  Each counter is scaled by
 known_bytes / counter for the copy kernel.  A default run reads that file.
+
+MFMA utilisation of the attention launch (SQ_VALU_MFMA_BUSY_CYCLES, MFMA
+instruction and MOPS counts, GRBM_GUI_ACTIVE, kernel trace) comes from
+
+    python bench.py --measure-mfma        # writes profiles/verify_attn_cfg2_mfma.txt
 """
 from __future__ import annotations
 
@@ -150,6 +155,92 @@ def _counter_means(csv_path: Path, counter: str) -> dict:
             sums[key] = sums.get(key, 0.0) + float(row["Counter_Value"])
             counts[key] = counts.get(key, 0) + 1
     return {k: sums[k] / counts[k] for k in sums}
+
+
+def _pmc_pass(counters, outdir: Path, args, kernel_trace: bool = False):
+    """One rocprofv3 counter pass over the traffic workload (a child process);
+    returns the directory it wrote, or None after printing the failure."""
+    import subprocess
+    cmd = ["rocprofv3", "--pmc", *counters]
+    if kernel_trace:
+        cmd.append("--kernel-trace")
+    cmd += ["--kernel-include-regex", "verify_attn_kernel|copyBuffer",
+            "-d", str(outdir), "-o", "run", "--output-format", "csv", "--",
+            sys.executable, str(Path(__file__).resolve()), "--traffic-workload",
+            "--layers", str(args.layers), "--seed", str(args.seed), "--merge-mode", args.merge_mode]
+    log("running " + " ".join(cmd))
+    r = subprocess.run(cmd, timeout=300, capture_output=True, text=True)
+    if r.returncode != 0:
+        print(r.stdout[-2000:], r.stderr[-2000:], file=sys.stderr)
+        return None
+    return outdir
+
+
+def _attention_mean_ns(trace_csv: Path) -> float:
+    import csv
+    durs = []
+    with open(trace_csv) as f:
+        for row in csv.DictReader(f):
+            if "verify_attn_kernel" in row["Kernel_Name"]:
+                durs.append(int(row["End_Timestamp"]) - int(row["Start_Timestamp"]))
+    return statistics.mean(durs)
+
+
+MFMA_FILE = ROOT / "profiles" / "verify_attn_cfg2_mfma.txt"
+MFMA_COUNTERS = ("SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_INSTS_VALU_MFMA_BF16",
+                 "SQ_BUSY_CYCLES", "GRBM_GUI_ACTIVE")
+
+
+def measure_mfma(args) -> int:
+    """MFMA utilisation of the attention launch: one rocprofv3 pass with the
+    SQ MFMA counters and the kernel trace over the traffic workload; writes
+    MFMA_FILE.  MOPS counts units of 512 flops; one v_mfma_f32_32x32x16_bf16
+    is 32*32*16*2 = 32768 flops = 64 MOPS."""
+    import tempfile
+    from d2sd import workloads as wl
+    with tempfile.TemporaryDirectory(dir=os.environ.get("TMPDIR", "/tmp")) as tmp:
+        out = _pmc_pass(MFMA_COUNTERS, Path(tmp) / "mfma", args, kernel_trace=True)
+        if out is None:
+            return 1
+        files = list(out.rglob("*counter_collection.csv"))
+        traces = list(out.rglob("*kernel_trace.csv"))
+        if not files or not traces:
+            print("rocprofv3 wrote no counter_collection.csv / kernel_trace.csv", file=sys.stderr)
+            return 1
+        c = {name: _counter_means(files[0], name)["attention"] for name in MFMA_COUNTERS}
+        dur_ns = _attention_mean_ns(traces[0])
+    prob = wl.config2(args.seed, layers=args.layers)
+    _, af = wl.attention_launch_bytes_flops(prob)
+    cus, simds = 256, 4
+    exec_flops = c["SQ_INSTS_VALU_MFMA_MOPS_BF16"] * 512.0
+    busy, grbm_xcd = c["SQ_VALU_MFMA_BUSY_CYCLES"], c["GRBM_GUI_ACTIVE"] / 8.0
+    lines = [
+        "# MFMA utilisation of the cascade verify attention launch, config 2 (Qwen3-8B, L=4096 paged, 36 layers)",
+        f"# command: python bench.py --measure-mfma --layers {args.layers} --seed {args.seed}",
+        "#   = rocprofv3 --pmc " + " ".join(MFMA_COUNTERS) + " --kernel-trace",
+        "#     --kernel-include-regex 'verify_attn_kernel|copyBuffer' --output-format csv -- python bench.py --traffic-workload",
+        "# counters: mean per attention dispatch; duration: mean kernel-trace duration of the same dispatches",
+    ]
+    lines += [f"{k}: {v:.0f}" for k, v in c.items()]
+    lines += [
+        f"attention_duration_ns: {dur_ns:.0f}",
+        f"mops_per_mfma_instruction: {c['SQ_INSTS_VALU_MFMA_MOPS_BF16'] / max(c['SQ_INSTS_VALU_MFMA_BF16'], 1):.2f}",
+        f"executed_mfma_flops_per_launch: {exec_flops:.0f}",
+        f"algorithmic_flops_per_launch: {af:.0f}",
+        f"executed_over_algorithmic: {exec_flops / af:.3f}",
+        f"executed_tflops: {exec_flops / dur_ns / 1e3:.1f}",
+        f"executed_frac_of_2500_tflops: {exec_flops / dur_ns / 1e3 / MFMA_BF16_PEAK_TFLOPS:.3f}",
+        f"mfma_busy_cycles_per_instruction: {c['SQ_VALU_MFMA_BUSY_CYCLES'] / max(c['SQ_INSTS_VALU_MFMA_BF16'], 1):.2f}",
+        # the csv value of GRBM_GUI_ACTIVE is the sum over the 8 XCD instances;
+        # rocprof's MfmaUtil expression divides by one instance (its max)
+        f"grbm_gui_active_per_xcd: {grbm_xcd:.0f}",
+        f"mfma_util_rocprof_expr: {busy / (grbm_xcd * cus * simds):.4f}",
+        f"mfma_util_over_trace_duration_at_2400MHz: {busy / (dur_ns * 2.4 * cus * simds):.4f}",
+    ]
+    MFMA_FILE.parent.mkdir(exist_ok=True)
+    MFMA_FILE.write_text("\n".join(lines) + "\n")
+    print("\n".join(lines))
+    return 0
 
 
 def measure_traffic(args) -> int:
@@ -511,6 +602,8 @@ def main() -> int:
     ap.add_argument("--measure-traffic", action="store_true",
                     help="run the two rocprofv3 counter passes and write the traffic summary")
     ap.add_argument("--traffic-workload", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--measure-mfma", action="store_true",
+                    help="run one rocprofv3 pass of the SQ MFMA counters and write the utilisation summary")
     ap.add_argument("--commit", action="store_true",
                     help="time the accepted-branch KV commit instead (one JSON line)")
     ap.add_argument("--accepted", type=int, default=20, help="accepted tokens per step for --commit")
@@ -534,6 +627,8 @@ def main() -> int:
         return traffic_workload(args)
     if args.measure_traffic:
         return measure_traffic(args)
+    if args.measure_mfma:
+        return measure_mfma(args)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: every path here runs on a single MI355X "
               "(multi-GPU sharding is a design note, not a measured configuration).", file=sys.stderr)
