@@ -242,6 +242,64 @@ def test_cascade_config5_subset():
     _check_problem(mp, outs, reqs=[0, 31], dtype=torch.float32, tag="cfg5")
 
 
+def _torch_fp32_request(mp, li, r):
+    """fp32 torch reference of one request on the GPU, in the oracle's
+    single-pass form: one masked softmax over [windowed prefix || suffix] with
+    mask [ones || ancestor mask].  Paged HND prefix only.  Products run as
+    fp32 matmuls of contiguous operands."""
+    prob = mp.problem
+    lt = mp.layers[li]
+    a, b = prob.qo_indptr[r], prob.qo_indptr[r + 1]
+    req = prob.requests[r]
+    n, hq, hkv, d = b - a, prob.num_qo_heads, prob.num_kv_heads, prob.head_dim
+    assert prob.page_size > 0 and req.prefix_len > 0
+    pages = mp.page_table[mp.page_indptr[r]:mp.page_indptr[r + 1]].long()
+
+    def gather(pool, scale):
+        raw = pool.view(torch.uint8)[pages] if pool.dtype == torch.float8_e4m3fn else pool[pages]
+        x = raw.view(pool.dtype).permute(0, 2, 1, 3).reshape(-1, hkv, d)[:req.prefix_len].float()
+        return x * scale[None, :, None].float() if scale is not None else x
+
+    kp, vp = gather(lt.k_prefix, mp.k_scale), gather(lt.v_prefix, mp.v_scale)
+    if prob.window_left >= 0:
+        keep = min(req.prefix_len, prob.window_left)
+        kp, vp = kp[kp.shape[0] - keep:], vp[vp.shape[0] - keep:]
+    k_all = torch.cat([kp, lt.k_suffix[a:b].float()], 0)
+    v_all = torch.cat([vp, lt.v_suffix[a:b].float()], 0)
+    mask = torch.ones(n, k_all.shape[0], dtype=torch.bool, device=k_all.device)
+    mask[:, kp.shape[0]:] = torch.as_tensor(req.tree.ancestor_mask(), device=k_all.device).bool()
+    g = hq // hkv
+    qf = lt.q[a:b].float().transpose(0, 1).contiguous()                          # [Hq, n, D]
+    kt = k_all.repeat_interleave(g, dim=1).permute(1, 2, 0).contiguous()         # [Hq, D, Lt]
+    vf = v_all.repeat_interleave(g, dim=1).transpose(0, 1).contiguous()          # [Hq, Lt, D]
+    s = torch.matmul(qf, kt) * d ** -0.5
+    s = s.masked_fill(~mask[None], -math.inf)
+    lse = torch.logsumexp(s, dim=-1)                                             # every node sees itself
+    o = torch.matmul(torch.exp(s - lse[..., None]), vf)
+    if mp.sinks is not None:
+        o = o * torch.sigmoid(lse - mp.sinks.float()[:, None])[..., None]
+    return o.transpose(0, 1).cpu(), lse.transpose(0, 1).cpu()
+
+
+@pytest.mark.parametrize("cfg", ["config3", "config5"])
+def test_full_size_every_request_vs_torch_fp32(cfg):
+    """Configs 3 and 5 at their full sizes (8 requests with prefixes of
+    8K-32K; 32 requests with fp8 prefixes of 8192): every request against the
+    fp32 torch reference on the GPU, which is itself held to the CPU oracle
+    (fp32) on request 0 within 1e-4."""
+    mp, _, outs = _run_problem(getattr(wl, cfg)(0))
+    prob = mp.problem
+    o, lse = outs[0]
+    t_o, t_lse = _torch_fp32_request(mp, 0, 0)
+    r_o, r_lse = _oracle_request(mp, 0, 0, torch.float32)
+    assert (t_o - r_o).abs().max().item() <= 1e-4, "torch fp32 reference drifts from the oracle (O)"
+    assert (t_lse - r_lse).abs().max().item() <= 1e-4, "torch fp32 reference drifts from the oracle (LSE)"
+    qo = prob.qo_indptr
+    for r in range(len(prob.requests)):
+        o_ref, lse_ref = (t_o, t_lse) if r == 0 else _torch_fp32_request(mp, 0, r)
+        check_close(o[qo[r]:qo[r + 1]], o_ref, lse[qo[r]:qo[r + 1]], lse_ref, f"{cfg} req {r}")
+
+
 @pytest.mark.parametrize("L,shared,window,waves", [
     (0, [16, 4, 9], -1, 0),        # empty prefix: suffix level alone
     (1, [1], -1, 0),               # single key, single node
