@@ -127,7 +127,7 @@ def traffic_workload(args) -> int:
     prob = wl.config2(args.seed, layers=args.layers)
     mp = wl.materialize(prob, dev)
     attn = d2sd.CascadeVerifyAttention(dev)
-    wl.plan_for(attn, mp, merge_mode=args.merge_mode)
+    wl.plan_for(attn, mp)
     T, hq, d = prob.total_q, prob.num_qo_heads, prob.head_dim
     o = torch.empty(T, hq, d, dtype=torch.bfloat16, device=dev)
     lse = torch.empty(T, hq, dtype=torch.float32, device=dev)
@@ -167,7 +167,7 @@ def _pmc_pass(counters, outdir: Path, args, kernel_trace: bool = False):
     cmd += ["--kernel-include-regex", "verify_attn_kernel|copyBuffer",
             "-d", str(outdir), "-o", "run", "--output-format", "csv", "--",
             sys.executable, str(Path(__file__).resolve()), "--traffic-workload",
-            "--layers", str(args.layers), "--seed", str(args.seed), "--merge-mode", args.merge_mode]
+            "--layers", str(args.layers), "--seed", str(args.seed)]
     log("running " + " ".join(cmd))
     r = subprocess.run(cmd, timeout=300, capture_output=True, text=True)
     if r.returncode != 0:
@@ -255,7 +255,7 @@ def measure_traffic(args) -> int:
             cmd = ["rocprofv3", "--pmc", counter, "--kernel-include-regex", "verify_attn_kernel|copyBuffer",
                    "-d", str(outdir), "-o", "run", "--output-format", "csv", "--",
                    sys.executable, str(Path(__file__).resolve()), "--traffic-workload",
-                   "--layers", str(args.layers), "--seed", str(args.seed), "--merge-mode", args.merge_mode]
+                   "--layers", str(args.layers), "--seed", str(args.seed)]
             log("running " + " ".join(cmd))
             r = subprocess.run(cmd, timeout=300, capture_output=True, text=True)
             if r.returncode != 0:
@@ -529,7 +529,7 @@ def measure_workload(args) -> int:
         log(f"materialising {prob.name} ({nl} KV pools)")
         mp = wl.materialize(prob, dev, layers=nl)
         attn = d2sd.CascadeVerifyAttention(dev)
-        wl.plan_for(attn, mp, merge_mode=args.merge_mode)
+        wl.plan_for(attn, mp)
         info = attn.info
         T, hq, d = prob.total_q, prob.num_qo_heads, prob.head_dim
         outs = [(torch.empty(T, hq, d, dtype=torch.bfloat16, device=dev),
@@ -597,8 +597,6 @@ def main() -> int:
     ap.add_argument("--cpu-reps", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=50)
-    ap.add_argument("--merge-mode", default="launch", choices=["launch", "last_producer"],
-                    help="where split partial states are merged (plan merge_mode)")
     ap.add_argument("--measure-traffic", action="store_true",
                     help="run the two rocprofv3 counter passes and write the traffic summary")
     ap.add_argument("--traffic-workload", action="store_true", help=argparse.SUPPRESS)
@@ -644,7 +642,7 @@ def main() -> int:
     log(f"materialising {prob.name}: N={prob.total_q} nodes, {args.layers} layers")
     mp = wl.materialize(prob, dev)
     attn = d2sd.CascadeVerifyAttention(dev)
-    wl.plan_for(attn, mp, merge_mode=args.merge_mode)
+    wl.plan_for(attn, mp)
     info = attn.info
     T, hq, d = prob.total_q, prob.num_qo_heads, prob.head_dim
     outs = [(torch.empty(T, hq, d, dtype=torch.bfloat16, device=dev),
@@ -666,17 +664,13 @@ def main() -> int:
     with g_attn.capture():
         for i in range(len(mp.layers)):
             layer_call(i, attn.run_attention)
-    fused = bool(info.merge_in_attention)
-    g_merge = None
-    if not fused:
-        g_merge = d2sd.HipGraph()
-        with g_merge.capture():
-            for i in range(len(mp.layers)):
-                layer_call(i, attn.run_merge)
+    g_merge = d2sd.HipGraph()
+    with g_merge.capture():
+        for i in range(len(mp.layers)):
+            layer_call(i, attn.run_merge)
     log(f"plan: attention {info.num_items} workgroups x {info.waves_per_block} waves "
         f"({info.rows_per_tile} rows each), {info.max_splits_used} prefix splits, {info.num_slots} partial "
-        f"slots, " + (f"merged inside the attention launch (mode {info.merge_mode})" if fused
-                       else f"{info.num_merges} merge groups"))
+        f"slots, {info.num_merges} merge workgroups")
 
     for _ in range(args.warmup):
         step.replay()
@@ -695,7 +689,7 @@ def main() -> int:
 
     # per-kernel averages (graphs of the 36 launches of one kernel)
     attn_us = time_graph(g_attn, args.kernel_reps, torch) * 1000.0 / len(mp.layers)
-    merge_us = time_graph(g_merge, args.kernel_reps, torch) * 1000.0 / len(mp.layers) if g_merge else 0.0
+    merge_us = time_graph(g_merge, args.kernel_reps, torch) * 1000.0 / len(mp.layers)
     log(f"attention kernel {attn_us:.3f} us/launch, merge kernel {merge_us:.3f} us/launch")
 
     vb, vf = wl.verify_bytes_flops(prob)

@@ -3,6 +3,7 @@
 // allocated here except the executable of a captured graph.
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -298,9 +299,9 @@ int d2sd_cascade_plan(const d2sd_cascade_plan_desc* desc, int32_t* host_plan, si
   in.max_splits = desc->max_splits;
   in.waves = desc->waves_per_block;
   in.page_size = desc->page_size;
-  if (desc->merge_mode != D2SD_MERGE_LAUNCH && desc->merge_mode != D2SD_MERGE_LAST_PRODUCER)
-    return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: merge_mode must be one of D2SD_MERGE_*");
-  in.merge_mode = desc->merge_mode;
+  if (desc->dynamic_prefix != 0 && desc->dynamic_prefix != 1)
+    return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: dynamic_prefix must be 0 or 1");
+  if (desc->window_left < -1) return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: window_left must be >= -1");
   d2sd::VerifyPlanOutput out{};
   d2sd::plan_verify(in, out);
   static_assert(sizeof(d2sd::VerifyItem) == 16 * sizeof(int32_t), "VerifyItem layout");
@@ -321,9 +322,17 @@ int d2sd_cascade_plan(const d2sd_cascade_plan_desc* desc, int32_t* host_plan, si
   info->kv_dtype = desc->kv_dtype;
   info->page_size = desc->page_size;
   info->num_groups = out.num_groups;
-  info->merge_in_attention = out.merge_in_attention ? 1 : 0;
-  info->counters_offset = out.counters_offset;
-  info->merge_mode = out.merge_mode;
+  info->dynamic_prefix = desc->dynamic_prefix;
+  info->window_left = desc->window_left;
+  int64_t extent = 0;
+  for (int r = 0; r < desc->num_reqs; ++r) {
+    if (desc->page_size > 0)
+      extent = desc->page_indptr[desc->num_reqs];
+    else if (desc->prefix_len[r] > 0)
+      extent = std::max<int64_t>(
+          extent, (int64_t)(desc->prefix_tok_indptr ? desc->prefix_tok_indptr[r] : 0) + desc->prefix_len[r]);
+  }
+  info->prefix_extent = extent;
   if (host_plan) {
     if (host_plan_ints < (size_t)info->plan_ints)
       return fail(D2SD_ERR_WORKSPACE, "cascade_plan: host_plan too small (need " +
@@ -358,6 +367,14 @@ static int build_verify_params(const d2sd_cascade_plan_info* info, const d2sd_ca
   if (info->max_splits_used > 0 && !has_prefix)
     return fail(D2SD_ERR_INVALID_ARG, "cascade_run: the plan has prefix keys but k_prefix is null");
   if (has_prefix) {
+    if (info->page_size > 0 ? (a->prefix_extent <= 0 || a->prefix_extent > INT32_MAX)
+                            : a->prefix_extent < info->prefix_extent)
+      return fail(D2SD_ERR_INVALID_ARG, info->page_size > 0
+                                            ? "cascade_run: prefix_extent must be the pool's page count"
+                                            : "cascade_run: k_prefix holds fewer tokens than the plan reads (need " +
+                                                  std::to_string(info->prefix_extent) + ")");
+    if (info->dynamic_prefix && !a->prefix_len)
+      return fail(D2SD_ERR_INVALID_ARG, "cascade_run: a dynamic-prefix plan needs the device prefix_len array");
     const int esz = info->kv_dtype == D2SD_KV_FP8_E4M3 ? 1 : 2;
     auto ok = [&](int64_t st) { return (st * esz) % 16 == 0; };
     if (!a->v_prefix || !aligned16(a->k_prefix) || !aligned16(a->v_prefix) || !ok(a->prefix_stride_tok) ||
@@ -391,7 +408,8 @@ static int build_verify_params(const d2sd_cascade_plan_info* info, const d2sd_ca
   p.part_lse = a->workspace ? (float*)((char*)a->workspace + (long long)info->num_slots * rows * D * 2) : nullptr;
   p.items = (const d2sd::VerifyItem*)a->plan;
   p.merges = (const d2sd::VerifyMerge*)(a->plan + 16 * (long long)info->num_items);
-  if (info->merge_in_attention) p.counters = (int*)((char*)a->workspace + info->counters_offset);
+  p.prefix_len = info->dynamic_prefix ? a->prefix_len : nullptr;
+  p.window_left = info->window_left;
   p.sinks = a->sinks;
   p.tree_mask = (const unsigned long long*)a->tree_mask;
   d2sd::VerifySource& pre = p.pre;
@@ -407,6 +425,7 @@ static int build_verify_params(const d2sd_cascade_plan_info* info, const d2sd_ca
   while (info->page_size > 0 && (1 << lg) < info->page_size) ++lg;
   pre.log2_page = lg;
   pre.fp8 = info->kv_dtype == D2SD_KV_FP8_E4M3;
+  pre.num_pages = info->page_size > 0 ? (int)a->prefix_extent : 0;
   d2sd::VerifySource& suf = p.suf;
   suf.k = a->k_suffix;
   suf.v = a->v_suffix;
@@ -437,7 +456,6 @@ int d2sd_cascade_merge(const d2sd_cascade_plan_info* info, const d2sd_cascade_ru
   g_last_error.clear();
   d2sd::VerifyParams p{};
   if (int rc = build_verify_params(info, a, p)) return rc;
-  if (info->merge_in_attention) return D2SD_OK;  // the attention launch merged
   hipError_t e = d2sd::launch_verify_merge(p, info->head_dim, info->rows_per_tile, info->num_merges,
                                            (hipStream_t)stream);
   return e == hipSuccess ? D2SD_OK : fail_hip(e, "cascade merge launch");

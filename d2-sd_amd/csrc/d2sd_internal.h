@@ -14,12 +14,6 @@ enum : int {
   MODE_NOOP = 3,     // padding item, exits immediately
 };
 
-// Where a cascade plan merges the partial states of a split group.
-enum : int {
-  MERGE_LAUNCH = 0,         // a separate merge launch
-  MERGE_LAST_PRODUCER = 1,  // the group's last producer, inside the attention launch
-};
-
 enum : int { MASK_NONE = 0, MASK_CAUSAL = 1, MASK_TREE = 2 };
 
 // Page ids one attention workgroup stages in LDS (its split's pages).
@@ -104,16 +98,16 @@ enum : int { SRC_PREFIX = 0, SRC_SUFFIX = 1 };
 // the kernel's first dependent load is the item itself.
 struct VerifyItem {
   int req, kvh, qtile, src;
-  int kv_begin, kv_end;  // keys [kv_begin, kv_end) of the source
+  int kv_begin, kv_end;  // keys [kv_begin, kv_end) of the source (prefix: at the planned length)
   int slot;              // partial slot (MODE_PARTIAL)
   int mode;              // MODE_PARTIAL / MODE_FINAL / MODE_NOOP
   int q0, nq;            // the request's first query row and query count
   int base;              // paged: page_table index of the request's page 0;
                          // contiguous: token offset of the request's key 0
   int causal_off;        // MASK_CAUSAL: key j visible to query i iff j <= i + causal_off
-  int group;             // MODE_PARTIAL: completion counter of the item's (request, kv head, q-tile)
-  int slot0, nprod;      // ... whose nprod partial slots are [slot0, slot0 + nprod)
-  int pad;
+  int kv0;               // prefix: first visible key at the planned length (window start)
+  int plan_len;          // prefix: the request's planned prefix length
+  int pad[2];
 };
 
 // One 32-row block `blk` of a group whose partial slots
@@ -131,6 +125,8 @@ struct VerifySource {
   const float* v_scale;
   int log2_page;
   int fp8;
+  int num_pages;           // paged: pages of the pool (page ids are clamped below it)
+  int pad;
 };
 
 struct VerifyParams {
@@ -144,7 +140,7 @@ struct VerifyParams {
   float* part_lse;         // [slot][ROWS]
   const VerifyItem* items;
   const VerifyMerge* merges;
-  int* counters;           // [groups] producer arrivals, zero between launches (MERGE_LAST_PRODUCER)
+  const int* prefix_len;   // nullable: per-request prefix lengths read at run time (dynamic plans)
   const float* sinks;      // nullable, [Hq]
   const unsigned long long* tree_mask;  // [total_q][mask_words]
   VerifySource pre, suf;
@@ -155,10 +151,11 @@ struct VerifyParams {
   int mask_words;
   int lse_base2;
   int num_merges;
-  int pad;
+  int window_left;         // dynamic plans: the visible window (-1: whole prefix)
 };
 
-// Splits per group are capped so that one merge batch holds all partials.
+// Prefix key chunks per group are capped so that one merge batch holds all
+// partials of a group (the chunks plus the suffix partial).
 constexpr int kMaxVerifySplits = 15;
 
 // ---------------------------------------------------------------------------

@@ -119,26 +119,6 @@ __device__ __forceinline__ void dma16s(const void* sbase, unsigned voff, unsigne
       : "memory", "m0");
 }
 
-// Device-coherent (agent scope) stores and loads of the partial states that
-// one workgroup hands to another: relaxed atomics, which need no cache
-// write-back or invalidation (unlike a release / acquire fence on plain data).
-// Ordering comes from completion: the producer waits for its stores
-// (vmcnt(0)) before it counts itself done; the consumer loads after the count
-// told it so.
-__device__ __forceinline__ void store_agent(u32x2* p, u32x2 v) {
-  __hip_atomic_store((unsigned long long*)p, __builtin_bit_cast(unsigned long long, v), __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void store_agent(float* p, float v) {
-  __hip_atomic_store((unsigned*)p, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ u32x2 load_agent(const u32x2* p) {
-  return __builtin_bit_cast(u32x2, __hip_atomic_load((unsigned long long*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-}
-__device__ __forceinline__ float load_agent(const float* p) {
-  return __uint_as_float(__hip_atomic_load((unsigned*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-}
-
 __device__ __forceinline__ unsigned lds_address(const void* p) {
   return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
 }

@@ -26,47 +26,6 @@ int choose_waves(int rows_per_head_max) {
 
 int blocks_per_cu(int waves) { return waves == 4 ? 2 : 1; }
 
-// Deal sets of work items to the 8 XCDs (largest first onto the least-loaded
-// XCD) and interleave them so that item k of XCD x lands at workgroup index
-// 8k + x (workgroups are dispatched to XCDs round-robin); shorter XCD lists are
-// padded with NOOP items.
-template <typename Item>
-struct ItemSet {
-  long long cost;
-  std::vector<Item> items;
-};
-
-// Returns, per input set (input order), the XCD it was dealt to.
-template <typename Item>
-static std::vector<int> order_for_xcds(std::vector<ItemSet<Item>>& sets, std::vector<Item>& out) {
-  std::vector<int> idx(sets.size());
-  for (size_t i = 0; i < idx.size(); ++i) idx[i] = (int)i;
-  std::stable_sort(idx.begin(), idx.end(), [&](int a, int b) { return sets[a].cost > sets[b].cost; });
-  std::vector<long long> load(8, 0);
-  std::vector<std::vector<Item>> lists(8);
-  std::vector<int> xcd_of(sets.size(), 0);
-  for (int i : idx) {
-    const int x = (int)(std::min_element(load.begin(), load.end()) - load.begin());
-    load[x] += sets[i].cost;
-    xcd_of[i] = x;
-    lists[x].insert(lists[x].end(), sets[i].items.begin(), sets[i].items.end());
-  }
-  size_t maxlen = 0;
-  for (auto& l : lists) maxlen = std::max(maxlen, l.size());
-  for (size_t k = 0; k < maxlen; ++k)
-    for (int x = 0; x < 8; ++x) {
-      if (k < lists[x].size()) {
-        out.push_back(lists[x][k]);
-      } else {
-        Item w{};
-        w.mode = MODE_NOOP;
-        out.push_back(w);
-      }
-    }
-  while (!out.empty() && out.back().mode == MODE_NOOP) out.pop_back();
-  return xcd_of;
-}
-
 // Interleave per-XCD merge lists: merge workgroup 8k + x runs on XCD x.
 static void interleave_merges(const std::vector<std::vector<VerifyMerge>>& lists, std::vector<VerifyMerge>& out) {
   size_t maxlen = 0;
@@ -109,13 +68,45 @@ int verify_auto_waves(const VerifyPlanInput& in, int num_cus) {
   return max_rows > verify_rows(4) && groups >= (long long)num_cus * verify_wgs_per_cu(4) ? 8 : 4;
 }
 
-// Cascade verify plan.  Groups are (request, kv head, q-tile of ROWS packed
-// rows).  Each group gets S key chunks of its visible prefix (S partial
-// slots) plus one suffix item (slot S), merged by one merge item; a group
-// with no prefix keys has only its suffix item, which writes the output.
-// The chunk length is the smallest that keeps every item of the launch
-// resident at once (verify_wgs_per_cu per CU), capped so that S stays within
-// kMaxVerifySplits and a chunk's page ids fit the kernel's LDS staging.
+// Cascade verify plan.
+//
+// Groups are (request, kv head, q-tile of ROWS packed rows); each group's
+// visible prefix is cut into key chunks (split-KV), one partial state each,
+// plus one suffix (tree) item, and the merge launch combines the group's
+// partials.  A group with no prefix keys has only its suffix item, which
+// writes the output.
+//
+// Placement.  Workgroups are dealt to the 8 XCDs round-robin (workgroup i on
+// XCD i % 8), and inside an XCD the k-th workgroup of the first round and the
+// k-th of the second round land on the same CU (measured on MI355X with
+// per-workgroup HW_ID / XCC_ID reads).  Sets = all q-tiles of one (request,
+// kv head), or of one key range of it when there are fewer than 8 such sets,
+// so that every key tile is read from HBM once and re-read from that XCD's
+// L2 by the other q-tiles; sets go to XCDs largest first onto the least-loaded
+// XCD.
+//
+// Balance.  Per XCD the prefix chunks are sized to fill its workgroup slots
+// (CUs per XCD x workgroups per CU) after the suffix items: the largest chunk
+// T is the smallest that fits, then the remaining slots split the groups whose
+// chunks are longest.  With one or two rounds of workgroups per XCD, the
+// longest items run alone and the rest are paired longest-with-shortest on a
+// CU; beyond two rounds items go longest first.
+namespace {
+
+struct Piece {            // the q-tiles of one (request, kv head) over prefix tiles [t0, t1)
+  int req, kvh, t0, t1;
+  bool suffix;            // the set's q-tiles also get their suffix items here
+};
+
+struct PlanItem {
+  VerifyItem w;
+  int cost;               // in prefix-tile units
+};
+
+int ceil_div(long long a, long long b) { return (int)((a + b - 1) / b); }
+
+}  // namespace
+
 int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
   out.items.clear();
   out.merges.clear();
@@ -125,13 +116,15 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
   const int num_cus = in.num_cus > 0 ? in.num_cus : 256;
   const int W = in.waves ? in.waves : verify_auto_waves(in, num_cus);
   const int ROWS = verify_rows(W);
-  const long long capacity = (long long)num_cus * verify_wgs_per_cu(W);
-  const int split_cap =
-      in.max_splits > 0 ? std::min(in.max_splits, kMaxVerifySplits) : kMaxVerifySplits;
+  const int wpc = verify_wgs_per_cu(W);
+  const int cus_per_xcd = std::max(1, num_cus / 8);
+  const int xcd_slots = cus_per_xcd * wpc;
+  const int split_cap = in.max_splits > 0 ? std::min(in.max_splits, kMaxVerifySplits) : kMaxVerifySplits;
+  // a chunk's page ids must fit the kernel's LDS staging
+  const int max_chunk = in.page_size > 0 ? std::max(1, ((kMaxStagedPages - 8) * in.page_size) / 64) : (1 << 30);
+  constexpr int kMinChunk = 2;  // shorter chunks cost more in partials than they gain in balance
 
-  std::vector<int> nq(R), qtiles(R), ptiles(R), stiles(R), kv0(R), kv1(R), splits(R, 0);
-  long long units = 0, groups = 0;
-  int max_ptiles = 1;
+  std::vector<int> nq(R), qtiles(R), ptiles(R), stiles(R), kv0(R), kv1(R);
   for (int r = 0; r < R; ++r) {
     nq[r] = in.qo_indptr[r + 1] - in.qo_indptr[r];
     qtiles[r] = (nq[r] * g + ROWS - 1) / ROWS;
@@ -141,161 +134,223 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
     kv1[r] = L;
     ptiles[r] = nq[r] > 0 ? (Leff + 63) / 64 : 0;
     stiles[r] = (nq[r] + 63) / 64;
-    max_ptiles = std::max(max_ptiles, ptiles[r]);
-    units += (long long)Hkv * qtiles[r] * (ptiles[r] + stiles[r]);
-    groups += (long long)Hkv * qtiles[r];
   }
-  auto wgs = [&](int c) {
-    long long t = 0;
-    for (int r = 0; r < R; ++r)
-      if (nq[r] > 0) t += (long long)Hkv * qtiles[r] * ((ptiles[r] + c - 1) / c + 1);
-    return t;
-  };
-  int chunk = (int)std::max<long long>(1, (units + capacity - 1) / std::max<long long>(capacity, 1));
-  while (chunk < max_ptiles && wgs(chunk) > capacity) ++chunk;
-  for (int r = 0; r < R; ++r) chunk = std::max(chunk, (ptiles[r] + split_cap - 1) / split_cap);
-  if (in.page_size > 0) {
-    const int max_chunk = std::max(1, ((kMaxStagedPages - 8) * in.page_size) / 64);
-    chunk = std::min(chunk, max_chunk);
-  }
-  (void)groups;
-
-  // consecutive slots per group: S prefix partials, then the suffix partial
   std::vector<int> grp0(R + 1, 0);
   for (int r = 0; r < R; ++r) grp0[r + 1] = grp0[r] + Hkv * qtiles[r];
-  std::vector<int> slot0(grp0[R], -1);
-  int slot = 0, max_splits_used = 0;
+  const int ngroups = grp0[R];
+
+  // ---- sets of pieces, dealt to XCDs ----
+  int nsets = 0;
+  for (int r = 0; r < R; ++r) nsets += nq[r] > 0 ? Hkv : 0;
+  std::vector<std::vector<Piece>> sets;
+  std::vector<long long> set_cost;
   for (int r = 0; r < R; ++r) {
-    const int S = ptiles[r] == 0 ? 0 : (ptiles[r] + chunk - 1) / chunk;
-    splits[r] = S;
-    max_splits_used = std::max(max_splits_used, S);
-    for (int gi = grp0[r]; gi < grp0[r + 1]; ++gi) {
-      if (S > 0) {
-        slot0[gi] = slot;
-        slot += S + 1;
+    if (nq[r] == 0) continue;
+    const int ranges = (nsets >= 8 || ptiles[r] == 0) ? 1
+                       : std::min({ceil_div(8, nsets), ptiles[r], split_cap});
+    for (int h = 0; h < Hkv; ++h)
+      for (int k = 0; k < ranges; ++k) {
+        Piece pc{r, h, (int)((long long)ptiles[r] * k / ranges), (int)((long long)ptiles[r] * (k + 1) / ranges),
+                 k == 0};
+        sets.push_back({pc});
+        set_cost.push_back((long long)qtiles[r] * ((pc.t1 - pc.t0) + (pc.suffix ? 2 * stiles[r] : 0)));
       }
+  }
+  std::vector<int> order(sets.size());
+  for (size_t i = 0; i < order.size(); ++i) order[i] = (int)i;
+  std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return set_cost[a] > set_cost[b]; });
+  std::vector<long long> load(8, 0);
+  std::vector<std::vector<int>> xcd_sets(8);
+  for (int s : order) {
+    const int x = (int)(std::min_element(load.begin(), load.end()) - load.begin());
+    load[x] += set_cost[s];
+    xcd_sets[x].push_back(s);
+  }
+
+  // ---- chunk counts per (piece, q-tile), XCD by XCD ----
+  // nchunk[set][qt]: prefix chunks of q-tile qt of the set's piece
+  std::vector<std::vector<int>> nchunk(sets.size());
+  for (int x = 0; x < 8; ++x) {
+    struct Cell { int set, qt, pt, cap; };
+    std::vector<Cell> cells;
+    int suffix_items = 0;
+    for (int s : xcd_sets[x]) {
+      const Piece& pc = sets[s][0];
+      nchunk[s].assign(qtiles[pc.req], 0);
+      const int pieces_per_group = (nsets >= 8 || ptiles[pc.req] == 0) ? 1
+                                   : std::min({ceil_div(8, nsets), ptiles[pc.req], split_cap});
+      const int cap = std::max(1, split_cap / pieces_per_group);
+      for (int qt = 0; qt < qtiles[pc.req]; ++qt) {
+        if (pc.t1 > pc.t0) cells.push_back({s, qt, pc.t1 - pc.t0, cap});
+        if (pc.suffix) ++suffix_items;
+      }
+    }
+    if (cells.empty()) continue;
+    const long long budget = std::max<long long>((long long)xcd_slots - suffix_items, (long long)cells.size());
+    int maxpt = 1, tmin = 1;
+    for (auto& c : cells) {
+      maxpt = std::max(maxpt, c.pt);
+      tmin = std::max(tmin, ceil_div(c.pt, c.cap));
+    }
+    int T = std::max(tmin, std::min(kMinChunk, maxpt));
+    auto count = [&](int t) {
+      long long n = 0;
+      for (auto& c : cells) n += ceil_div(c.pt, t);
+      return n;
+    };
+    while (T < maxpt && count(T) > budget) ++T;
+    T = std::min(T, std::max(max_chunk, tmin));
+    long long used = 0;
+    std::vector<int> n(cells.size());
+    for (size_t i = 0; i < cells.size(); ++i) {
+      n[i] = ceil_div(cells[i].pt, T);
+      used += n[i];
+    }
+    // remaining slots: one more chunk to the cell whose chunks are longest
+    // (most chunks at that length first), while chunks stay >= kMinChunk
+    for (long long extra = budget - used; extra > 0; --extra) {
+      int best = -1;
+      long long best_key = -1;
+      for (size_t i = 0; i < cells.size(); ++i) {
+        const int len = ceil_div(cells[i].pt, n[i]);
+        if (n[i] + 1 > cells[i].cap || cells[i].pt / (n[i] + 1) < kMinChunk) continue;
+        const int at_len = cells[i].pt % n[i] ? cells[i].pt % n[i] : n[i];
+        const long long key = (long long)len * 4096 + at_len;
+        if (key > best_key) { best_key = key; best = (int)i; }
+      }
+      if (best < 0) break;
+      ++n[best];
+    }
+    for (size_t i = 0; i < cells.size(); ++i) nchunk[cells[i].set][cells[i].qt] = n[i];
+  }
+
+  // ---- partial slots: per group its prefix chunks in key order, then the suffix ----
+  std::vector<int> gchunks(ngroups, 0);
+  for (size_t s = 0; s < sets.size(); ++s) {
+    const Piece& pc = sets[s][0];
+    for (int qt = 0; qt < qtiles[pc.req]; ++qt) gchunks[grp0[pc.req] + pc.kvh * qtiles[pc.req] + qt] += nchunk[s][qt];
+  }
+  std::vector<int> slot0(ngroups, -1), next_slot(ngroups, 0);
+  int slot = 0, max_splits_used = 0;
+  for (int gi = 0; gi < ngroups; ++gi) {
+    max_splits_used = std::max(max_splits_used, gchunks[gi]);
+    if (gchunks[gi] > 0) {
+      slot0[gi] = slot;
+      next_slot[gi] = slot;
+      slot += gchunks[gi] + 1;
     }
   }
 
-  // One set per (request, kv head): all its q-tiles, key chunks and suffix
-  // items run on one XCD, so the head's K/V and Q come from HBM once and its
-  // partial states stay in that XCD's L2.  With fewer such sets than XCDs,
-  // each key chunk (with all q-tiles reading it) is a set of its own.
-  long long nheads_sets = 0;
-  for (int r = 0; r < R; ++r) nheads_sets += nq[r] > 0 ? Hkv : 0;
-  const bool per_head = nheads_sets >= 8;
-  std::vector<ItemSet<VerifyItem>> sets;
-  std::vector<std::vector<VerifyMerge>> set_merges;
-  for (int r = 0; r < R; ++r) {
-    if (nq[r] == 0) continue;
-    const int S = splits[r];
+  // ---- items per XCD (sets in key order within a group, so slots follow key order) ----
+  std::vector<std::vector<PlanItem>> lists(8);
+  std::vector<std::vector<VerifyMerge>> mlists(8);
+  std::vector<int> set_order(sets.size());
+  for (size_t i = 0; i < set_order.size(); ++i) set_order[i] = (int)i;  // creation order = (req, head, range)
+  std::vector<int> set_xcd(sets.size(), 0);
+  for (int x = 0; x < 8; ++x)
+    for (int s : xcd_sets[x]) set_xcd[s] = x;
+  for (int s : set_order) {
+    const Piece& pc = sets[s][0];
+    const int r = pc.req, h = pc.kvh, x = set_xcd[s];
     const int q0 = in.qo_indptr[r];
     const int pbase = in.page_size > 0 ? in.page_indptr[r] : (in.prefix_tok_indptr ? in.prefix_tok_indptr[r] : 0);
-    for (int h = 0; h < Hkv; ++h) {
-      ItemSet<VerifyItem> head_set;
-      head_set.cost = 0;
-      for (int s_ = 0; s_ < S; ++s_) {
-        const int base = ptiles[r] / S, rem = ptiles[r] % S;
-        const int t0 = s_ * base + std::min(s_, rem);
-        const int nt = base + (s_ < rem ? 1 : 0);
-        ItemSet<VerifyItem> set;
-        set.cost = (long long)nt * qtiles[r];
-        for (int qt = 0; qt < qtiles[r]; ++qt) {
-          VerifyItem w{};
-          w.req = r;
-          w.kvh = h;
-          w.qtile = qt;
-          w.src = SRC_PREFIX;
-          w.kv_begin = kv0[r] + 64 * t0;
-          w.kv_end = std::min(kv1[r], kv0[r] + 64 * (t0 + nt));
-          w.slot = slot0[grp0[r] + h * qtiles[r] + qt] + s_;
-          w.mode = MODE_PARTIAL;
-          w.group = grp0[r] + h * qtiles[r] + qt;
-          w.slot0 = slot0[w.group];
-          w.nprod = S + 1;
-          w.q0 = q0;
-          w.nq = nq[r];
-          w.base = pbase;
-          w.causal_off = 0;
-          set.items.push_back(w);
-        }
-        if (per_head) {
-          head_set.cost += set.cost;
-          head_set.items.insert(head_set.items.end(), set.items.begin(), set.items.end());
-        } else {
-          sets.push_back(std::move(set));
-          set_merges.emplace_back();
-        }
-      }
-      ItemSet<VerifyItem> set;
-      set.cost = (long long)stiles[r] * qtiles[r];
-      std::vector<VerifyMerge> merges;
-      for (int qt = 0; qt < qtiles[r]; ++qt) {
-        const int gi = grp0[r] + h * qtiles[r] + qt;
+    for (int qt = 0; qt < qtiles[r]; ++qt) {
+      const int gi = grp0[r] + h * qtiles[r] + qt;
+      const int S = nchunk[s][qt];
+      const int span = pc.t1 - pc.t0;
+      for (int c = 0; c < S; ++c) {
+        const int a = pc.t0 + (int)((long long)span * c / S), b = pc.t0 + (int)((long long)span * (c + 1) / S);
         VerifyItem w{};
         w.req = r;
         w.kvh = h;
         w.qtile = qt;
-        w.src = SRC_SUFFIX;
-        w.kv_begin = 0;
-        w.kv_end = nq[r];
-        w.slot = S > 0 ? slot0[gi] + S : -1;
-        w.mode = S > 0 ? MODE_PARTIAL : MODE_FINAL;
-        w.group = gi;
-        w.slot0 = S > 0 ? slot0[gi] : -1;
-        w.nprod = S + 1;
+        w.src = SRC_PREFIX;
+        w.kv0 = kv0[r];
+        w.plan_len = kv1[r];
+        w.kv_begin = kv0[r] + 64 * a;
+        w.kv_end = std::min(kv1[r], kv0[r] + 64 * b);
+        w.slot = next_slot[gi]++;
+        w.mode = MODE_PARTIAL;
         w.q0 = q0;
         w.nq = nq[r];
-        w.base = q0;  // the request's suffix keys are rows q0.. of k/v_suffix
-        w.causal_off = 0;
-        set.items.push_back(w);
-        if (S > 0) {
-          // one merge workgroup per 32-row block holding valid rows
-          for (int blk = 0; blk < ROWS / 32 && qt * ROWS + blk * 32 < nq[r] * g; ++blk) {
-            VerifyMerge m{};
-            m.req = r;
-            m.kvh = h;
-            m.qtile = qt;
-            m.slot0 = slot0[gi];
-            m.nslots = S + 1;
-            m.q0 = q0;
-            m.nq = nq[r];
-            m.blk = blk;
-            merges.push_back(m);
-          }
-        }
-      }
-      if (per_head) {
-        head_set.cost += set.cost;
-        head_set.items.insert(head_set.items.end(), set.items.begin(), set.items.end());
-        sets.push_back(std::move(head_set));
-        set_merges.push_back(std::move(merges));
-      } else {
-        sets.push_back(std::move(set));
-        set_merges.push_back(std::move(merges));
+        w.base = pbase;
+        lists[x].push_back({w, b - a});
       }
     }
+    if (!pc.suffix) continue;
+    for (int qt = 0; qt < qtiles[r]; ++qt) {
+      const int gi = grp0[r] + h * qtiles[r] + qt;
+      const bool split = gchunks[gi] > 0;
+      VerifyItem w{};
+      w.req = r;
+      w.kvh = h;
+      w.qtile = qt;
+      w.src = SRC_SUFFIX;
+      w.kv_begin = 0;
+      w.kv_end = nq[r];
+      w.slot = split ? slot0[gi] + gchunks[gi] : -1;
+      w.mode = split ? MODE_PARTIAL : MODE_FINAL;
+      w.q0 = q0;
+      w.nq = nq[r];
+      w.base = q0;  // the request's suffix keys are rows q0.. of k/v_suffix
+      lists[x].push_back({w, 2 * stiles[r]});
+      if (split)  // one merge workgroup per 32-row block holding valid rows
+        for (int blk = 0; blk < ROWS / 32 && qt * ROWS + blk * 32 < nq[r] * g; ++blk) {
+          VerifyMerge m{};
+          m.req = r;
+          m.kvh = h;
+          m.qtile = qt;
+          m.slot0 = slot0[gi];
+          m.nslots = gchunks[gi] + 1;
+          m.q0 = q0;
+          m.nq = nq[r];
+          m.blk = blk;
+          mlists[x].push_back(m);
+        }
+    }
   }
-  const std::vector<int> xcd = order_for_xcds(sets, out.items);
-  std::vector<std::vector<VerifyMerge>> mlists(8);
-  for (size_t i = 0; i < set_merges.size(); ++i)
-    mlists[xcd[i]].insert(mlists[xcd[i]].end(), set_merges[i].begin(), set_merges[i].end());
+
+  // ---- dispatch order per XCD, then interleave the XCDs ----
+  std::vector<std::vector<VerifyItem>> ordered(8);
+  for (int x = 0; x < 8; ++x) {
+    auto& L = lists[x];
+    std::stable_sort(L.begin(), L.end(), [](const PlanItem& a, const PlanItem& b) { return a.cost > b.cost; });
+    const int m = (int)L.size(), K = cus_per_xcd;
+    auto& o = ordered[x];
+    if (wpc == 2 && m > K && m <= 2 * K) {
+      // p CUs run a pair, K - p run one item: first round = the pairs' longer
+      // halves, then the singles (the longest items); second round = the
+      // pairs' shorter halves, k-th with k-th
+      const int p = m - K, s = K - p;
+      for (int i = 0; i < p; ++i) o.push_back(L[s + i].w);
+      for (int i = 0; i < s; ++i) o.push_back(L[i].w);
+      for (int i = 0; i < p; ++i) o.push_back(L[m - 1 - i].w);
+    } else {
+      for (auto& it : L) o.push_back(it.w);
+    }
+  }
+  size_t maxlen = 0;
+  for (auto& l : ordered) maxlen = std::max(maxlen, l.size());
+  for (size_t k = 0; k < maxlen; ++k)
+    for (int x = 0; x < 8; ++x) {
+      if (k < ordered[x].size()) {
+        out.items.push_back(ordered[x][k]);
+      } else {
+        VerifyItem w{};
+        w.mode = MODE_NOOP;
+        out.items.push_back(w);
+      }
+    }
+  while (!out.items.empty() && out.items.back().mode == MODE_NOOP) out.items.pop_back();
   interleave_merges(mlists, out.merges);
 
   out.waves = W;
   out.rows = ROWS;
   out.num_slots = slot;
   out.max_splits_used = max_splits_used;
-  out.num_groups = grp0[R];
-  out.merge_mode = slot > 0 ? in.merge_mode : MERGE_LAUNCH;
-  out.merge_in_attention = out.merge_mode != MERGE_LAUNCH;
-  if (out.merge_in_attention) out.merges.clear();
-  // bf16 partial O + fp32 LSE per (slot, row), then the int32 counters
-  // (16-byte aligned)
-  const size_t part_bytes = (size_t)slot * ROWS * ((size_t)in.head_dim * 2 + sizeof(float));
-  out.counters_offset = (part_bytes + 15) & ~(size_t)15;
-  out.workspace_bytes = out.merge_in_attention ? out.counters_offset + (size_t)out.num_groups * sizeof(int)
-                                               : part_bytes;
+  out.num_groups = ngroups;
+  // bf16 partial O + fp32 LSE per (slot, row)
+  out.workspace_bytes = (size_t)slot * ROWS * ((size_t)in.head_dim * 2 + sizeof(float));
   return 0;
 }
 

@@ -23,7 +23,6 @@ struct VerifyPlanInput {
   int max_splits;  // 0: no limit beyond kMaxVerifySplits
   int waves;       // 0: choose; else 2, 4 or 8
   int page_size;   // 0: contiguous prefix
-  int merge_mode;  // MERGE_*
 };
 
 struct VerifyPlanOutput {
@@ -33,11 +32,7 @@ struct VerifyPlanOutput {
   int rows;                         // rows per workgroup tile (= per partial slot)
   int num_slots;
   int max_splits_used;
-  int num_groups;                   // (request, kv head, q-tile) groups with split prefixes
-  int merge_mode;                   // MERGE_* in effect (MERGE_LAUNCH when nothing is split)
-  bool merge_in_attention;          // merge_mode != MERGE_LAUNCH
-  size_t counters_offset;           // workspace byte offset of the int32 counters: the producer
-                                    // arrivals of each group
+  int num_groups;                   // (request, kv head, q-tile) groups
   size_t workspace_bytes;
 };
 

@@ -79,7 +79,6 @@ struct VerifySmem {
       bf16_t Vt[2][D * (64 + 8)];      // register-staged V^T tiles (row pitch 64 + 8)
       int pages[kMaxStagedPages];
     } st;
-    int last;                          // after the tile loop: this workgroup is its group's last producer
   };
 };
 #pragma clang diagnostic pop
@@ -91,10 +90,6 @@ __device__ __forceinline__ void wait_vmcnt_units(int k) {
     if (k == (int)decltype(i)::value) wait_vmcnt<decltype(i)::value * UNIT>();
   });
 }
-
-// Partial slots merged per batch by a group's last producer (all loads of a
-// batch are in flight together).
-constexpr int kMergeBatch = 4;
 
 template <int D>
 __device__ __forceinline__ void store_out(const VerifyParams& p, int qrow, int qh, int hh,
@@ -156,7 +151,17 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
     n[rb] = rv[rb] ? row / g : 0;
     qh[rb] = w.kvh * g + (rv[rb] ? row - n[rb] * g : 0);
   }
-  const int kv_begin = w.kv_begin, kv_end = w.kv_end;
+  int kv_begin = w.kv_begin, kv_end = w.kv_end;
+  if constexpr (!MASKED) {
+    // dynamic plan: the item's key range relative to the window start, at
+    // the run-time prefix length (never beyond the planned length)
+    if (p.prefix_len) {
+      const int L = min(max(p.prefix_len[w.req], 0), w.plan_len);
+      const int k0 = L - (p.window_left >= 0 ? min(L, p.window_left) : L);
+      kv_begin = k0 + (w.kv_begin - w.kv0);
+      kv_end = min(k0 + (w.kv_end - w.kv0), L);
+    }
+  }
   const int ntiles = kv_end > kv_begin ? (kv_end - kv_begin + 63) >> 6 : 0;
 
   // ---- suffix masks: the rows' tree-mask words held in registers ----
@@ -212,6 +217,8 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
       // the LDS stores below counts exactly the loads issued after these
 #pragma unroll
       for (int j = 0; j < PPT; ++j) pgv[j] = pt[min(tid + j * NT, npg - 1)];
+#pragma unroll
+      for (int j = 0; j < PPT; ++j) pgv[j] = (int)min((unsigned)pgv[j], (unsigned)S.num_pages - 1u);
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -258,7 +265,8 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
     if constexpr (STAGED)
       return (long long)pages[(t >> log2p) - pg_first] * page_b + (long long)(t & pmask) * tok_b;
     else if constexpr (PAGED)
-      return (long long)S.page_table[w.base + (t >> log2p)] * page_b + (long long)(t & pmask) * tok_b;
+      return (long long)min((unsigned)S.page_table[w.base + (t >> log2p)], (unsigned)S.num_pages - 1u) * page_b +
+             (long long)(t & pmask) * tok_b;
     else
       return (long long)t * tok_b;
   };
@@ -513,7 +521,8 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
           return pages[min(max(pi - pg_first, 0), kMaxStagedPages - 1)];
         } else {
           typedef const __attribute__((address_space(4))) int const_int;
-          return ntiles > 0 ? ((const_int*)S.page_table)[w.base + pi] : 0;
+          return ntiles > 0 ? (int)min((unsigned)((const_int*)S.page_table)[w.base + pi], (unsigned)S.num_pages - 1u)
+                            : 0;
         }
       }
       return 0;
@@ -790,90 +799,13 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
           for (int q4 = 0; q4 < 4; ++q4) {
             const u32x2 val = {pack_bf16x2(o[rb][mt][4 * q4], o[rb][mt][4 * q4 + 1]),
                                pack_bf16x2(o[rb][mt][4 * q4 + 2], o[rb][mt][4 * q4 + 3])};
-            u32x2* dst = (u32x2*)(po + image_offset<D>(blk, mt, q4, lane));
-            if (p.counters) store_agent(dst, val);
-            else *dst = val;
+            *(u32x2*)(po + image_offset<D>(blk, mt, q4, lane)) = val;
           }
-        if (hh == 0) {
-          if (p.counters) store_agent(pl, lse_r[rb]);
-          else *pl = lse_r[rb];
-        }
+        if (hh == 0) *pl = lse_r[rb];
       } else if (rv[rb]) {
         store_out<D>(p, w.q0 + n[rb], qh[rb], hh, o[rb], lse_r[rb]);
       }
     }
-  }
-  if (w.mode != MODE_PARTIAL || !p.counters) return;
-
-  // ---- merge in the group's last producer (no waiting: whoever completes
-  // the count does the merge; flashinfer.merge_state_in_place semantics,
-  // generation/verification.py:163-165, and the sink of :173-176).  The
-  // partial states are exchanged through device-scope stores and loads; all
-  // workgroups of a group run on one XCD (the planner's placement), whose L2
-  // they share. ----
-  wait_vmcnt<0>();  // this wave's partial stores are complete (device-visible)
-  __syncthreads();
-  if (tid == 0)
-    sm.last = __hip_atomic_fetch_add(&p.counters[w.group], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-              w.nprod - 1;
-  __syncthreads();
-  if (!sm.last) return;
-  if (tid == 0) __hip_atomic_exchange(&p.counters[w.group], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next launch
-  if (!live) return;
-  const long long slot_elems = (long long)ROWS * D;
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-    const int blk = RB * wv + rb;
-    // every slot, this workgroup's own included, in slot order from the
-    // workspace: the result does not depend on which producer came last
-    float mval = -INFINITY, wsum = 0.f;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) o[rb][mt] = f32x16{};
-    for (int s0 = 0; s0 < w.nprod; s0 += kMergeBatch) {
-      float ls[kMergeBatch];
-      u32x2 v[kMergeBatch][MT][4];
-#pragma unroll
-      for (int b = 0; b < kMergeBatch; ++b) {
-        const int slot = w.slot0 + s0 + b;
-        const bool use = s0 + b < w.nprod;
-        ls[b] = use ? load_agent(p.part_lse + (long long)slot * ROWS + blk * 32 + l32) : -INFINITY;
-        const bf16_t* po = (const bf16_t*)p.part_o + (long long)slot * slot_elems;
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4)
-            v[b][mt][q4] = use ? load_agent((const u32x2*)(po + image_offset<D>(blk, mt, q4, lane))) : (u32x2){0u, 0u};
-      }
-      float bm = -INFINITY;
-#pragma unroll
-      for (int b = 0; b < kMergeBatch; ++b) bm = fmaxf(bm, ls[b]);
-      const float nm = fmaxf(mval, bm);
-      if (nm == -INFINITY) continue;  // nothing visible so far
-      const float f = mval == -INFINITY ? 0.f : __expf(mval - nm);  // 1 when the max holds
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) o[rb][mt] *= f;
-      wsum *= f;
-#pragma unroll
-      for (int b = 0; b < kMergeBatch; ++b) {
-        const float wt = ls[b] == -INFINITY ? 0.f : __expf(ls[b] - nm);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4) {
-            o[rb][mt][4 * q4] += wt * bf16_lo(v[b][mt][q4][0]);
-            o[rb][mt][4 * q4 + 1] += wt * bf16_hi(v[b][mt][q4][0]);
-            o[rb][mt][4 * q4 + 2] += wt * bf16_lo(v[b][mt][q4][1]);
-            o[rb][mt][4 * q4 + 3] += wt * bf16_hi(v[b][mt][q4][1]);
-          }
-        wsum += wt;
-      }
-      mval = nm;
-    }
-    const bool nonempty = wsum > 0.f;
-    const float inv = nonempty ? 1.f / wsum : 0.f;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) o[rb][mt] *= inv;
-    if (rv[rb]) store_out<D>(p, w.q0 + n[rb], qh[rb], hh, o[rb], nonempty ? mval + logf(wsum) : -INFINITY);
   }
 }
 
@@ -921,9 +853,8 @@ void verify_attn_kernel(const VerifyParams p) {
 // 163-165) and the GPT-OSS sink (verification.py:173-176), written to O and
 // LSE.  Lane l owns row l%32 and head dims 32mt + 8q4 + 4(l/32) + e; all
 // partial loads (up to kMaxVerifySplits + 1 slots) are in flight at once.
-// COHERENT: the partials were written inside this launch (device-scope loads).
 // ---------------------------------------------------------------------------
-template <int D, int ROWS, bool COHERENT>
+template <int D, int ROWS>
 __device__ __forceinline__ void merge_rows(const VerifyParams& p, int slot0, int nslots, int blk, int mt,
                                            int lane, int q0, int nq, int kvh, int qtile) {
   constexpr int B = kMaxVerifySplits + 1;
@@ -950,12 +881,12 @@ __device__ __forceinline__ void merge_rows(const VerifyParams& p, int slot0, int
       if (b < cnt) {
         const long long s = slot0 + s0 + b;
         const float* pl = p.part_lse + s * ROWS + blk * 32 + l32;
-        ls[b] = COHERENT ? load_agent(pl) : *pl;
+        ls[b] = *pl;
         const bf16_t* po = (const bf16_t*)p.part_o + s * slot_elems;
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
           const u32x2* src = (const u32x2*)(po + image_offset<D>(blk, mt, q4, lane));
-          v[b][q4] = COHERENT ? load_agent(src) : *src;
+          v[b][q4] = *src;
         }
       }
     }
@@ -1012,7 +943,7 @@ __global__ __launch_bounds__(64) void verify_merge_kernel(const VerifyParams p) 
   const VerifyMerge m = p.merges[mi];
   __asm__ volatile("" ::"s"(m.kvh), "s"(m.qtile), "s"(m.slot0), "s"(m.nslots), "s"(m.q0), "s"(m.nq), "s"(m.blk));
   if (m.nslots == 0) return;  // padding
-  merge_rows<D, ROWS, false>(p, m.slot0, m.nslots, m.blk, mt, threadIdx.x, m.q0, m.nq, m.kvh, m.qtile);
+  merge_rows<D, ROWS>(p, m.slot0, m.nslots, m.blk, mt, threadIdx.x, m.q0, m.nq, m.kvh, m.qtile);
 }
 
 // ---------------------------------------------------------------------------

@@ -16,8 +16,6 @@ D2SD_KV_FP8_E4M3 = 1
 D2SD_MASK_NONE = 0
 D2SD_MASK_CAUSAL = 1
 D2SD_MASK_TREE = 2
-D2SD_MERGE_LAUNCH = 0
-D2SD_MERGE_LAST_PRODUCER = 1
 D2SD_DTYPE_BF16 = 0
 D2SD_DTYPE_F32 = 1
 
@@ -60,7 +58,7 @@ class PlanDesc(C.Structure):
         ("num_cus", C.c_int),
         ("max_splits", C.c_int),
         ("waves_per_block", C.c_int),
-        ("merge_mode", C.c_int),
+        ("dynamic_prefix", C.c_int),
     ]
 
 
@@ -81,9 +79,9 @@ class PlanInfo(C.Structure):
         ("kv_dtype", C.c_int),
         ("page_size", C.c_int),
         ("num_groups", C.c_int),
-        ("merge_in_attention", C.c_int),
-        ("counters_offset", C.c_size_t),
-        ("merge_mode", C.c_int),
+        ("dynamic_prefix", C.c_int),
+        ("window_left", C.c_int),
+        ("prefix_extent", C.c_int64),
     ]
 
 
@@ -107,6 +105,8 @@ class RunArgs(C.Structure):
         ("prefix_stride_page", C.c_int64),
         ("page_size", C.c_int),
         ("page_table", C.c_void_p),
+        ("prefix_extent", C.c_int64),
+        ("prefix_len", C.c_void_p),
         ("k_scale", C.c_void_p),
         ("v_scale", C.c_void_p),
         ("sinks", C.c_void_p),

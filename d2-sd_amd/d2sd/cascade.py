@@ -16,6 +16,15 @@ plan() does all host work and device uploads; run() only launches kernels
 (two per call: attention over prefix key chunks and suffix trees, writing
 partial states, then their merge), allocates nothing when `out`/`lse` are
 given, and can be captured into a HipGraph.
+
+Device buffers (plan, workspace, tree mask, page table, prefix lengths) are
+kept across plan() calls: a re-plan with the same shape (work items, merges,
+partial slots, mask width) rewrites them in place, so a graph captured
+earlier replays the new plan; a re-plan of another shape allocates new
+buffers, and a graph captured earlier keeps (and keeps using) its own.  With
+dynamic_prefix=True, prefix_len is each request's largest prefix and the
+kernels read the current lengths from `prefix_len_dev` (int32, on the
+device), so one captured step replays while the cache grows.
 """
 from __future__ import annotations
 
@@ -27,18 +36,24 @@ import torch
 
 from . import _lib
 from ._lib import check, lib
+from .graph import keep_alive
 from .tree import pack_tree_masks
 
 _MASK_MODES = {"none": _lib.D2SD_MASK_NONE, "causal": _lib.D2SD_MASK_CAUSAL, "tree": _lib.D2SD_MASK_TREE}
-# where the partial states of a split (request, kv head, q-tile) group are merged
-_MERGE_MODES = {
-    "launch": _lib.D2SD_MERGE_LAUNCH,  # a second (merge) launch
-    "last_producer": _lib.D2SD_MERGE_LAST_PRODUCER,  # the group's last producer, same launch
-}
 
 
 def _i32(x) -> np.ndarray:
     return np.ascontiguousarray(np.asarray(x, dtype=np.int32))
+
+
+def _reuse(old: Optional[torch.Tensor], new: torch.Tensor, same_shape: bool) -> torch.Tensor:
+    """`new` copied into `old` when the plan keeps its shape (old buffer large
+    enough, same dtype), else `new` itself."""
+    if (same_shape and old is not None and old.dtype == new.dtype and old.device == new.device
+            and old.numel() >= new.numel()):
+        old.view(-1)[:new.numel()].copy_(new.view(-1))
+        return old
+    return new
 
 
 class CascadeVerifyAttention:
@@ -72,7 +87,7 @@ class CascadeVerifyAttention:
         max_splits: int = 0,
         waves_per_block: int = 0,
         num_cus: int = 0,
-        merge_mode: str = "launch",
+        dynamic_prefix: bool = False,
     ) -> "CascadeVerifyAttention":
         """Plan one verify call.
 
@@ -88,17 +103,16 @@ class CascadeVerifyAttention:
         window_left >= 0 keeps the last window_left prefix keys for all queries
         (verification.py:133-135).  sinks [Hq] fp32 applies O *= sigmoid(lse - sink).
         kv_dtype torch.float8_e4m3fn takes per-kv-head fp32 k_scale / v_scale.
-        merge_mode: "launch" (a second launch merges the split partial states) or
-        "last_producer" (each group's last producer workgroup merges them inside
-        the attention launch).
+        dynamic_prefix: prefix_len is each request's largest prefix; run() uses
+        the current lengths in self.prefix_len_dev (set_prefix_len(), or any
+        device write, e.g. PagedKVCommit's advance), each clamped to
+        [0, planned length].
         """
         qo = _i32(qo_indptr)
         pl = _i32(prefix_len)
         R = int(pl.shape[0])
         if qo.shape[0] != R + 1:
             raise ValueError("qo_indptr must have len(prefix_len) + 1 entries")
-        if merge_mode not in _MERGE_MODES:
-            raise ValueError(f"merge_mode must be one of {sorted(_MERGE_MODES)}")
         if mask_mode not in _MASK_MODES:
             raise ValueError(f"mask_mode must be one of {sorted(_MASK_MODES)}")
         if kv_layout not in ("HND", "NHD"):
@@ -132,20 +146,26 @@ class CascadeVerifyAttention:
         desc.num_cus = num_cus
         desc.max_splits = max_splits
         desc.waves_per_block = waves_per_block
-        desc.merge_mode = _MERGE_MODES[merge_mode]
+        desc.dynamic_prefix = int(bool(dynamic_prefix))
         info = _lib.PlanInfo()
         check(lib.d2sd_cascade_plan(C.byref(desc), None, 0, C.byref(info)), "cascade_plan (size)")
         host = np.zeros(max(info.plan_ints, 8), dtype=np.int32)
         check(lib.d2sd_cascade_plan(C.byref(desc), host.ctypes.data_as(C.POINTER(C.c_int32)), host.size,
                                     C.byref(info)), "cascade_plan")
+        old = getattr(self, "info", None) if self._planned else None
+        same = old is not None and all(
+            getattr(old, f) == getattr(info, f) for f in
+            ("num_items", "num_merges", "waves_per_block", "rows_per_tile", "num_slots", "num_reqs",
+             "num_qo_heads", "num_kv_heads", "head_dim", "kv_dtype", "page_size", "dynamic_prefix"))
         self.info = info
         self.plan_host = host
         self.qo_indptr_host = qo
         self.prefix_len_host = pl
-        self.plan_dev = torch.from_numpy(host).to(dev)
-        # zero-filled once: the counters at its end start at 0, and every run
-        # leaves them at 0
-        self.workspace = torch.zeros(max(int(info.workspace_bytes), 16), dtype=torch.uint8, device=dev)
+        self.plan_dev = _reuse(getattr(self, "plan_dev", None), torch.from_numpy(host).to(dev), same)
+        ws = int(max(int(info.workspace_bytes), 16))
+        self.workspace = (self.workspace if same and getattr(self, "workspace", None) is not None
+                          and self.workspace.numel() >= ws else torch.empty(ws, dtype=torch.uint8, device=dev))
+        self.prefix_len_dev = _reuse(getattr(self, "prefix_len_dev", None), torch.from_numpy(pl.copy()).to(dev), same)
         self.mask_mode = _MASK_MODES[mask_mode]
         self.total_q = int(qo[-1])
         if self.mask_mode == _lib.D2SD_MASK_TREE:
@@ -156,17 +176,23 @@ class CascadeVerifyAttention:
                 if m.shape != (n, n):
                     raise ValueError(f"tree_masks[{r}] must be [{n}, {n}], got {m.shape}")
             packed = pack_tree_masks([np.asarray(m, dtype=bool) for m in tree_masks])
+            same_mask = same and getattr(self, "mask_words", None) == int(packed.shape[1])
             self.mask_words = int(packed.shape[1])
-            self.tree_mask_dev = torch.from_numpy(packed.view(np.int64)).to(dev)
+            self.tree_mask_dev = _reuse(getattr(self, "tree_mask_dev", None),
+                                        torch.from_numpy(packed.view(np.int64)).to(dev), same_mask)
         else:
             self.mask_words = 0
             self.tree_mask_dev = None
         self.page_size = int(page_size)
         if self.page_size > 0:
             pt = page_table if isinstance(page_table, torch.Tensor) else torch.from_numpy(_i32(page_table))
-            self.page_table_dev = pt.to(device=dev, dtype=torch.int32).contiguous()
-            if self.page_table_dev.numel() < int(pi[-1]):
+            if pt.numel() < int(pi[-1]):
                 raise ValueError("page_table shorter than page_indptr[-1]")
+            # a device int32 table is used in place (the caller may update it
+            # between replays); anything else is uploaded
+            self.page_table_dev = pt.to(device=dev, dtype=torch.int32).contiguous()
+            ids = pt[:int(pi[-1])].to("cpu", torch.int64)
+            self._page_id_range = (int(ids.min()), int(ids.max())) if ids.numel() else (0, -1)
         else:
             self.page_table_dev = None
         self.kv_layout = kv_layout
@@ -188,9 +214,18 @@ class CascadeVerifyAttention:
         self._planned = True
         return self
 
+    def set_prefix_len(self, prefix_len: Sequence[int]) -> None:
+        """Current prefix lengths of a dynamic_prefix plan (host write into
+        prefix_len_dev; each is clamped to the planned length by the kernels)."""
+        v = torch.from_numpy(_i32(prefix_len))
+        if v.numel() != self.prefix_len_dev.numel():
+            raise ValueError("one prefix length per request")
+        self.prefix_len_dev.copy_(v)
+
     # ------------------------------------------------------------------- run
-    def _prefix_strides(self, k_prefix: torch.Tensor) -> Tuple[int, int, int]:
-        """(stride_tok, stride_head, stride_page) in elements."""
+    def _prefix_strides(self, k_prefix: torch.Tensor) -> Tuple[int, int, int, int]:
+        """(stride_tok, stride_head, stride_page, extent) in elements; extent =
+        pages of a paged pool or tokens of a contiguous prefix."""
         if self.page_size > 0:
             if k_prefix.dim() != 4:
                 raise ValueError("paged prefix pool must be 4-D")
@@ -202,20 +237,26 @@ class CascadeVerifyAttention:
                 st, sh, sp = k_prefix.stride(1), k_prefix.stride(2), k_prefix.stride(0)
             if P != self.page_size:
                 raise ValueError(f"pool page size {P} != planned {self.page_size}")
+            extent = k_prefix.shape[0]
+            lo, hi = self._page_id_range
+            if lo < 0 or hi >= extent:
+                raise ValueError(f"page_table holds page ids outside the pool's {extent} pages")
         else:
             if k_prefix.dim() == 4 and k_prefix.shape[0] == 1:
                 k_prefix = k_prefix[0]   # DynamicCache [1, Hkv, L, D]
             if k_prefix.dim() != 3:
                 raise ValueError("contiguous prefix must be [Hkv, L, D] (HND) or [L, Hkv, D] (NHD)")
             if self.kv_layout == "HND":
-                hkv, _, D = k_prefix.shape
+                hkv, extent, D = k_prefix.shape
                 st, sh, sp = k_prefix.stride(1), k_prefix.stride(0), 0
             else:
-                _, hkv, D = k_prefix.shape
+                extent, hkv, D = k_prefix.shape
                 st, sh, sp = k_prefix.stride(0), k_prefix.stride(1), 0
+            if extent < int(self.info.prefix_extent):
+                raise ValueError(f"k_prefix holds {extent} tokens; the plan reads {int(self.info.prefix_extent)}")
         if hkv != self.num_kv_heads or D != self.head_dim or k_prefix.stride(-1) != 1:
             raise ValueError("prefix KV head count / head_dim / contiguity mismatch")
-        return st, sh, sp
+        return st, sh, sp, extent
 
     def run(
         self,
@@ -274,11 +315,13 @@ class CascadeVerifyAttention:
                 raise ValueError("v_prefix must match k_prefix in shape and strides")
             if k_prefix.dtype != self.kv_dtype or v_prefix.dtype != self.kv_dtype:
                 raise TypeError(f"prefix KV must be {self.kv_dtype}")
-            st, sh, sp = self._prefix_strides(k_prefix)
+            st, sh, sp, extent = self._prefix_strides(k_prefix)
             a.k_prefix, a.v_prefix = k_prefix.data_ptr(), v_prefix.data_ptr()
             a.prefix_stride_tok, a.prefix_stride_head, a.prefix_stride_page = st, sh, sp
+            a.prefix_extent = extent
         a.page_size = self.page_size
         a.page_table = self.page_table_dev.data_ptr() if self.page_table_dev is not None else None
+        a.prefix_len = self.prefix_len_dev.data_ptr()
         a.k_scale = self.k_scale.data_ptr() if self.k_scale is not None else None
         a.v_scale = self.v_scale.data_ptr() if self.v_scale is not None else None
         a.sinks = self.sinks.data_ptr() if self.sinks is not None else None
@@ -292,4 +335,6 @@ class CascadeVerifyAttention:
         a.workspace_bytes = self.workspace.numel()
         fn = getattr(lib, fn_name)
         check(fn(C.byref(self.info), C.byref(a), C.c_void_p(torch.cuda.current_stream().cuda_stream)), fn_name)
+        keep_alive(self.plan_dev, self.workspace, self.tree_mask_dev, self.page_table_dev, self.prefix_len_dev,
+                   self.sinks, self.k_scale, self.v_scale, q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse)
         return out, lse

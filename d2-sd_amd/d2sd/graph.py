@@ -16,10 +16,23 @@ import torch
 from ._lib import check, lib
 
 
+_CAPTURING: list = []
+
+
+def keep_alive(*objs) -> None:
+    """Called by d2sd ops with the device buffers a launch reads or writes:
+    while a HipGraph is capturing, it holds references to them for as long as
+    the graph exists, so a captured launch never sees freed memory (e.g. after
+    the op's owner re-plans into new buffers)."""
+    if _CAPTURING:
+        _CAPTURING[-1]._keep.extend(o for o in objs if o is not None)
+
+
 class HipGraph:
     def __init__(self) -> None:
         self._exec: Optional[C.c_void_p] = None
         self.stream: Optional[torch.cuda.Stream] = None
+        self._keep: list = []
 
     @contextmanager
     def capture(self, stream: Optional[torch.cuda.Stream] = None):
@@ -30,9 +43,11 @@ class HipGraph:
         with torch.cuda.stream(self.stream):
             check(lib.d2sd_graph_begin_capture(C.c_void_p(self.stream.cuda_stream)), "graph begin capture")
             exec_ = C.c_void_p()
+            _CAPTURING.append(self)
             try:
                 yield self
             finally:
+                _CAPTURING.pop()
                 rc = lib.d2sd_graph_end_capture(C.c_void_p(self.stream.cuda_stream), C.byref(exec_))
             check(rc, "graph end capture")
             self._exec = exec_
@@ -48,6 +63,7 @@ class HipGraph:
         if self._exec is not None:
             check(lib.d2sd_graph_destroy(self._exec), "graph destroy")
             self._exec = None
+        self._keep = []
 
     def __del__(self) -> None:
         try:

@@ -46,12 +46,6 @@ typedef struct ihipStream_t* d2sd_stream_t; /* == hipStream_t */
 #define D2SD_MASK_CAUSAL 1 /* key j visible to query i iff j <= i + (kv_len - qo_len) */
 #define D2SD_MASK_TREE 2   /* ancestor bitmask, see d2sd_cascade_run_args */
 
-/* Where a cascade plan merges the partial states of a split group */
-#define D2SD_MERGE_LAUNCH 0        /* a second (merge) launch */
-#define D2SD_MERGE_LAST_PRODUCER 1 /* the group's last producer, inside the attention launch
-                                      (needs a group's workgroups on one XCD: the planner's
-                                      placement, with workgroups dealt to XCDs round-robin) */
-
 /* Message for the last failed call on this thread ("" if none). */
 const char* d2sd_last_error(void);
 /* Library version string. */
@@ -156,12 +150,22 @@ int d2sd_graph_destroy(void* graph_exec);
  * plan() bakes every per-request offset into a work list the caller uploads;
  * run() is the attention launch (prefix key chunks and suffix trees, each
  * writing a partial state to the workspace, or the output directly when a
- * request has no prefix) and, with D2SD_MERGE_LAUNCH, a merge launch
- * (log-sum-exp merge + sink into out / lse); the other merge modes merge
- * inside the attention launch.
+ * request has no prefix) and a merge launch (log-sum-exp merge + sink into
+ * out / lse).
  * run() allocates nothing and never synchronises the host, so it may be
  * captured into a hipGraph; the device plan, page_table contents and tensors
  * may change between replays as long as the plan's shape does not.
+ *
+ * Growing prefixes (dynamic_prefix = 1): plan() then takes prefix_len[r] as
+ * the largest prefix request r will have, and run() reads the current length
+ * of each request from the device array args.prefix_len (clamped to
+ * [0, planned length]), so one captured graph replays while the cache grows
+ * step by step (the page table must hold the pages of the current length).
+ * Chunks past the current length produce empty partial states.
+ *
+ * Paged page ids are clamped below args.prefix_extent (the pool's page
+ * count): an id outside the pool reads a wrong page but never memory outside
+ * the pool.
  * ---------------------------------------------------------------------- */
 typedef struct {
   int num_reqs;
@@ -179,8 +183,8 @@ typedef struct {
   int max_splits;      /* 0: default cap */
   int waves_per_block; /* 0 = choose; 2 (64-row waves, 128-row tiles), 4 (32-row
                           waves, 128-row tiles) or 8 (32-row waves, 256-row tiles) */
-  int merge_mode;      /* D2SD_MERGE_*: where the partial states of a split
-                          (request, kv head, q-tile) group are merged */
+  int dynamic_prefix;  /* 1: prefix_len is each request's largest prefix; run()
+                          reads the current lengths from args.prefix_len */
 } d2sd_cascade_plan_desc;
 
 typedef struct {
@@ -198,12 +202,12 @@ typedef struct {
   int head_dim;
   int kv_dtype;
   int page_size;
-  int num_groups;         /* (request, kv head, q-tile) groups with split prefixes */
-  int merge_in_attention; /* 1: run() is the attention launch alone */
-  size_t counters_offset; /* byte offset of the groups' int32 completion counters
-                             in the workspace (merge_in_attention); zero before
-                             the first run(), and left zero by every run() */
-  int merge_mode;         /* the plan's D2SD_MERGE_* */
+  int num_groups;         /* (request, kv head, q-tile) groups */
+  int dynamic_prefix;     /* the plan's dynamic_prefix */
+  int window_left;        /* the plan's window_left */
+  int64_t prefix_extent;  /* contiguous prefix: tokens k_prefix must hold
+                             (max_r prefix_tok_indptr[r] + prefix_len[r]);
+                             paged: page_table entries the plan reads */
 } d2sd_cascade_plan_info;
 
 /* Fills host_plan (capacity host_plan_ints int32) with the work list; the
@@ -227,6 +231,10 @@ typedef struct {
   int64_t prefix_stride_tok, prefix_stride_head, prefix_stride_page;
   int page_size;            /* must equal the planned page size */
   const int32_t* page_table;/* device (paged) */
+  int64_t prefix_extent;    /* contiguous: tokens in k_prefix (>= info.prefix_extent);
+                               paged: pages in the pool */
+  const int32_t* prefix_len;/* device [num_reqs]: current prefix lengths
+                               (dynamic plans; ignored otherwise) */
   const float* k_scale;     /* fp8: [Hkv] */
   const float* v_scale;
   const float* sinks;       /* nullable, [Hq] */

@@ -323,34 +323,6 @@ def test_split_count_does_not_change_result():
     check_close(outs_a[0][0], outs_b[0][0].float().cpu(), outs_a[0][1], outs_b[0][1].cpu(), "splits")
 
 
-def _counters(attn):
-    info = attn.info
-    off = int(info.counters_offset)
-    return attn.workspace[off:off + 4 * info.num_groups].view(torch.int32).cpu()
-
-
-@pytest.mark.parametrize("cfg", ["config2", "config3"])
-def test_merge_in_attention_matches_oracle_and_repeats(cfg):
-    """The single-launch form (each group's last producer merges) matches the
-    oracle, is bit-identical to itself over replays (whichever producer comes
-    last) and to the two-launch form's tolerance, and leaves every completion
-    counter at zero for the next launch."""
-    merge_mode = "last_producer"
-    prob = wl.config2(6, layers=1) if cfg == "config2" else wl.config3(2, num_reqs=2)
-    mp, attn, outs = _run_problem(prob, merge_mode=merge_mode)
-    assert attn.info.merge_in_attention == 1 and attn.info.num_merges == 0
-    assert not _counters(attn).any()
-    _check_problem(mp, outs, tag=f"{cfg} merged in attention ({merge_mode})")
-    lt = mp.layers[0]
-    for _ in range(3):
-        o2, l2 = attn.run(lt.q, lt.k_suffix, lt.v_suffix, lt.k_prefix, lt.v_prefix)
-        torch.cuda.synchronize()
-        assert torch.equal(o2, outs[0][0]) and torch.equal(l2, outs[0][1])
-    assert not _counters(attn).any()
-    _, _, outs_sep = _run_problem(prob, merge_mode="launch")
-    check_close(outs[0][0], outs_sep[0][0].float().cpu(), outs[0][1], outs_sep[0][1].cpu(), "merge forms")
-
-
 def test_page_permutation_is_bit_invariant():
     prob = wl.config2(4, layers=1)
     mp, attn, outs = _run_problem(prob)

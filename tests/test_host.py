@@ -36,7 +36,7 @@ def test_version_and_error_strings():
 
 
 def _plan(qo, pl, hq=32, hkv=8, d=128, window=-1, num_cus=256, waves=0, max_splits=0, page_size=16,
-          page_indptr=None, tok_indptr=None, merge_mode=0):
+          page_indptr=None, tok_indptr=None, dynamic=0):
     desc = _lib.PlanDesc()
     qo = np.asarray(qo, dtype=np.int32)
     pl = np.asarray(pl, dtype=np.int32)
@@ -56,7 +56,7 @@ def _plan(qo, pl, hq=32, hkv=8, d=128, window=-1, num_cus=256, waves=0, max_spli
     desc.num_cus = num_cus
     desc.max_splits = max_splits
     desc.waves_per_block = waves
-    desc.merge_mode = merge_mode
+    desc.dynamic_prefix = dynamic
     info = _lib.PlanInfo()
     assert _lib.lib.d2sd_cascade_plan(C.byref(desc), None, 0, C.byref(info)) == 0, _lib.lib.d2sd_last_error()
     host = np.zeros(max(info.plan_ints, 8), dtype=np.int32)
@@ -71,9 +71,8 @@ def _plan(qo, pl, hq=32, hkv=8, d=128, window=-1, num_cus=256, waves=0, max_spli
 
 MODE_PARTIAL, MODE_FINAL, MODE_NOOP = 0, 1, 3
 SRC_PREFIX, SRC_SUFFIX = 0, 1
-MERGE_LAUNCH, MERGE_LAST_PRODUCER = 0, 1
 # VerifyItem fields
-REQ, KVH, QT, SRC, KB, KE, SLOT, MODE, Q0, NQ, BASE, COFF, GROUP, SLOT0, NPROD = range(15)
+REQ, KVH, QT, SRC, KB, KE, SLOT, MODE, Q0, NQ, BASE, COFF, KV0, PLAN_LEN = range(14)
 
 
 @pytest.mark.parametrize("qo,pl,window,page,hq,waves", [
@@ -90,31 +89,22 @@ REQ, KVH, QT, SRC, KB, KE, SLOT, MODE, Q0, NQ, BASE, COFF, GROUP, SLOT0, NPROD =
     ([64 * i for i in range(33)], [8192] * 32, -1, 16, 32, 0),
     ([0, 0, 40], [100, 5000], -1, 16, 32, 0),                       # a request with no queries
 ])
-@pytest.mark.parametrize("merge_mode", [MERGE_LAUNCH, MERGE_LAST_PRODUCER])
-def test_plan_partitions_work(qo, pl, window, page, hq, waves, merge_mode):
+def test_plan_partitions_work(qo, pl, window, page, hq, waves):
     """Every (request, kv head, q-tile) group: prefix items partition its
-    visible prefix on 64-key tile boundaries into consecutive slots, one suffix
-    item covers its nodes, and the group's slots are merged exactly once: by
-    one merge item per 32-row block (separate merge) or by whichever of the
-    group's producers completes its counter (every producer names the same
-    counter, first slot and producer count); a group without prefix keys has a
-    FINAL suffix item and no merge."""
+    visible prefix on 64-key tile boundaries into consecutive slots (each
+    naming the window start and the planned length), one suffix item covers
+    its nodes, and the group's slots are merged exactly once, by one merge
+    item per 32-row block; a group without prefix keys has a FINAL suffix item
+    and no merge."""
     hkv = 8
     g = hq // hkv
     page_indptr = None
     if page:
         page_indptr = np.concatenate([[0], np.cumsum((np.asarray(pl) + page - 1) // page)])
     info, items, merges = _plan(qo, pl, hq, hkv, 128, window, page_size=page, waves=waves,
-                                page_indptr=page_indptr, merge_mode=merge_mode)
-    fused = bool(info.merge_in_attention)
-    assert fused == (merge_mode != MERGE_LAUNCH and info.num_slots > 0)
-    assert info.merge_mode == (merge_mode if info.num_slots > 0 else MERGE_LAUNCH)
-    part_bytes = info.num_slots * info.rows_per_tile * (128 * 2 + 4)
-    if fused:
-        assert info.num_merges == 0 and info.counters_offset >= part_bytes and info.counters_offset % 16 == 0
-        assert info.workspace_bytes == info.counters_offset + 4 * info.num_groups
-    else:
-        assert info.workspace_bytes == part_bytes
+                                page_indptr=page_indptr)
+    assert info.workspace_bytes == info.num_slots * info.rows_per_tile * (128 * 2 + 4)
+    assert info.prefix_extent == (page_indptr[-1] if page else max([p for p in pl if p > 0] + [0]))
     rows = info.rows_per_tile
     assert info.waves_per_block in (2, 4, 8)
     assert rows == {2: 128, 4: 128, 8: 256}[info.waves_per_block]
@@ -129,6 +119,8 @@ def test_plan_partitions_work(qo, pl, window, page, hq, waves, merge_mode):
         if it[SRC] == SRC_PREFIX:
             assert it[MODE] == MODE_PARTIAL
             assert it[BASE] == (page_indptr[r] if page else 0)
+            Leff = min(pl[r], window) if window >= 0 else pl[r]
+            assert it[KV0] == pl[r] - Leff and it[PLAN_LEN] == pl[r]
             pre.setdefault(key, []).append((it[KB], it[KE], it[SLOT]))
         else:
             assert it[SRC] == SRC_SUFFIX and key not in suf
@@ -153,7 +145,6 @@ def test_plan_partitions_work(qo, pl, window, page, hq, waves, merge_mode):
     heads = sum(hkv for r in range(len(pl)) if qo[r + 1] > qo[r])
     if heads >= 8:
         assert all(len(v) == 1 for v in xcd_of.values())
-    groups_seen = set()
     for r in range(len(pl)):
         n = qo[r + 1] - qo[r]
         L = pl[r]
@@ -172,20 +163,12 @@ def test_plan_partitions_work(qo, pl, window, page, hq, waves, merge_mode):
                 s0 = ch[0][2]
                 assert [c[2] for c in ch] == list(range(s0, s0 + len(ch)))
                 assert suf[key] == (s0 + len(ch), MODE_PARTIAL)
-                if fused:
-                    grp = {(it[GROUP], it[SLOT0], it[NPROD]) for it in live.tolist()
-                           if (it[REQ], it[KVH], it[QT]) == key}
-                    assert len(grp) == 1 and next(iter(grp))[1:] == (s0, len(ch) + 1)
-                    gid = next(iter(grp))[0]
-                    assert 0 <= gid < info.num_groups and gid not in groups_seen
-                    groups_seen.add(gid)
-                else:
-                    blks = [b for b in range(rows // 32) if qt * rows + b * 32 < n * g]
-                    assert sorted(mg[key]) == blks
-                    for b in blks:
-                        assert mg[key][b][:4] == (s0, len(ch) + 1, qo[r], n)
-                        if heads >= 8:
-                            assert {mg[key][b][4]} == xcd_of[key]
+                blks = [b for b in range(rows // 32) if qt * rows + b * 32 < n * g]
+                assert sorted(mg[key]) == blks
+                for b in blks:
+                    assert mg[key][b][:4] == (s0, len(ch) + 1, qo[r], n)
+                    if heads >= 8:
+                        assert {mg[key][b][4]} == xcd_of[key]
                 assert len(ch) <= 15
                 if page:
                     for a, b, _ in ch:
@@ -214,6 +197,22 @@ def test_plan_fills_the_device_once():
     assert info.waves_per_block == 4 and 256 < live <= 512
     info, items, _ = _plan([0, 41], [1024], page_size=0)
     assert (items[:, MODE] != MODE_NOOP).sum() <= 512
+
+
+def test_plan_balances_cu_pairs():
+    """One request of 4096 keys, 150 nodes (the Qwen3-8B verify step): every
+    XCD gets 64 workgroups (two per CU), and the two that share a CU (k-th of
+    the first and k-th of the second round of that XCD) hold at most 11
+    64-key tiles together, a suffix item counting as twice its tiles."""
+    info, items, _ = _plan([0, 150], [4096])
+    assert info.num_items == 512 and info.waves_per_block == 4
+    cost = [(w[KE] - w[KB] + 63) // 64 if w[SRC] == SRC_PREFIX else 2 * ((w[NQ] + 63) // 64)
+            for w in items.tolist()]
+    for x in range(8):
+        c = cost[x::8]
+        assert len(c) == 64
+        pairs = [c[k] + c[k + 32] for k in range(32)]
+        assert max(pairs) <= 11, pairs
 
 
 def test_plan_contiguous_token_offsets():
