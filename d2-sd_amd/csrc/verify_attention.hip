@@ -224,16 +224,19 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- Q fragments (B operand of S^T = K Q^T): lane holds 8 consecutive
-  // head dims at offset 8*hh of every 16-wide k step, for row block rb ----
+  // head dims at offset 8*hh of every 16-wide k step, for row block rb.  The
+  // bf16 prefix level stages Q through LDS (below); the others load it here ----
   bf16x8 qf[RB][KS];
+  if constexpr (MASKED || FP8) {
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-    const bf16_t* qp = (const bf16_t*)p.q + (long long)(w.q0 + n[rb]) * p.q_stride_n +
-                       (long long)qh[rb] * p.q_stride_h + 8 * hh;
+    for (int rb = 0; rb < RB; ++rb) {
+      const bf16_t* qp = (const bf16_t*)p.q + (long long)(w.q0 + n[rb]) * p.q_stride_n +
+                         (long long)qh[rb] * p.q_stride_h + 8 * hh;
 #pragma unroll
-    // unconditional: rows past the group's end read a valid row (node 0);
-    // their results are never stored or merged
-    for (int ks = 0; ks < KS; ++ks) qf[rb][ks] = *(const bf16x8*)(qp + 16 * ks);
+      // unconditional: rows past the group's end read a valid row (node 0);
+      // their results are never stored or merged
+      for (int ks = 0; ks < KS; ++ks) qf[rb][ks] = *(const bf16x8*)(qp + 16 * ks);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -597,23 +600,63 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
     if constexpr (!MASKED) {
       // ---- prefix level: software-pipelined tiles ----
       // K(j) is read one step before V(j) (QK^T of tile j runs under the
-      // softmax of tile j-1).  Issue order: K(0), K(1), then step s issues
-      // V(s + VST - 1) and K(s + KST); the prologue plays steps
-      // -(VST - 1) .. -1.  Slots: K(j) in j % KST, V(j) in j % VST; step s
-      // refills the slots of K(s) (read in step s-1) and V(s-1).
-      if (0 < ntiles) issue_k(0, wave_page(0));
+      // softmax of tile j-1).  Issue order: Q, K(0), V(0), K(1), K(2), then
+      // V / K pairs for steps -(VST - 2) .. -1, then step s issues
+      // V(s + VST - 1) and K(s + KST).  Slots: K(j) in j % KST, V(j) in
+      // j % VST; step s refills the slots of K(s) (read in step s-1) and
+      // V(s-1).
+      //
+      // Q: each wave's rows are DMA'd into ring slots the first tiles do not
+      // use (K slots 2.., then V slots 1..), in the chunk-swizzled K layout,
+      // so that the first QK^T waits for Q and K(0) only (a register load of
+      // Q would make the compiler drain every outstanding DMA before its
+      // first use); the slots are handed back once all waves hold their Q
+      // fragments.
+      constexpr int QB = RB * 32 * D * 2;  // bytes of one wave's Q rows
+      constexpr int NQI = QB / 1024;       // its DMA instructions
+      constexpr int FREE1 = (KST - 2) * TB;
+      static_assert(W * QB <= FREE1 + (VST - 1) * TB && TB % QB == 0, "Q staging must fit free ring slots");
+      const unsigned qdst = wv * QB < FREE1 ? kring + 2 * TB + wv * QB : vring + TB + (wv * QB - FREE1);
+      if (ntiles > 0) {
+#pragma unroll
+        for (int i = 0; i < NQI; ++i) {
+          const int byte = i * 1024 + 16 * lane;
+          const int rw = byte / (D * 2), cst = (byte % (D * 2)) / 16;
+          const int row = wrow0 + rw;
+          // rows past the group's end read a valid row (node 0); their
+          // results are never stored or merged
+          const int nn = row < R ? row / g : 0;
+          const int qq = w.kvh * g + (row < R ? row - nn * g : 0);
+          dma16((const bf16_t*)p.q + (long long)(w.q0 + nn) * p.q_stride_n + (long long)qq * p.q_stride_h +
+                    8 * (cst ^ chunk_swizzle<D>(rw)),
+                qdst + i * 1024);
+        }
+        const int pg0 = wave_page(0);
+        issue_k(0, pg0);
+        issue_v(0, pg0);
+      }
       if (1 < ntiles) issue_k(1, wave_page(1));
-      static_for<VST - 1>([&](auto j) {
-        constexpr int st = decltype(j)::value - (VST - 1);
+      // Q and K(0) have landed once at most V(0) and K(1) are outstanding
+      wait_vmcnt_units<IPW, 2>((0 < ntiles ? 1 : 0) + (1 < ntiles ? 1 : 0));
+      __builtin_amdgcn_s_barrier();  // every wave's share of K(0) is visible
+      if (ntiles > 0) {
+        const lds_char* qs = (const lds_char*)(uintptr_t)qdst;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks)
+            qf[rb][ks] = *(const __attribute__((address_space(3))) bf16x8*)(qs + rb * 32 * D * 2 + koff[ks]);
+      }
+      // all Q fragments are in registers before the slots are refilled
+      __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      if (2 < ntiles) issue_k(2, wave_page(2));
+      static_for<VST - 2>([&](auto j) {
+        constexpr int st = decltype(j)::value - (VST - 2);
         if (st + VST - 1 < ntiles) issue_v(st + VST - 1, wave_page(st + VST - 1));
         if (st + KST < ntiles) issue_k(st + KST, wave_page(st + KST));
       });
       int pv_next = wave_page(VST - 1), pk_next = wave_page(KST);
-      // Complete the Q loads and the first tiles here, visibly to the
-      // compiler: otherwise it keeps the Q loads pending into the tile loop
-      // and waits vmcnt(0) there, which would also drain the DMA rings.
-      wait_vmcnt<0>();
-      __builtin_amdgcn_s_barrier();
       f32x16 sc[RB][2];
       if (live && ntiles > 0) {
         auto kf = kfrag_at(0);
