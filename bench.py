@@ -78,20 +78,42 @@ def time_graph(graph, reps: int, torch) -> float:
     return e0.elapsed_time(e1) / reps
 
 
-def cpu_baseline(mp, reps: int, torch) -> dict:
-    """The oracle's fp32 torch-sdpa form of one layer on the host cores."""
+def cpu_threads() -> dict:
+    """Host threads for the CPU baseline: os.cpu_count() (BASELINE.md's
+    recipe), bounded by the process's CPU affinity and by OMP_NUM_THREADS when
+    the environment sets it (a GPU box grants a share of its host cores)."""
+    count = os.cpu_count() or 1
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = count
+    threads = min(count, affinity)
+    omp = os.environ.get("OMP_NUM_THREADS")
+    if omp and omp.isdigit() and int(omp) > 0:
+        threads = min(threads, int(omp))
+    return {"os_cpu_count": count, "affinity": affinity, "omp_num_threads": omp, "threads": threads}
+
+
+def cpu_baseline(mp, reps: int, torch, sample: str) -> dict:
+    """The oracle's fp32 torch-sdpa form of request 0 of one layer on the host
+    cores (3 warm-ups, median of `reps`)."""
     from oracle import cascade_oracle as orc
     prob = mp.problem
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    threads = max(1, min(threads, os.cpu_count() or 1))
-    torch.set_num_threads(threads)
+    th = cpu_threads()
+    torch.set_num_threads(th["threads"])
     lt = mp.layers[0]
     req = prob.requests[0]
     L = req.prefix_len
-    pages = mp.page_table[mp.page_indptr[0]:mp.page_indptr[1]].cpu().tolist()
-    kp = orc.gather_paged(lt.k_prefix.cpu(), pages, L).float()
-    vp = orc.gather_paged(lt.v_prefix.cpu(), pages, L).float()
-    q, ks, vs = lt.q.cpu().float(), lt.k_suffix.cpu().float(), lt.v_suffix.cpu().float()
+    if prob.page_size > 0:
+        pages = mp.page_table[mp.page_indptr[0]:mp.page_indptr[1]].cpu().tolist()
+        kp = orc.gather_paged(lt.k_prefix.cpu(), pages, L).float()
+        vp = orc.gather_paged(lt.v_prefix.cpu(), pages, L).float()
+    else:
+        s0 = mp.prefix_tok_indptr[0]
+        kp = lt.k_prefix.cpu()[:, s0:s0 + L].transpose(0, 1).float()
+        vp = lt.v_prefix.cpu()[:, s0:s0 + L].transpose(0, 1).float()
+    a, b = prob.qo_indptr[0], prob.qo_indptr[1]
+    q, ks, vs = lt.q[a:b].cpu().float(), lt.k_suffix[a:b].cpu().float(), lt.v_suffix[a:b].cpu().float()
     m = torch.as_tensor(req.tree.ancestor_mask())
     sm = prob.head_dim ** -0.5
 
@@ -107,10 +129,11 @@ def cpu_baseline(mp, reps: int, torch) -> dict:
         once()
         times.append(time.perf_counter() - t0)
     us = statistics.median(times) * 1e6
+    nq = b - a
     return {"value": us, "unit": "us/layer", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"layer 0 of 36 (N={prob.total_q} queries, prefix {L} + tree), fp32 torch "
-                      f"scaled_dot_product_attention + logsumexp on the host, median of {reps} after 3 warm-ups",
-            "queries_per_s": prob.total_q / (us * 1e-6), "cpu_model": cpu_model()}
+            "sample": f"{sample}: one layer, {nq} queries, prefix {L} + tree; fp32 torch scaled_dot_product_attention "
+                      f"+ logsumexp on the host, median of {reps} after 3 warm-ups",
+            "queries_per_s": nq / (us * 1e-6), "cpu_model": cpu_model(), **th}
 
 
 def traffic_workload(args) -> int:
@@ -570,6 +593,8 @@ def measure_workload(args) -> int:
             "call_bytes": vb, "call_flops": vf, "queries_per_s": T / (call_us * 1e-6),
             "plan": {"workgroups": info.num_items, "waves": info.waves_per_block,
                      "splits": info.max_splits_used, "merges": info.num_merges},
+            **({"cpu_baseline": cpu_baseline(mp, max(args.cpu_reps, 20), torch, prob.name)}
+               if name == "config1" and not args.no_cpu_baseline else {}),
         }), flush=True)
         del graphs, mp, attn, outs
         torch.cuda.empty_cache()
@@ -743,8 +768,10 @@ def main() -> int:
         "roofline": roof,
     }
     if not args.no_cpu_baseline:
-        log("timing the CPU baseline (oracle, fp32 torch sdpa)")
-        result["cpu_baseline"] = cpu_baseline(mp, args.cpu_reps, torch)
+        log("timing the CPU baseline (oracle, fp32 torch sdpa): config 2 layer 0, then config 1")
+        result["cpu_baseline"] = cpu_baseline(mp, args.cpu_reps, torch, "config 2 layer 0 of 36")
+        mp1 = wl.materialize(wl.config1(args.seed), dev, layers=1)
+        result["cpu_baseline_config1"] = cpu_baseline(mp1, max(args.cpu_reps, 20), torch, "config 1")
     print(json.dumps(result), flush=True)
     return 0
 

@@ -569,8 +569,12 @@ int d2sd_paged_kv_append(const d2sd_kv_append_args* a, d2sd_stream_t stream) {
       return fail(D2SD_ERR_INVALID_ARG, "paged_kv_append: strides must be positive multiples of 8 elements");
   if ((int64_t)a->prefix_len + a->num_accepted > (int64_t)INT32_MAX)
     return fail(D2SD_ERR_INVALID_ARG, "paged_kv_append: cache position overflows int32");
-  if (((int64_t)a->prefix_len + a->num_accepted + a->page_size - 1) / a->page_size > (int64_t)a->page_table_len)
+  if (!a->prefix_len_dev &&
+      ((int64_t)a->prefix_len + a->num_accepted + a->page_size - 1) / a->page_size > (int64_t)a->page_table_len)
     return fail(D2SD_ERR_INVALID_ARG, "paged_kv_append: page_table does not cover prefix_len + num_accepted");
+  if (a->page_table_len <= 0) return fail(D2SD_ERR_INVALID_ARG, "paged_kv_append: empty page_table");
+  if (a->advance_prefix && !a->prefix_len_dev)
+    return fail(D2SD_ERR_INVALID_ARG, "paged_kv_append: advance_prefix needs prefix_len_dev");
   d2sd::KvAppendParams p{};
   p.node_ids = a->node_ids;
   p.page_table = a->page_table;
@@ -594,7 +598,9 @@ int d2sd_paged_kv_append(const d2sd_kv_append_args* a, d2sd_stream_t stream) {
   p.num_rows = a->num_rows;
   p.pool_pages = a->pool_pages;
   p.num_accepted_dev = a->num_accepted_dev;
-  hipError_t e = d2sd::launch_kv_append(p, (hipStream_t)stream);
+  p.prefix_len_dev = a->prefix_len_dev;
+  p.page_table_len = a->page_table_len;
+  hipError_t e = d2sd::launch_kv_append(p, a->advance_prefix != 0, (hipStream_t)stream);
   return e == hipSuccess ? D2SD_OK : fail_hip(e, "paged_kv_append launch");
 }
 

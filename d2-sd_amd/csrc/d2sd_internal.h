@@ -176,6 +176,8 @@ struct KvAppendParams {
   int num_rows;    // rows of k_new / v_new (node ids outside are skipped)
   int pool_pages;  // pages of each pool (page ids outside are skipped)
   const int* num_accepted_dev;  // nullable: the count is read here (clamped to [0, num_accepted])
+  int* prefix_len_dev;          // nullable: the cache length is read here
+  int page_table_len;           // entries of page_table (device lengths are range-checked against it)
 };
 
 // ---------------------------------------------------------------------------

@@ -24,7 +24,10 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const KvAppendParams p) 
   if (p.num_accepted_dev && i >= min(max(*p.num_accepted_dev, 0), p.num_accepted)) return;
   const int node = p.node_ids[i];
   if (node < 0 || node >= p.num_rows) return;  // not a row of k_new / v_new: nothing written
-  const int t = p.prefix_len + i;              // cache position of the token
+  const int L = p.prefix_len_dev ? *p.prefix_len_dev : p.prefix_len;
+  if (L < 0) return;
+  const int t = L + i;  // cache position of the token
+  if ((t >> p.log2_page) >= p.page_table_len) return;  // no page reserved for it
   const int page = p.page_table[t >> p.log2_page];
   if (page < 0 || page >= p.pool_pages) return;
   const int slot = t & ((1 << p.log2_page) - 1);
@@ -46,9 +49,19 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const KvAppendParams p) 
   }
 }
 
-hipError_t launch_kv_append(const KvAppendParams& p, hipStream_t s) {
+// After the commit: the device cache length grows by the accepted count (a
+// launch of its own, so that every block of the commit read the old length).
+__global__ void advance_prefix_kernel(int* prefix_len, const int* num_accepted_dev, int num_accepted) {
+  if (threadIdx.x == 0)
+    *prefix_len += num_accepted_dev ? min(max(*num_accepted_dev, 0), num_accepted) : num_accepted;
+}
+
+hipError_t launch_kv_append(const KvAppendParams& p, bool advance, hipStream_t s) {
   if (p.num_accepted <= 0 || p.num_layers <= 0) return hipSuccess;
   hipLaunchKernelGGL(kv_append_kernel, dim3((unsigned)p.num_accepted, (unsigned)p.num_layers), dim3(256), 0, s, p);
+  if (advance && p.prefix_len_dev)
+    hipLaunchKernelGGL(advance_prefix_kernel, dim3(1), dim3(64), 0, s, p.prefix_len_dev, p.num_accepted_dev,
+                       p.num_accepted);
   return hipGetLastError();
 }
 

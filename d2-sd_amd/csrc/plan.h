@@ -49,7 +49,7 @@ hipError_t launch_verify_attention(const VerifyParams& p, int head_dim, int wave
 hipError_t launch_verify_merge(const VerifyParams& p, int head_dim, int rows, int nmerges, hipStream_t s);
 
 // ---- accepted-branch KV commit (kv_append.hip) ----
-hipError_t launch_kv_append(const KvAppendParams& p, hipStream_t s);
+hipError_t launch_kv_append(const KvAppendParams& p, bool advance, hipStream_t s);
 
 // ---- QK RMSNorm + RoPE (qk_rope.hip) ----
 hipError_t launch_qk_norm_rope(const QkRopeParams& p, hipStream_t s);

@@ -145,6 +145,8 @@ class KvAppendArgs(C.Structure):
         ("pool_stride_head", C.c_int64),
         ("pool_stride_tok", C.c_int64),
         ("num_accepted_dev", C.c_void_p),
+        ("prefix_len_dev", C.c_void_p),
+        ("advance_prefix", C.c_int),
     ]
 
 

@@ -15,6 +15,7 @@ import torch
 
 from . import _lib
 from ._lib import check, lib
+from .graph import keep_alive
 
 
 class GreedyAccept:
@@ -64,4 +65,5 @@ class GreedyAccept:
         a.workspace_bytes = self.workspace.numel()
         check(lib.d2sd_greedy_accept(C.byref(a), C.c_void_p(torch.cuda.current_stream().cuda_stream)),
               "greedy_accept")
+        keep_alive(logits, node_index, draft_ids, self.workspace, self.accept_ids, self.accept_nodes, self.result)
         return self.accept_ids, self.accept_nodes, self.result

@@ -20,6 +20,7 @@ import torch
 
 from . import _lib
 from ._lib import check, lib
+from .graph import keep_alive
 
 
 def _layout_strides(pool: torch.Tensor, kv_layout: str):
@@ -79,13 +80,18 @@ class PagedKVCommit:
         self._args = a
         self.page_size = page_size
 
-    def commit(self, page_table: torch.Tensor, prefix_len: int, node_ids: torch.Tensor,
-               num_accepted: int | None = None, num_accepted_dev: torch.Tensor | None = None) -> None:
+    def commit(self, page_table: torch.Tensor, prefix_len, node_ids: torch.Tensor,
+               num_accepted: int | None = None, num_accepted_dev: torch.Tensor | None = None,
+               advance: bool = False) -> None:
         """Writes rows node_ids[:num_accepted] of every layer's k_new / v_new to
         cache positions prefix_len .. prefix_len + num_accepted - 1 of the
         request whose pages are page_table (device int32, covering them).
         num_accepted_dev (device int32, e.g. GreedyAccept's result) makes the
-        kernel read the count from the device, capped at num_accepted."""
+        kernel read the count from the device, capped at num_accepted.
+        prefix_len may be a device int32 tensor of one element (e.g. a slice
+        of CascadeVerifyAttention.prefix_len_dev): the kernel then reads the
+        length there, and advance=True adds the accepted count to it after the
+        commit, so that a captured step replays as the cache grows."""
         if page_table.dtype != torch.int32 or node_ids.dtype != torch.int32:
             raise TypeError("page_table and node_ids must be int32")
         if not (page_table.is_contiguous() and node_ids.is_contiguous()):
@@ -93,10 +99,20 @@ class PagedKVCommit:
         n = int(node_ids.numel() if num_accepted is None else num_accepted)
         if n < 0 or n > node_ids.numel():
             raise ValueError("num_accepted out of range")
-        if (int(prefix_len) + n + self.page_size - 1) // self.page_size > page_table.numel():
-            raise ValueError("page_table does not cover prefix_len + num_accepted tokens")
+        dev_len = isinstance(prefix_len, torch.Tensor)
+        if dev_len:
+            if (prefix_len.dtype != torch.int32 or prefix_len.numel() != 1 or not prefix_len.is_cuda
+                    or not prefix_len.is_contiguous()):
+                raise TypeError("a device prefix_len must be one contiguous int32 element")
+        else:
+            if advance:
+                raise ValueError("advance needs a device prefix_len")
+            if (int(prefix_len) + n + self.page_size - 1) // self.page_size > page_table.numel():
+                raise ValueError("page_table does not cover prefix_len + num_accepted tokens")
         a = self._args
-        a.prefix_len = int(prefix_len)
+        a.prefix_len = 0 if dev_len else int(prefix_len)
+        a.prefix_len_dev = prefix_len.data_ptr() if dev_len else None
+        a.advance_prefix = int(bool(advance))
         a.num_accepted = n
         a.node_ids = node_ids.data_ptr()
         a.page_table = page_table.data_ptr()
@@ -109,3 +125,4 @@ class PagedKVCommit:
             a.num_accepted_dev = None
         check(lib.d2sd_paged_kv_append(C.byref(a), C.c_void_p(torch.cuda.current_stream().cuda_stream)),
               "paged_kv_append")
+        keep_alive(page_table, node_ids, num_accepted_dev, prefix_len if dev_len else None, *self._addr)

@@ -266,6 +266,8 @@ int d2sd_cascade_merge(const d2sd_cascade_plan_info* info, const d2sd_cascade_ru
  * prefix_len + i: page page_table[(prefix_len + i) / page_size], slot
  * (prefix_len + i) % page_size, for all layers in one launch.  The page
  * table must already hold the pages for prefix_len + num_accepted tokens.
+ * With prefix_len_dev the length lives on the device and may advance there,
+ * so one captured commit replays step after step.
  * Node ids outside [0, num_rows) and page ids outside [0, pool_pages) are
  * skipped (nothing written).  bf16 pools only; strides in elements must be
  * multiples of 8 and every address 16-byte aligned.  No allocation, no host
@@ -292,6 +294,12 @@ typedef struct {
   const int32_t* num_accepted_dev; /* nullable: device count read by the kernel
                                       (e.g. d2sd_greedy_accept's result[0]),
                                       clamped to [0, num_accepted] */
+  int32_t* prefix_len_dev;   /* nullable: the cache length is read here instead of
+                                prefix_len (e.g. a dynamic cascade plan's
+                                prefix_len array); tokens whose page index
+                                reaches page_table_len are skipped */
+  int advance_prefix;        /* with prefix_len_dev: a second launch then adds the
+                                accepted count to *prefix_len_dev */
 } d2sd_kv_append_args;
 
 int d2sd_paged_kv_append(const d2sd_kv_append_args* args, d2sd_stream_t stream);

@@ -365,32 +365,53 @@ def test_tree_flow_equals_reference_row_flow():
     check_close(o_sh, outs[0][0][idx].float().cpu(), lse_sh, outs[0][1][idx].cpu(), "row vs tree")
 
 
+def decided_vocabulary(o_ref: torch.Tensor, w: torch.Tensor, k_sigma: float = 8.0, max_rounds: int = 64):
+    """Columns of the random lm_head `w` [Hq*D, V] on which every row's
+    greedy decision is well defined, chosen from the oracle output alone.
+
+    Any bf16-output kernel (the reference's FlashInfer included) rounds O to
+    bf16: a relative perturbation of up to 2^-9 per element.  A row's
+    top-1/top-2 logit margin then moves with standard deviation
+    sigma = sqrt(sum_d (ulp_d / sqrt(12))^2 (w[d, top1] - w[d, top2])^2).
+    Rows whose margin is under k_sigma * sigma lose their runner-up column;
+    repeated until every row clears the bound.  Returns (kept columns,
+    number of columns removed)."""
+    n = o_ref.shape[0]
+    o_flat = o_ref.reshape(n, -1).float()
+    ulp = torch.exp2(torch.floor(torch.log2(o_flat.abs().clamp_min(1e-30))) - 7)
+    keep = torch.arange(w.shape[1])
+    for _ in range(max_rounds):
+        logits = o_flat @ w[:, keep]
+        top2 = logits.topk(2, dim=-1)
+        margin = top2.values[:, 0] - top2.values[:, 1]
+        dw = w[:, keep[top2.indices[:, 0]]] - w[:, keep[top2.indices[:, 1]]]        # [Hq*D, n]
+        sigma = torch.sqrt(((ulp.T / math.sqrt(12.0)) ** 2 * dw ** 2).sum(0))
+        bad = margin <= k_sigma * sigma
+        if not bad.any():
+            return keep, w.shape[1] - keep.numel()
+        drop = torch.unique(keep[top2.indices[bad, 1]])
+        keep = keep[~torch.isin(keep, drop)]
+    raise AssertionError("no decided vocabulary within the round limit")
+
+
 @pytest.mark.parametrize("cfg", ["config1", "config2"])
 def test_greedy_argmax_bit_identical(cfg):
+    """Greedy argmax of a fixed random lm_head projection of O: identical to
+    the oracle's on every row (model/utils.py:28-33 greedy sample), over the
+    vocabulary on which each row's decision survives bf16 output rounding
+    (decided from the oracle alone, see decided_vocabulary)."""
     prob = getattr(wl, cfg)(0) if cfg == "config1" else wl.config2(0, layers=1)
     mp, _, outs = _run_problem(prob)
     o_ref, _ = _oracle_request(mp, 0, 0)
     n = prob.total_q
     w = torch.randn(prob.num_qo_heads * prob.head_dim, 32000, generator=torch.Generator().manual_seed(1234))
-    logits_ref = o_ref.reshape(n, -1).float() @ w
-    logits_gpu = outs[0][0].reshape(n, -1).float().cpu() @ w
-    top2 = logits_ref.topk(2, dim=-1)
-    margin = top2.values[:, 0] - top2.values[:, 1]
-    # Any bf16-output kernel (the reference's FlashInfer included) rounds O
-    # to bf16: a relative perturbation of up to 2^-9 per element, uniform.  A
-    # row's greedy decision is robust when its top-1/top-2 margin exceeds 6
-    # standard deviations of the margin change that rounding causes (computed
-    # from the oracle alone).  Robust rows must agree exactly; the rest must
-    # pick one of the reference's top-2; robust rows must be the majority.
-    o_flat = o_ref.reshape(n, -1).float()
-    ulp = torch.exp2(torch.floor(torch.log2(o_flat.abs().clamp_min(1e-30))) - 7)
-    dw = w[:, top2.indices[:, 0]] - w[:, top2.indices[:, 1]]          # [Hq*D, n]
-    sigma = torch.sqrt(((ulp.T / math.sqrt(12.0)) ** 2 * dw ** 2).sum(0))
-    decided = margin > 6 * sigma
-    am_gpu, am_ref = logits_gpu.argmax(-1), logits_ref.argmax(-1)
-    assert torch.equal(am_gpu[decided], am_ref[decided])
-    assert bool(((am_gpu == top2.indices[:, 0]) | (am_gpu == top2.indices[:, 1]))[~decided].all())
-    assert decided.float().mean().item() >= 0.5, f"too many ties: {(~decided).sum().item()} of {n}"
+    keep, removed = decided_vocabulary(o_ref, w)
+    print(f"{cfg}: {n} rows, all decided over {keep.numel()} of {w.shape[1]} columns ({removed} removed)")
+    assert removed <= w.shape[1] // 100
+    wk = w[:, keep]
+    am_ref = (o_ref.reshape(n, -1).float() @ wk).argmax(-1)
+    am_gpu = (outs[0][0].reshape(n, -1).float().cpu() @ wk).argmax(-1)
+    assert torch.equal(am_gpu, am_ref), f"{(am_gpu != am_ref).sum().item()} of {n} rows differ"
 
 
 def test_hipgraph_replays_match_eager():
