@@ -466,6 +466,25 @@ int d2sd_cascade_run(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_
   return d2sd_cascade_merge(info, a, stream);
 }
 
+size_t d2sd_cascade_scratch_bytes(void) { return (size_t)d2sd::kVerifyScratchBytes; }
+
+int d2sd_cascade_run_noalloc(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* a,
+                             d2sd_stream_t stream) {
+  g_last_error.clear();
+  if (!info || !a) return fail(D2SD_ERR_INVALID_ARG, "cascade_run_noalloc: null info/args");
+  if (info->workspace_bytes > d2sd::kVerifyScratchBytes)
+    return fail(D2SD_ERR_WORKSPACE, "cascade_run_noalloc: the plan needs " + std::to_string(info->workspace_bytes) +
+                                        " bytes of partial states, more than the library's " +
+                                        std::to_string(d2sd::kVerifyScratchBytes) + "-byte workspace");
+  void* ws = nullptr;
+  if (hipError_t e = d2sd::verify_scratch(&ws)) return fail_hip(e, "cascade_run_noalloc: workspace lookup");
+  d2sd_cascade_run_args b = *a;
+  b.workspace = ws;
+  b.workspace_bytes = (size_t)d2sd::kVerifyScratchBytes;
+  if (int rc = d2sd_cascade_attention(info, &b, stream)) return rc;
+  return d2sd_cascade_merge(info, &b, stream);
+}
+
 // QK RMSNorm + RoPE (replaces generation/verification.py:113-123).
 int d2sd_qk_norm_rope(const d2sd_qk_norm_rope_args* a, d2sd_stream_t stream) {
   g_last_error.clear();

@@ -158,6 +158,9 @@ struct VerifyParams {
 // partials of a group (the chunks plus the suffix partial).
 constexpr int kMaxVerifySplits = 15;
 
+// Size of the library-owned workspace of d2sd_cascade_run_noalloc (per GPU).
+constexpr unsigned long long kVerifyScratchBytes = 32ull << 20;
+
 // ---------------------------------------------------------------------------
 // Accepted-branch KV commit (kv_append.hip).
 // ---------------------------------------------------------------------------

@@ -47,6 +47,8 @@ int verify_auto_waves(const VerifyPlanInput& in, int num_cus);
 hipError_t launch_verify_attention(const VerifyParams& p, int head_dim, int waves, bool paged, bool fp8, int nitems,
                                    hipStream_t s);
 hipError_t launch_verify_merge(const VerifyParams& p, int head_dim, int rows, int nmerges, hipStream_t s);
+// Device address of this GPU's library-owned workspace (kVerifyScratchBytes).
+hipError_t verify_scratch(void** ptr);
 
 // ---- accepted-branch KV commit (kv_append.hip) ----
 hipError_t launch_kv_append(const KvAppendParams& p, bool advance, hipStream_t s);

@@ -37,7 +37,9 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <mutex>
 #include <type_traits>
+#include <vector>
 
 #include "d2sd_internal.h"
 #include "kernel_common.h"
@@ -1030,6 +1032,33 @@ hipError_t launch_verify_merge(const VerifyParams& p, int head_dim, int rows, in
   else if (head_dim == 64 && rows == 256) hipLaunchKernelGGL((verify_merge_kernel<64, 256>), grid, block, 0, s, p);
   else return hipErrorInvalidValue;
   return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Library-owned partial-state workspace of d2sd_cascade_run_noalloc: one
+// static device array per GPU (kVerifyScratchBytes), held until the process
+// ends.  In host code `scratch` names a host-side stand-in, so its device
+// address is looked up once per device (hipGetSymbolAddress, with that device
+// current) and only that address is ever handed to kernels.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[kVerifyScratchBytes];
+
+hipError_t verify_scratch(void** ptr) {
+  static std::mutex mu;
+  static std::vector<void*> per_device;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(mu);
+  if ((int)per_device.size() <= dev) per_device.resize(dev + 1, nullptr);
+  if (!per_device[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    per_device[dev] = p;
+  }
+  *ptr = per_device[dev];
+  return hipSuccess;
 }
 
 }  // namespace d2sd

@@ -35,6 +35,8 @@ EXPORTED_SYMBOLS = (
     "d2sd_cascade_run",
     "d2sd_cascade_attention",
     "d2sd_cascade_merge",
+    "d2sd_cascade_scratch_bytes",
+    "d2sd_cascade_run_noalloc",
     "d2sd_paged_kv_append",
     "d2sd_greedy_accept_workspace_size",
     "d2sd_greedy_accept",
@@ -228,7 +230,9 @@ def _load() -> C.CDLL:
     lib.d2sd_graph_destroy.argtypes = [vp]
     lib.d2sd_cascade_plan.restype = i32
     lib.d2sd_cascade_plan.argtypes = [C.POINTER(PlanDesc), C.POINTER(C.c_int32), sz, C.POINTER(PlanInfo)]
-    for name in ("d2sd_cascade_run", "d2sd_cascade_attention", "d2sd_cascade_merge"):
+    lib.d2sd_cascade_scratch_bytes.restype = sz
+    lib.d2sd_cascade_scratch_bytes.argtypes = []
+    for name in ("d2sd_cascade_run", "d2sd_cascade_attention", "d2sd_cascade_merge", "d2sd_cascade_run_noalloc"):
         fn = getattr(lib, name)
         fn.restype = i32
         fn.argtypes = [C.POINTER(PlanInfo), C.POINTER(RunArgs), vp]

@@ -272,6 +272,14 @@ class CascadeVerifyAttention:
         planned.  Returns (out [total_q, Hq, D] bf16, lse [total_q, Hq] fp32)."""
         return self._launch("d2sd_cascade_run", q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse)
 
+    def run_no_alloc(self, q, k_suffix, v_suffix, k_prefix=None, v_prefix=None, out=None, lse=None):
+        """run() on the library's own per-GPU workspace
+        (d2sd_cascade_run_noalloc; at most d2sd_cascade_scratch_bytes() of
+        partial states): for callers that cannot allocate.  Calls on one GPU
+        share that workspace, so overlapping calls (other streams) race."""
+        return self._launch("d2sd_cascade_run_noalloc", q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse,
+                            workspace=False)
+
     def run_attention(self, q, k_suffix, v_suffix, k_prefix=None, v_prefix=None, out=None, lse=None):
         """First half of run(): the attention launch alone (prefix key chunks
         and suffix trees; partial states in the plan's workspace).
@@ -283,7 +291,7 @@ class CascadeVerifyAttention:
         out / lse."""
         return self._launch("d2sd_cascade_merge", q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse)
 
-    def _launch(self, fn_name, q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse):
+    def _launch(self, fn_name, q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse, workspace=True):
         if not self._planned:
             raise RuntimeError("run() before plan()")
         T, hq, d = self.total_q, self.num_qo_heads, self.head_dim
@@ -331,10 +339,10 @@ class CascadeVerifyAttention:
         a.lse_stride_n = lse.stride(0)
         a.sm_scale = self.sm_scale
         a.lse_base2 = int(self.lse_base2)
-        a.workspace = self.workspace.data_ptr()
-        a.workspace_bytes = self.workspace.numel()
+        a.workspace = self.workspace.data_ptr() if workspace else None
+        a.workspace_bytes = self.workspace.numel() if workspace else 0
         fn = getattr(lib, fn_name)
         check(fn(C.byref(self.info), C.byref(a), C.c_void_p(torch.cuda.current_stream().cuda_stream)), fn_name)
-        keep_alive(self.plan_dev, self.workspace, self.tree_mask_dev, self.page_table_dev, self.prefix_len_dev,
+        keep_alive(self.plan_dev, self.workspace if workspace else None, self.tree_mask_dev, self.page_table_dev, self.prefix_len_dev,
                    self.sinks, self.k_scale, self.v_scale, q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse)
         return out, lse

@@ -256,6 +256,22 @@ int d2sd_cascade_attention(const d2sd_cascade_plan_info* info, const d2sd_cascad
 int d2sd_cascade_merge(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* args,
                        d2sd_stream_t stream);
 
+/* d2sd_cascade_run without a caller workspace.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * partial states live in a library-owned device array of
+ * d2sd_cascade_scratch_bytes() bytes (32 MiB) per GPU, kept until the process
+ * ends; args.workspace / workspace_bytes are ignored, and a plan whose
+ * info.workspace_bytes exceeds the array is rejected (D2SD_ERR_WORKSPACE).
+ * Every call on one GPU shares that array: calls that overlap on one GPU
+ * (other streams, other threads) race.  Nothing in it needs clearing: each
+ * partial state is written by its producer before the merge reads it.
+ * The first call on a device looks the array's address up; later calls make
+ * no runtime call besides the two launches. */
+size_t d2sd_cascade_scratch_bytes(void);
+int d2sd_cascade_run_noalloc(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* args,
+                             d2sd_stream_t stream);
+
 /* ----------------------------------------------------------------------
  * Accepted-branch KV commit into the paged prefix cache.
  * Replaces generation/d3_generator.py:227-232: per layer
