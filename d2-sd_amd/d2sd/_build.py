@@ -1,4 +1,5 @@
-"""Builds libd2sd.so (the C-ABI library) in-tree with hipcc for gfx950.
+"""Builds libd2sd.so (the C-ABI library) in-tree with hipcc for gfx950, and
+libd2sd_torch.so (torch.ops.d2sd.*, host C++ over that C ABI) with g++.
 
     python d2-sd_amd/d2sd/_build.py     (or __graft_entry__.build())
 
@@ -18,6 +19,7 @@ ROOT = PKG_DIR.parent                               # d2-sd_amd
 CSRC = ROOT / "csrc"
 OBJ_DIR = ROOT / "_build"
 LIB_PATH = PKG_DIR / "libd2sd.so"
+TORCH_LIB_PATH = PKG_DIR / "libd2sd_torch.so"
 INCLUDE = ROOT.parent / "include"
 
 ARCH = "gfx950"
@@ -60,14 +62,38 @@ def build(verbose: bool = False) -> Path:
     with cf.ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-soname,libd2sd.so", *map(str, objs),
+           "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
     os.replace(tmp, LIB_PATH)
     if verbose:
         print(f"built {LIB_PATH}")
+    build_torch_ops(verbose)
     return LIB_PATH
+
+
+def build_torch_ops(verbose: bool = False) -> Path:
+    """torch_ops.cpp -> libd2sd_torch.so: the TORCH_LIBRARY(d2sd, ...)
+    registrations, linked against libd2sd.so (found next to it, by soname)."""
+    import torch
+    from torch.utils import cpp_extension as ce
+    torch_lib = Path(torch.__file__).resolve().parent / "lib"
+    tmp = TORCH_LIB_PATH.with_suffix(".so.tmp")
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-fPIC", "-shared", "-std=c++17", "-Wall", "-Wno-unused-function",
+           f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}", "-D__HIP_PLATFORM_AMD__", "-DUSE_ROCM",
+           *[f"-I{p}" for p in ce.include_paths()], f"-I{INCLUDE}", "-I/opt/rocm/include",
+           str(CSRC / "torch_ops.cpp"), "-o", str(tmp),
+           f"-L{torch_lib}", "-ltorch", "-ltorch_cpu", "-lc10", "-lc10_hip", "-ltorch_hip",
+           f"-L{PKG_DIR}", "-ld2sd", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{torch_lib}"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"torch ops build failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, TORCH_LIB_PATH)
+    if verbose:
+        print(f"built {TORCH_LIB_PATH}")
+    return TORCH_LIB_PATH
 
 
 if __name__ == "__main__":

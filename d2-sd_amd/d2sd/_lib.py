@@ -9,6 +9,7 @@ import ctypes as C
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libd2sd.so"
+TORCH_LIB_PATH = Path(__file__).resolve().parent / "libd2sd_torch.so"
 
 D2SD_OK = 0
 D2SD_KV_BF16 = 0
@@ -203,7 +204,8 @@ def _load() -> C.CDLL:
         raise ImportError(
             f"{LIB_PATH} is missing: build it first (python -c 'import __graft_entry__ as g; g.build()' "
             "or python d2-sd_amd/d2sd/_build.py)")
-    lib = C.CDLL(str(LIB_PATH))
+    # global: libd2sd_torch.so (torch.ops.d2sd) links this same instance by soname
+    lib = C.CDLL(str(LIB_PATH), mode=C.RTLD_GLOBAL)
     vp, i64, i32, f32, sz = C.c_void_p, C.c_int64, C.c_int, C.c_float, C.c_size_t
     lib.d2sd_last_error.restype = C.c_char_p
     lib.d2sd_last_error.argtypes = []
@@ -248,6 +250,17 @@ def _load() -> C.CDLL:
 
 
 lib = _load()
+
+
+def _load_torch_ops() -> None:
+    """Registers torch.ops.d2sd.* (libd2sd_torch.so, built with libd2sd.so)."""
+    import torch
+    if not TORCH_LIB_PATH.exists():
+        raise ImportError(f"{TORCH_LIB_PATH} is missing: build it first (d2-sd_amd/d2sd/_build.py)")
+    torch.ops.load_library(str(TORCH_LIB_PATH))
+
+
+_load_torch_ops()
 
 
 def check(rc: int, what: str) -> None:

@@ -158,6 +158,7 @@ class CascadeVerifyAttention:
             ("num_items", "num_merges", "waves_per_block", "rows_per_tile", "num_slots", "num_reqs",
              "num_qo_heads", "num_kv_heads", "head_dim", "kv_dtype", "page_size", "dynamic_prefix"))
         self.info = info
+        self.info_bytes = torch.frombuffer(bytearray(bytes(info)), dtype=torch.uint8)
         self.plan_host = host
         self.qo_indptr_host = qo
         self.prefix_len_host = pl
@@ -270,14 +271,14 @@ class CascadeVerifyAttention:
     ) -> Tuple[torch.Tensor, torch.Tensor]:
         """q [total_q, Hq, D], k/v_suffix [total_q, Hkv, D] (bf16); prefix KV as
         planned.  Returns (out [total_q, Hq, D] bf16, lse [total_q, Hq] fp32)."""
-        return self._launch("d2sd_cascade_run", q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse)
+        return self._launch("cascade_run", q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse)
 
     def run_no_alloc(self, q, k_suffix, v_suffix, k_prefix=None, v_prefix=None, out=None, lse=None):
         """run() on the library's own per-GPU workspace
         (d2sd_cascade_run_noalloc; at most d2sd_cascade_scratch_bytes() of
         partial states): for callers that cannot allocate.  Calls on one GPU
         share that workspace, so overlapping calls (other streams) race."""
-        return self._launch("d2sd_cascade_run_noalloc", q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse,
+        return self._launch("cascade_run_no_alloc", q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse,
                             workspace=False)
 
     def run_attention(self, q, k_suffix, v_suffix, k_prefix=None, v_prefix=None, out=None, lse=None):
@@ -341,8 +342,17 @@ class CascadeVerifyAttention:
         a.lse_base2 = int(self.lse_base2)
         a.workspace = self.workspace.data_ptr() if workspace else None
         a.workspace_bytes = self.workspace.numel() if workspace else 0
-        fn = getattr(lib, fn_name)
-        check(fn(C.byref(self.info), C.byref(a), C.c_void_p(torch.cuda.current_stream().cuda_stream)), fn_name)
+        if fn_name.startswith("cascade_run"):
+            # the whole call: through the torch operator (torch.ops.d2sd.cascade_run*)
+            getattr(torch.ops.d2sd, fn_name)(
+                self.info_bytes, self.plan_dev, self.workspace, q, k_suffix, v_suffix, k_prefix, v_prefix,
+                [a.prefix_stride_tok, a.prefix_stride_head, a.prefix_stride_page, a.prefix_extent],
+                self.page_table_dev, self.tree_mask_dev, self.mask_mode, self.mask_words, self.prefix_len_dev,
+                self.k_scale, self.v_scale, self.sinks, self.sm_scale, self.lse_base2, out, lse)
+        else:
+            fn = getattr(lib, fn_name)
+            check(fn(C.byref(self.info), C.byref(a), C.c_void_p(torch.cuda.current_stream().cuda_stream)),
+                  fn_name)
         keep_alive(self.plan_dev, self.workspace if workspace else None, self.tree_mask_dev, self.page_table_dev, self.prefix_len_dev,
                    self.sinks, self.k_scale, self.v_scale, q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse)
         return out, lse

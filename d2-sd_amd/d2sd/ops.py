@@ -9,8 +9,9 @@
     merge_state                   <- flashinfer.merge_state (out-of-place form)
 
 Same names, argument meaning and return convention as the FlashInfer calls the
-reference makes; every call runs the gfx950 kernels of libd2sd.so on the
-current HIP stream.  The returned LSE is the natural logarithm of the softmax
+reference makes; every call goes through the torch operators torch.ops.d2sd.*
+(libd2sd_torch.so) to the gfx950 kernels of libd2sd.so on the current HIP
+stream.  The returned LSE is the natural logarithm of the softmax
 denominator (pass lse_base2=True for base 2).
 """
 from __future__ import annotations
@@ -98,17 +99,8 @@ def single_prefill_with_kv_cache(
         raise ValueError("q and k head_dim differ")
     if sm_scale is None:
         sm_scale = d ** -0.5
-    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-    lse = torch.empty((qo_len, hq), dtype=torch.float32, device=q.device) if return_lse else None
-    ws_bytes = lib.d2sd_single_prefill_workspace_size(qo_len, kv_len, hq, hkv, d, -1)
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
-    with torch.cuda.device(q.device):
-        rc = lib.d2sd_single_prefill_with_kv_cache(
-            q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), v.data_ptr(), s_n, s_h,
-            out.data_ptr(), out.stride(0), out.stride(1), lse.data_ptr() if lse is not None else None,
-            qo_len, kv_len, hq, hkv, d, int(bool(causal)), -1, float(sm_scale), int(bool(lse_base2)),
-            ws.data_ptr(), ws.numel(), _stream())
-    check(rc, "single_prefill_with_kv_cache")
+    out, lse = torch.ops.d2sd.single_prefill_with_kv_cache(q, k, v, bool(causal), kv_layout, float(sm_scale),
+                                                           bool(lse_base2))
     return (out, lse) if return_lse else out
 
 
@@ -129,13 +121,7 @@ def merge_state_in_place(v: torch.Tensor, s: torch.Tensor, v_other: torch.Tensor
         raise TypeError("merge_state_in_place: s and s_other must be float32")
     if s.stride(1) != 1 or s_other.stride(1) != 1:
         raise ValueError("merge_state_in_place: s / s_other need a contiguous head dimension")
-    n, h, d = v.shape
-    with torch.cuda.device(v.device):
-        rc = lib.d2sd_merge_state_in_place(
-            v.data_ptr(), v.stride(0), v.stride(1), s.data_ptr(), s.stride(0),
-            v_other.data_ptr(), v_other.stride(0), v_other.stride(1), s_other.data_ptr(), s_other.stride(0),
-            n, h, d, int(bool(lse_base2)), _stream())
-    check(rc, "merge_state_in_place")
+    torch.ops.d2sd.merge_state_in_place(v, s, v_other, s_other, bool(lse_base2))
 
 
 def merge_state(v_a: torch.Tensor, s_a: torch.Tensor, v_b: torch.Tensor, s_b: torch.Tensor,
@@ -165,18 +151,11 @@ def local_attention_merge(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out
     hkv = k.shape[2]
     if k.shape[0] != bsz or k.shape[1] != lb or k.shape[3] != d:
         raise ValueError("local_attention_merge: k/v shape mismatch")
-    sk = None
     if sinks is not None:
         if sinks.dtype != torch.float32 or sinks.numel() != hq or not sinks.is_contiguous():
             raise ValueError("sinks must be a contiguous float32 [Hq] tensor")
-        sk = sinks.data_ptr()
-    with torch.cuda.device(q.device):
-        rc = lib.d2sd_local_attention_merge(
-            q.data_ptr(), q.stride(0), q.stride(1), q.stride(2), k.data_ptr(), v.data_ptr(),
-            k.stride(0), k.stride(1), k.stride(2), out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
-            lse.data_ptr(), lse.stride(0), lse.stride(1), bsz, lb, hq, hkv, d, int(bool(causal)),
-            float(sm_scale), sk, int(bool(lse_base2)), _stream())
-    check(rc, "local_attention_merge")
+    torch.ops.d2sd.local_attention_merge(q, k, v, out, lse, bool(causal), float(sm_scale), sinks,
+                                         bool(lse_base2))
 
 
 __all__ = ["single_prefill_with_kv_cache", "merge_state_in_place", "merge_state", "local_attention_merge"]

@@ -352,3 +352,25 @@ def test_bench_workloads_build_and_plan():
         info, items, _ = _plan(qo.tolist(), pl.tolist(), prob.num_qo_heads, prob.num_kv_heads, prob.head_dim,
                                prob.window_left, page_size=page, page_indptr=page_indptr)
         assert info.num_items > 0 and info.waves_per_block in (4, 8), name
+
+
+def test_torch_ops_registered_with_meta_kernels():
+    """torch.ops.d2sd.* (libd2sd_torch.so over the C ABI) is registered at
+    import; the meta kernels give the output shapes without a device."""
+    for op in ("single_prefill_with_kv_cache", "merge_state_in_place", "local_attention_merge", "cascade_run",
+               "cascade_run_no_alloc"):
+        assert hasattr(torch.ops.d2sd, op)
+    q = torch.empty(10, 32, 128, dtype=torch.bfloat16, device="meta")
+    k = torch.empty(8, 100, 128, dtype=torch.bfloat16, device="meta")
+    o, lse = torch.ops.d2sd.single_prefill_with_kv_cache(q, k, k, True, "HND", 0.1, False)
+    assert o.shape == q.shape and o.dtype == torch.bfloat16 and lse.shape == (10, 32) and lse.dtype == torch.float32
+    v = torch.empty(10, 32, 128, dtype=torch.bfloat16, device="meta")
+    s = torch.empty(10, 32, dtype=torch.float32, device="meta")
+    torch.ops.d2sd.merge_state_in_place(v, s, v, s, False)
+
+
+def test_torch_ops_reject_cpu_tensors():
+    q = torch.zeros(4, 32, 128, dtype=torch.bfloat16)
+    k = torch.zeros(16, 8, 128, dtype=torch.bfloat16)
+    with pytest.raises((RuntimeError, NotImplementedError)):
+        torch.ops.d2sd.single_prefill_with_kv_cache(q, k, k, False, "NHD", None, False)
