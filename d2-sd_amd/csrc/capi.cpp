@@ -485,6 +485,45 @@ int d2sd_cascade_run_noalloc(const d2sd_cascade_plan_info* info, const d2sd_casc
   return d2sd_cascade_merge(info, &b, stream);
 }
 
+// Candidate-tree build (replaces generation/d3_generator.py:116-180).
+int d2sd_d3_tree_build(const d2sd_d3_tree_args* a, d2sd_stream_t stream) {
+  g_last_error.clear();
+  if (!a) return fail(D2SD_ERR_INVALID_ARG, "d3_tree_build: null args");
+  if (a->block_size < 2 || a->block_size > 65 || a->block_size_2 < a->block_size || a->topk < 1)
+    return fail(D2SD_ERR_INVALID_ARG, "d3_tree_build: need 2 <= block_size <= 65, block_size_2 >= block_size, topk >= 1");
+  if (a->conf_dtype != D2SD_DTYPE_BF16 && a->conf_dtype != D2SD_DTYPE_F32)
+    return fail(D2SD_ERR_INVALID_ARG, "d3_tree_build: conf_dtype must be D2SD_DTYPE_BF16 or D2SD_DTYPE_F32");
+  const int k = std::min(a->topk, a->block_size - 1);
+  const long long worst = (long long)a->block_size_2 + (long long)k * (a->block_size_2 - 1);
+  if (a->capacity < worst || a->capacity > (1 << 24))
+    return fail(D2SD_ERR_INVALID_ARG, "d3_tree_build: capacity must hold the largest tree (" + std::to_string(worst) +
+                                          " nodes)");
+  if (a->rows_cap < k + 1 || a->rows_cap > d2sd::kTreeMaxRows)
+    return fail(D2SD_ERR_INVALID_ARG, "d3_tree_build: rows_cap must be in [min(topk, block_size - 1) + 1, 65]");
+  if ((long long)a->mask_words * 64 < a->capacity)
+    return fail(D2SD_ERR_INVALID_ARG, "d3_tree_build: mask_words too small for capacity");
+  if (!a->conf || !a->num_nodes || !a->parents || !a->node_index || !a->tree_mask)
+    return fail(D2SD_ERR_INVALID_ARG, "d3_tree_build: null pointer");
+  d2sd::TreeBuildParams p{};
+  p.conf = a->conf;
+  p.conf_bf16 = a->conf_dtype == D2SD_DTYPE_BF16 ? 1 : 0;
+  p.block_size = a->block_size;
+  p.block_size_2 = a->block_size_2;
+  p.topk = a->topk;
+  p.capacity = a->capacity;
+  p.rows_cap = a->rows_cap;
+  p.mask_words = a->mask_words;
+  p.num_nodes = a->num_nodes;
+  p.num_rows = a->num_rows;
+  p.parents = a->parents;
+  p.node_index = a->node_index;
+  p.tree_mask = (unsigned long long*)a->tree_mask;
+  p.shared = a->shared;
+  p.rates = a->rates;
+  hipError_t e = d2sd::launch_d3_tree_build(p, (hipStream_t)stream);
+  return e == hipSuccess ? D2SD_OK : fail_hip(e, "d3_tree_build launch");
+}
+
 // QK RMSNorm + RoPE (replaces generation/verification.py:113-123).
 int d2sd_qk_norm_rope(const d2sd_qk_norm_rope_args* a, d2sd_stream_t stream) {
   g_last_error.clear();

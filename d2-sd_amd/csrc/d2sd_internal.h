@@ -203,6 +203,26 @@ struct QkRopeParams {
   int half_cos;             // cos / sin hold D/2 columns
 };
 
+// ---------------------------------------------------------------------------
+// Candidate-tree build (tree_build.hip).
+// ---------------------------------------------------------------------------
+constexpr int kTreeMaxRows = 65;  // DFlash row + at most 64 boundaries
+struct TreeBuildParams {
+  const void* conf;          // [block_size - 1] bf16 or fp32
+  int conf_bf16;
+  int block_size, block_size_2, topk;
+  int capacity;              // nodes of parents / tree_mask
+  int rows_cap;              // rows of node_index / shared
+  int mask_words;
+  int* num_nodes;            // [1]
+  int* num_rows;             // [1] nullable
+  int* parents;              // [capacity]
+  int* node_index;           // [rows_cap, block_size_2]
+  unsigned long long* tree_mask;  // [capacity, mask_words]
+  int* shared;               // [rows_cap] nullable
+  float* rates;              // [block_size - 1] nullable
+};
+
 constexpr int kAcceptMaxNodes = 4096;  // logits rows of one walk
 constexpr int kAcceptMaxCells = 2048;  // candidate rows x positions
 struct AcceptParams {

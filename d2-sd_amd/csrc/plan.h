@@ -53,6 +53,9 @@ hipError_t verify_scratch(void** ptr);
 // ---- accepted-branch KV commit (kv_append.hip) ----
 hipError_t launch_kv_append(const KvAppendParams& p, bool advance, hipStream_t s);
 
+// ---- candidate-tree build (tree_build.hip) ----
+hipError_t launch_d3_tree_build(const TreeBuildParams& p, hipStream_t s);
+
 // ---- QK RMSNorm + RoPE (qk_rope.hip) ----
 hipError_t launch_qk_norm_rope(const QkRopeParams& p, hipStream_t s);
 

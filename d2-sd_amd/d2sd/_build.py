@@ -23,7 +23,8 @@ TORCH_LIB_PATH = PKG_DIR / "libd2sd_torch.so"
 INCLUDE = ROOT.parent / "include"
 
 ARCH = "gfx950"
-SOURCES = ["attention.hip", "verify_attention.hip", "kv_append.hip", "accept.hip", "qk_rope.hip", "plan.cpp", "capi.cpp"]
+SOURCES = ["attention.hip", "verify_attention.hip", "kv_append.hip", "accept.hip", "qk_rope.hip", "tree_build.hip",
+           "plan.cpp", "capi.cpp"]
 
 COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function", f"-I{INCLUDE}", f"-I{CSRC}"]
 # Device code: never let the compiler emit packed-fp32 VALU forms.

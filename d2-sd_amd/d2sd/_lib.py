@@ -42,6 +42,7 @@ EXPORTED_SYMBOLS = (
     "d2sd_greedy_accept_workspace_size",
     "d2sd_greedy_accept",
     "d2sd_qk_norm_rope",
+    "d2sd_d3_tree_build",
 )
 
 
@@ -175,6 +176,26 @@ class QkRopeArgs(C.Structure):
     ]
 
 
+class TreeArgs(C.Structure):
+    _fields_ = [
+        ("conf", C.c_void_p),
+        ("conf_dtype", C.c_int),
+        ("block_size", C.c_int),
+        ("block_size_2", C.c_int),
+        ("topk", C.c_int),
+        ("capacity", C.c_int),
+        ("rows_cap", C.c_int),
+        ("mask_words", C.c_int),
+        ("num_nodes", C.c_void_p),
+        ("num_rows", C.c_void_p),
+        ("parents", C.c_void_p),
+        ("node_index", C.c_void_p),
+        ("tree_mask", C.c_void_p),
+        ("shared", C.c_void_p),
+        ("rates", C.c_void_p),
+    ]
+
+
 class AcceptArgs(C.Structure):
     _fields_ = [
         ("num_rows", C.c_int),
@@ -244,6 +265,8 @@ def _load() -> C.CDLL:
     lib.d2sd_greedy_accept_workspace_size.argtypes = [i32, i32]
     lib.d2sd_greedy_accept.restype = i32
     lib.d2sd_greedy_accept.argtypes = [C.POINTER(AcceptArgs), vp]
+    lib.d2sd_d3_tree_build.restype = i32
+    lib.d2sd_d3_tree_build.argtypes = [C.POINTER(TreeArgs), vp]
     lib.d2sd_qk_norm_rope.restype = i32
     lib.d2sd_qk_norm_rope.argtypes = [C.POINTER(QkRopeArgs), vp]
     return lib

@@ -321,6 +321,42 @@ typedef struct {
 int d2sd_paged_kv_append(const d2sd_kv_append_args* args, d2sd_stream_t stream);
 
 /* ----------------------------------------------------------------------
+ * Candidate-tree build of one D2SD step on the device.
+ * Replaces generation/d3_generator.py:116-180 up to the rows it verifies:
+ * rejection rates from the draft confidences (rates[0] = 1 - c0,
+ * rates[k] = cumprod(c)[k-1] * (1 - c_k), with torch's arithmetic for the
+ * confidences' dtype), the top-k boundaries (torch.topk + sorted + .tolist()
+ * at :123-125; equal rates ranked by index), and the rows: the DFlash row
+ * (with its continuation when block_size_2 > block_size, else last) and per
+ * boundary pl a row sharing its first pl + 1 tokens.  Outputs the token tree
+ * of those rows in fixed capacity: unique nodes (row-major order of first
+ * appearance), node_index [rows_cap, block_size_2], parents [capacity]
+ * (-1 = root) and the ancestor mask [capacity, mask_words] in the layout
+ * d2sd_cascade_run reads (bit j of row i: node j is i or an ancestor of i).
+ * Nodes past num_nodes are roots seeing only themselves; rows past num_rows
+ * repeat the DFlash row.  One single-wave launch, no host synchronisation.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  const void* conf;     /* device [block_size - 1], dtype conf_dtype */
+  int conf_dtype;       /* D2SD_DTYPE_BF16 or D2SD_DTYPE_F32 */
+  int block_size;       /* DFlash block (2..65) */
+  int block_size_2;     /* >= block_size */
+  int topk;             /* >= 1 */
+  int capacity;         /* >= block_size_2 + min(topk, block_size - 1) * (block_size_2 - 1) */
+  int rows_cap;         /* >= min(topk, block_size - 1) + 1, <= 65 */
+  int mask_words;       /* >= ceil(capacity / 64) */
+  int32_t* num_nodes;   /* device [1] */
+  int32_t* num_rows;    /* device [1], nullable */
+  int32_t* parents;     /* device [capacity] */
+  int32_t* node_index;  /* device [rows_cap, block_size_2] */
+  uint64_t* tree_mask;  /* device [capacity, mask_words] */
+  int32_t* shared;      /* device [rows_cap], nullable: tokens each row shares with the DFlash row */
+  float* rates;         /* device [block_size - 1], nullable */
+} d2sd_d3_tree_args;
+
+int d2sd_d3_tree_build(const d2sd_d3_tree_args* args, d2sd_stream_t stream);
+
+/* ----------------------------------------------------------------------
  * Per-head RMSNorm of the new queries and keys, then rotary embedding, in
  * place, one launch.  Replaces generation/verification.py:113-123 (Qwen3:
  * attn.q_norm / k_norm + _apply_rotary_pos_emb_qwen3; GPT-OSS: RoPE only)

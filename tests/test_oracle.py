@@ -298,8 +298,57 @@ def test_d3_tree_sizes_match_reference_geometry():
 
 def test_d3_rates_formula():
     conf = np.array([0.9, 0.5, 0.8, 0.3])
-    r = dtree.d3_rejection_rates(conf)
+    r = dtree.d3_rejection_rates(conf, "float32")
     assert np.allclose(r, [0.1, 0.9 * 0.5, 0.9 * 0.5 * 0.2, 0.9 * 0.5 * 0.8 * 0.7])
+
+
+def _reference_rates_torch(conf: torch.Tensor) -> torch.Tensor:
+    """generation/d3_generator.py:117-121, executed with torch on conf's
+    dtype; the cumulative product as a sequential loop of torch bf16 products,
+    which is what torch.cumprod computes on a device tensor (pinned in
+    tests/test_gpu_tree_build.py; its CPU kernel keeps a float32 running
+    product instead)."""
+    cum_prod = conf.clone()
+    for i in range(1, conf.shape[0]):
+        cum_prod[i] = cum_prod[i - 1] * conf[i]
+    rates = torch.empty(conf.shape[0])
+    rates[0] = 1.0 - conf[0]
+    rates[1:] = cum_prod[:-1] * (1.0 - conf[1:])
+    return rates
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16"])
+def test_d3_rates_match_torch_arithmetic(dtype):
+    """The restatement equals the reference's own torch lines, bit for bit,
+    on random and on coarse (tie-rich) confidences (bf16, the draft
+    probabilities' dtype; fp32 is pinned on the GPU, where torch's cumprod
+    runs as the reference ran it)."""
+    rng = np.random.default_rng(17)
+    tdt = getattr(torch, dtype)
+    for i in range(300):
+        conf = rng.uniform(size=15) if i % 2 else rng.choice([0.0, 0.25, 0.5, 0.75, 1.0, 0.9, 0.1], size=15)
+        c = torch.tensor(conf, dtype=torch.float32).to(tdt)
+        ref = _reference_rates_torch(c).numpy()
+        got = dtree.d3_rejection_rates(c.float().numpy(), dtype)
+        assert np.array_equal(ref.view(np.uint32), got.view(np.uint32)), (i, ref, got)
+
+
+def test_d3_selection_matches_torch_topk_without_boundary_ties():
+    """sorted(torch.topk(rates, 4)) == the restatement whenever the 4th and
+    5th largest rates differ (ties there are ordered by index here; torch.topk
+    leaves their order unspecified)."""
+    rng = np.random.default_rng(23)
+    checked = 0
+    for _ in range(400):
+        c = torch.tensor(rng.uniform(size=15), dtype=torch.float32).to(torch.bfloat16)
+        rates = _reference_rates_torch(c)
+        srt = torch.sort(rates, descending=True).values
+        if srt[3] == srt[4]:
+            continue
+        ref = sorted(torch.topk(rates, 4).indices.tolist())
+        assert ref == dtree.d3_select_boundaries(dtree.d3_rejection_rates(c.float().numpy()), 4)
+        checked += 1
+    assert checked > 300
 
 
 def test_pack_mask_bits():
