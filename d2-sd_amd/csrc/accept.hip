@@ -1,21 +1,34 @@
-// gfx950 kernels of the greedy acceptance walk of a verify tree, on the device.
+// gfx950 kernels of the acceptance walk of a verify tree, on the device.
 //
-// Replaces generation/d3_generator.py:204-225 at temperature 0
-// (model/utils.py:28-33: greedy sampling is torch.argmax, first index on
-// ties): starting with every candidate row valid, step a takes the first
-// valid row, samples the argmax of the target's logits at that row's
-// position a, accepts it, and keeps only the rows whose draft token at
-// position a + 1 equals it; the walk ends when no row is valid or the rows are
-// exhausted.  The reference runs this loop on the host (nonzero(), sum() and a
-// host-side list per step); here it is two launches with no host
-// synchronisation, and its outputs feed the KV commit directly.
+// Replaces generation/d3_generator.py:204-225: starting with every candidate
+// row valid, step a takes the first valid row, samples a token from the
+// target's logits at that row's position a (model/utils.py:28-37), accepts
+// it, and keeps only the rows whose draft token at position a + 1 equals it;
+// the walk ends when no row is valid or the rows are exhausted.  The
+// reference runs this loop on the host (nonzero(), sum() and a host-side list
+// per step); here it is two launches with no host synchronisation, and its
+// outputs feed the KV commit directly.
+//
+// Sampling.  At temperature 0 the token is torch.argmax (first index on
+// ties).  At temperature T > 0 the reference draws torch.multinomial of
+// softmax(logits / T), which torch computes as argmax(p / E), E ~ Exp(1)
+// per token.  Here every node's token is drawn the same way in log space,
+// argmax over tokens of x log2(e) - log2(E) with x = logits * (1/T) rounded
+// to the logits dtype (torch's GPU division by a scalar), so no softmax pass
+// is needed.  Each walk step visits a different node, so drawing all nodes'
+// tokens up front and walking over them is the same process.  E = -ln(u),
+// u uniform from Philox4x32-10 (Salmon et al., SC 2011) with counter
+// (token / 4, node, step) and key seed; `step` is a device counter the walk
+// advances, so every call, and every replay of a captured call, draws anew.
 //
 //   argmax_chunks_kernel  [N nodes] x [C chunks of the vocabulary]: the max
-//                         of each chunk as one 64-bit key (order-preserving
-//                         float bits, then the complement of the index, so a
-//                         larger key is a larger logit or, on ties, a smaller
-//                         index).  HBM bound: N * V logits read once.
-//   greedy_walk_kernel    one workgroup: every node's argmax from its C keys
+//                         score of each chunk as one 64-bit key
+//                         (order-preserving float bits, then the complement
+//                         of the index, so a larger key is a larger score or,
+//                         on ties, a smaller index).  Greedy: HBM bound, N * V
+//                         logits read once; sampling: one Philox call per
+//                         four tokens and two log2 per token on top.
+//   greedy_walk_kernel    one workgroup: every node's token from its C keys
 //                         and the rows' node ids and draft tokens into LDS,
 //                         then the walk in one wave from LDS.
 #include <hip/hip_runtime.h>
@@ -60,12 +73,76 @@ struct LaneMax {
   }
 };
 
+// Philox4x32-10: ten rounds of
+// (c0, c1, c2, c3) <- (hi(M1 c2) ^ c1 ^ k0, lo(M1 c2), hi(M0 c0) ^ c3 ^ k1, lo(M0 c0)),
+// the key bumped by the Weyl constants between rounds.
+__device__ __forceinline__ uint4 philox4x32_10(uint4 c, unsigned k0, unsigned k1) {
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const unsigned hi0 = __umulhi(0xD2511F53u, c.x), lo0 = 0xD2511F53u * c.x;
+    const unsigned hi1 = __umulhi(0xCD9E8D57u, c.z), lo1 = 0xCD9E8D57u * c.z;
+    c = uint4{hi1 ^ c.y ^ k0, lo1, hi0 ^ c.w ^ k1, lo0};
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  return c;
+}
+
+// -log2(E), E = -ln(u), u = (2 (w >> 9) + 1) 2^-24 in (0, 1) (exact in fp32).
+// For u >= 15/16, E comes from the series of -ln(1 - d), d = 1 - u exact, so
+// the smallest E (the largest scores) keep their relative precision.
+__device__ __forceinline__ float neg_log2_exp(unsigned w) {
+  const float u = (float)((w >> 9) * 2u + 1u) * 0x1p-24f;
+  const float d = (float)((0x7FFFFFu - (w >> 9)) * 2u + 1u) * 0x1p-24f;  // 1 - u
+  float e;
+  if (d <= 0.0625f) {
+    // d + d^2/2 + ... + d^7/7: truncation below 2^-28 relative
+    e = d * (1.f + d * (0.5f + d * (1.f / 3.f + d * (0.25f + d * (0.2f + d * (1.f / 6.f + d * (1.f / 7.f)))))));
+  } else {
+    e = -__builtin_amdgcn_logf(u) * 0.69314718055994531f;
+  }
+  return -__builtin_amdgcn_logf(e);
+}
+
 template <bool BF16>
+__device__ __forceinline__ float logit_at(const void* row, int t) {
+  return BF16 ? __uint_as_float((unsigned)((const uint16_t*)row)[t] << 16) : ((const float*)row)[t];
+}
+
+template <bool BF16>
+__device__ __forceinline__ float scaled_logit(float l, float inv_t) {
+  const float x = l * inv_t;
+  if (!BF16) return x;
+  unsigned u = __float_as_uint(x);  // round to nearest even bf16 (finite logits)
+  u = (u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u;
+  return __uint_as_float(u);
+}
+
+template <bool BF16, bool SAMPLE>
 __global__ __launch_bounds__(256) void argmax_chunks_kernel(const AcceptParams p) {
   const int chunk = blockIdx.x, node = blockIdx.y;
   const int v0 = chunk * p.chunk_len, v1 = min(p.vocab, v0 + p.chunk_len);  // v0: a multiple of 8
   LaneMax m;
-  if (BF16) {
+  if (SAMPLE) {
+    // four tokens per Philox call: quads [v0 / 4, ceil(v1 / 4))
+    const void* row = BF16 ? (const void*)((const uint16_t*)p.logits + (long long)node * p.logits_stride)
+                           : (const void*)((const float*)p.logits + (long long)node * p.logits_stride);
+    const unsigned long long step = (unsigned long long)*p.rng_step;
+    const float kLog2e = 1.4426950408889634f;
+    for (int qd = v0 / 4 + (int)threadIdx.x; 4 * qd < v1; qd += (int)blockDim.x) {
+      const uint4 w = philox4x32_10(uint4{(unsigned)qd, (unsigned)node, (unsigned)step, (unsigned)(step >> 32)},
+                                    p.seed_lo, p.seed_hi);
+      const unsigned ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int t = 4 * qd + e;
+        if (t < v1) {
+          const float x = scaled_logit<BF16>(logit_at<BF16>(row, t), p.inv_temperature);
+          m.add(x * kLog2e + neg_log2_exp(ws[e]), t);
+        }
+      }
+    }
+  } else if (BF16) {
     const uint16_t* row = (const uint16_t*)p.logits + (long long)node * p.logits_stride;
     // 16-byte vectors of 8 logits over [v0, vend) when rows are 16-byte
     // aligned; then the rest one by one
@@ -137,6 +214,10 @@ __global__ __launch_bounds__(256) void greedy_walk_kernel(const AcceptParams p) 
     draft_at[c] = p.draft_ids[c];
   }
   __syncthreads();
+  if (p.node_tokens)
+    for (int nd = tid; nd < p.num_nodes; nd += nt)
+      p.node_tokens[nd] = (long long)(0xFFFFFFFFu - (unsigned)key_of[nd]);
+  if (tid == 0 && p.rng_step) p.rng_step[0] += 1;  // the chunk pass has read it
   if (tid >= 64) return;
   const int lane = tid;
   bool valid = lane < p.num_rows;
@@ -175,8 +256,14 @@ void greedy_accept_chunks(int num_nodes, int vocab, int& chunks, int& chunk_len)
 hipError_t launch_greedy_accept(const AcceptParams& p, bool bf16, hipStream_t s) {
   if (p.num_nodes <= 0) return hipSuccess;
   const dim3 grid((unsigned)p.chunks, (unsigned)p.num_nodes);
-  if (bf16) hipLaunchKernelGGL(argmax_chunks_kernel<true>, grid, dim3(256), 0, s, p);
-  else hipLaunchKernelGGL(argmax_chunks_kernel<false>, grid, dim3(256), 0, s, p);
+  const bool sample = p.rng_step != nullptr;
+  if (sample) {
+    if (bf16) hipLaunchKernelGGL((argmax_chunks_kernel<true, true>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((argmax_chunks_kernel<false, true>), grid, dim3(256), 0, s, p);
+  } else {
+    if (bf16) hipLaunchKernelGGL((argmax_chunks_kernel<true, false>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((argmax_chunks_kernel<false, false>), grid, dim3(256), 0, s, p);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(greedy_walk_kernel, dim3(1), dim3(256), 0, s, p);

@@ -567,8 +567,10 @@ size_t d2sd_greedy_accept_workspace_size(int num_nodes, int vocab) {
   return (size_t)num_nodes * chunks * sizeof(unsigned long long);
 }
 
-int d2sd_greedy_accept(const d2sd_greedy_accept_args* a, d2sd_stream_t stream) {
-  g_last_error.clear();
+namespace {
+
+// Checks the walk's arguments and fills its parameters (sampling fields zero).
+int walk_params(const d2sd_greedy_accept_args* a, d2sd::AcceptParams& p) {
   if (!a) return fail(D2SD_ERR_INVALID_ARG, "greedy_accept: null args");
   if (a->num_rows < 1 || a->num_rows > 64)
     return fail(D2SD_ERR_INVALID_ARG, "greedy_accept: num_rows must be in [1, 64]");
@@ -587,7 +589,7 @@ int d2sd_greedy_accept(const d2sd_greedy_accept_args* a, d2sd_stream_t stream) {
     return fail(D2SD_ERR_WORKSPACE, "greedy_accept: workspace too small (need " +
                                         std::to_string(d2sd_greedy_accept_workspace_size(a->num_nodes, a->vocab)) +
                                         " bytes)");
-  d2sd::AcceptParams p{};
+  p = d2sd::AcceptParams{};
   p.logits = a->logits;
   p.logits_stride = a->logits_stride;
   p.node_index = a->node_index;
@@ -601,8 +603,38 @@ int d2sd_greedy_accept(const d2sd_greedy_accept_args* a, d2sd_stream_t stream) {
   p.num_nodes = a->num_nodes;
   p.vocab = a->vocab;
   d2sd::greedy_accept_chunks(a->num_nodes, a->vocab, p.chunks, p.chunk_len);
+  return D2SD_OK;
+}
+
+}  // namespace
+
+int d2sd_greedy_accept(const d2sd_greedy_accept_args* a, d2sd_stream_t stream) {
+  g_last_error.clear();
+  d2sd::AcceptParams p;
+  if (int rc = walk_params(a, p)) return rc;
   hipError_t e = d2sd::launch_greedy_accept(p, a->logits_dtype == D2SD_DTYPE_BF16, (hipStream_t)stream);
   return e == hipSuccess ? D2SD_OK : fail_hip(e, "greedy_accept launch");
+}
+
+// The walk at any temperature (generation/d3_generator.py:204-225 with
+// model/utils.py:28-37).
+int d2sd_sample_accept(const d2sd_sample_accept_args* a, d2sd_stream_t stream) {
+  g_last_error.clear();
+  if (!a) return fail(D2SD_ERR_INVALID_ARG, "sample_accept: null args");
+  if (!(a->temperature >= 0.f) || !std::isfinite(a->temperature))
+    return fail(D2SD_ERR_INVALID_ARG, "sample_accept: temperature must be finite and >= 0");
+  d2sd::AcceptParams p;
+  if (int rc = walk_params(&a->walk, p)) return rc;
+  p.node_tokens = (long long*)a->node_tokens;
+  if (a->temperature >= 1e-5f) {
+    if (!a->rng_step) return fail(D2SD_ERR_INVALID_ARG, "sample_accept: rng_step is required when sampling");
+    p.inv_temperature = 1.f / a->temperature;
+    p.seed_lo = (unsigned)(a->seed & 0xFFFFFFFFull);
+    p.seed_hi = (unsigned)(a->seed >> 32);
+    p.rng_step = (long long*)a->rng_step;
+  }
+  hipError_t e = d2sd::launch_greedy_accept(p, a->walk.logits_dtype == D2SD_DTYPE_BF16, (hipStream_t)stream);
+  return e == hipSuccess ? D2SD_OK : fail_hip(e, "sample_accept launch");
 }
 
 // Accepted-branch KV commit (replaces generation/d3_generator.py:227-232).

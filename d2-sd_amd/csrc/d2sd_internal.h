@@ -236,6 +236,14 @@ struct AcceptParams {
   unsigned long long* keys;       // workspace [num_nodes, chunks]
   int num_rows, row_len, num_nodes, vocab;
   int chunks, chunk_len;          // vocabulary chunks per node (chunk_len a multiple of 8)
+  // sampling (temperature > 0): each node's token is the argmax of
+  // x log2(e) - log2(E), x = logits * inv_temperature rounded to the logits
+  // dtype, E = -ln(u), u from Philox4x32-10 with counter
+  // (token / 4, node, step) and key seed
+  float inv_temperature;
+  unsigned seed_lo, seed_hi;
+  long long* rng_step;            // [1] the step counter; the walk advances it by one
+  long long* node_tokens;         // out [num_nodes] nullable: every node's token
 };
 
 }  // namespace d2sd

@@ -6,7 +6,7 @@ Drop-in surface of the reference's verify path:
 and the tree-level API
   CascadeVerifyAttention.plan() / .run()
   PagedKVCommit.commit()        (accepted-branch KV append, d3_generator.py:227-232)
-  GreedyAccept()                (greedy acceptance walk, d3_generator.py:204-225)
+  GreedyAccept() / TreeAccept() (acceptance walk, greedy or sampled, d3_generator.py:204-225)
 All device work runs hand-written HIP kernels in libd2sd.so (C ABI:
 include/d2sd.h); importing raises if the library has not been built.
 """
@@ -17,11 +17,11 @@ from .graph import HipGraph
 from .cascade_graph import CascadeGraphRunner
 from .cascade import CascadeVerifyAttention
 from .kv_commit import PagedKVCommit
-from .accept import GreedyAccept
+from .accept import GreedyAccept, TreeAccept
 from . import tree
 
 __all__ = [
     "LIB_PATH", "version", "single_prefill_with_kv_cache", "merge_state_in_place", "merge_state",
-    "local_attention_merge", "qk_norm_rope", "HipGraph", "CascadeGraphRunner", "CascadeVerifyAttention", "PagedKVCommit", "GreedyAccept",
+    "local_attention_merge", "qk_norm_rope", "HipGraph", "CascadeGraphRunner", "CascadeVerifyAttention", "PagedKVCommit", "GreedyAccept", "TreeAccept",
     "tree",
 ]

@@ -41,6 +41,7 @@ EXPORTED_SYMBOLS = (
     "d2sd_paged_kv_append",
     "d2sd_greedy_accept_workspace_size",
     "d2sd_greedy_accept",
+    "d2sd_sample_accept",
     "d2sd_qk_norm_rope",
     "d2sd_d3_tree_build",
 )
@@ -215,6 +216,16 @@ class AcceptArgs(C.Structure):
     ]
 
 
+class SampleAcceptArgs(C.Structure):
+    _fields_ = [
+        ("walk", AcceptArgs),
+        ("temperature", C.c_float),
+        ("seed", C.c_uint64),
+        ("rng_step", C.c_void_p),
+        ("node_tokens", C.c_void_p),
+    ]
+
+
 # int32 entries per attention item / merge item in the host plan
 PLAN_ITEM_INTS = 16
 PLAN_MERGE_INTS = 8
@@ -265,6 +276,8 @@ def _load() -> C.CDLL:
     lib.d2sd_greedy_accept_workspace_size.argtypes = [i32, i32]
     lib.d2sd_greedy_accept.restype = i32
     lib.d2sd_greedy_accept.argtypes = [C.POINTER(AcceptArgs), vp]
+    lib.d2sd_sample_accept.restype = i32
+    lib.d2sd_sample_accept.argtypes = [C.POINTER(SampleAcceptArgs), vp]
     lib.d2sd_d3_tree_build.restype = i32
     lib.d2sd_d3_tree_build.argtypes = [C.POINTER(TreeArgs), vp]
     lib.d2sd_qk_norm_rope.restype = i32

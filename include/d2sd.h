@@ -424,6 +424,33 @@ typedef struct {
 size_t d2sd_greedy_accept_workspace_size(int num_nodes, int vocab);
 int d2sd_greedy_accept(const d2sd_greedy_accept_args* args, d2sd_stream_t stream);
 
+/* ----------------------------------------------------------------------
+ * The same walk at any temperature (generation/d3_generator.py:204-225 with
+ * sample(logit, temperature), model/utils.py:28-37).  temperature < 1e-5 is
+ * the greedy walk above (the reference's own threshold) and leaves
+ * *rng_step alone.  Otherwise each accepted token is drawn from
+ * softmax(logits / temperature): logits / temperature is computed as torch
+ * does on the GPU (logits times the fp32 reciprocal, rounded to the logits
+ * dtype) and the draw is torch.multinomial's exponential race,
+ * argmax_v p_v / E_v, E_v ~ Exp(1), taken in log space.  E_v = -ln(u_v), u_v
+ * from Philox4x32-10 with counter (v / 4, node, *rng_step) and key seed, so
+ * the draws are a pure function of (logits, seed, *rng_step); the call
+ * reads *rng_step and then advances it by one, so consecutive calls, and
+ * replays of a captured call, draw independently.  The random stream is not
+ * torch's: a sampled walk matches the reference in distribution, not token
+ * for token.  node_tokens (nullable) receives every node's token (argmax at
+ * temperature 0).  Workspace: d2sd_greedy_accept_workspace_size bytes.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  d2sd_greedy_accept_args walk;
+  float temperature;          /* >= 0, finite */
+  uint64_t seed;
+  int64_t* rng_step;          /* device [1]: step counter; required when temperature >= 1e-5 */
+  int64_t* node_tokens;       /* device out [num_nodes], nullable */
+} d2sd_sample_accept_args;
+
+int d2sd_sample_accept(const d2sd_sample_accept_args* args, d2sd_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,6 +18,10 @@ It restates the reference's verify-attention algorithm on the CPU in float64
   the same over unique tree nodes, single pass     cascade_tree_ref
   d3_generator.py:227-232 (accepted-branch commit) commit_accepted_ref
   d3_generator.py:204-225 (greedy acceptance walk) greedy_accept_ref
+  d3_generator.py:204-225 at temperature > 0 (model/utils.py:34-37,
+  torch.multinomial's exponential race)            sample_scores_ref, sampled_accept_ref
+  Philox4x32-10 (the counter-based generator the sampled walk draws from)
+                                                   philox4x32_10
   verification.py:113-123 (QK RMSNorm + RoPE)       qk_norm_rope_ref
 
 FlashInfer itself (flashinfer-python>=0.2.0, requirements.txt:13) is not
@@ -39,6 +43,10 @@ pure tree attention; chain tree == causal; constant V -> that V; page-table
 permutation invariance); against the reference's three-step row-layout
 algorithm vs. the single-pass tree form; and, for the sink, against the
 installed transformers GPT-OSS eager attention (a library routine).
+philox4x32_10 is pinned to the published known-answer vectors of Random123
+(the generator's authors' reference release); sample_scores_ref to the
+mathematics it restates: sampled frequencies follow softmax(x) (chi-square),
+and its choice equals torch.multinomial's argmax(p / E) on the same E.
 """
 from __future__ import annotations
 
@@ -309,9 +317,80 @@ def greedy_accept_ref(node_logits: Tensor, node_index, draft_ids) -> Tuple[List[
     return accept_ids, nodes, acceptance_length, valid_block
 
 
+PHILOX_M = (0xD2511F53, 0xCD9E8D57)
+PHILOX_W = (0x9E3779B9, 0xBB67AE85)
+
+
+def philox4x32_10(ctr: np.ndarray, key: Tuple[int, int]) -> np.ndarray:
+    """Philox4x32-10 (Salmon, Moraes, Dror and Shaw, "Parallel random numbers:
+    as easy as 1, 2, 3", SC 2011), vectorised: ctr [..., 4] uint32 words
+    (c0..c3), key (k0, k1) -> [..., 4] uint32.  Ten rounds of
+    (c0, c1, c2, c3) <- (hi(M1 c2) ^ c1 ^ k0, lo(M1 c2), hi(M0 c0) ^ c3 ^ k1, lo(M0 c0))
+    with the key bumped by the Weyl constants (W0, W1) between rounds."""
+    m32 = np.uint64(0xFFFFFFFF)
+    c = [np.asarray(ctr, dtype=np.uint64)[..., i] for i in range(4)]
+    k0, k1 = np.uint64(key[0] & 0xFFFFFFFF), np.uint64(key[1] & 0xFFFFFFFF)
+    for _ in range(10):
+        p0 = c[0] * np.uint64(PHILOX_M[0])
+        p1 = c[2] * np.uint64(PHILOX_M[1])
+        c = [(p1 >> np.uint64(32)) ^ c[1] ^ k0, p1 & m32, (p0 >> np.uint64(32)) ^ c[3] ^ k1, p0 & m32]
+        k0 = (k0 + np.uint64(PHILOX_W[0])) & m32
+        k1 = (k1 + np.uint64(PHILOX_W[1])) & m32
+    return np.stack(c, -1).astype(np.uint32)
+
+
+def sample_uniforms_ref(num_nodes: int, vocab: int, seed: int, offset: int) -> np.ndarray:
+    """The uniform variate of (node n, token v) at step counter `offset`: word
+    v % 4 of Philox4x32-10 with counter (v // 4, n, offset low, offset high)
+    and key (seed low, seed high), as u = (2 (w >> 9) + 1) 2^-24, in (0, 1)
+    and exact in fp32.  float64 [num_nodes, vocab]."""
+    q = np.arange((vocab + 3) // 4, dtype=np.uint64)
+    n = np.arange(num_nodes, dtype=np.uint64)
+    ctr = np.zeros((num_nodes, q.size, 4), dtype=np.uint64)
+    ctr[..., 0] = q[None, :]
+    ctr[..., 1] = n[:, None]
+    ctr[..., 2] = offset & 0xFFFFFFFF
+    ctr[..., 3] = (offset >> 32) & 0xFFFFFFFF
+    w = philox4x32_10(ctr, (seed & 0xFFFFFFFF, (seed >> 32) & 0xFFFFFFFF)).reshape(num_nodes, -1)[:, :vocab]
+    return ((w >> np.uint32(9)).astype(np.float64) * 2.0 + 1.0) * 2.0 ** -24
+
+
+def scaled_logits_ref(node_logits: Tensor, temperature: float) -> np.ndarray:
+    """`logits / temperature` as torch computes it on the GPU for a Python
+    scalar (model/utils.py:34): logits times the fp32 reciprocal of the
+    temperature in fp32, rounded to the logits dtype.  float64 array."""
+    inv = np.float32(1.0) / np.float32(temperature)
+    x = node_logits.float() * torch.tensor(inv, dtype=torch.float32)
+    return x.to(node_logits.dtype).double().numpy()
+
+
+def sample_scores_ref(node_logits: Tensor, temperature: float, seed: int, offset: int) -> np.ndarray:
+    """Per (node, token) score whose argmax is the token sampled from
+    softmax(x) (model/utils.py:34-37), x = scaled_logits_ref: torch.multinomial
+    of one sample is argmax(p / E) with E ~ Exp(1) (the exponential race), and
+    log2(p / E) = x log2(e) - log2(E) - log2(sum) ranks the same.  E = -ln(u)
+    of sample_uniforms_ref.  float64 [num_nodes, vocab]."""
+    x = scaled_logits_ref(node_logits, temperature)
+    u = sample_uniforms_ref(x.shape[0], x.shape[1], seed, offset)
+    e = -np.log1p(-(1.0 - u))
+    return x * (1.0 / math.log(2.0)) - np.log2(e)
+
+
+def sampled_accept_ref(node_logits: Tensor, node_index, draft_ids, temperature: float, seed: int,
+                       offset: int) -> Tuple[List[int], List[int], int, int]:
+    """The acceptance loop of d3_generator.py:204-225 at temperature > 0:
+    sample() draws each accepted token from softmax(logits / T) of the first
+    valid row's node.  Each node is visited at most once per walk, so drawing
+    every node's token up front (sample_scores_ref at this step counter) and
+    walking greedily over those scores is the same process."""
+    scores = torch.from_numpy(sample_scores_ref(node_logits, temperature, seed, offset))
+    return greedy_accept_ref(scores, node_index, draft_ids)
+
+
 __all__ = [
     "attention_ref", "attention_sdpa_ref", "causal_mask", "single_prefill_ref", "merge_state_ref",
     "sink_rescale_ref", "window_prefix_ref", "cascade_verify_rows_ref", "cascade_tree_ref",
     "ancestor_mask_from_rows", "fp8_dequant_ref", "gather_paged", "commit_accepted_ref",
-    "greedy_accept_ref", "qk_norm_rope_ref",
+    "greedy_accept_ref", "qk_norm_rope_ref", "philox4x32_10", "sample_uniforms_ref", "scaled_logits_ref",
+    "sample_scores_ref", "sampled_accept_ref",
 ]

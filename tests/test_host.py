@@ -334,6 +334,34 @@ def test_greedy_accept_rejects_bad_arguments():
     assert _lib.lib.d2sd_greedy_accept(C.byref(a), None) == 3   # D2SD_ERR_WORKSPACE
 
 
+def test_sample_accept_rejects_bad_arguments():
+    s = _lib.SampleAcceptArgs()
+    a = s.walk
+    a.num_rows, a.row_len, a.num_nodes, a.vocab, a.logits_dtype = 5, 32, 150, 1000, 0
+    a.logits_stride = 1000
+    for f in ("logits", "node_index", "draft_ids", "accept_ids", "accept_nodes", "result", "workspace"):
+        setattr(a, f, 8)
+    a.workspace_bytes = 1 << 30
+    for t in (-0.5, float("nan"), float("inf")):
+        s.temperature = t
+        assert _lib.lib.d2sd_sample_accept(C.byref(s), None) == 1
+        assert _lib.lib.d2sd_last_error().startswith(b"sample_accept: temperature")
+    s.temperature, s.rng_step = 0.7, None       # sampling needs the step counter
+    assert _lib.lib.d2sd_sample_accept(C.byref(s), None) == 1
+    assert b"rng_step" in _lib.lib.d2sd_last_error()
+    s.rng_step = 8
+    a.num_rows = 65                              # the walk's own checks apply
+    assert _lib.lib.d2sd_sample_accept(C.byref(s), None) == 1
+    assert _lib.lib.d2sd_last_error().startswith(b"greedy_accept: num_rows")
+
+
+def test_accept_rejects_bad_temperature():
+    import d2sd
+    for t in (-1.0, float("nan"), float("inf")):
+        with pytest.raises(ValueError):
+            d2sd.TreeAccept(10, 100, 4, "cpu", temperature=t)
+
+
 def test_bench_workloads_build_and_plan():
     """Every `bench.py --workload` name builds its problem, whose sizes the
     planner accepts (host work only: the plan is computed, nothing runs)."""

@@ -446,6 +446,118 @@ def test_accept_argmax_ties_take_the_first_index():
     assert ids == [3] and n == 1
 
 
+# ---- sampled acceptance (d3_generator.py:204-225 at temperature > 0) ----
+
+def test_philox_known_answer_vectors():
+    """Philox4x32-10 against the known-answer vectors published with
+    Random123 (counter, key -> output)."""
+    kat = [
+        ([0, 0, 0, 0], (0, 0), [0x6627e8d5, 0xe169c58d, 0xbc57ac4c, 0x9b00dbd8]),
+        ([0xffffffff] * 4, (0xffffffff, 0xffffffff), [0x408f276d, 0x41c83b0e, 0xa20bc7c6, 0x6d5451fd]),
+        ([0x243f6a88, 0x85a308d3, 0x13198a2e, 0x03707344], (0xa4093822, 0x299f31d0),
+         [0xd16cfe09, 0x94fdcceb, 0x5001e420, 0x24126ea1]),
+    ]
+    ctr = np.array([c for c, _, _ in kat], dtype=np.uint64)
+    for i, (c, k, want) in enumerate(kat):
+        assert orc.philox4x32_10(ctr[i], k).tolist() == want
+    # vectorised form == one counter at a time
+    out = orc.philox4x32_10(ctr, (0xa4093822, 0x299f31d0))
+    assert out[2].tolist() == kat[2][2]
+
+
+def test_sample_uniforms_range_and_independence():
+    u = orc.sample_uniforms_ref(64, 1001, seed=5, offset=3)
+    assert u.shape == (64, 1001) and u.min() > 0.0 and u.max() < 1.0
+    assert abs(u.mean() - 0.5) < 0.01 and abs(u.var() - 1 / 12) < 0.005
+    # exactly representable in fp32
+    assert np.array_equal(u.astype(np.float32).astype(np.float64), u)
+    # another step, seed or node gives another stream
+    assert not np.array_equal(u, orc.sample_uniforms_ref(64, 1001, seed=5, offset=4))
+    assert not np.array_equal(u, orc.sample_uniforms_ref(64, 1001, seed=6, offset=3))
+    assert not np.array_equal(u[0], u[1])
+    # token v uses word v % 4 of counter (v // 4, node, step): truncating the
+    # vocabulary does not change the variates of the tokens kept
+    assert np.array_equal(orc.sample_uniforms_ref(64, 13, seed=5, offset=3), u[:, :13])
+
+
+def _sample_counts(logits_row, temperature, nodes, seed, scores_fn=orc.sample_scores_ref):
+    lg = logits_row.expand(nodes, -1).contiguous()
+    choice = scores_fn(lg, temperature, seed, 0).argmax(-1)
+    return np.bincount(choice, minlength=lg.shape[1])
+
+
+def _chi2_pvalue(counts, probs):
+    from scipy import stats
+    exp = probs * counts.sum()
+    keep = exp >= 5  # pool the rare tokens into one cell
+    obs = np.append(counts[keep], counts[~keep].sum())
+    ex = np.append(exp[keep], exp[~keep].sum())
+    if ex[-1] == 0:
+        obs, ex = obs[:-1], ex[:-1]
+    return stats.chisquare(obs, ex).pvalue
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_sampled_tokens_follow_softmax(dtype):
+    """The draws are multinomial samples of softmax(x), x = the scaled logits
+    (model/utils.py:34-37), and a plausible mistake in the scores is caught."""
+    gen = torch.Generator().manual_seed(1)
+    row = (torch.randn(1, 24, generator=gen) * 2.0).to(dtype)
+    temp = 0.8
+    x = torch.from_numpy(orc.scaled_logits_ref(row, temp))[0]
+    probs = torch.softmax(x, -1).numpy()
+    counts = _sample_counts(row, temp, 40000, seed=11)
+    assert _chi2_pvalue(counts, probs) > 1e-4
+
+    def wrong_temperature(lg, t, seed, off):   # planted: T applied twice
+        return orc.sample_scores_ref(lg, t * t, seed, off)
+
+    def wrong_sign(lg, t, seed, off):          # planted: + log2(E) instead of - log2(E)
+        xs = orc.scaled_logits_ref(lg, t)
+        e = -np.log(orc.sample_uniforms_ref(xs.shape[0], xs.shape[1], seed, off))
+        return xs / math.log(2.0) + np.log2(e)
+
+    for planted in (wrong_temperature, wrong_sign):
+        assert _chi2_pvalue(_sample_counts(row, temp, 40000, 11, planted), probs) < 1e-6
+
+
+def test_sampled_choice_equals_torch_multinomial_race():
+    """torch.multinomial(p, 1) is argmax(p / E) with E ~ Exp(1)
+    (aten/src/ATen/native/Distributions.cpp); on the same E the log-space
+    scores choose the same token."""
+    gen = torch.Generator().manual_seed(2)
+    lg = torch.randn(200, 1000, generator=gen).to(torch.bfloat16)
+    temp = 0.7
+    scores = orc.sample_scores_ref(lg, temp, seed=9, offset=4)
+    x = torch.from_numpy(orc.scaled_logits_ref(lg, temp))
+    e = torch.from_numpy(-np.log(orc.sample_uniforms_ref(200, 1000, 9, 4)))
+    race = (torch.softmax(x, -1) / e).argmax(-1)
+    assert torch.equal(race, torch.from_numpy(scores.argmax(-1)))
+
+
+def test_sampled_walk_at_tiny_temperature_is_greedy():
+    gen = torch.Generator().manual_seed(4)
+    tr = dtree.d3_verify_tree(np.random.default_rng(4).uniform(size=15))
+    lg = torch.randn(tr.num_nodes, 500, generator=gen)
+    am = lg.argmax(-1)
+    drafts = torch.randint(0, 500, tr.node_index.shape, generator=gen)
+    drafts[0, 1:] = am[torch.as_tensor(tr.node_index[0, :-1], dtype=torch.long)]
+    greedy = orc.greedy_accept_ref(lg, tr.node_index, drafts)
+    assert orc.sampled_accept_ref(lg, tr.node_index, drafts, 1e-4, seed=1, offset=0) == greedy
+    assert greedy[2] == tr.node_index.shape[1]
+
+
+def test_scaled_logits_follow_torch_gpu_division():
+    """torch divides a GPU tensor by a Python scalar as a multiplication by
+    the fp32 reciprocal; on bf16 logits the product is rounded to bf16."""
+    lg = torch.tensor([[1.0, 3.0, -7.5, 0.1]]).to(torch.bfloat16)
+    x = orc.scaled_logits_ref(lg, 0.3)
+    inv = np.float32(1) / np.float32(0.3)
+    want = (lg.float() * torch.tensor(inv)).to(torch.bfloat16).double().numpy()
+    assert np.array_equal(x, want)
+    assert np.array_equal(x, x.astype(np.float32).astype(np.float64))
+
+
 # ---- QK RMSNorm + RoPE (generation/verification.py:113-123) ----
 
 def test_qk_norm_rope_ref_matches_transformers_qwen3():
