@@ -136,10 +136,14 @@ def cpu_baseline(mp, reps: int, torch, sample: str) -> dict:
             "queries_per_s": nq / (us * 1e-6), "cpu_model": cpu_model(), **th}
 
 
+CAL_BYTES = 1 << 30   # fill / sum calibration buffers: 32x the 32 MiB of L2 over all XCDs
+
+
 def traffic_workload(args) -> int:
-    """The workload the counter runs profile: one plain device copy of
-    COPY_BYTES (calibration) then the attention launch of every layer, each
-    repeated a few times."""
+    """The workload the counter runs profile, per round: a 1 GiB fill
+    (write-only calibration), a 1 GiB sum of another buffer (read-only
+    calibration), a COPY_BYTES device copy, then the attention launch of every
+    layer; three rounds."""
     import torch
     import d2sd
     from d2sd import workloads as wl
@@ -147,6 +151,8 @@ def traffic_workload(args) -> int:
     torch.cuda.set_device(dev)
     src = torch.ones(COPY_BYTES, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
+    wbuf = torch.empty(CAL_BYTES // 4, dtype=torch.float32, device=dev)
+    rbuf = torch.ones(CAL_BYTES // 4, dtype=torch.float32, device=dev)
     prob = wl.config2(args.seed, layers=args.layers)
     mp = wl.materialize(prob, dev)
     attn = d2sd.CascadeVerifyAttention(dev)
@@ -156,12 +162,26 @@ def traffic_workload(args) -> int:
     lse = torch.empty(T, hq, dtype=torch.float32, device=dev)
     torch.cuda.synchronize()
     for _ in range(3):
+        wbuf.fill_(1.5)
+        rbuf.sum()
         dst.copy_(src)
         for lt in mp.layers:
             attn.run_attention(lt.q, lt.k_suffix, lt.v_suffix, lt.k_prefix, lt.v_prefix, out=o, lse=lse)
         torch.cuda.synchronize()
-    print("traffic workload done", flush=True)
+    print(f"traffic workload done: {attn.info.num_slots} partial slots, {attn.info.num_items} items", flush=True)
     return 0
+
+
+def _kernel_class(name: str):
+    if "verify_attn_kernel" in name:
+        return "attention"
+    if "copyBuffer" in name:
+        return "copy"
+    if "FillFunctor" in name:
+        return "fill"
+    if "reduce_kernel" in name:
+        return "sum"
+    return None
 
 
 def _counter_means(csv_path: Path, counter: str) -> dict:
@@ -171,8 +191,7 @@ def _counter_means(csv_path: Path, counter: str) -> dict:
         for row in csv.DictReader(f):
             if row["Counter_Name"] != counter:
                 continue
-            name = row["Kernel_Name"]
-            key = "attention" if "verify_attn_kernel" in name else ("copy" if "copyBuffer" in name else None)
+            key = _kernel_class(row["Kernel_Name"])
             if key is None:
                 continue
             sums[key] = sums.get(key, 0.0) + float(row["Counter_Value"])
@@ -184,19 +203,28 @@ def _pmc_pass(counters, outdir: Path, args, kernel_trace: bool = False):
     """One rocprofv3 counter pass over the traffic workload (a child process);
     returns the directory it wrote, or None after printing the failure."""
     import subprocess
-    cmd = ["rocprofv3", "--pmc", *counters]
+    # each pass in its own process under a hard time limit: a counter set the
+    # hardware cannot collect makes rocprofv3 stop responding
+    cmd = ["timeout", "-s", "KILL", "120", "rocprofv3", "--pmc", *counters]
     if kernel_trace:
         cmd.append("--kernel-trace")
-    cmd += ["--kernel-include-regex", "verify_attn_kernel|copyBuffer",
+    cmd += ["--kernel-include-regex", TRAFFIC_KERNELS,
             "-d", str(outdir), "-o", "run", "--output-format", "csv", "--",
             sys.executable, str(Path(__file__).resolve()), "--traffic-workload",
             "--layers", str(args.layers), "--seed", str(args.seed)]
     log("running " + " ".join(cmd))
-    r = subprocess.run(cmd, timeout=300, capture_output=True, text=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    _PMC_STDOUT.append(r.stdout)
     if r.returncode != 0:
         print(r.stdout[-2000:], r.stderr[-2000:], file=sys.stderr)
         return None
     return outdir
+
+
+_PMC_STDOUT: list = []
+
+
+TRAFFIC_KERNELS = "verify_attn_kernel|copyBuffer|FillFunctor|reduce_kernel"
 
 
 def _attention_mean_ns(trace_csv: Path) -> float:
@@ -241,7 +269,7 @@ def measure_mfma(args) -> int:
         "# MFMA utilisation of the cascade verify attention launch, config 2 (Qwen3-8B, L=4096 paged, 36 layers)",
         f"# command: python bench.py --measure-mfma --layers {args.layers} --seed {args.seed}",
         "#   = rocprofv3 --pmc " + " ".join(MFMA_COUNTERS) + " --kernel-trace",
-        "#     --kernel-include-regex 'verify_attn_kernel|copyBuffer' --output-format csv -- python bench.py --traffic-workload",
+        f"#     --kernel-include-regex '{TRAFFIC_KERNELS}' --output-format csv -- python bench.py --traffic-workload",
         "# counters: mean per attention dispatch; duration: mean kernel-trace duration of the same dispatches",
     ]
     lines += [f"{k}: {v:.0f}" for k, v in c.items()]
@@ -266,50 +294,114 @@ def measure_mfma(args) -> int:
     return 0
 
 
+TRAFFIC_PASSES = (
+    ("FETCH_SIZE",),
+    ("WRITE_SIZE",),
+    ("TCC_EA0_RDREQ_sum", "TCC_EA0_RDREQ_32B_sum", "TCC_EA0_RDREQ_64B_sum", "TCC_EA0_RDREQ_128B_sum"),
+    ("TCC_EA0_WRREQ_sum", "TCC_EA0_WRREQ_64B_sum", "TCC_EA0_RDREQ_DRAM_sum", "TCC_EA0_WRREQ_DRAM_sum"),
+)
+
+
 def measure_traffic(args) -> int:
-    """Two counter runs (FETCH_SIZE, WRITE_SIZE) of the traffic workload as
-    child processes; writes TRAFFIC_FILE."""
-    import subprocess
+    """HBM traffic of the attention launch: four counter passes of the
+    traffic workload (FETCH_SIZE; WRITE_SIZE; the L2-to-fabric read requests
+    by size; write requests), each a child process; writes TRAFFIC_FILE.
+
+    Calibration: the 1 GiB fill writes and the 1 GiB sum reads known bytes
+    with no reuse, so measured / known is what the counters see of a
+    streaming kernel spread over all XCDs; the attention launch's figures are
+    divided by it.  Itemisation: its reads are the unique prefix and suffix
+    K/V, Q, the page table, the tree mask and the plan records, plus re-reads
+    of K/V chunks by the q-tiles that share them; its writes are the partial
+    slots (bf16 [rows, D] + fp32 [rows] each)."""
+    import re
     import tempfile
-    res = {}
+    from d2sd import workloads as wl
+    res, slots_seen = {}, []
     with tempfile.TemporaryDirectory(dir=os.environ.get("TMPDIR", "/tmp")) as tmp:
-        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
-            outdir = Path(tmp) / counter
-            cmd = ["rocprofv3", "--pmc", counter, "--kernel-include-regex", "verify_attn_kernel|copyBuffer",
-                   "-d", str(outdir), "-o", "run", "--output-format", "csv", "--",
-                   sys.executable, str(Path(__file__).resolve()), "--traffic-workload",
-                   "--layers", str(args.layers), "--seed", str(args.seed)]
-            log("running " + " ".join(cmd))
-            r = subprocess.run(cmd, timeout=300, capture_output=True, text=True)
-            if r.returncode != 0:
-                print(r.stdout[-2000:], r.stderr[-2000:], file=sys.stderr)
-                return r.returncode
-            files = list(outdir.rglob("*counter_collection.csv"))
+        for i, counters in enumerate(TRAFFIC_PASSES):
+            out = _pmc_pass(counters, Path(tmp) / f"pass{i}", args)
+            if out is None:
+                return 1
+            m = re.search(r"traffic workload done: (\d+) partial slots, (\d+) items", _PMC_STDOUT[-1])
+            slots_seen.append((int(m.group(1)), int(m.group(2))))
+            files = list(out.rglob("*counter_collection.csv"))
             if not files:
                 print("no counter_collection.csv from rocprofv3", file=sys.stderr)
                 return 1
-            res[counter] = _counter_means(files[0], counter)
-    # FETCH_SIZE / WRITE_SIZE are in KiB per dispatch; the copy kernel reads
-    # and writes COPY_BYTES each
-    fetch_scale = COPY_BYTES / (res["FETCH_SIZE"]["copy"] * 1024.0)
-    write_scale = COPY_BYTES / (res["WRITE_SIZE"]["copy"] * 1024.0)
-    fetch_b = res["FETCH_SIZE"]["attention"] * 1024.0 * fetch_scale
-    write_b = res["WRITE_SIZE"]["attention"] * 1024.0 * write_scale
+            for c in counters:
+                res[c] = _counter_means(files[0], c)
+    prob = wl.config2(args.seed, layers=args.layers)
+    hq, hkv, d, T = prob.num_qo_heads, prob.num_kv_heads, prob.head_dim, prob.total_q
+    L, P = prob.requests[0].prefix_len, prob.page_size
+    ab, _ = wl.attention_launch_bytes_flops(prob)
+    slots, nitems = slots_seen[0]
+    rows = 128
+    items = {
+        "prefix_kv_unique": 2 * L * hkv * d * 2,
+        "suffix_kv": 2 * T * hkv * d * 2,
+        "q": T * hq * d * 2,
+        "page_table": 4 * ((L + P - 1) // P),
+        "tree_mask": T * ((T + 63) // 64) * 8,
+        "plan_items": nitems * 64,
+    }
+    w_items = {"partial_slots": slots * (rows * d * 2 + rows * 4)}
+
+    def hist_reads(k):
+        return (32 * res["TCC_EA0_RDREQ_32B_sum"][k] + 64 * res["TCC_EA0_RDREQ_64B_sum"][k]
+                + 128 * res["TCC_EA0_RDREQ_128B_sum"][k])
+
+    def hist_writes(k):
+        return (32 * (res["TCC_EA0_WRREQ_sum"][k] - res["TCC_EA0_WRREQ_64B_sum"][k])
+                + 64 * res["TCC_EA0_WRREQ_64B_sum"][k])
+
+    read_cov = hist_reads("sum") / CAL_BYTES
+    write_cov = hist_writes("fill") / CAL_BYTES
+    fetch_cov = res["FETCH_SIZE"]["sum"] * 1024 / CAL_BYTES
+    wsize_cov = res["WRITE_SIZE"]["fill"] * 1024 / CAL_BYTES
+    a_reads = hist_reads("attention") / read_cov
+    a_writes = hist_writes("attention") / write_cov
     lines = [
         "# HBM traffic of the cascade verify attention launch, config 2 (Qwen3-8B, L=4096 paged, 36 layers)",
         f"# command: python bench.py --measure-traffic --layers {args.layers} --seed {args.seed}",
-        "#   = rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) --kernel-include-regex 'verify_attn_kernel|copyBuffer'",
-        "#     --output-format csv -- python bench.py --traffic-workload",
-        f"copy_kernel_bytes: {COPY_BYTES}",
-        f"copy_FETCH_SIZE_KiB: {res['FETCH_SIZE']['copy']:.1f}",
-        f"copy_WRITE_SIZE_KiB: {res['WRITE_SIZE']['copy']:.1f}",
-        f"fetch_scale: {fetch_scale:.4f}",
-        f"write_scale: {write_scale:.4f}",
-        f"attention_FETCH_SIZE_KiB_per_dispatch: {res['FETCH_SIZE']['attention']:.1f}",
-        f"attention_WRITE_SIZE_KiB_per_dispatch: {res['WRITE_SIZE']['attention']:.1f}",
-        f"attention_fetch_bytes_per_launch: {fetch_b:.0f}",
-        f"attention_write_bytes_per_launch: {write_b:.0f}",
-        f"traffic_bytes_per_launch: {fetch_b + write_b:.0f}",
+        "#   = four passes, each: timeout -s KILL 120 rocprofv3 --pmc <counters>",
+        f"#     --kernel-include-regex '{TRAFFIC_KERNELS}' --output-format csv -- python bench.py --traffic-workload",
+        "#   passes: " + " | ".join(" ".join(c) for c in TRAFFIC_PASSES),
+        "# per dispatch means; fill = 1 GiB written, sum = 1 GiB read, copy = 256 MiB read + written",
+        "",
+        "## raw counters (requests; FETCH_SIZE / WRITE_SIZE in KiB)",
+    ]
+    for c in ("FETCH_SIZE", "WRITE_SIZE", "TCC_EA0_RDREQ_sum", "TCC_EA0_RDREQ_32B_sum", "TCC_EA0_RDREQ_64B_sum",
+              "TCC_EA0_RDREQ_128B_sum", "TCC_EA0_WRREQ_sum", "TCC_EA0_WRREQ_64B_sum", "TCC_EA0_RDREQ_DRAM_sum",
+              "TCC_EA0_WRREQ_DRAM_sum"):
+        lines.append(f"{c}: " + ", ".join(f"{k} {res[c].get(k, float('nan')):.1f}"
+                                         for k in ("fill", "sum", "copy", "attention")))
+    lines += [
+        "",
+        "## calibration (what the counters see of known bytes)",
+        f"read_request_bytes_over_known (sum kernel): {read_cov:.4f}",
+        f"write_request_bytes_over_known (fill kernel): {write_cov:.4f}",
+        f"FETCH_SIZE_over_known (sum kernel): {fetch_cov:.4f}",
+        f"WRITE_SIZE_over_known (fill kernel): {wsize_cov:.4f}",
+        f"copy_reads_calibrated_over_known: {hist_reads('copy') / read_cov / COPY_BYTES:.4f}",
+        f"copy_writes_calibrated_over_known: {hist_writes('copy') / write_cov / COPY_BYTES:.4f}",
+        "",
+        "## attention launch, calibrated bytes per launch",
+        f"reads: {a_reads:.0f}",
+        f"writes: {a_writes:.0f}",
+        "",
+        "## itemised (bytes per launch)",
+    ]
+    lines += [f"read {k}: {v}" for k, v in items.items()]
+    unique = sum(items.values())
+    lines += [
+        f"read unique total: {unique}  (algorithmic bytes of the launch: {ab})",
+        f"read beyond unique (K/V chunks re-read by q-tiles sharing them): {a_reads - unique:.0f} "
+        f"= {(a_reads - unique) / items['prefix_kv_unique']:.3f} x prefix K/V",
+        f"write partial_slots: {w_items['partial_slots']}  ({slots} slots x ({rows} rows x {d} x 2 + {rows} x 4))",
+        f"writes measured / itemised: {a_writes / w_items['partial_slots']:.3f}",
+        "",
+        f"traffic_bytes_per_launch: {a_reads + a_writes:.0f}",
     ]
     TRAFFIC_FILE.parent.mkdir(exist_ok=True)
     TRAFFIC_FILE.write_text("\n".join(lines) + "\n")
@@ -537,6 +629,193 @@ OTHER_WORKLOADS = {
 }
 
 
+SYSTEM_WORKLOADS = ("dropin", "step")
+
+
+def _events_us(fn, reps: int, torch) -> float:
+    """Mean µs per call of fn() over reps calls, HIP events on the current
+    stream around the whole loop (eager: host dispatch included where it is
+    slower than the GPU)."""
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(s)
+    for _ in range(reps):
+        fn()
+    e1.record(s)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / reps
+
+
+def measure_dropin(args) -> int:
+    """The reference's own per-layer call site after `import d2sd as
+    flashinfer` (generation/verification.py:137-165): at config 2's shape (the
+    d3 tree's 5 rows x 32 positions, Qwen3-8B heads, DynamicCache prefix
+    [Hkv, 4096, D] per layer), the transpose copies of the call site, then
+    d2sd.single_prefill_with_kv_cache over all rows' queries and the
+    CascadeGraphRunner's local attention + merge.  Eager, as the reference runs
+    it; 36 layers of distinct KV so nothing stays in L2."""
+    import numpy as np
+    import torch
+    import d2sd
+    from d2sd import tree as dtree
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    conf = np.random.default_rng(args.seed).uniform(0.0, 1.0, size=15)
+    tr = dtree.d3_verify_tree(conf, block_size=16, block_size_2=32, topk=4)
+    bsz, lb, hq, hkv, d, L, nl = tr.num_rows, tr.row_len, 32, 8, 128, 4096, args.layers
+    gen = torch.Generator(device=dev).manual_seed(args.seed + 1)
+
+    def rnd(*shape):
+        return torch.randn(shape, generator=gen, device=dev).to(torch.bfloat16)
+
+    layers = [dict(q=rnd(bsz, hq, lb, d), k_new=rnd(bsz, hkv, lb, d), v_new=rnd(bsz, hkv, lb, d),
+                   k=rnd(hkv, L, d), v=rnd(hkv, L, d)) for _ in range(nl)]
+    scale = d ** -0.5
+    runner = d2sd.CascadeGraphRunner(lb, hq, hkv, d, torch.bfloat16, dev, scale, causal=True)
+
+    def call_site(x):
+        k_fi = x["k"].transpose(0, 1).contiguous()
+        v_fi = x["v"].transpose(0, 1).contiguous()
+        q_fi = x["q"].transpose(1, 2)
+        q_all = q_fi.reshape(bsz * lb, hq, d)
+        out, lse = d2sd.single_prefill_with_kv_cache(q_all, k_fi, v_fi, causal=False, return_lse=True,
+                                                     sm_scale=scale)
+        out = out.view(bsz, lb, hq, d)
+        lse = lse.view(bsz, lb, hq)
+        runner.run(q_fi.contiguous(), x["k_new"].transpose(1, 2).contiguous(),
+                   x["v_new"].transpose(1, 2).contiguous(), out, lse)
+        return out
+
+    # prepared inputs: the single-prefill and the runner alone
+    prep = [dict(q_all=x["q"].transpose(1, 2).reshape(bsz * lb, hq, d), k_fi=x["k"].transpose(0, 1).contiguous(),
+                 v_fi=x["v"].transpose(0, 1).contiguous(), q_fi=x["q"].transpose(1, 2).contiguous(),
+                 k_new=x["k_new"].transpose(1, 2).contiguous(), v_new=x["v_new"].transpose(1, 2).contiguous())
+            for x in layers]
+    outs = [d2sd.single_prefill_with_kv_cache(x["q_all"], x["k_fi"], x["v_fi"], causal=False, return_lse=True,
+                                              sm_scale=scale) for x in prep]
+    torch.cuda.synchronize()
+
+    def all_layers(fn, xs):
+        def go():
+            for x in xs:
+                fn(x)
+        return go
+
+    for _ in range(3):
+        all_layers(call_site, layers)()
+    reps = max(5, args.kernel_reps // 5)
+    site_us = _events_us(all_layers(call_site, layers), reps, torch) / nl
+    prefill_us = _events_us(all_layers(lambda x: d2sd.single_prefill_with_kv_cache(
+        x["q_all"], x["k_fi"], x["v_fi"], causal=False, return_lse=True, sm_scale=scale), prep), reps, torch) / nl
+    runner_us = _events_us(lambda: [runner.run(x["q_fi"], x["k_new"], x["v_new"], o.view(bsz, lb, hq, d),
+                                               l.view(bsz, lb, hq)) for x, (o, l) in zip(prep, outs)],
+                           reps, torch) / nl
+    print(json.dumps({
+        "workload": "dropin_cfg2_rows_qwen3_8b_L4096_contiguous", "value": site_us, "unit": "us/layer",
+        "higher_is_better": False, "rows": bsz, "row_len": lb, "queries": bsz * lb, "layers": nl,
+        "call_site_us": site_us, "single_prefill_us": prefill_us, "runner_us": runner_us,
+        "note": "eager, as verification.py:137-165 runs it: the call site's transpose copies, "
+                "d2sd.single_prefill_with_kv_cache (outputs and workspace from torch's caching allocator), "
+                "CascadeGraphRunner.run (copies in, one captured local-attention+merge launch, copies out)",
+    }), flush=True)
+    return 0
+
+
+def measure_step(args) -> int:
+    """One whole verify step captured in one HipGraph and replayed as the cache
+    grows: candidate tree built on the device from the draft confidences
+    (d3_generator.py:116-180), 36 layers of dynamic-prefix cascade attention
+    (verification.py:127-176), the acceptance walk over [nodes, 151936] bf16
+    logits (d3_generator.py:204-225) and the commit of the accepted branch into
+    the paged cache of every layer (d3_generator.py:227-232).  Synthetic
+    logits and drafts, so about one token is accepted per step."""
+    import numpy as np
+    import torch
+    import d2sd
+    from d2sd import tree as dtree
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    hq, hkv, d, P, nl, vocab, L0 = 32, 8, 128, 16, args.layers, 151936, 4096
+    builder = dtree.D3TreeBuilder(16, 32, 4, dev)
+    cap, rows, lb = builder.capacity, builder.rows_cap, builder.block_size_2
+    Lmax = L0 + 512
+    npages = (Lmax + P - 1) // P
+    gen = torch.Generator(device=dev).manual_seed(args.seed + 1)
+
+    def rnd(*shape):
+        return torch.randn(shape, generator=gen, device=dev).to(torch.bfloat16)
+
+    kp = [rnd(npages, hkv, P, d) for _ in range(nl)]
+    vp = [rnd(npages, hkv, P, d) for _ in range(nl)]
+    table = torch.randperm(npages, generator=gen, device=dev).to(torch.int32)
+    q = [rnd(cap, hq, d) for _ in range(nl)]
+    ks = [rnd(cap, hkv, d) for _ in range(nl)]
+    vs = [rnd(cap, hkv, d) for _ in range(nl)]
+    out = [torch.empty(cap, hq, d, dtype=torch.bfloat16, device=dev) for _ in range(nl)]
+    lse = [torch.empty(cap, hq, dtype=torch.float32, device=dev) for _ in range(nl)]
+    logits = rnd(cap, vocab)
+    drafts = torch.randint(0, vocab, (rows, lb), generator=gen, device=dev)
+    conf = torch.from_numpy(np.random.default_rng(args.seed).uniform(0.0, 1.0, size=15)).to(torch.bfloat16).to(dev)
+
+    t0 = time.perf_counter()
+    attn = d2sd.CascadeVerifyAttention(dev).plan(
+        [0, cap], [Lmax], hq, hkv, d, tree_masks=[np.eye(cap, dtype=bool)], page_size=P, page_indptr=[0, npages],
+        page_table=table, kv_layout="HND", dynamic_prefix=True)
+    plan_ms = (time.perf_counter() - t0) * 1e3
+    attn.set_prefix_len([L0])
+    acc = d2sd.TreeAccept(cap, vocab, lb, dev, temperature=args.temperature, seed=args.seed)
+    commit = d2sd.PagedKVCommit(kp, vp, ks, vs)
+
+    def tree_part():
+        builder.build(conf, tree_mask=attn.tree_mask_dev)
+
+    def attn_part():
+        for i in range(nl):
+            attn.run(q[i], ks[i], vs[i], kp[i], vp[i], out=out[i], lse=lse[i])
+
+    def accept_part():
+        return acc(logits, builder.node_index, drafts)
+
+    def whole():
+        tree_part()
+        attn_part()
+        _, nodes, res = accept_part()
+        commit.commit(table, attn.prefix_len_dev[0:1], nodes, num_accepted=lb, num_accepted_dev=res, advance=True)
+
+    graphs = {}
+    for key, fn in (("step", whole), ("tree", tree_part), ("attention", attn_part), ("accept", accept_part)):
+        tree_part()
+        torch.cuda.synchronize()
+        graphs[key] = d2sd.HipGraph()
+        with graphs[key].capture():
+            fn()
+    reps = max(10, args.steps // 2)
+    for _ in range(args.warmup):
+        graphs["step"].replay()
+    attn.set_prefix_len([L0])
+    torch.cuda.synchronize()
+    step_us = _events_us(graphs["step"].replay, reps, torch)
+    grown = int(attn.prefix_len_dev[0]) - L0
+    attn.set_prefix_len([L0])
+    parts = {k: _events_us(graphs[k].replay, reps, torch) for k in ("tree", "attention", "accept")}
+    print(json.dumps({
+        "workload": "verify_step_cfg2_qwen3_8b_L4096_paged16_36layers_vocab151936", "value": step_us,
+        "unit": "us/step", "higher_is_better": False, "layers": nl, "tree_capacity": cap,
+        "temperature": args.temperature, "replays": reps, "prefix_growth_tokens": grown,
+        "attention_us_per_layer": parts["attention"] / nl, "tree_build_us": parts["tree"],
+        "accept_us": parts["accept"],
+        "commit_and_rest_us": step_us - parts["tree"] - parts["attention"] - parts["accept"],
+        "plan_ms_dynamic_prefix": plan_ms,
+        "note": "one hipGraph per step, no host work between steps: the prefix length lives on the device and "
+                "the commit advances it; attention planned once for prefix <= %d (a plan for the largest tree)"
+                % Lmax,
+    }), flush=True)
+    return 0
+
+
 def measure_workload(args) -> int:
     """One JSON line per named workload: µs per verify-attention call (attention
     + merge launch), and the attention launch alone against its roofline
@@ -548,6 +827,12 @@ def measure_workload(args) -> int:
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     for name in args.workload.split(","):
+        if name == "dropin":
+            measure_dropin(args)
+            continue
+        if name == "step":
+            measure_step(args)
+            continue
         prob, nl = OTHER_WORKLOADS[name](wl, args.seed)
         log(f"materialising {prob.name} ({nl} KV pools)")
         mp = wl.materialize(prob, dev, layers=nl)
@@ -633,8 +918,9 @@ def main() -> int:
     ap.add_argument("--accept", action="store_true",
                     help="time the greedy acceptance walk instead (one JSON line)")
     ap.add_argument("--workload", default=None,
-                    help="comma-separated: " + ", ".join(OTHER_WORKLOADS) + " (one JSON line each instead of "
-                         "the verify-step line)")
+                    help="comma-separated: " + ", ".join(list(OTHER_WORKLOADS) + list(SYSTEM_WORKLOADS)) +
+                         " (one JSON line each instead of the verify-step line)")
+    ap.add_argument("--temperature", type=float, default=0.0, help="acceptance temperature for --workload step")
     ap.add_argument("--qk-rope", action="store_true",
                     help="time the fused QK RMSNorm + RoPE instead (one JSON line)")
     args = ap.parse_args()
@@ -717,6 +1003,23 @@ def main() -> int:
     merge_us = time_graph(g_merge, args.kernel_reps, torch) * 1000.0 / len(mp.layers)
     log(f"attention kernel {attn_us:.3f} us/launch, merge kernel {merge_us:.3f} us/launch")
 
+    # host work around the step: plan() from scratch, a same-shape re-plan
+    # into the existing device buffers, and issuing one replay of the step
+    def median_us(fn, n):
+        ts = []
+        for _ in range(n):
+            t0 = time.perf_counter()
+            fn()
+            ts.append((time.perf_counter() - t0) * 1e6)
+        return float(sorted(ts)[n // 2])
+
+    plan_us = median_us(lambda: wl.plan_for(d2sd.CascadeVerifyAttention(dev), mp), 11)
+    replan_us = median_us(lambda: wl.plan_for(attn, mp), 11)
+    torch.cuda.synchronize()
+    replay_us = median_us(step.replay, 21)
+    torch.cuda.synchronize()
+    log(f"host: plan {plan_us:.0f} us, same-shape re-plan {replan_us:.0f} us, replay issue {replay_us:.1f} us")
+
     vb, vf = wl.verify_bytes_flops(prob)
     ab, af = wl.attention_launch_bytes_flops(prob)
     # dominant kernel: the attention launch (prefix key chunks + suffix trees),
@@ -766,6 +1069,8 @@ def main() -> int:
         "layer_flops": vf,
         "kernels_us": {"attention": attn_us, "merge": merge_us},
         "roofline": roof,
+        "host_us": {"plan": plan_us, "replan_same_shape": replan_us, "step_replay_issue": replay_us,
+                    "note": "outside the timed region; with a dynamic-prefix plan no host work runs per step"},
     }
     if not args.no_cpu_baseline:
         log("timing the CPU baseline (oracle, fp32 torch sdpa): config 2 layer 0, then config 1")

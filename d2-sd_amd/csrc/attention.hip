@@ -109,63 +109,6 @@ __device__ __forceinline__ void store_row(const AttnParams& p, int req, int q0, 
   if (lrow && hh == 0) *lrow = p.lse_base2 ? lse * kLog2e : lse;
 }
 
-// Merge `nslots` split partials (register image, slots slot0.. of a tile of
-// `prows` rows; this lane's row is `prow` of it) into the lane's state
-// (o, lse); o holds normalised values on entry and on return.
-template <int D>
-__device__ __forceinline__ void merge_partials(const AttnParams& p, int slot0, int nslots, int prows, int prow,
-                                               int lane, f32x16 (&o)[D / 32], float& lse) {
-  const float* lse_base = p.part_lse + (long long)slot0 * prows + prow;
-  float m = lse;
-  for (int s = 0; s < nslots; ++s) m = fmaxf(m, lse_base[(long long)s * prows]);
-  if (m == -INFINITY) return;  // nothing anywhere: o stays 0, lse -inf
-  const float w_own = __expf(lse - m);
-  float wsum = w_own;
-#pragma unroll
-  for (int mt = 0; mt < D / 32; ++mt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[mt][r] *= w_own;
-  const long long slot_elems = (long long)prows * D;
-  const bf16_t* img = (const bf16_t*)p.part_o + (long long)slot0 * slot_elems;
-  const int wave = prow >> 5;
-  // kMergeBatch slots per round, all loads issued before any is consumed
-  // (slots past nslots reload the last one with weight 0).
-  constexpr int kMergeBatch = 4;
-  for (int s0 = 0; s0 < nslots; s0 += kMergeBatch) {
-    u32x2 v[kMergeBatch][D / 32][4];
-    float wt[kMergeBatch];
-#pragma unroll
-    for (int b = 0; b < kMergeBatch; ++b) {
-      const int s = min(s0 + b, nslots - 1);
-      wt[b] = (s0 + b < nslots) ? __expf(lse_base[(long long)s * prows] - m) : 0.f;  // 0 for an empty split
-      const bf16_t* po = img + (long long)s * slot_elems;
-#pragma unroll
-      for (int mt = 0; mt < D / 32; ++mt)
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) v[b][mt][q4] = *(const u32x2*)(po + image_offset<D>(wave, mt, q4, lane));
-    }
-#pragma unroll
-    for (int b = 0; b < kMergeBatch; ++b) {
-#pragma unroll
-      for (int mt = 0; mt < D / 32; ++mt)
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          o[mt][4 * q4] += wt[b] * bf16_lo(v[b][mt][q4][0]);
-          o[mt][4 * q4 + 1] += wt[b] * bf16_hi(v[b][mt][q4][0]);
-          o[mt][4 * q4 + 2] += wt[b] * bf16_lo(v[b][mt][q4][1]);
-          o[mt][4 * q4 + 3] += wt[b] * bf16_hi(v[b][mt][q4][1]);
-        }
-      wsum += wt[b];
-    }
-  }
-  const float inv = 1.f / wsum;
-#pragma unroll
-  for (int mt = 0; mt < D / 32; ++mt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[mt][r] *= inv;
-  lse = m + logf(wsum);
-}
-
 // Epilogue of the attention kernel: normalise the accumulators and write a
 // split partial or the final output, or merge with the stored state first.
 template <int D, int W>
@@ -515,37 +458,90 @@ __global__ __launch_bounds__(64 * W) void attn_dma_kernel(const AttnParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Split-KV merge (single_prefill): one wave per 32 rows of a tile group; the
-// partials are read in their register image, the output written like the
-// attention kernel's FINAL epilogue.
+// Split-KV merge (single_prefill): one single-wave workgroup per (tile group,
+// 32-row block, 32-wide head-dim block mt), so that the partial loads spread
+// over every CU; the partials are read in their register image, a batch of
+// kMergeBatch slots in flight at once, and the output written like the
+// attention kernel's FINAL epilogue (+ the GPT-OSS sink factor).
 // ---------------------------------------------------------------------------
 template <int D>
-__global__ __launch_bounds__(256) void merge_kernel(const AttnParams p, int rows_per_tile) {
+__global__ __launch_bounds__(64) void merge_kernel(const AttnParams p, int rows_per_tile) {
+  constexpr int kMergeBatch = 8;
   const int waves_per_tile = rows_per_tile / 32;
-  const int gwave = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int item_idx = gwave / waves_per_tile;
-  const int wt = gwave % waves_per_tile;
+  const int item_idx = blockIdx.x / waves_per_tile, blk = blockIdx.x % waves_per_tile, mt = blockIdx.y;
   if (item_idx >= p.num_merge) return;
-  const int lane = threadIdx.x & 63, l32 = lane & 31, hh = lane >> 5;
+  const int lane = threadIdx.x, l32 = lane & 31, hh = lane >> 5;
   const int Q = p.imp.qtiles;
   const int qt = item_idx % Q;
   const int rest = item_idx / Q;
   const int kvh = rest % p.num_kv_heads;
   const int req = rest / p.num_kv_heads;
   const int g = p.group;
-  const int nq = p.imp.qo_len;
-  const int row = qt * rows_per_tile + wt * 32 + l32;
-  if (row >= nq * g) return;
-  const int n = row / g, j = row - n * g;
-  const int qh = kvh * g + j;
-  f32x16 o[D / 32];
+  const int row = qt * rows_per_tile + blk * 32 + l32;
+  if (row >= p.imp.qo_len * g) return;
+  const int n = row / g, qh = kvh * g + (row - n * g);
+  const int nslots = p.imp.splits;
+  const long long slot0 = (long long)item_idx * nslots;
+  const long long slot_elems = (long long)rows_per_tile * D;
+
+  float acc[16];
 #pragma unroll
-  for (int mt = 0; mt < D / 32; ++mt)
+  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+  float mval = -INFINITY, wsum = 0.f;
+  for (int s0 = 0; s0 < nslots; s0 += kMergeBatch) {
+    float ls[kMergeBatch];
+    u32x2 v[kMergeBatch][4];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) o[mt][r] = 0.f;
-  float lse = -INFINITY;
-  merge_partials<D>(p, item_idx * p.imp.splits, p.imp.splits, rows_per_tile, wt * 32 + l32, lane, o, lse);
-  store_row<D>(p, req, 0, n, qh, hh, o, 1.f, lse);
+    for (int b = 0; b < kMergeBatch; ++b) {
+      ls[b] = -INFINITY;
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) v[b][q4] = (u32x2){0u, 0u};
+      if (s0 + b < nslots) {
+        const long long s = slot0 + s0 + b;
+        ls[b] = p.part_lse[s * rows_per_tile + blk * 32 + l32];
+        const bf16_t* po = (const bf16_t*)p.part_o + s * slot_elems;
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) v[b][q4] = *(const u32x2*)(po + image_offset<D>(blk, mt, q4, lane));
+      }
+    }
+    float bm = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < kMergeBatch; ++b) bm = fmaxf(bm, ls[b]);
+    const float nm = fmaxf(mval, bm);
+    if (nm == -INFINITY) continue;  // nothing visible so far
+    const float f = (mval == -INFINITY) ? 0.f : __expf(mval - nm);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] *= f;
+    wsum *= f;
+#pragma unroll
+    for (int b = 0; b < kMergeBatch; ++b) {
+      const float wt = (ls[b] == -INFINITY) ? 0.f : __expf(ls[b] - nm);
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        acc[4 * q4] += wt * bf16_lo(v[b][q4][0]);
+        acc[4 * q4 + 1] += wt * bf16_hi(v[b][q4][0]);
+        acc[4 * q4 + 2] += wt * bf16_lo(v[b][q4][1]);
+        acc[4 * q4 + 3] += wt * bf16_hi(v[b][q4][1]);
+      }
+      wsum += wt;
+    }
+    mval = nm;
+  }
+  const bool nonempty = wsum > 0.f;
+  const float lse = nonempty ? mval + logf(wsum) : -INFINITY;
+  float sc = nonempty ? 1.f / wsum : 0.f;
+  if (p.sinks) sc *= nonempty ? 1.f / (1.f + __expf(p.sinks[qh] - lse)) : 0.f;
+  bf16_t* orow = (bf16_t*)p.o + (long long)req * p.o_stride_req + (long long)n * p.o_stride_n +
+                 (long long)qh * p.o_stride_h;
+#pragma unroll
+  for (int q4 = 0; q4 < 4; ++q4)
+    *(u32x2*)(orow + 32 * mt + 8 * q4 + 4 * hh) =
+        (u32x2){pack_bf16x2(acc[4 * q4] * sc, acc[4 * q4 + 1] * sc),
+                pack_bf16x2(acc[4 * q4 + 2] * sc, acc[4 * q4 + 3] * sc)};
+  if (p.lse && mt == 0 && hh == 0) {
+    float* lrow = p.lse + (long long)req * p.lse_stride_req + (long long)n * p.lse_stride_n + qh;
+    *lrow = p.lse_base2 ? lse * kLog2e : lse;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -629,12 +625,11 @@ hipError_t launch_merge(const AttnParams& p, int head_dim, int rows_per_tile, in
   if (nitems <= 0) return hipSuccess;
   AttnParams q = p;
   q.num_merge = nitems;
-  const int waves = nitems * (rows_per_tile / 32);
-  const int blocks = (waves + 3) / 4;
+  const dim3 grid((unsigned)(nitems * (rows_per_tile / 32)), (unsigned)(head_dim / 32));
   if (head_dim == 128)
-    hipLaunchKernelGGL(merge_kernel<128>, dim3(blocks), dim3(256), 0, s, q, rows_per_tile);
+    hipLaunchKernelGGL(merge_kernel<128>, grid, dim3(64), 0, s, q, rows_per_tile);
   else if (head_dim == 64)
-    hipLaunchKernelGGL(merge_kernel<64>, dim3(blocks), dim3(256), 0, s, q, rows_per_tile);
+    hipLaunchKernelGGL(merge_kernel<64>, grid, dim3(64), 0, s, q, rows_per_tile);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
