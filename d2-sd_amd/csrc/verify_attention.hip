@@ -155,13 +155,22 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
   }
   int kv_begin = w.kv_begin, kv_end = w.kv_end;
   if constexpr (!MASKED) {
-    // dynamic plan: the item's key range relative to the window start, at
-    // the run-time prefix length (never beyond the planned length)
+    // dynamic plan: the planned chunks of the span [kv0, plan_len) scaled to
+    // the run-time span [k0, L) (L never beyond the planned length), each
+    // boundary rounded down to a 64-key tile and the last one kept at L, so
+    // the chunks stay contiguous, keep their relative sizes (the plan's
+    // balance over XCDs and CUs) and no workgroup idles on keys past L
     if (p.prefix_len) {
       const int L = min(max(p.prefix_len[w.req], 0), w.plan_len);
-      const int k0 = L - (p.window_left >= 0 ? min(L, p.window_left) : L);
-      kv_begin = k0 + (w.kv_begin - w.kv0);
-      kv_end = min(k0 + (w.kv_end - w.kv0), L);
+      const int span = p.window_left >= 0 ? min(L, p.window_left) : L;
+      const int k0 = L - span;
+      const long long pspan = (long long)w.plan_len - w.kv0;
+      auto scale = [&](int x) -> int {
+        if (pspan <= 0 || x >= pspan) return span;
+        return min(span, (int)(((long long)x * span / pspan) & ~63ll));
+      };
+      kv_begin = k0 + scale(w.kv_begin - w.kv0);
+      kv_end = k0 + scale(w.kv_end - w.kv0);
     }
   }
   const int ntiles = kv_end > kv_begin ? (kv_end - kv_begin + 63) >> 6 : 0;
@@ -835,6 +844,9 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) o[rb][mt] *= inv;
       if (w.mode == MODE_PARTIAL) {
+        // streaming stores: the merge launch reads each partial once, and
+        // lines that leave L2 during the epilogue are not written back at
+        // the kernel's end
         const int blk = RB * wv + rb;
         bf16_t* po = (bf16_t*)p.part_o + (long long)w.slot * ROWS * D;
         float* pl = p.part_lse + (long long)w.slot * ROWS + blk * 32 + l32;
@@ -844,9 +856,9 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
           for (int q4 = 0; q4 < 4; ++q4) {
             const u32x2 val = {pack_bf16x2(o[rb][mt][4 * q4], o[rb][mt][4 * q4 + 1]),
                                pack_bf16x2(o[rb][mt][4 * q4 + 2], o[rb][mt][4 * q4 + 3])};
-            *(u32x2*)(po + image_offset<D>(blk, mt, q4, lane)) = val;
+            __builtin_nontemporal_store(val, (u32x2*)(po + image_offset<D>(blk, mt, q4, lane)));
           }
-        if (hh == 0) *pl = lse_r[rb];
+        if (hh == 0) __builtin_nontemporal_store(lse_r[rb], pl);
       } else if (rv[rb]) {
         store_out<D>(p, w.q0 + n[rb], qh[rb], hh, o[rb], lse_r[rb]);
       }

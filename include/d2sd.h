@@ -161,7 +161,9 @@ int d2sd_graph_destroy(void* graph_exec);
  * of each request from the device array args.prefix_len (clamped to
  * [0, planned length]), so one captured graph replays while the cache grows
  * step by step (the page table must hold the pages of the current length).
- * Chunks past the current length produce empty partial states.
+ * The planned key chunks are scaled to the current span (each boundary
+ * b -> floor(b * span / planned_span) rounded down to 64 keys, the last at the
+ * span's end), so every workgroup keeps its share of the work at any length.
  *
  * Paged page ids are clamped below args.prefix_extent (the pool's page
  * count): an id outside the pool reads a wrong page but never memory outside

@@ -315,6 +315,67 @@ def test_cascade_edges(L, shared, window, waves):
     _check_problem(mp, outs, tag="edge")
 
 
+@pytest.mark.parametrize("paged,window", [(True, -1), (True, 300), (False, -1)])
+def test_dynamic_prefix_at_every_length(paged, window):
+    """One dynamic-prefix plan (planned for prefixes 3000 and 700) run at
+    shorter and ragged lengths, empty included: each request against the
+    oracle at its run-time length (the planned chunks are scaled to it)."""
+    rng = np.random.default_rng(5)
+    reqs = [wl.Request(wl.random_branch_tree(rng, 4, 16), 3000), wl.Request(wl.random_branch_tree(rng, 2, 16), 700)]
+    prob = wl.VerifyProblem("dyn", 32, 8, 128, reqs, page_size=16 if paged else 0, window_left=window, seed=9)
+    mp = wl.materialize(prob, DEV, layers=1)
+    attn = d2sd.CascadeVerifyAttention(DEV)
+    wl.plan_for(attn, mp, dynamic_prefix=True)
+    lt = mp.layers[0]
+    qo = prob.qo_indptr
+    for lens in ([3000, 700], [2999, 1], [1537, 700], [64, 0], [0, 65], [1, 699], [300, 299]):
+        attn.set_prefix_len(lens)
+        o, lse = attn.run(lt.q, lt.k_suffix, lt.v_suffix, lt.k_prefix, lt.v_prefix)
+        torch.cuda.synchronize()
+        for r, L in enumerate(lens):
+            if L == 0:
+                kp = vp = None
+            elif paged:
+                pages = mp.page_table[mp.page_indptr[r]:mp.page_indptr[r + 1]].cpu().tolist()
+                kp = orc.gather_paged(lt.k_prefix.cpu(), pages, L)
+                vp = orc.gather_paged(lt.v_prefix.cpu(), pages, L)
+            else:
+                s = mp.prefix_tok_indptr[r]
+                kp = lt.k_prefix.cpu()[:, s:s + L].transpose(0, 1)
+                vp = lt.v_prefix.cpu()[:, s:s + L].transpose(0, 1)
+            a, b = qo[r], qo[r + 1]
+            o_ref, lse_ref = orc.cascade_tree_ref(lt.q.cpu()[a:b], lt.k_suffix.cpu()[a:b], lt.v_suffix.cpu()[a:b],
+                                                  kp, vp, torch.as_tensor(reqs[r].tree.ancestor_mask()),
+                                                  128 ** -0.5, window)
+            check_close(o[a:b], o_ref, lse[a:b], lse_ref, f"lengths {lens} req {r}")
+
+
+def test_dynamic_prefix_many_requests():
+    """Ten requests (more than the kernel preloads with the work item): each
+    at a ragged run-time length below its planned one, against the oracle."""
+    rng = np.random.default_rng(6)
+    planned = [int(x) for x in rng.integers(100, 600, size=10)]
+    reqs = [wl.Request(wl.random_branch_tree(rng, 2, 8), L) for L in planned]
+    prob = wl.VerifyProblem("dyn10", 32, 8, 128, reqs, page_size=16, seed=10)
+    mp = wl.materialize(prob, DEV, layers=1)
+    attn = d2sd.CascadeVerifyAttention(DEV)
+    wl.plan_for(attn, mp, dynamic_prefix=True)
+    lt = mp.layers[0]
+    qo = prob.qo_indptr
+    lens = [int(rng.integers(0, L + 1)) for L in planned]
+    attn.set_prefix_len(lens)
+    o, lse = attn.run(lt.q, lt.k_suffix, lt.v_suffix, lt.k_prefix, lt.v_prefix)
+    torch.cuda.synchronize()
+    for r, L in enumerate(lens):
+        pages = mp.page_table[mp.page_indptr[r]:mp.page_indptr[r + 1]].cpu().tolist()
+        kp = orc.gather_paged(lt.k_prefix.cpu(), pages, L) if L else None
+        vp = orc.gather_paged(lt.v_prefix.cpu(), pages, L) if L else None
+        a, b = qo[r], qo[r + 1]
+        o_ref, lse_ref = orc.cascade_tree_ref(lt.q.cpu()[a:b], lt.k_suffix.cpu()[a:b], lt.v_suffix.cpu()[a:b],
+                                              kp, vp, torch.as_tensor(reqs[r].tree.ancestor_mask()), 128 ** -0.5)
+        check_close(o[a:b], o_ref, lse[a:b], lse_ref, f"req {r} length {L} of {planned[r]}")
+
+
 def test_split_count_does_not_change_result():
     """Split-KV merge == unsplit (size-independent property at full size)."""
     prob = wl.config2(3, layers=1)
