@@ -302,6 +302,64 @@ TRAFFIC_PASSES = (
 )
 
 
+MIX_FILE = ROOT / "profiles" / "verify_attn_cfg2_instmix.txt"
+MIX_PASSES = (
+    ("SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_LDS", "SQ_INSTS_SALU", "SQ_INSTS_VALU_TRANS_F32",
+     "SQ_ACTIVE_INST_VALU", "SQ_VALU_MFMA_COEXEC_CYCLES", "SQ_WAIT_INST_LDS"),
+    ("SQ_ACTIVE_INST_LDS", "SQ_ACTIVE_INST_ANY", "SQ_WAIT_ANY", "SQ_WAIT_INST_ANY", "SQ_BUSY_CYCLES",
+     "SQ_INSTS_VALU_CVT", "SQ_THREAD_CYCLES_VALU", "SQ_INSTS_SMEM"),
+)
+
+
+def measure_mix(args) -> int:
+    """Instruction mix of the attention launch: two rocprofv3 passes of SQ
+    counters over the traffic workload; writes MIX_FILE.  Per wave-tile
+    figures divide by the launch's prefix wave-tiles (items x waves x 64-key
+    tiles of their ranges; the suffix items' few tiles are left out)."""
+    import tempfile
+    from d2sd import workloads as wl
+    res = {}
+    with tempfile.TemporaryDirectory(dir=os.environ.get("TMPDIR", "/tmp")) as tmp:
+        for i, counters in enumerate(MIX_PASSES):
+            out = _pmc_pass(counters, Path(tmp) / f"mix{i}", args)
+            if out is None:
+                return 1
+            files = list(out.rglob("*counter_collection.csv"))
+            if not files:
+                print("no counter_collection.csv from rocprofv3", file=sys.stderr)
+                return 1
+            for c in counters:
+                res[c] = _counter_means(files[0], c)["attention"]
+    prob = wl.config2(args.seed, layers=args.layers)
+    hkv, T, L = prob.num_kv_heads, prob.total_q, prob.requests[0].prefix_len
+    qtiles = (T * prob.num_qo_heads // hkv + 127) // 128
+    wave_tiles = hkv * qtiles * (L // 64) * 4
+    valu = res["SQ_INSTS_VALU"] - res["SQ_INSTS_MFMA"]
+    lines = [
+        "# Instruction mix of the cascade verify attention launch, config 2 (Qwen3-8B, L=4096 paged, 36 layers)",
+        f"# command: python bench.py --measure-mix --layers {args.layers} --seed {args.seed}",
+        "#   = two passes, each: timeout -s KILL 120 rocprofv3 --pmc <counters>",
+        f"#     --kernel-include-regex '{TRAFFIC_KERNELS}' --output-format csv -- python bench.py --traffic-workload",
+        "#   passes: " + " | ".join(" ".join(c) for c in MIX_PASSES),
+        "# mean per attention dispatch",
+    ]
+    lines += [f"{k}: {v:.0f}" for k, v in res.items()]
+    lines += [
+        "",
+        f"prefix_wave_tiles (8 kv heads x {qtiles} q-tiles x {L // 64} tiles x 4 waves): {wave_tiles}",
+        f"mfma_per_wave_tile: {res['SQ_INSTS_MFMA'] / wave_tiles:.1f}",
+        f"valu_non_mfma_per_wave_tile: {valu / wave_tiles:.1f}  (includes the per-item prologue and epilogue)",
+        f"trans_per_wave_tile: {res['SQ_INSTS_VALU_TRANS_F32'] / wave_tiles:.1f}",
+        f"lds_per_wave_tile: {res['SQ_INSTS_LDS'] / wave_tiles:.1f}",
+        f"salu_per_wave_tile: {res['SQ_INSTS_SALU'] / wave_tiles:.1f}",
+        f"valu_per_mfma: {valu / res['SQ_INSTS_MFMA']:.2f}",
+    ]
+    MIX_FILE.parent.mkdir(exist_ok=True)
+    MIX_FILE.write_text("\n".join(lines) + "\n")
+    print("\n".join(lines))
+    return 0
+
+
 def measure_traffic(args) -> int:
     """HBM traffic of the attention launch: four counter passes of the
     traffic workload (FETCH_SIZE; WRITE_SIZE; the L2-to-fabric read requests
@@ -910,6 +968,8 @@ def main() -> int:
     ap.add_argument("--measure-traffic", action="store_true",
                     help="run the two rocprofv3 counter passes and write the traffic summary")
     ap.add_argument("--traffic-workload", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--measure-mix", action="store_true",
+                    help="run two rocprofv3 passes of SQ instruction counters and write the instruction-mix summary")
     ap.add_argument("--measure-mfma", action="store_true",
                     help="run one rocprofv3 pass of the SQ MFMA counters and write the utilisation summary")
     ap.add_argument("--commit", action="store_true",
@@ -938,6 +998,8 @@ def main() -> int:
         return measure_traffic(args)
     if args.measure_mfma:
         return measure_mfma(args)
+    if args.measure_mix:
+        return measure_mix(args)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: every path here runs on a single MI355X "
               "(multi-GPU sharding is a design note, not a measured configuration).", file=sys.stderr)

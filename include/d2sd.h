@@ -167,7 +167,8 @@ int d2sd_graph_destroy(void* graph_exec);
  *
  * Paged page ids are clamped below args.prefix_extent (the pool's page
  * count): an id outside the pool reads a wrong page but never memory outside
- * the pool.
+ * the pool.  Q, K and V must be NaN-free (the kernels are built without NaN
+ * semantics); the result of a NaN input is undefined but stays in bounds.
  * ---------------------------------------------------------------------- */
 typedef struct {
   int num_reqs;
