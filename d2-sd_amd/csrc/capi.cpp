@@ -665,6 +665,10 @@ int d2sd_paged_kv_append(const d2sd_kv_append_args* a, d2sd_stream_t stream) {
   if (a->page_table_len <= 0) return fail(D2SD_ERR_INVALID_ARG, "paged_kv_append: empty page_table");
   if (a->advance_prefix && !a->prefix_len_dev)
     return fail(D2SD_ERR_INVALID_ARG, "paged_kv_append: advance_prefix needs prefix_len_dev");
+  if (a->pool_dtype != D2SD_KV_BF16 && a->pool_dtype != D2SD_KV_FP8_E4M3)
+    return fail(D2SD_ERR_INVALID_ARG, "paged_kv_append: pool_dtype must be D2SD_KV_BF16 or D2SD_KV_FP8_E4M3");
+  if (a->pool_dtype == D2SD_KV_FP8_E4M3 && (!a->k_scale || !a->v_scale))
+    return fail(D2SD_ERR_INVALID_ARG, "paged_kv_append: fp8 pools need k_scale and v_scale");
   d2sd::KvAppendParams p{};
   p.node_ids = a->node_ids;
   p.page_table = a->page_table;
@@ -690,6 +694,9 @@ int d2sd_paged_kv_append(const d2sd_kv_append_args* a, d2sd_stream_t stream) {
   p.num_accepted_dev = a->num_accepted_dev;
   p.prefix_len_dev = a->prefix_len_dev;
   p.page_table_len = a->page_table_len;
+  p.pool_dtype = a->pool_dtype == D2SD_KV_FP8_E4M3 ? d2sd::KV_FP8 : d2sd::KV_BF16;
+  p.k_scale = a->k_scale;
+  p.v_scale = a->v_scale;
   hipError_t e = d2sd::launch_kv_append(p, a->advance_prefix != 0, (hipStream_t)stream);
   return e == hipSuccess ? D2SD_OK : fail_hip(e, "paged_kv_append launch");
 }

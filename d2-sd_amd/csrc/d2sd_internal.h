@@ -181,6 +181,9 @@ struct KvAppendParams {
   const int* num_accepted_dev;  // nullable: the count is read here (clamped to [0, num_accepted])
   int* prefix_len_dev;          // nullable: the cache length is read here
   int page_table_len;           // entries of page_table (device lengths are range-checked against it)
+  int pool_dtype;               // KV_BF16 or KV_FP8 (e4m3fn bytes, value / scale)
+  const uint64_t* k_scale;      // KV_FP8: [num_layers] addresses of fp32 [Hkv]
+  const uint64_t* v_scale;
 };
 
 // ---------------------------------------------------------------------------

@@ -10,7 +10,13 @@
 // Work: block (i, layer) copies accepted token i of one layer: K and V rows of
 // Hkv x D bf16 (2 KB each at Hkv 8, D 128), 16 bytes per lane.  Pure data
 // movement, HBM bound: 2 * num_accepted * Hkv * D * 2 bytes read and written
-// per layer.
+// per layer (half the writes into fp8 pools).
+//
+// fp8 pools (OCP e4m3fn bytes holding value / scale[head], the format the
+// cascade kernels dequantise): each value becomes e4m3fn(x / scale), the
+// quotient correctly rounded in fp32, clamped to +-448 (the largest finite
+// e4m3fn) and rounded to nearest even - torch's float -> float8_e4m3fn cast
+// after a clamp (the cast alone turns |q| >= 480 into NaN).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -18,6 +24,24 @@
 #include "plan.h"
 
 namespace d2sd {
+
+// e4m3fn byte of f, |f| <= 448: round to nearest even.  Below 2^-6 the
+// format is subnormal with step 2^-9 (f * 512 rounded; 8 is the smallest
+// normal, byte 0x08); above, the exponent is rebiased from 127 to 7 and the
+// 20 dropped mantissa bits are rounded half to even.
+__device__ __forceinline__ unsigned e4m3fn_byte(float f) {
+  unsigned u = __float_as_uint(f);
+  const unsigned sign = (u >> 24) & 0x80u;
+  u &= 0x7FFFFFFFu;
+  unsigned r;
+  if (u < 0x3C800000u) {
+    r = (unsigned)rintf(__uint_as_float(u) * 512.f);
+  } else {
+    u = u - 0x3C000000u + 0x7FFFFu + ((u >> 20) & 1u);
+    r = u >> 20;
+  }
+  return r | sign;
+}
 
 __global__ __launch_bounds__(256) void kv_append_kernel(const KvAppendParams p) {
   const int i = blockIdx.x, layer = blockIdx.y;
@@ -35,8 +59,9 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const KvAppendParams p) 
   const int nch = p.num_kv_heads * cpr;
   const uint16_t* knew = (const uint16_t*)p.k_new[layer];
   const uint16_t* vnew = (const uint16_t*)p.v_new[layer];
-  uint16_t* kpool = (uint16_t*)p.k_pool[layer];
-  uint16_t* vpool = (uint16_t*)p.v_pool[layer];
+  const bool fp8 = p.pool_dtype == KV_FP8;
+  const float* kscale = fp8 ? (const float*)p.k_scale[layer] : nullptr;
+  const float* vscale = fp8 ? (const float*)p.v_scale[layer] : nullptr;
   for (int c = threadIdx.x; c < 2 * nch; c += blockDim.x) {
     const bool is_v = c >= nch;
     const int cc = is_v ? c - nch : c;
@@ -45,7 +70,23 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const KvAppendParams p) 
     const long long dst = (long long)page * p.pool_stride_page + (long long)h * p.pool_stride_head +
                           (long long)slot * p.pool_stride_tok + d;
     const uint4 val = *(const uint4*)((is_v ? vnew : knew) + src);
-    *(uint4*)((is_v ? vpool : kpool) + dst) = val;
+    if (fp8) {
+      // 8 values -> 8 e4m3fn bytes
+      const float s = (is_v ? vscale : kscale)[h];
+      const unsigned w[4] = {val.x, val.y, val.z, val.w};
+      unsigned b[2] = {0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const unsigned bits = (w[e >> 1] >> (16 * (e & 1))) << 16;
+        const float q = fminf(fmaxf(__fdiv_rn(__uint_as_float(bits & 0xFFFF0000u), s), -448.f), 448.f);
+        b[e >> 2] |= e4m3fn_byte(q) << (8 * (e & 3));
+      }
+      uint8_t* pool = (uint8_t*)(is_v ? p.v_pool[layer] : p.k_pool[layer]);
+      *(uint2*)(pool + dst) = uint2{b[0], b[1]};
+    } else {
+      uint16_t* pool = (uint16_t*)(is_v ? p.v_pool[layer] : p.k_pool[layer]);
+      *(uint4*)(pool + dst) = val;
+    }
   }
 }
 

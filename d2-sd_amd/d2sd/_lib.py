@@ -152,6 +152,9 @@ class KvAppendArgs(C.Structure):
         ("num_accepted_dev", C.c_void_p),
         ("prefix_len_dev", C.c_void_p),
         ("advance_prefix", C.c_int),
+        ("pool_dtype", C.c_int),
+        ("k_scale", C.c_void_p),
+        ("v_scale", C.c_void_p),
     ]
 
 

@@ -10,6 +10,11 @@ i.e. copies the whole cache.  Here the accepted branch's tokens (their tree
 node rows of each layer's suffix K/V, in order) are written in place into the
 pages that follow the prefix, for all layers in one launch; the prefix stays
 put, so page tables and hipGraphs stay valid across steps.
+
+Pools may also hold fp8 (torch.float8_e4m3fn) with per-layer, per-kv-head
+fp32 scales (the cascade kernels' fp8 format, value / scale): the new bf16
+rows are quantised on the way in, as clamp(x / scale, -448, 448) cast to
+e4m3fn with round-to-nearest-even.
 """
 from __future__ import annotations
 
@@ -35,24 +40,29 @@ def _layout_strides(pool: torch.Tensor, kv_layout: str):
 class PagedKVCommit:
     """Commits accepted tree nodes of every layer into paged K/V pools.
 
-    k_pools / v_pools: per layer a bf16 page pool ([pages, Hkv, P, D] for
-    kv_layout "HND", [pages, P, Hkv, D] for "NHD"); k_new / v_new: per layer the
-    step's suffix K/V, bf16 [rows, Hkv, D] (the tree nodes, as passed to
-    CascadeVerifyAttention.run).  All layers share shapes and strides.  The
+    k_pools / v_pools: per layer a bf16 or float8_e4m3fn page pool
+    ([pages, Hkv, P, D] for kv_layout "HND", [pages, P, Hkv, D] for "NHD");
+    k_new / v_new: per layer the step's suffix K/V, bf16 [rows, Hkv, D] (the
+    tree nodes, as passed to CascadeVerifyAttention.run).  fp8 pools need
+    k_scales / v_scales: per layer fp32 [Hkv] (or one tensor for every layer).
+    All layers share shapes and strides.  The
     per-layer addresses are kept in device arrays built here once, so that
     commit() allocates nothing and may be captured into a hipGraph (the
     tensors must stay alive and in place).
     """
 
     def __init__(self, k_pools: Sequence[torch.Tensor], v_pools: Sequence[torch.Tensor],
-                 k_new: Sequence[torch.Tensor], v_new: Sequence[torch.Tensor], kv_layout: str = "HND"):
+                 k_new: Sequence[torch.Tensor], v_new: Sequence[torch.Tensor], kv_layout: str = "HND",
+                 k_scales=None, v_scales=None):
         n = len(k_pools)
         if not (n == len(v_pools) == len(k_new) == len(v_new)) or n == 0:
             raise ValueError("one k/v pool and one k/v new tensor per layer are required")
         ref_pool, ref_new = k_pools[0], k_new[0]
+        if ref_pool.dtype not in (torch.bfloat16, torch.float8_e4m3fn):
+            raise TypeError("pools must be bf16 or float8_e4m3fn")
         for t in list(k_pools) + list(v_pools):
-            if t.dtype != torch.bfloat16 or t.shape != ref_pool.shape or t.stride() != ref_pool.stride():
-                raise ValueError("pools must be bf16 with one shape and stride for all layers")
+            if t.dtype != ref_pool.dtype or t.shape != ref_pool.shape or t.stride() != ref_pool.stride():
+                raise ValueError("pools must share one dtype, shape and stride for all layers")
             if t.stride(-1) != 1 or t.device != ref_pool.device:
                 raise ValueError("pools must have a contiguous head_dim on one device")
         for t in list(k_new) + list(v_new):
@@ -67,6 +77,24 @@ class PagedKVCommit:
         as_addr = lambda ts: torch.tensor([t.data_ptr() for t in ts], dtype=torch.int64, device=dev)
         self._addr = [as_addr(k_new), as_addr(v_new), as_addr(k_pools), as_addr(v_pools)]
         self._keep = (list(k_pools), list(v_pools), list(k_new), list(v_new))
+        fp8 = ref_pool.dtype == torch.float8_e4m3fn
+        if fp8:
+            if k_scales is None or v_scales is None:
+                raise ValueError("float8_e4m3fn pools need k_scales and v_scales")
+
+            def per_layer(s):
+                ts = [s] * n if isinstance(s, torch.Tensor) else list(s)
+                if len(ts) != n:
+                    raise ValueError("one scale tensor per layer (or one for all layers)")
+                for x in ts:
+                    if x.dtype != torch.float32 or x.numel() != hkv or not x.is_contiguous() or x.device != dev:
+                        raise ValueError("scales must be contiguous fp32 [Hkv] tensors on the pools' device")
+                return ts
+            ks, vs = per_layer(k_scales), per_layer(v_scales)
+            self._addr += [as_addr(ks), as_addr(vs)]
+            self._keep += (ks, vs)
+        elif k_scales is not None or v_scales is not None:
+            raise ValueError("scales apply to float8_e4m3fn pools only")
         a = _lib.KvAppendArgs()
         a.num_layers = n
         a.num_kv_heads = hkv
@@ -74,9 +102,12 @@ class PagedKVCommit:
         a.page_size = page_size
         a.num_rows = ref_new.shape[0]
         a.pool_pages = ref_pool.shape[0]
-        a.k_new, a.v_new, a.k_pool, a.v_pool = (t.data_ptr() for t in self._addr)
+        a.k_new, a.v_new, a.k_pool, a.v_pool = (t.data_ptr() for t in self._addr[:4])
         a.new_stride_n, a.new_stride_h = ref_new.stride(0), ref_new.stride(1)
         a.pool_stride_page, a.pool_stride_head, a.pool_stride_tok = sp, sh, st
+        if fp8:
+            a.pool_dtype = _lib.D2SD_KV_FP8_E4M3
+            a.k_scale, a.v_scale = self._addr[4].data_ptr(), self._addr[5].data_ptr()
         self._args = a
         self.page_size = page_size
 

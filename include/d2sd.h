@@ -288,8 +288,13 @@ int d2sd_cascade_run_noalloc(const d2sd_cascade_plan_info* info, const d2sd_casc
  * With prefix_len_dev the length lives on the device and may advance there,
  * so one captured commit replays step after step.
  * Node ids outside [0, num_rows) and page ids outside [0, pool_pages) are
- * skipped (nothing written).  bf16 pools only; strides in elements must be
- * multiples of 8 and every address 16-byte aligned.  No allocation, no host
+ * skipped (nothing written).  Pools are bf16, or (pool_dtype =
+ * D2SD_KV_FP8_E4M3) e4m3fn bytes holding value / scale[kv head], the format
+ * d2sd_cascade_run reads: each new bf16 value x is stored as
+ * e4m3fn(clamp(x / scale, -448, 448)), the quotient correctly rounded in fp32
+ * and the byte rounded to nearest even (torch's float8_e4m3fn cast after the
+ * clamp).  Strides in elements must be multiples of 8, new rows 16-byte and
+ * pool rows 16-byte (bf16) or 8-byte (fp8) aligned.  No allocation, no host
  * synchronisation (capturable).
  * ---------------------------------------------------------------------- */
 typedef struct {
@@ -319,6 +324,9 @@ typedef struct {
                                 reaches page_table_len are skipped */
   int advance_prefix;        /* with prefix_len_dev: a second launch then adds the
                                 accepted count to *prefix_len_dev */
+  int pool_dtype;            /* D2SD_KV_BF16 (0) or D2SD_KV_FP8_E4M3 */
+  const uint64_t* k_scale;   /* fp8 pools: device [num_layers] addresses of fp32 [num_kv_heads] */
+  const uint64_t* v_scale;
 } d2sd_kv_append_args;
 
 int d2sd_paged_kv_append(const d2sd_kv_append_args* args, d2sd_stream_t stream);

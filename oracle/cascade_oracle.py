@@ -17,6 +17,7 @@ It restates the reference's verify-attention algorithm on the CPU in float64
   verification.py:127-176 as a whole (row layout)  cascade_verify_rows_ref
   the same over unique tree nodes, single pass     cascade_tree_ref
   d3_generator.py:227-232 (accepted-branch commit) commit_accepted_ref
+  the same into an fp8 e4m3fn pool                  quantize_e4m3fn_ref
   d3_generator.py:204-225 (greedy acceptance walk) greedy_accept_ref
   d3_generator.py:204-225 at temperature > 0 (model/utils.py:34-37,
   torch.multinomial's exponential race)            sample_scores_ref, sampled_accept_ref
@@ -240,13 +241,24 @@ def gather_paged(pool: Tensor, page_table: List[int], length: int, layout: str =
     return flat[:length]
 
 
+def quantize_e4m3fn_ref(x: Tensor, scale: Tensor) -> Tensor:
+    """bf16 values [.., Hkv, D] into an fp8 pool's format: x / scale[head] in
+    fp32, clamped to the largest finite e4m3fn (448), then torch's
+    float -> float8_e4m3fn cast (round to nearest even)."""
+    q = x.float() / scale.float()[:, None]
+    return q.clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+
+
 def commit_accepted_ref(pool: Tensor, page_table: List[int], prefix_len: int, new: Tensor,
-                        node_ids: List[int], layout: str = "HND") -> Tensor:
+                        node_ids: List[int], layout: str = "HND", scale: Optional[Tensor] = None) -> Tensor:
     """Accepted-branch commit (generation/d3_generator.py:227-232): the cache
     grows by the accepted row's tokens, here the tree nodes node_ids of `new`
     ([rows, Hkv, D]) in order, at positions prefix_len .. prefix_len + n - 1 of
     the paged pool.  Returns a new pool; nodes outside [0, rows) are skipped
-    (nothing written), as by the kernel."""
+    (nothing written), as by the kernel.  An fp8 pool stores
+    quantize_e4m3fn_ref(row, scale) (scale: fp32 [Hkv])."""
+    if pool.dtype == torch.float8_e4m3fn:
+        new = quantize_e4m3fn_ref(new, scale)
     out = pool.clone()
     P = pool.shape[2] if layout == "HND" else pool.shape[1]
     for i, node in enumerate(node_ids):
@@ -390,7 +402,7 @@ def sampled_accept_ref(node_logits: Tensor, node_index, draft_ids, temperature: 
 __all__ = [
     "attention_ref", "attention_sdpa_ref", "causal_mask", "single_prefill_ref", "merge_state_ref",
     "sink_rescale_ref", "window_prefix_ref", "cascade_verify_rows_ref", "cascade_tree_ref",
-    "ancestor_mask_from_rows", "fp8_dequant_ref", "gather_paged", "commit_accepted_ref",
+    "ancestor_mask_from_rows", "fp8_dequant_ref", "gather_paged", "commit_accepted_ref", "quantize_e4m3fn_ref",
     "greedy_accept_ref", "qk_norm_rope_ref", "philox4x32_10", "sample_uniforms_ref", "scaled_logits_ref",
     "sample_scores_ref", "sampled_accept_ref",
 ]

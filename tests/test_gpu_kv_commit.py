@@ -101,3 +101,105 @@ def test_commit_replays_in_a_graph():
         torch.cuda.synchronize()
         for l in range(layers):
             assert torch.equal(kpd[l].cpu(), ref[l]), f"replay {rep} layer {l}"
+
+
+# ---- fp8 e4m3fn pools (the cascade kernels' fp8 format, value / scale) ----
+
+def _every_finite_bf16(rows, hkv, d):
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16)
+    x = bits.view(torch.bfloat16)
+    x = torch.where(torch.isfinite(x), x, torch.zeros_like(x))
+    return x.view(rows, hkv, d)
+
+
+def test_fp8_commit_quantises_every_bf16_value_like_the_oracle():
+    """All 65536 bf16 bit patterns (non-finite ones as 0) committed into an
+    fp8 pool, kv head 0 at scale 1 (the cast alone) and head 1 at 0.37 (the
+    fp32 quotient first): every byte equals the oracle's."""
+    hkv, d, P = 2, 128, 16
+    rows = 65536 // (hkv * d)
+    new = _every_finite_bf16(rows, hkv, d)
+    pages = rows // P
+    g = torch.Generator().manual_seed(3)
+    pool = (torch.randn(pages + 2, hkv, P, d, generator=g)).to(torch.float8_e4m3fn)
+    scale = torch.tensor([1.0, 0.37], dtype=torch.float32)
+    table = torch.randperm(pages + 2, generator=g)[:pages].to(torch.int32)
+    nodes = torch.arange(rows, dtype=torch.int32)
+    exp = orc.commit_accepted_ref(pool, table.tolist(), 0, new, nodes.tolist(), "HND", scale)
+    kpd, vpd = pool.to(DEV), pool.clone().to(DEV)
+    c = d2sd.PagedKVCommit([kpd], [vpd], [new.to(DEV)], [new.to(DEV)], k_scales=scale.to(DEV),
+                           v_scales=scale.to(DEV))
+    c.commit(table.to(DEV), 0, nodes.to(DEV))
+    torch.cuda.synchronize()
+    for name, got in (("K", kpd), ("V", vpd)):
+        diff = (got.cpu().view(torch.uint8) != exp.view(torch.uint8))
+        assert not diff.any(), f"{name}: {int(diff.sum())} bytes differ"
+
+
+@pytest.mark.parametrize("layout", ["HND", "NHD"])
+def test_fp8_commit_matches_oracle_with_per_layer_scales(layout):
+    layers, P, hkv, d, L, n, rows = 3, 16, 8, 128, 37, 21, 40
+    pages_needed = (L + n + P - 1) // P
+    pool_pages = pages_needed + 4
+    g, kp, vp, kn, vn = _setup(layers, pool_pages, P, hkv, d, rows, layout, seed=5)
+    kp = [t.to(torch.float8_e4m3fn) for t in kp]
+    vp = [t.to(torch.float8_e4m3fn) for t in vp]
+    ks = [torch.rand(hkv, generator=g) * 0.02 + 0.001 for _ in range(layers)]   # large quotients saturate
+    vs = [torch.rand(hkv, generator=g) * 0.5 + 0.01 for _ in range(layers)]
+    table = torch.randperm(pool_pages, generator=g)[:pages_needed].to(torch.int32)
+    nodes = torch.randint(0, rows, (n,), generator=g, dtype=torch.int32)
+    exp_k = [orc.commit_accepted_ref(kp[l], table.tolist(), L, kn[l], nodes.tolist(), layout, ks[l]) for l in range(layers)]
+    exp_v = [orc.commit_accepted_ref(vp[l], table.tolist(), L, vn[l], nodes.tolist(), layout, vs[l]) for l in range(layers)]
+    kpd = [t.to(DEV) for t in kp]
+    vpd = [t.to(DEV) for t in vp]
+    c = d2sd.PagedKVCommit(kpd, vpd, [t.to(DEV) for t in kn], [t.to(DEV) for t in vn], kv_layout=layout,
+                           k_scales=[s.to(DEV) for s in ks], v_scales=[s.to(DEV) for s in vs])
+    c.commit(table.to(DEV), L, nodes.to(DEV))
+    torch.cuda.synchronize()
+    for l in range(layers):
+        assert torch.equal(kpd[l].cpu().view(torch.uint8), exp_k[l].view(torch.uint8)), f"layer {l} K"
+        assert torch.equal(vpd[l].cpu().view(torch.uint8), exp_v[l].view(torch.uint8)), f"layer {l} V"
+
+
+def test_fp8_commit_then_cascade_reads_it_back():
+    """Qwen3-32B heads (64/8, D 128) over an fp8 paged prefix with per-kv-head
+    scales: commit an accepted branch of a d3 tree into the fp8 pool, then run
+    the next step's cascade attention over the grown prefix; the result
+    matches the oracle on the dequantised pool (the commit writes the format
+    the attention reads)."""
+    hq, hkv, d, P, L0 = 64, 8, 128, 16, 300
+    tr = dtree.d3_verify_tree(np.random.default_rng(2).uniform(size=15))
+    N = tr.num_nodes
+    n = 20
+    pages = (L0 + n + P - 1) // P
+    g = torch.Generator().manual_seed(11)
+    kf = torch.randn(pages + 3, hkv, P, d, generator=g)
+    vf = torch.randn(pages + 3, hkv, P, d, generator=g)
+    ks = (kf.abs().amax(dim=(0, 2, 3)) / 448.0).float()
+    vs = (vf.abs().amax(dim=(0, 2, 3)) / 448.0).float()
+    kpool = (kf / ks[None, :, None, None]).to(torch.float8_e4m3fn).to(DEV)
+    vpool = (vf / vs[None, :, None, None]).to(torch.float8_e4m3fn).to(DEV)
+    table = torch.randperm(pages + 3, generator=g)[:pages].to(torch.int32).to(DEV)
+    kn = torch.randn(N, hkv, d, generator=g).to(torch.bfloat16).to(DEV)
+    vn = torch.randn(N, hkv, d, generator=g).to(torch.bfloat16).to(DEV)
+    nodes = torch.as_tensor(tr.node_index[1, :n], dtype=torch.int32, device=DEV)
+    c = d2sd.PagedKVCommit([kpool], [vpool], [kn], [vn], k_scales=ks.to(DEV), v_scales=vs.to(DEV))
+    c.commit(table, L0, nodes)
+    L = L0 + n
+    q = torch.randn(N, hq, d, generator=g).to(torch.bfloat16).to(DEV)
+    ks2 = torch.randn(N, hkv, d, generator=g).to(torch.bfloat16).to(DEV)
+    vs2 = torch.randn(N, hkv, d, generator=g).to(torch.bfloat16).to(DEV)
+    attn = d2sd.CascadeVerifyAttention(DEV).plan(
+        [0, N], [L], hq, hkv, d, tree_masks=[tr.ancestor_mask()], page_size=P, page_indptr=[0, pages],
+        page_table=table, kv_layout="HND", kv_dtype=torch.float8_e4m3fn, k_scale=ks.to(DEV), v_scale=vs.to(DEV))
+    o, lse = attn.run(q, ks2, vs2, kpool, vpool)
+    torch.cuda.synchronize()
+    pl = table.cpu().tolist()
+    kp = orc.gather_paged(kpool.cpu(), pl, L).float() * ks[None, :, None]
+    vp = orc.gather_paged(vpool.cpu(), pl, L).float() * vs[None, :, None]
+    # the committed rows read back as the quantised new rows
+    assert torch.equal(kp[L0:], orc.quantize_e4m3fn_ref(kn.cpu()[nodes.cpu().long()], ks).float() * ks[None, :, None])
+    o_ref, lse_ref = orc.cascade_tree_ref(q.cpu(), ks2.cpu(), vs2.cpu(), kp, vp, torch.as_tensor(tr.ancestor_mask()),
+                                          d ** -0.5)
+    from test_gpu_parity import check_close
+    check_close(o, o_ref, lse, lse_ref, "fp8 commit then cascade")

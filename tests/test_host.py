@@ -296,12 +296,29 @@ def _kv_args(**kw):
 
 @pytest.mark.parametrize("bad", [dict(page_size=12), dict(head_dim=100), dict(num_rows=0), dict(k_pool=None),
                                  dict(new_stride_h=100), dict(prefix_len=-1), dict(page_table_len=6),
-                                 dict(pool_stride_tok=0)])
+                                 dict(pool_stride_tok=0), dict(pool_dtype=2), dict(pool_dtype=1),
+                                 dict(pool_dtype=1, k_scale=8)])
 def test_kv_append_rejects_bad_arguments(bad):
     """Argument checks of d2sd_paged_kv_append happen before any GPU work."""
     rc = _lib.lib.d2sd_paged_kv_append(C.byref(_kv_args(**bad)), None)
     assert rc == 1, _lib.lib.d2sd_last_error()            # D2SD_ERR_INVALID_ARG
     assert _lib.lib.d2sd_last_error().startswith(b"paged_kv_append")
+
+
+def test_commit_rejects_scales_and_dtypes_on_the_host():
+    import d2sd
+    pool = torch.zeros(4, 2, 16, 8, dtype=torch.float8_e4m3fn)
+    new = torch.zeros(3, 2, 8, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):   # fp8 pools need scales
+        d2sd.PagedKVCommit([pool], [pool], [new], [new])
+    with pytest.raises(ValueError):   # scales of the wrong size
+        d2sd.PagedKVCommit([pool], [pool], [new], [new], k_scales=torch.ones(3), v_scales=torch.ones(2))
+    with pytest.raises(ValueError):   # scales with bf16 pools
+        b = torch.zeros(4, 2, 16, 8, dtype=torch.bfloat16)
+        d2sd.PagedKVCommit([b], [b], [new], [new], k_scales=torch.ones(2), v_scales=torch.ones(2))
+    with pytest.raises(TypeError):
+        f = torch.zeros(4, 2, 16, 8, dtype=torch.float16)
+        d2sd.PagedKVCommit([f], [f], [new], [new])
 
 
 def test_kv_append_with_nothing_to_append_launches_nothing():

@@ -407,6 +407,33 @@ def test_commit_known_answer_and_skipped_nodes():
     assert out[1, 0, 1, 0] == 0. and out[0, 0, 0, 0] == 20. and out.sum() == 20.
 
 
+def test_fp8_quantiser_is_round_to_nearest_even_with_clamp():
+    """quantize_e4m3fn_ref against brute force over every finite bf16 value:
+    the nearest of the 253 finite e4m3fn values to clamp(x, +-448), ties to
+    the even mantissa; and each e4m3fn value maps to itself."""
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    vals = codes.view(torch.float8_e4m3fn).float()
+    fin = torch.isfinite(vals)
+    grid = vals[fin].double().numpy()
+    grid_codes = codes[fin].numpy()
+    # each finite e4m3fn value maps to itself
+    back = orc.quantize_e4m3fn_ref(vals[fin].view(1, -1, 1), torch.ones(1)).view(torch.uint8).flatten()
+    assert torch.equal(back.float(), vals[fin].to(torch.float8_e4m3fn).view(torch.uint8).float())
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    x = bits[torch.isfinite(bits)]
+    got = orc.quantize_e4m3fn_ref(x.view(1, -1, 1), torch.ones(1)).view(-1).float().double().numpy()
+    xc = np.clip(x.double().numpy(), -448.0, 448.0)
+    dist = np.abs(xc[:, None] - grid[None, :])
+    best = dist.min(1)
+    cand = dist <= best[:, None]
+    # among equidistant candidates the even mantissa (code & 1 == 0), +0 for zero
+    pick = np.where(cand & ((grid_codes[None, :] & 1) == 0), 1, 0) * 2 + cand
+    want = grid[pick.argmax(1)]
+    zero = xc == 0
+    assert np.array_equal(got[~zero], want[~zero])
+    assert np.all(got[zero] == 0)
+
+
 # ---- greedy acceptance walk (generation/d3_generator.py:204-225) ----
 
 def _chain_logits(tokens_per_node, vocab=11):
