@@ -1,13 +1,16 @@
 // extern "C" entry points of libd2sd.so (declared in include/d2sd.h).
 // Argument validation, work planning and kernel launches; no device memory is
-// allocated here except the executable of a captured graph.
+// allocated here except the executable of a captured graph and the cached
+// device plans of the single-prefill drop-in (a few tens of KB per shape).
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
+#include <array>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -67,6 +70,15 @@ int check_heads(int hq, int hkv, int d) {
 
 extern "C" {
 
+static size_t single_cascade_workspace(int qo_len, int kv_len, int num_qo_heads, int num_kv_heads, int head_dim,
+                                       int window_left);
+static int single_prefill_cascade(const void* q, int64_t q_stride_n, int64_t q_stride_h, const void* k,
+                                  const void* v, int64_t kv_stride_n, int64_t kv_stride_h, void* o,
+                                  int64_t o_stride_n, int64_t o_stride_h, float* lse, int qo_len, int kv_len,
+                                  int num_qo_heads, int num_kv_heads, int head_dim, int causal, float sm_scale,
+                                  int lse_base2, void* workspace, size_t workspace_bytes, hipStream_t stream,
+                                  bool* used);
+
 const char* d2sd_last_error(void) { return g_last_error.c_str(); }
 
 const char* d2sd_version(void) { return "d2sd-mi355x 0.1.0 (gfx950)"; }
@@ -97,7 +109,7 @@ size_t d2sd_single_prefill_workspace_size(int qo_len, int kv_len, int num_qo_hea
   size_t ws = 0;
   d2sd::plan_single(qo_len, kv_len, num_qo_heads, num_kv_heads, head_dim, window_left, device_num_cus(), imp,
                     waves, ws);
-  return ws;
+  return std::max(ws, single_cascade_workspace(qo_len, kv_len, num_qo_heads, num_kv_heads, head_dim, window_left));
 }
 
 int d2sd_single_prefill_with_kv_cache(const void* q, int64_t q_stride_n, int64_t q_stride_h, const void* k,
@@ -117,6 +129,15 @@ int d2sd_single_prefill_with_kv_cache(const void* q, int64_t q_stride_n, int64_t
       !stride_ok(o_stride_h))
     return fail(D2SD_ERR_INVALID_ARG, "single_prefill: tensors must be 16-byte aligned with strides % 8 == 0");
   if (!(sm_scale > 0.f) || !std::isfinite(sm_scale)) return fail(D2SD_ERR_INVALID_ARG, "single_prefill: bad sm_scale");
+
+  // the cascade kernels when the shape maps onto them (see single_prefill_cascade)
+  bool used = false;
+  if (int rc = single_prefill_cascade(q, q_stride_n, q_stride_h, k, v, kv_stride_n, kv_stride_h, o, o_stride_n,
+                                      o_stride_h, lse, qo_len, kv_len, num_qo_heads, num_kv_heads, head_dim,
+                                      window_left >= 0 ? -1 : causal, sm_scale, lse_base2, workspace,
+                                      workspace_bytes, (hipStream_t)stream, &used))
+    return rc;
+  if (used) return D2SD_OK;
 
   d2sd::AttnParams p{};
   int waves = 0;
@@ -438,6 +459,155 @@ static int build_verify_params(const d2sd_cascade_plan_info* info, const d2sd_ca
   p.mask_words = a->mask_words;
   p.lse_base2 = a->lse_base2;
   p.num_merges = info->num_merges;
+  return D2SD_OK;
+}
+
+// ---------------------------------------------------------------------------
+// single_prefill_with_kv_cache on the cascade kernels.  With qo_len <= kv_len
+// and no window, a single prefill is a one-request cascade: the first
+// kv_len - qo_len keys are a contiguous prefix every query sees, the last
+// qo_len keys the suffix level, fully visible (non-causal) or a chain
+// (causal: query i sees suffix keys 0..i, FlashInfer's bottom-right
+// alignment).  The plan is a dynamic-prefix plan for the largest prefix of a
+// 512-key bucket of kv_len, cached per (device, qo_len, bucket, heads,
+// head_dim), and the kernel takes the current prefix length as an argument,
+// so a cache that grows step by step reuses one plan per bucket.  The first
+// call of a shape plans and uploads (hipMalloc, hipMemcpy); under stream
+// capture, past kSinglePlanCap cached shapes, or for shapes the cascade form
+// does not cover, the caller falls back to the single-source kernels.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int kSingleBucket = 512;
+constexpr size_t kSinglePlanCap = 512;
+
+struct SinglePlan {
+  d2sd_cascade_plan_info info;
+  int32_t* plan_dev;
+};
+
+std::mutex g_single_mu;
+std::map<std::array<int, 6>, SinglePlan> g_single_plans;
+
+bool single_cascade_applies(int qo_len, int kv_len, int window_left) {
+  return window_left < 0 && qo_len > 0 && qo_len <= kv_len && kv_len <= INT32_MAX - kSingleBucket;
+}
+
+// Plans the cascade form on the host; false if it does not apply.
+bool single_cascade_plan(int qo_len, int kv_len, int hq, int hkv, int d, d2sd_cascade_plan_info* info,
+                         std::vector<int32_t>* host) {
+  const int bucket = (kv_len + kSingleBucket - 1) / kSingleBucket * kSingleBucket;
+  int32_t qo_indptr[2] = {0, qo_len}, prefix_len[1] = {bucket - qo_len}, tok0[1] = {0};
+  d2sd_cascade_plan_desc desc{};
+  desc.num_reqs = 1;
+  desc.qo_indptr = qo_indptr;
+  desc.prefix_len = prefix_len;
+  desc.prefix_tok_indptr = tok0;
+  desc.num_qo_heads = hq;
+  desc.num_kv_heads = hkv;
+  desc.head_dim = d;
+  desc.window_left = -1;
+  desc.kv_dtype = D2SD_KV_BF16;
+  desc.page_size = 0;
+  desc.dynamic_prefix = 1;
+  const std::string saved = g_last_error;
+  bool ok = d2sd_cascade_plan(&desc, nullptr, 0, info) == D2SD_OK;
+  if (ok && host) {
+    host->assign((size_t)info->plan_ints, 0);
+    ok = d2sd_cascade_plan(&desc, host->data(), host->size(), info) == D2SD_OK;
+  }
+  g_last_error = saved;
+  return ok;
+}
+
+}  // namespace
+
+static size_t single_cascade_workspace(int qo_len, int kv_len, int hq, int hkv, int d, int window_left) {
+  if (!single_cascade_applies(qo_len, kv_len, window_left)) return 0;
+  d2sd_cascade_plan_info info{};
+  return single_cascade_plan(qo_len, kv_len, hq, hkv, d, &info, nullptr) ? info.workspace_bytes : 0;
+}
+
+static int single_prefill_cascade(const void* q, int64_t q_stride_n, int64_t q_stride_h, const void* k,
+                                  const void* v, int64_t kv_stride_n, int64_t kv_stride_h, void* o,
+                                  int64_t o_stride_n, int64_t o_stride_h, float* lse, int qo_len, int kv_len,
+                                  int hq, int hkv, int d, int causal, float sm_scale, int lse_base2,
+                                  void* workspace, size_t workspace_bytes, hipStream_t stream, bool* used) {
+  *used = false;
+  if (causal < 0 || !single_cascade_applies(qo_len, kv_len, -1)) return D2SD_OK;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return D2SD_OK;
+  }
+  const int bucket = (kv_len + kSingleBucket - 1) / kSingleBucket * kSingleBucket;
+  const std::array<int, 6> key = {dev, qo_len, bucket, hq, hkv, d};
+  SinglePlan sp{};
+  {
+    std::lock_guard<std::mutex> lk(g_single_mu);
+    auto it = g_single_plans.find(key);
+    if (it != g_single_plans.end()) {
+      sp = it->second;
+    } else {
+      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+      if (hipStreamIsCapturing(stream, &cs) != hipSuccess) {
+        (void)hipGetLastError();
+        return D2SD_OK;
+      }
+      if (cs != hipStreamCaptureStatusNone || g_single_plans.size() >= kSinglePlanCap) return D2SD_OK;
+      std::vector<int32_t> host;
+      if (!single_cascade_plan(qo_len, kv_len, hq, hkv, d, &sp.info, &host)) return D2SD_OK;
+      if (hipMalloc((void**)&sp.plan_dev, host.size() * sizeof(int32_t)) != hipSuccess) {
+        (void)hipGetLastError();
+        return D2SD_OK;
+      }
+      if (hipError_t e = hipMemcpy(sp.plan_dev, host.data(), host.size() * sizeof(int32_t), hipMemcpyHostToDevice)) {
+        (void)hipFree(sp.plan_dev);
+        return fail_hip(e, "single_prefill: plan upload");
+      }
+      g_single_plans.emplace(key, sp);
+    }
+  }
+  if (sp.info.workspace_bytes > workspace_bytes || (sp.info.workspace_bytes > 0 && !workspace))
+    return fail(D2SD_ERR_WORKSPACE, "single_prefill: workspace too small (need " +
+                                        std::to_string(sp.info.workspace_bytes) + " bytes)");
+  const int L = kv_len - qo_len;
+  d2sd_cascade_run_args a{};
+  a.plan = sp.plan_dev;
+  a.q = q;
+  a.q_stride_n = q_stride_n;
+  a.q_stride_h = q_stride_h;
+  a.k_suffix = (const char*)k + (size_t)L * (size_t)kv_stride_n * 2;
+  a.v_suffix = (const char*)v + (size_t)L * (size_t)kv_stride_n * 2;
+  a.suffix_stride_n = kv_stride_n;
+  a.suffix_stride_h = kv_stride_h;
+  a.mask_mode = causal ? D2SD_MASK_CAUSAL : D2SD_MASK_NONE;
+  a.k_prefix = k;
+  a.v_prefix = v;
+  a.prefix_stride_tok = kv_stride_n;
+  a.prefix_stride_head = kv_stride_h;
+  // the planned extent is the bucket's; the kernels read only the first L keys
+  a.prefix_extent = sp.info.prefix_extent;
+  a.prefix_len = sp.plan_dev;  // (a dynamic plan needs the field; the value below is used instead)
+  a.out = o;
+  a.o_stride_n = o_stride_n;
+  a.o_stride_h = o_stride_h;
+  a.lse = lse;
+  a.lse_stride_n = hq;
+  a.sm_scale = sm_scale;
+  a.lse_base2 = lse_base2;
+  a.workspace = workspace;
+  a.workspace_bytes = workspace_bytes;
+  d2sd::VerifyParams p{};
+  if (int rc = build_verify_params(&sp.info, &a, p)) return rc;
+  p.prefix_len = nullptr;
+  p.prefix_len_set = 1;
+  p.prefix_len_value = L;
+  hipError_t e = d2sd::launch_verify_attention(p, d, sp.info.waves_per_block, false, false, sp.info.num_items, stream);
+  if (e != hipSuccess) return fail_hip(e, "single_prefill attention launch");
+  e = d2sd::launch_verify_merge(p, d, sp.info.rows_per_tile, sp.info.num_merges, stream);
+  if (e != hipSuccess) return fail_hip(e, "single_prefill merge launch");
+  *used = true;
   return D2SD_OK;
 }
 

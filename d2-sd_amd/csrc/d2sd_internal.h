@@ -152,6 +152,8 @@ struct VerifyParams {
   int lse_base2;
   int num_merges;
   int window_left;         // dynamic plans: the visible window (-1: whole prefix)
+  int prefix_len_set;      // dynamic single-request plans: the current prefix length is
+  int prefix_len_value;    //   prefix_len_value (a kernel argument) instead of prefix_len[0]
 };
 
 // Prefix key chunks per group are capped so that one merge batch holds all

@@ -160,8 +160,8 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
     // boundary rounded down to a 64-key tile and the last one kept at L, so
     // the chunks stay contiguous, keep their relative sizes (the plan's
     // balance over XCDs and CUs) and no workgroup idles on keys past L
-    if (p.prefix_len) {
-      const int L = min(max(p.prefix_len[w.req], 0), w.plan_len);
+    if (p.prefix_len || p.prefix_len_set) {
+      const int L = min(max(p.prefix_len_set ? p.prefix_len_value : p.prefix_len[w.req], 0), w.plan_len);
       const int span = p.window_left >= 0 ? min(L, p.window_left) : L;
       const int k0 = L - span;
       const long long pspan = (long long)w.plan_len - w.kv0;

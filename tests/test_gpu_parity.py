@@ -92,6 +92,26 @@ def test_single_prefill(qo, kv, hq, hkv, d, causal, layout):
     check_close(o, o_ref, lse, lse_ref, f"single_prefill {qo}x{kv}")
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_single_prefill_as_the_cache_grows(causal):
+    """The reference's call site with a cache that grows every step
+    (verification.py:145 at kv_len = prefix + accepted tokens): one plan per
+    512-key bucket serves every length in it; each call against the oracle,
+    across a bucket edge and at qo_len == kv_len."""
+    hq, hkv, d, qo = 32, 8, 128, 96
+    gen = torch.Generator().manual_seed(5 + causal)
+    q = bf16_randn(gen, qo, hq, d)
+    kmax = 1600
+    k, v = bf16_randn(gen, kmax, hkv, d), bf16_randn(gen, kmax, hkv, d)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    for kv in (1000, 1001, 1023, 1024, 1025, 1536, 1537, 96, 600):
+        o, lse = d2sd.single_prefill_with_kv_cache(qd, kd[:kv], vd[:kv], causal=causal, sm_scale=d ** -0.5,
+                                                   return_lse=True)
+        torch.cuda.synchronize()
+        o_ref, lse_ref = orc.single_prefill_ref(q, k[:kv], v[:kv], causal, d ** -0.5)
+        check_close(o, o_ref, lse, lse_ref, f"kv {kv}")
+
+
 def test_single_prefill_strided_q():
     """q as the transposed view the reference builds (verification.py:142-144)."""
     gen = torch.Generator().manual_seed(11)
