@@ -775,8 +775,9 @@ def measure_dropin(args) -> int:
         "higher_is_better": False, "rows": bsz, "row_len": lb, "queries": bsz * lb, "layers": nl,
         "call_site_us": site_us, "single_prefill_us": prefill_us, "runner_us": runner_us,
         "note": "eager, as verification.py:137-165 runs it: the call site's transpose copies, "
-                "d2sd.single_prefill_with_kv_cache (outputs and workspace from torch's caching allocator), "
-                "CascadeGraphRunner.run (copies in, one captured local-attention+merge launch, copies out)",
+                "d2sd.single_prefill_with_kv_cache (cascade kernels, a cached plan per 512-key bucket; outputs "
+                "and workspace from torch's caching allocator), CascadeGraphRunner.run (one fused local-attention "
+                "+ merge launch on the caller's tensors)",
     }), flush=True)
     return 0
 

@@ -1,12 +1,17 @@
 """CascadeGraphRunner — drop-in for model/cascade_graph.py:5-112.
 
 Same constructor, `_capture(bsz)` and `run(q, k, v, out_shared, lse_shared)`
-contract as the reference: per bsz, static buffers + a captured graph of the
-local (per-row) attention and its merge into the shared-prefix state; `run`
-copies inputs in, replays and copies the merged `out_shared` and `lse_shared`
-back (cascade_graph.py:100-112).  The captured body is ONE fused kernel
-launch (local attention of every row + merge_state epilogue) instead of
-2*bsz FlashInfer launches (cascade_graph.py:52-60).
+contract as the reference: after `run(q, k, v, out_shared, lse_shared)` the
+caller's out_shared / lse_shared hold the shared-prefix state merged with
+every row's local (causal) attention (cascade_graph.py:100-112).  The work is
+ONE fused kernel launch (local attention of every row + merge_state
+epilogue) instead of 2*bsz FlashInfer launches (cascade_graph.py:52-60), so
+`run` launches it directly on the caller's tensors: the reference's graph
+exists to amortise those 2*bsz launches, and its five copies into static
+buffers and two copies back would cost more than the kernel.  With
+staged=True (or inputs the fused kernel cannot read in place) `run` keeps the
+reference's form: per bsz static buffers and a captured graph
+(`_capture(bsz)`), copies in, replay, copies out.
 """
 from __future__ import annotations
 
@@ -30,6 +35,7 @@ class CascadeGraphRunner:
         sm_scale: float,
         causal: bool,
         sinks: Optional[torch.Tensor] = None,
+        staged: bool = False,
     ):
         if dtype != torch.bfloat16:
             raise TypeError("CascadeGraphRunner supports bfloat16")
@@ -45,6 +51,7 @@ class CascadeGraphRunner:
         # (generation/verification.py:173-176); None keeps the reference
         # runner's behaviour (no sink inside the runner).
         self.sinks = sinks.to(device=self.device, dtype=torch.float32).contiguous() if sinks is not None else None
+        self.staged = bool(staged)
         self._graphs: Dict[int, HipGraph] = {}
         self._buffers: Dict[int, Dict[str, torch.Tensor]] = {}
 
@@ -78,6 +85,9 @@ class CascadeGraphRunner:
         """q_local [bsz, Lb, Hq, D], k/v_local [bsz, Lb, Hkv, D],
         out_shared [bsz, Lb, Hq, D] and lse_shared [bsz, Lb, Hq] (in/out).
         After return out_shared / lse_shared hold the merged state."""
+        if not self.staged and self._direct_ok(q_local, k_local, v_local, out_shared, lse_shared):
+            self.run_direct(q_local, k_local, v_local, out_shared, lse_shared)
+            return
         bsz = q_local.shape[0]
         if bsz not in self._graphs:
             self._capture(bsz)
@@ -90,6 +100,20 @@ class CascadeGraphRunner:
         self._graphs[bsz].replay()
         out_shared.copy_(bufs["out_shared"])
         lse_shared.copy_(bufs["lse_shared"])
+
+    @staticmethod
+    def _direct_ok(q, k, v, out, lse) -> bool:
+        # what the fused kernel reads in place: contiguous head_dim, K and V
+        # with one set of strides, heads of the LSE contiguous, 16-byte
+        # aligned rows
+        if q.dim() != 4 or k.dim() != 4 or out.shape != q.shape or k.shape != v.shape:
+            return False
+        if q.stride(-1) != 1 or k.stride(-1) != 1 or out.stride(-1) != 1 or k.stride() != v.stride():
+            return False
+        if lse.dtype != torch.float32 or lse.stride(-1) != 1:
+            return False
+        ts = (q, k, v, out)
+        return all(t.data_ptr() % 16 == 0 and all(s % 8 == 0 for s in t.stride()[:-1]) for t in ts)
 
     def run_direct(self, q_local: torch.Tensor, k_local: torch.Tensor, v_local: torch.Tensor,
                    out_shared: torch.Tensor, lse_shared: torch.Tensor) -> None:

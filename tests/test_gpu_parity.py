@@ -156,6 +156,17 @@ def test_reference_row_flow(bsz, causal, with_sinks):
     runner.run_direct(qd, kl.to(DEV), vl.to(DEV), o2, l2)
     torch.cuda.synchronize()
     assert torch.equal(o2, o_sh) and torch.equal(l2, lse_sh)
+    # the reference's staged form (static buffers, captured graph, copies)
+    # gives the same numbers too
+    staged = d2sd.CascadeGraphRunner(lb, hq, hkv, d, torch.bfloat16, torch.device(DEV), d ** -0.5, causal,
+                                     sinks=sinks, staged=True)
+    o3, l3 = d2sd.single_prefill_with_kv_cache(qd.reshape(bsz * lb, hq, d), kp.to(DEV), vp.to(DEV),
+                                               causal=False, return_lse=True, sm_scale=d ** -0.5)
+    o3, l3 = o3.view(bsz, lb, hq, d), l3.view(bsz, lb, hq)
+    staged.run(qd, kl.to(DEV), vl.to(DEV), o3, l3)
+    torch.cuda.synchronize()
+    assert torch.equal(o3, o_sh) and torch.equal(l3, lse_sh)
+    assert bsz in staged._graphs and not runner._graphs
 
 
 # --------------------------------------------------- cascade plan / run
