@@ -22,12 +22,20 @@ O_MAX, O_MEAN, LSE_MAX = 2e-2, 2e-3, 1e-3
 DEV = "cuda"
 
 
-def check_close(o, o_ref, lse=None, lse_ref=None, tag=""):
+def check_close(o, o_ref, lse=None, lse_ref=None, tag="", o_rel=0.0):
+    """The stated tolerances: bf16 O max-abs <= 2e-2 and mean <= 2e-3, fp32
+    LSE <= 1e-3.  o_rel > 0 (stress inputs outside N(0,1) only) widens the
+    max bound element-wise by o_rel * |O_ref|: the bf16 rounding of a partial
+    state and of the output can each move a value by up to 2^-8 of itself."""
     o = o.detach().float().cpu().double()
     o_ref = o_ref.double()
     err = (o - o_ref).abs()
     assert torch.isfinite(o).all(), f"{tag}: non-finite output"
-    assert err.max().item() <= O_MAX, f"{tag}: O max err {err.max().item():.3e}"
+    if o_rel > 0:
+        over = err - o_rel * o_ref.abs()
+        assert over.max().item() <= O_MAX, f"{tag}: O err beyond 2e-2 + {o_rel:g}|O|: {over.max().item():.3e}"
+    else:
+        assert err.max().item() <= O_MAX, f"{tag}: O max err {err.max().item():.3e}"
     assert err.mean().item() <= O_MEAN, f"{tag}: O mean err {err.mean().item():.3e}"
     if lse is not None:
         lse = lse.detach().cpu().double()
@@ -209,7 +217,7 @@ def _oracle_request(mp, li, r, dtype=torch.float64):
                                 prob.head_dim ** -0.5, prob.window_left, sinks, dtype=dtype)
 
 
-def _check_problem(mp, outs, reqs=None, layers=None, dtype=torch.float64, tag=""):
+def _check_problem(mp, outs, reqs=None, layers=None, dtype=torch.float64, tag="", o_rel=0.0):
     prob = mp.problem
     qo = prob.qo_indptr
     for li in (layers if layers is not None else range(len(outs))):
@@ -217,7 +225,7 @@ def _check_problem(mp, outs, reqs=None, layers=None, dtype=torch.float64, tag=""
         for r in (reqs if reqs is not None else range(len(prob.requests))):
             o_ref, lse_ref = _oracle_request(mp, li, r, dtype)
             a, b = qo[r], qo[r + 1]
-            check_close(o[a:b], o_ref, lse[a:b], lse_ref, f"{tag} layer {li} req {r}")
+            check_close(o[a:b], o_ref, lse[a:b], lse_ref, f"{tag} layer {li} req {r}", o_rel=o_rel)
 
 
 def test_cascade_golden_d64(golden):
@@ -405,6 +413,48 @@ def test_dynamic_prefix_many_requests():
         o_ref, lse_ref = orc.cascade_tree_ref(lt.q.cpu()[a:b], lt.k_suffix.cpu()[a:b], lt.v_suffix.cpu()[a:b],
                                               kp, vp, torch.as_tensor(reqs[r].tree.ancestor_mask()), 128 ** -0.5)
         check_close(o[a:b], o_ref, lse[a:b], lse_ref, f"req {r} length {L} of {planned[r]}")
+
+
+@pytest.mark.parametrize("qscale", [8.0, 0.01])
+def test_cascade_extreme_score_scales(qscale):
+    """Config 2's tree over a 4096-key paged prefix with Q scaled so that
+    the scores are very sharp (std ~8 in natural units: one key per row
+    carries nearly all the weight, the running max grows in large steps) or
+    nearly flat; against the oracle.  Sharp rows copy one value row (|O| up
+    to ~4.5), where two bf16 roundings alone reach 2e-2, so the max bound is
+    2e-2 + 2^-7 |O| (twice the bf16 half-ulp of |O|); mean and LSE bounds are
+    the stated ones."""
+    prob = wl.config2(6, layers=1)
+    mp = wl.materialize(prob, DEV, layers=1)
+    lt = mp.layers[0]
+    lt.q.copy_((lt.q.float() * qscale).to(torch.bfloat16))
+    attn = d2sd.CascadeVerifyAttention(DEV)
+    wl.plan_for(attn, mp)
+    o, lse = attn.run(lt.q, lt.k_suffix, lt.v_suffix, lt.k_prefix, lt.v_prefix)
+    torch.cuda.synchronize()
+    _check_problem(mp, [(o, lse)], tag=f"q x {qscale}", o_rel=2.0 ** -7)
+
+
+def test_cascade_one_dominating_prefix_key():
+    """Every row of kv head 0 sees one prefix key (in the last chunk) whose
+    score is 60 above the rest, other heads unchanged: the weight moves to a
+    late split, whose partial must dominate the merge."""
+    prob = wl.config2(7, layers=1)
+    mp = wl.materialize(prob, DEV, layers=1)
+    lt = mp.layers[0]
+    hq, hkv, d = prob.num_qo_heads, prob.num_kv_heads, prob.head_dim
+    g = hq // hkv
+    key_tok = 4000
+    pages = mp.page_table.cpu().tolist()
+    page, slot = pages[key_tok // prob.page_size], key_tok % prob.page_size
+    qdir = lt.q[:, :g].float().mean(dim=(0, 1))
+    kvec = qdir / qdir.norm() * (60.0 * d ** 0.5 / max(lt.q[:, :g].float().norm(dim=-1).mean().item(), 1e-3))
+    lt.k_prefix[page, 0, slot] = kvec.to(torch.bfloat16)
+    attn = d2sd.CascadeVerifyAttention(DEV)
+    wl.plan_for(attn, mp)
+    o, lse = attn.run(lt.q, lt.k_suffix, lt.v_suffix, lt.k_prefix, lt.v_prefix)
+    torch.cuda.synchronize()
+    _check_problem(mp, [(o, lse)], tag="dominating key", o_rel=2.0 ** -7)
 
 
 def test_split_count_does_not_change_result():
