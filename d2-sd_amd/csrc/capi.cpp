@@ -487,7 +487,8 @@ struct SinglePlan {
 };
 
 std::mutex g_single_mu;
-std::map<std::array<int, 6>, SinglePlan> g_single_plans;
+std::map<std::array<int, 6>, SinglePlan> g_single_plans;      // uploaded plans
+std::map<std::array<int, 6>, size_t> g_single_workspace;     // workspace sizes (host planning only)
 
 bool single_cascade_applies(int qo_len, int kv_len, int window_left) {
   return window_left < 0 && qo_len > 0 && qo_len <= kv_len && kv_len <= INT32_MAX - kSingleBucket;
@@ -524,8 +525,17 @@ bool single_cascade_plan(int qo_len, int kv_len, int hq, int hkv, int d, d2sd_ca
 
 static size_t single_cascade_workspace(int qo_len, int kv_len, int hq, int hkv, int d, int window_left) {
   if (!single_cascade_applies(qo_len, kv_len, window_left)) return 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) (void)hipGetLastError();
+  const int bucket = (kv_len + kSingleBucket - 1) / kSingleBucket * kSingleBucket;
+  const std::array<int, 6> key = {dev, qo_len, bucket, hq, hkv, d};
+  std::lock_guard<std::mutex> lk(g_single_mu);
+  auto it = g_single_workspace.find(key);
+  if (it != g_single_workspace.end()) return it->second;
   d2sd_cascade_plan_info info{};
-  return single_cascade_plan(qo_len, kv_len, hq, hkv, d, &info, nullptr) ? info.workspace_bytes : 0;
+  const size_t ws = single_cascade_plan(qo_len, kv_len, hq, hkv, d, &info, nullptr) ? info.workspace_bytes : 0;
+  if (g_single_workspace.size() < 4 * kSinglePlanCap) g_single_workspace.emplace(key, ws);
+  return ws;
 }
 
 static int single_prefill_cascade(const void* q, int64_t q_stride_n, int64_t q_stride_h, const void* k,
