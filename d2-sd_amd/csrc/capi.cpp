@@ -469,9 +469,12 @@ static int build_verify_params(const d2sd_cascade_plan_info* info, const d2sd_ca
 // qo_len keys the suffix level, fully visible (non-causal) or a chain
 // (causal: query i sees suffix keys 0..i, FlashInfer's bottom-right
 // alignment).  The plan is a dynamic-prefix plan for the largest prefix of a
-// 512-key bucket of kv_len, cached per (device, qo_len, bucket, heads,
-// head_dim), and the kernel takes the current prefix length as an argument,
-// so a cache that grows step by step reuses one plan per bucket.  The first
+// 512-key bucket of the prefix length kv_len - qo_len, cached per (device,
+// qo_len, bucket, heads, head_dim), and the kernel takes the current prefix
+// length as an argument, so a cache that grows step by step reuses one plan
+// per bucket.  Without a prefix (qo_len == kv_len, e.g. a row's local causal
+// attention) the plan has suffix items only, which write the output in one
+// launch.  The first
 // call of a shape plans and uploads (hipMalloc, hipMemcpy); under stream
 // capture, past kSinglePlanCap cached shapes, or for shapes the cascade form
 // does not cover, the caller falls back to the single-source kernels.
@@ -495,10 +498,16 @@ bool single_cascade_applies(int qo_len, int kv_len, int window_left) {
 }
 
 // Plans the cascade form on the host; false if it does not apply.
+// The planned prefix of a single prefill: kv_len - qo_len rounded up to the bucket.
+int single_bucket(int qo_len, int kv_len) {
+  const int pre = kv_len - qo_len;
+  return (pre + kSingleBucket - 1) / kSingleBucket * kSingleBucket;
+}
+
 bool single_cascade_plan(int qo_len, int kv_len, int hq, int hkv, int d, d2sd_cascade_plan_info* info,
                          std::vector<int32_t>* host) {
-  const int bucket = (kv_len + kSingleBucket - 1) / kSingleBucket * kSingleBucket;
-  int32_t qo_indptr[2] = {0, qo_len}, prefix_len[1] = {bucket - qo_len}, tok0[1] = {0};
+  const int bucket = single_bucket(qo_len, kv_len);
+  int32_t qo_indptr[2] = {0, qo_len}, prefix_len[1] = {bucket}, tok0[1] = {0};
   d2sd_cascade_plan_desc desc{};
   desc.num_reqs = 1;
   desc.qo_indptr = qo_indptr;
@@ -510,7 +519,7 @@ bool single_cascade_plan(int qo_len, int kv_len, int hq, int hkv, int d, d2sd_ca
   desc.window_left = -1;
   desc.kv_dtype = D2SD_KV_BF16;
   desc.page_size = 0;
-  desc.dynamic_prefix = 1;
+  desc.dynamic_prefix = bucket > 0 ? 1 : 0;
   const std::string saved = g_last_error;
   bool ok = d2sd_cascade_plan(&desc, nullptr, 0, info) == D2SD_OK;
   if (ok && host) {
@@ -527,7 +536,7 @@ static size_t single_cascade_workspace(int qo_len, int kv_len, int hq, int hkv, 
   if (!single_cascade_applies(qo_len, kv_len, window_left)) return 0;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) (void)hipGetLastError();
-  const int bucket = (kv_len + kSingleBucket - 1) / kSingleBucket * kSingleBucket;
+  const int bucket = single_bucket(qo_len, kv_len);
   const std::array<int, 6> key = {dev, qo_len, bucket, hq, hkv, d};
   std::lock_guard<std::mutex> lk(g_single_mu);
   auto it = g_single_workspace.find(key);
@@ -550,7 +559,7 @@ static int single_prefill_cascade(const void* q, int64_t q_stride_n, int64_t q_s
     (void)hipGetLastError();
     return D2SD_OK;
   }
-  const int bucket = (kv_len + kSingleBucket - 1) / kSingleBucket * kSingleBucket;
+  const int bucket = single_bucket(qo_len, kv_len);
   const std::array<int, 6> key = {dev, qo_len, bucket, hq, hkv, d};
   SinglePlan sp{};
   {
@@ -592,8 +601,9 @@ static int single_prefill_cascade(const void* q, int64_t q_stride_n, int64_t q_s
   a.suffix_stride_n = kv_stride_n;
   a.suffix_stride_h = kv_stride_h;
   a.mask_mode = causal ? D2SD_MASK_CAUSAL : D2SD_MASK_NONE;
-  a.k_prefix = k;
-  a.v_prefix = v;
+  const bool has_prefix = sp.info.dynamic_prefix != 0;
+  a.k_prefix = has_prefix ? k : nullptr;
+  a.v_prefix = has_prefix ? v : nullptr;
   a.prefix_stride_tok = kv_stride_n;
   a.prefix_stride_head = kv_stride_h;
   // the planned extent is the bucket's; the kernels read only the first L keys
@@ -611,12 +621,14 @@ static int single_prefill_cascade(const void* q, int64_t q_stride_n, int64_t q_s
   d2sd::VerifyParams p{};
   if (int rc = build_verify_params(&sp.info, &a, p)) return rc;
   p.prefix_len = nullptr;
-  p.prefix_len_set = 1;
+  p.prefix_len_set = has_prefix ? 1 : 0;
   p.prefix_len_value = L;
   hipError_t e = d2sd::launch_verify_attention(p, d, sp.info.waves_per_block, false, false, sp.info.num_items, stream);
   if (e != hipSuccess) return fail_hip(e, "single_prefill attention launch");
-  e = d2sd::launch_verify_merge(p, d, sp.info.rows_per_tile, sp.info.num_merges, stream);
-  if (e != hipSuccess) return fail_hip(e, "single_prefill merge launch");
+  if (sp.info.num_merges > 0) {
+    e = d2sd::launch_verify_merge(p, d, sp.info.rows_per_tile, sp.info.num_merges, stream);
+    if (e != hipSuccess) return fail_hip(e, "single_prefill merge launch");
+  }
   *used = true;
   return D2SD_OK;
 }
