@@ -238,6 +238,7 @@ def _attention_mean_ns(trace_csv: Path) -> float:
 
 
 MFMA_FILE = ROOT / "profiles" / "verify_attn_cfg2_mfma.txt"
+SHADER_ENGINES = 32  # MI355X: 8 XCDs x 4 shader engines (rocminfo)
 MFMA_COUNTERS = ("SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_INSTS_VALU_MFMA_BF16",
                  "SQ_BUSY_CYCLES", "GRBM_GUI_ACTIVE")
 
@@ -287,6 +288,14 @@ def measure_mfma(args) -> int:
         f"grbm_gui_active_per_xcd: {grbm_xcd:.0f}",
         f"mfma_util_rocprof_expr: {busy / (grbm_xcd * cus * simds):.4f}",
         f"mfma_util_over_trace_duration_at_2400MHz: {busy / (dur_ns * 2.4 * cus * simds):.4f}",
+        # SQ_BUSY_CYCLES sums the busy cycles of the 32 shader engines
+        # (rocminfo: 8 XCDs x 4); per engine over the traced duration it is
+        # the clock the launch actually ran at
+        f"sq_busy_cycles_per_shader_engine: {c['SQ_BUSY_CYCLES'] / SHADER_ENGINES:.0f}",
+        f"effective_clock_ghz: {c['SQ_BUSY_CYCLES'] / SHADER_ENGINES / dur_ns:.3f}",
+        f"mfma_peak_at_effective_clock_tflops: {cus * simds * 1024 * c['SQ_BUSY_CYCLES'] / SHADER_ENGINES / dur_ns / 1e3:.0f}",
+        f"executed_frac_of_peak_at_effective_clock: "
+        f"{exec_flops / (cus * simds * 1024.0 * c['SQ_BUSY_CYCLES'] / SHADER_ENGINES):.3f}",
     ]
     MFMA_FILE.parent.mkdir(exist_ok=True)
     MFMA_FILE.write_text("\n".join(lines) + "\n")
