@@ -273,7 +273,9 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
   const float cn = p.sm_scale * kscale;      // raw score -> natural domain
   const float slack_raw = c > 0.f ? kRescaleSlack / c : 0.f;  // kRescaleSlack in raw-score units
 
-  __syncthreads();  // page ids visible (each thread's stores waited for its page-id loads only)
+  // page ids visible (each thread's stores waited for its page-id loads only);
+  // nothing to publish when they are not staged
+  if constexpr (STAGED) __syncthreads();
 
   auto tok_off = [&](int t) -> long long {
     if constexpr (STAGED)
@@ -508,15 +510,17 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
     // lrow of its RPI-row group, stored chunk cs holding global chunk
     // cs ^ swizzle(row).  A wave's instructions cover WROWS consecutive key
     // rows of a tile.  Fast path: full tiles of an item whose key range starts
-    // on a 64-key boundary and, paged, whose pages hold 16..64 keys, at least
-    // WROWS: the wave's rows then lie in one page at a fixed in-page row, so
-    // one wave-uniform base per tile (page id * page bytes, a 32 x 32 -> 64-bit
-    // scalar multiply) plus this per-lane constant addresses every DMA.
+    // on a 64-key boundary and, paged, whose pages hold 16..64 keys and at
+    // least WROWS or 16 of them: each half of the wave's rows then lies in one
+    // page at a fixed in-page row (one page for WROWS <= 16, at most two for
+    // the 32 rows of a two-wave workgroup), so one wave-uniform base per half
+    // and tile (page id * page bytes, a 32 x 32 -> 64-bit scalar multiply)
+    // plus this per-lane constant addresses every DMA.
     constexpr int WROWS = IPW * RPI;
     const int lrow = lane / CH, cs = lane % CH;
     const int P = 1 << log2p;
     const bool fast = (kv_begin & 63) == 0 && tok_b < (1ll << 26) &&
-                      (!PAGED || (P >= WROWS && P <= 64 && page_b < (1ll << 32)));
+                      (!PAGED || (P >= min(WROWS, 16) && P <= 64 && page_b < (1ll << 32)));
     unsigned lane_off[IPW];
 #pragma unroll
     for (int i = 0; i < IPW; ++i) {
@@ -524,38 +528,50 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
       const int row_in_src = PAGED ? (r0 & pmask) : r0;
       lane_off[i] = (unsigned)((row_in_src + lrow) * tok_b) + (unsigned)((cs ^ chunk_swizzle<D>(r0 + lrow)) * 16);
     }
-    // Page id of this wave's rows of tile `it` (fast path; tiles past the
-    // range clamp to its last page), fetched one step before it is needed:
-    // from the staged list, or by a scalar load of the page table.
+    // Page ids of the two halves of this wave's rows of tile `it` (fast path;
+    // equal unless WROWS > 16; tiles past the range clamp to its last page),
+    // fetched one step before they are needed: from the staged list, or by
+    // scalar loads of the page table.
     const int last_page = ntiles > 0 ? (kv_end - 1) >> log2p : 0;
-    auto wave_page = [&](int it) -> int {
+    struct PagePair {
+      int a, b;
+    };
+    auto wave_page = [&](int it) -> PagePair {
       if constexpr (PAGED) {
-        const int pi = min((kv_begin + it * 64 + wv * WROWS) >> log2p, last_page);
-        if constexpr (STAGED) {
-          return pages[min(max(pi - pg_first, 0), kMaxStagedPages - 1)];
-        } else {
-          typedef const __attribute__((address_space(4))) int const_int;
-          return ntiles > 0 ? (int)min((unsigned)((const_int*)S.page_table)[w.base + pi], (unsigned)S.num_pages - 1u)
-                            : 0;
-        }
+        auto page_of = [&](int row) -> int {
+          const int pi = min(row >> log2p, last_page);
+          if constexpr (STAGED) {
+            return pages[min(max(pi - pg_first, 0), kMaxStagedPages - 1)];
+          } else {
+            typedef const __attribute__((address_space(4))) int const_int;
+            return ntiles > 0
+                       ? (int)min((unsigned)((const_int*)S.page_table)[w.base + pi], (unsigned)S.num_pages - 1u)
+                       : 0;
+          }
+        };
+        const int r = kv_begin + it * 64 + wv * WROWS;
+        const int a = page_of(r);
+        return {a, WROWS > 16 ? page_of(r + WROWS / 2) : a};
       }
-      return 0;
+      return {0, 0};
     };
 
     // DMA of K (or V) of tile `it` into its ring slot.  Keys past kv_end (tail
     // tile only) load the last valid key: finite data whose scores the tail
     // mask removes.
-    auto issue = [&](int it, int pg, const char* base, unsigned slot_lds) {
+    auto issue = [&](int it, PagePair pg, const char* base, unsigned slot_lds) {
       const int kb = kv_begin + it * 64;
       if (fast && kb + 64 <= kv_end) {
-        unsigned long long ub;
-        if constexpr (PAGED)
-          ub = (unsigned long long)(unsigned)__builtin_amdgcn_readfirstlane(pg) * (unsigned)page_b;
-        else
-          ub = (unsigned long long)(unsigned)kb * (unsigned)tok_b;
-        const char* b_ = base + ub;
+        unsigned long long ua, ub;
+        if constexpr (PAGED) {
+          ua = (unsigned long long)(unsigned)__builtin_amdgcn_readfirstlane(pg.a) * (unsigned)page_b;
+          ub = (unsigned long long)(unsigned)__builtin_amdgcn_readfirstlane(pg.b) * (unsigned)page_b;
+        } else {
+          ua = ub = (unsigned long long)(unsigned)kb * (unsigned)tok_b;
+        }
 #pragma unroll
-        for (int i = 0; i < IPW; ++i) dma16s(b_, lane_off[i], slot_lds + (wv * IPW + i) * 1024);
+        for (int i = 0; i < IPW; ++i)
+          dma16s(base + ((WROWS > 16 && i >= IPW / 2) ? ub : ua), lane_off[i], slot_lds + (wv * IPW + i) * 1024);
       } else {
 #pragma unroll
         for (int i = 0; i < IPW; ++i) {
@@ -565,8 +581,8 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
         }
       }
     };
-    auto issue_k = [&](int it, int pg) { issue(it, pg, kbase, kring + (it % KST) * TB); };
-    auto issue_v = [&](int it, int pg) { issue(it, pg, vbase, vring + (it % VST) * TB); };
+    auto issue_k = [&](int it, PagePair pg) { issue(it, pg, kbase, kring + (it % KST) * TB); };
+    auto issue_v = [&](int it, PagePair pg) { issue(it, pg, vbase, vring + (it % VST) * TB); };
 
     // LDS byte offsets (inside a tile) of this lane's fragments; the
     // key-row / head-dim steps are immediate offsets.  K: key row l32 (+32 for
@@ -611,7 +627,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
     if constexpr (!MASKED) {
       // ---- prefix level: software-pipelined tiles ----
       // K(j) is read one step before V(j) (QK^T of tile j runs under the
-      // softmax of tile j-1).  Issue order: Q, K(0), V(0), K(1), K(2), then
+      // softmax of tile j-1).  Issue order: K(0), Q, V(0), K(1), K(2), then
       // V / K pairs for steps -(VST - 2) .. -1, then step s issues
       // V(s + VST - 1) and K(s + KST).  Slots: K(j) in j % KST, V(j) in
       // j % VST; step s refills the slots of K(s) (read in step s-1) and
@@ -629,21 +645,34 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
       static_assert(W * QB <= FREE1 + (VST - 1) * TB && TB % QB == 0, "Q staging must fit free ring slots");
       const unsigned qdst = wv * QB < FREE1 ? kring + 2 * TB + wv * QB : vring + TB + (wv * QB - FREE1);
       if (ntiles > 0) {
+        // K(0) first: its address is ready, Q's take a division
+        const auto pg0 = wave_page(0);
+        issue_k(0, pg0);
+        // lane: row wrow0 + lr + QRPI*i of instruction i, 16-byte chunk qcs.
+        // Row -> (node, head) = (row / g, row % g) by one division, then
+        // stepped by QRPI = (QRPI / g) * g + QRPI % g rows per instruction.
+        constexpr int QRPI = 1024 / (D * 2);
+        const int lr = lane / (D / 8), qcs = lane % (D / 8);
+        const long long sn = p.q_stride_n, sh = p.q_stride_h;
+        int row = wrow0 + lr;
+        int qj = row % g;
+        long long qoff = (long long)(row / g) * sn + (long long)qj * sh;
+        const int dj = QRPI % g;
+        const long long dstep = (long long)(QRPI / g) * sn + (long long)dj * sh, wrap = sn - (long long)g * sh;
+        const bf16_t* q0p = (const bf16_t*)p.q + (long long)w.q0 * sn + (long long)(w.kvh * g) * sh;
 #pragma unroll
         for (int i = 0; i < NQI; ++i) {
-          const int byte = i * 1024 + 16 * lane;
-          const int rw = byte / (D * 2), cst = (byte % (D * 2)) / 16;
-          const int row = wrow0 + rw;
           // rows past the group's end read a valid row (node 0); their
           // results are never stored or merged
-          const int nn = row < R ? row / g : 0;
-          const int qq = w.kvh * g + (row < R ? row - nn * g : 0);
-          dma16((const bf16_t*)p.q + (long long)(w.q0 + nn) * p.q_stride_n + (long long)qq * p.q_stride_h +
-                    8 * (cst ^ chunk_swizzle<D>(rw)),
-                qdst + i * 1024);
+          dma16(q0p + (row < R ? qoff : 0ll) + 8 * (qcs ^ chunk_swizzle<D>(i * QRPI + lr)), qdst + i * 1024);
+          row += QRPI;
+          qoff += dstep;
+          qj += dj;
+          if (qj >= g) {
+            qj -= g;
+            qoff += wrap;
+          }
         }
-        const int pg0 = wave_page(0);
-        issue_k(0, pg0);
         issue_v(0, pg0);
       }
       if (1 < ntiles) issue_k(1, wave_page(1));
@@ -667,7 +696,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
         if (st + VST - 1 < ntiles) issue_v(st + VST - 1, wave_page(st + VST - 1));
         if (st + KST < ntiles) issue_k(st + KST, wave_page(st + KST));
       });
-      int pv_next = wave_page(VST - 1), pk_next = wave_page(KST);
+      auto pv_next = wave_page(VST - 1), pk_next = wave_page(KST);
       f32x16 sc[RB][2];
       if (live && ntiles > 0) {
         auto kf = kfrag_at(0);
@@ -712,7 +741,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
         if (st + VST - 1 >= 0 && st + VST - 1 < ntiles) issue_v(st + VST - 1, wave_page(st + VST - 1));
         if (st + KST - 1 < ntiles) issue_k(st + KST - 1, wave_page(st + KST - 1));
       });
-      int pk_next = wave_page(KST - 1), pv_next = wave_page(VST - 1);
+      auto pk_next = wave_page(KST - 1), pv_next = wave_page(VST - 1);
       wait_vmcnt<0>();  // Q / mask loads and the first tiles (see above)
 
       // One step: wait for tile `it`, refill the K and V slots freed by tile

@@ -354,6 +354,21 @@ def test_cascade_edges(L, shared, window, waves):
     _check_problem(mp, outs, tag="edge")
 
 
+@pytest.mark.parametrize("waves,page,d", [(2, 16, 128), (2, 32, 128), (2, 64, 128), (2, 16, 64), (4, 16, 128),
+                                          (8, 16, 128), (2, 8, 128)])
+def test_cascade_paged_workgroup_shapes(waves, page, d):
+    """Every workgroup shape over paged prefixes whose pages hold 8..64 keys:
+    a two-wave workgroup's 32-row wave share spans two 16-key pages (two page
+    ids per wave and tile), 8-key pages take the per-lane path; 1000 keys end
+    in a partial tile."""
+    t = dtree.tree_from_shared_prefixes(16, [16, 4, 9])
+    hq, hkv = (32, 8) if d == 128 else (64, 8)
+    prob = wl.VerifyProblem("shape", hq, hkv, d, [wl.Request(t, 1000), wl.Request(t, 333)], page_size=page,
+                            seed=page + waves)
+    mp, _, outs = _run_problem(prob, waves_per_block=waves)
+    _check_problem(mp, outs, tag=f"shape w{waves} p{page} d{d}")
+
+
 @pytest.mark.parametrize("paged,window", [(True, -1), (True, 300), (False, -1)])
 def test_dynamic_prefix_at_every_length(paged, window):
     """One dynamic-prefix plan (planned for prefixes 3000 and 700) run at
