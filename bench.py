@@ -317,7 +317,11 @@ MIX_PASSES = (
      "SQ_ACTIVE_INST_VALU", "SQ_VALU_MFMA_COEXEC_CYCLES", "SQ_WAIT_INST_LDS"),
     ("SQ_ACTIVE_INST_LDS", "SQ_ACTIVE_INST_ANY", "SQ_WAIT_ANY", "SQ_WAIT_INST_ANY", "SQ_BUSY_CYCLES",
      "SQ_INSTS_VALU_CVT", "SQ_THREAD_CYCLES_VALU", "SQ_INSTS_SMEM"),
+    ("SQ_LDS_IDX_ACTIVE", "SQ_LDS_BANK_CONFLICT", "SQ_INSTS_LDS_LOAD_BANDWIDTH", "SQ_ACTIVE_INST_VALU2",
+     "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_BUSY_CYCLES"),
+    ("LdsLatency",),
 )
+CUS, SIMDS = 256, 1024
 
 
 def measure_mix(args) -> int:
@@ -347,7 +351,7 @@ def measure_mix(args) -> int:
     lines = [
         "# Instruction mix of the cascade verify attention launch, config 2 (Qwen3-8B, L=4096 paged, 36 layers)",
         f"# command: python bench.py --measure-mix --layers {args.layers} --seed {args.seed}",
-        "#   = two passes, each: timeout -s KILL 120 rocprofv3 --pmc <counters>",
+        f"#   = {len(MIX_PASSES)} passes, each: timeout -s KILL 120 rocprofv3 --pmc <counters>",
         f"#     --kernel-include-regex '{TRAFFIC_KERNELS}' --output-format csv -- python bench.py --traffic-workload",
         "#   passes: " + " | ".join(" ".join(c) for c in MIX_PASSES),
         "# mean per attention dispatch",
@@ -362,6 +366,19 @@ def measure_mix(args) -> int:
         f"lds_per_wave_tile: {res['SQ_INSTS_LDS'] / wave_tiles:.1f}",
         f"salu_per_wave_tile: {res['SQ_INSTS_SALU'] / wave_tiles:.1f}",
         f"valu_per_mfma: {valu / res['SQ_INSTS_MFMA']:.2f}",
+        "",
+        "# per SIMD (1024) or CU (256) over the launch: SQ_BUSY_CYCLES summed over the",
+        f"# {SHADER_ENGINES} shader engines / {SHADER_ENGINES} = the launch's cycles",
+        f"launch_cycles: {res['SQ_BUSY_CYCLES'] / SHADER_ENGINES:.0f}",
+        f"valu_issue_cycles_per_simd (SQ_ACTIVE_INST_VALU quad-cycles x 4): "
+        f"{res['SQ_ACTIVE_INST_VALU'] * 4 / SIMDS:.0f}",
+        f"mfma_busy_cycles_per_simd: {res['SQ_VALU_MFMA_BUSY_CYCLES'] / SIMDS:.0f}",
+        f"valu_mfma_coexec_cycles_per_simd: {res['SQ_VALU_MFMA_COEXEC_CYCLES'] / SIMDS:.0f}",
+        f"lds_active_cycles_per_cu: {res['SQ_LDS_IDX_ACTIVE'] / CUS:.0f}",
+        f"lds_active_frac: {res['SQ_LDS_IDX_ACTIVE'] / CUS / (res['SQ_BUSY_CYCLES'] / SHADER_ENGINES):.3f}",
+        f"lds_read_bytes_per_active_cycle_per_cu: "
+        f"{res['SQ_INSTS_LDS_LOAD_BANDWIDTH'] * 64 / res['SQ_LDS_IDX_ACTIVE']:.0f}",
+        f"lds_latency_cycles (LdsLatency): {res['LdsLatency']:.1f}",
     ]
     MIX_FILE.parent.mkdir(exist_ok=True)
     MIX_FILE.write_text("\n".join(lines) + "\n")
