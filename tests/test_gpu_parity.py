@@ -369,6 +369,29 @@ def test_cascade_paged_workgroup_shapes(waves, page, d):
     _check_problem(mp, outs, tag=f"shape w{waves} p{page} d{d}")
 
 
+@pytest.mark.parametrize("paged", [False, True])
+def test_run_rejects_a_prefix_the_plan_overruns(paged):
+    """run() refuses, before any launch, a contiguous prefix shorter than the
+    keys the plan reads and a paged pool without the pages the page table
+    names; the full tensors then run and match the oracle."""
+    t = dtree.tree_from_shared_prefixes(16, [16, 4])
+    prob = wl.VerifyProblem("overrun", 32, 8, 128, [wl.Request(t, 500)], page_size=16 if paged else 0, seed=3)
+    mp = wl.materialize(prob, DEV, layers=1)
+    attn = d2sd.CascadeVerifyAttention(DEV)
+    wl.plan_for(attn, mp)
+    lt = mp.layers[0]
+    if paged:
+        top = int(mp.page_table.max().item())
+        short_k, short_v, msg = lt.k_prefix[:top], lt.v_prefix[:top], "outside the pool"
+    else:
+        short_k, short_v, msg = lt.k_prefix[:, :499], lt.v_prefix[:, :499], "holds 499 tokens"
+    with pytest.raises(ValueError, match=msg):
+        attn.run(lt.q, lt.k_suffix, lt.v_suffix, short_k, short_v)
+    o, lse = attn.run(lt.q, lt.k_suffix, lt.v_suffix, lt.k_prefix, lt.v_prefix)
+    torch.cuda.synchronize()
+    _check_problem(mp, [(o, lse)], tag="overrun")
+
+
 @pytest.mark.parametrize("paged,window", [(True, -1), (True, 300), (False, -1)])
 def test_dynamic_prefix_at_every_length(paged, window):
     """One dynamic-prefix plan (planned for prefixes 3000 and 700) run at

@@ -273,6 +273,27 @@ def test_c_abi_rejects_bad_arguments_without_launching():
     assert rc == 2
 
 
+@pytest.mark.parametrize("page_size,extent,msg", [(0, 299, b"fewer tokens"), (0, -1, b"fewer tokens"),
+                                                  (16, 0, b"page count")])
+def test_cascade_run_rejects_a_short_prefix_without_launching(page_size, extent, msg):
+    """A contiguous k_prefix shorter than the keys the plan reads (300 tokens
+    here), or a paged pool of no pages, is refused before any launch (the
+    pointers are never dereferenced)."""
+    info, _, _ = _plan([0, 10], [300], page_size=page_size)
+    assert info.prefix_extent == (300 if page_size == 0 else info.prefix_extent)
+    fake = 1 << 20
+    a = _lib.RunArgs()
+    a.plan = a.q = a.k_suffix = a.v_suffix = a.out = a.k_prefix = a.v_prefix = a.page_table = fake
+    a.workspace, a.workspace_bytes = fake, info.workspace_bytes
+    a.q_stride_n, a.q_stride_h = 32 * 128, 128
+    a.suffix_stride_n, a.suffix_stride_h = 8 * 128, 128
+    a.o_stride_n, a.o_stride_h = 32 * 128, 128
+    a.prefix_stride_tok, a.prefix_stride_head, a.prefix_stride_page = 128, 300 * 128, 16 * 8 * 128
+    a.page_size, a.prefix_extent, a.sm_scale = page_size, extent, 0.088
+    rc = _lib.lib.d2sd_cascade_run(C.byref(info), C.byref(a), None)
+    assert rc == 1 and msg in _lib.lib.d2sd_last_error()
+
+
 def test_python_surface_rejects_cpu_tensors():
     q = torch.zeros(4, 32, 128, dtype=torch.bfloat16)
     k = torch.zeros(16, 8, 128, dtype=torch.bfloat16)
