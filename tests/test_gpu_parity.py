@@ -427,6 +427,32 @@ def test_dynamic_prefix_at_every_length(paged, window):
             check_close(o[a:b], o_ref, lse[a:b], lse_ref, f"lengths {lens} req {r}")
 
 
+@pytest.mark.parametrize("seed", range(32))
+def test_cascade_random_problems(seed):
+    """Seeded random problems over the plan space: 1-4 requests with random
+    trees (rows of 8-32, branches chained to row 0 or to any earlier row) and
+    prefixes of 0-2500 keys, heads (32/8, 64/8, 8/8 and 16/2 at D = 128, 64/8
+    at D = 64), contiguous or paged (1-64 keys per page), bf16 or fp8 caches,
+    windows, sinks and every workgroup shape; each request against the oracle."""
+    rng = np.random.default_rng(1000 + seed)
+    hq, hkv, d = [(32, 8, 128), (64, 8, 128), (8, 8, 128), (16, 2, 128), (64, 8, 64)][seed % 5]
+    reqs = []
+    for _ in range(int(rng.integers(1, 5))):
+        tree = wl.random_branch_tree(rng, int(rng.integers(1, 6)), int(rng.choice([8, 16, 32])),
+                                     chain_to_row0=bool(rng.integers(0, 2)))
+        reqs.append(wl.Request(tree, int(rng.choice([0, 1, 64, 65] + [int(x) for x in rng.integers(2, 2500, 4)]))))
+    page = int(rng.choice([0, 1, 8, 16, 32, 64]))
+    fp8 = page > 0 and rng.random() < 0.3
+    window = int(rng.choice([-1, -1, int(rng.integers(1, 600))]))
+    prob = wl.VerifyProblem(f"random{seed}", hq, hkv, d, reqs, page_size=page, window_left=window,
+                            kv_dtype=torch.float8_e4m3fn if fp8 else torch.bfloat16,
+                            with_sinks=bool(rng.random() < 0.3), seed=seed)
+    waves = int(rng.choice([0, 2, 4, 8]))
+    mp, _, outs = _run_problem(prob, waves_per_block=waves)
+    _check_problem(mp, outs, tag=f"random {seed} ({hq}/{hkv}/{d}, page {page}, fp8 {fp8}, window {window}, "
+                                 f"waves {waves})")
+
+
 def test_dynamic_prefix_many_requests():
     """Ten requests (more than the kernel preloads with the work item): each
     at a ragged run-time length below its planned one, against the oracle."""
