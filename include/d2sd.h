@@ -77,6 +77,13 @@ int d2sd_merge_state_in_place(void* v, int64_t v_stride_n, int64_t v_stride_h,
  * (the prefix truncation rule of generation/verification.py:133-135);
  * -1 disables it.  lse may be NULL.  The workspace (device memory, at least
  * d2sd_single_prefill_workspace_size() bytes) holds split-KV partials.
+ * With window_left < 0 and 0 < qo_len <= kv_len the call runs as a
+ * one-request cascade (the first kv_len - qo_len keys a shared prefix, the
+ * last qo_len keys the suffix level, fully visible or causal): the first
+ * call of a (device, qo_len, 512-key bucket of kv_len - qo_len, heads,
+ * head_dim) shape plans it and uploads the plan to device memory the library
+ * keeps until the process ends (at most 512 shapes); a first call under
+ * stream capture, later shapes and other calls use the single-source kernel.
  * ---------------------------------------------------------------------- */
 size_t d2sd_single_prefill_workspace_size(int qo_len, int kv_len, int num_qo_heads,
                                           int num_kv_heads, int head_dim, int window_left);
