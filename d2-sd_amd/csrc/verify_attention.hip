@@ -660,8 +660,9 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
         const int dj = QRPI % g;
         const long long dstep = (long long)(QRPI / g) * sn + (long long)dj * sh, wrap = sn - (long long)g * sh;
         const bf16_t* q0p = (const bf16_t*)p.q + (long long)w.q0 * sn + (long long)(w.kvh * g) * sh;
+        // (a wave with no valid row computes nothing and needs no Q)
 #pragma unroll
-        for (int i = 0; i < NQI; ++i) {
+        for (int i = 0; i < NQI && live; ++i) {
           // rows past the group's end read a valid row (node 0); their
           // results are never stored or merged
           dma16(q0p + (row < R ? qoff : 0ll) + 8 * (qcs ^ chunk_swizzle<D>(i * QRPI + lr)), qdst + i * 1024);
