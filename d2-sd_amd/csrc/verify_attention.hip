@@ -459,6 +459,10 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
   // chunk j is converted while PV of chunk j-1 runs.
   auto pipelined_tile = [&](f32x16 (&sc)[RB][2], auto&& kfrag_n, auto&& vfrag) {
     constexpr int Q1 = KS / 4;  // QK^T k-steps beside the row max
+    // A wave computing a tile step wins instruction issue over a wave of its
+    // SIMD that is at its step's wait and DMA issue (config 2 attention
+    // -2.3%, config 4 -1.4%, the others within noise; A/B in one session).
+    __builtin_amdgcn_s_setprio(1);
     f32x16 sn[RB][2];
     static_for<Q1>([&](auto ks) { qk_ks(sn, kfrag_n, decltype(ks)::value); });
     float mc[RB];
@@ -489,6 +493,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
       sc[rb][0] = sn[rb][0];
       sc[rb][1] = sn[rb][1];
     }
+    __builtin_amdgcn_s_setprio(0);
   };
 
   if constexpr (!FP8) {
