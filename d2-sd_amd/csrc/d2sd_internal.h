@@ -88,9 +88,9 @@ struct AttnParams {
 
 // ---------------------------------------------------------------------------
 // Cascade verify attention (verify_attention.hip): one attention launch whose
-// workgroups each own ROWS = 64 * W packed rows of one (request, kv head,
-// q-tile) group and either one key chunk of the shared prefix or the whole
-// suffix tree, then one merge launch.
+// workgroups each own the packed rows of one (request, kv head, q-tile) group
+// (32 per wave; 64 per wave of a two-wave workgroup) and either one key chunk
+// of the shared prefix or the whole suffix tree, then one merge launch.
 // ---------------------------------------------------------------------------
 enum : int { SRC_PREFIX = 0, SRC_SUFFIX = 1 };
 
