@@ -32,9 +32,9 @@
 // Register image.  Lane l of wave w holds O^T[d][row] for row = 32w + l%32
 // and d = 32*mt + 8*q4 + 4*(l/32) + e (mt < D/32, q4 < 4, e < 4).  Split
 // partials (normalised O in bf16, LSE in fp32) are stored in exactly this
-// image — the 4 values (mt, q4) of lane l at element
-// ((w*(D/32) + mt)*4 + q4)*256 + 4*l of the slot — so that every partial
-// store and every merge load is one contiguous 512-byte wave access.
+// image — the 8 values (mt, q4 = 2pr, 2pr + 1) of lane l at element
+// ((w*(D/32) + mt)*2 + pr)*512 + 8*l of the slot — so that every partial
+// store and every merge load is one contiguous 1 KB wave access.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -132,9 +132,7 @@ __device__ __forceinline__ void finish_rows(const AttnParams& p, const WorkItem&
 #pragma unroll
     for (int mt = 0; mt < D / 32; ++mt)
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4)
-        *(u32x2*)(po + image_offset<D>(wv, mt, q4, lane)) =
-            (u32x2){pack_bf16x2(o[mt][4 * q4], o[mt][4 * q4 + 1]), pack_bf16x2(o[mt][4 * q4 + 2], o[mt][4 * q4 + 3])};
+      for (int pr = 0; pr < 2; ++pr) *(u32x4*)(po + image_offset<D>(wv, mt, pr, lane)) = image_piece(o[mt], pr, 1.f);
     if (hh == 0) p.part_lse[(long long)w.slot * ROWS + wv * 32 + l32] = lse;
     return;
   }
@@ -490,18 +488,18 @@ __global__ __launch_bounds__(64) void merge_kernel(const AttnParams p, int rows_
   float mval = -INFINITY, wsum = 0.f;
   for (int s0 = 0; s0 < nslots; s0 += kMergeBatch) {
     float ls[kMergeBatch];
-    u32x2 v[kMergeBatch][4];
+    u32x4 v[kMergeBatch][2];
 #pragma unroll
     for (int b = 0; b < kMergeBatch; ++b) {
       ls[b] = -INFINITY;
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) v[b][q4] = (u32x2){0u, 0u};
+      for (int pr = 0; pr < 2; ++pr) v[b][pr] = (u32x4){0u, 0u, 0u, 0u};
       if (s0 + b < nslots) {
         const long long s = slot0 + s0 + b;
         ls[b] = p.part_lse[s * rows_per_tile + blk * 32 + l32];
         const bf16_t* po = (const bf16_t*)p.part_o + s * slot_elems;
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) v[b][q4] = *(const u32x2*)(po + image_offset<D>(blk, mt, q4, lane));
+        for (int pr = 0; pr < 2; ++pr) v[b][pr] = *(const u32x4*)(po + image_offset<D>(blk, mt, pr, lane));
       }
     }
     float bm = -INFINITY;
@@ -517,11 +515,9 @@ __global__ __launch_bounds__(64) void merge_kernel(const AttnParams p, int rows_
     for (int b = 0; b < kMergeBatch; ++b) {
       const float wt = (ls[b] == -INFINITY) ? 0.f : __expf(ls[b] - nm);
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        acc[4 * q4] += wt * bf16_lo(v[b][q4][0]);
-        acc[4 * q4 + 1] += wt * bf16_hi(v[b][q4][0]);
-        acc[4 * q4 + 2] += wt * bf16_lo(v[b][q4][1]);
-        acc[4 * q4 + 3] += wt * bf16_hi(v[b][q4][1]);
+      for (int e = 0; e < 8; ++e) {
+        acc[2 * e] += wt * bf16_lo(v[b][e >> 2][e & 3]);
+        acc[2 * e + 1] += wt * bf16_hi(v[b][e >> 2][e & 3]);
       }
       wsum += wt;
     }

@@ -54,12 +54,22 @@ __device__ __forceinline__ unsigned pack_bf16x2(float a, float b) {
 __device__ __forceinline__ float bf16_lo(unsigned w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(unsigned w) { return __uint_as_float(w & 0xffff0000u); }
 
-// Element offset, inside one partial slot, of the 4 values (mt, q4) that lane
-// `lane` of 32-row block `blk` holds: the accumulator register image, so that
-// every partial store / load is one contiguous 512-byte wave access.
+// Element offset, inside one partial slot, of the 8 values (q4 = 2pr and
+// 2pr + 1 of block mt) that lane `lane` of 32-row block `blk` holds: the
+// accumulator register image in 16-byte lane pieces, so that every partial
+// store / load is one contiguous 1 KB wave access.  (8-byte pieces took twice
+// the load instructions in the merge, whose time follows their count:
+// 4.60 vs 4.15 us per merge launch at config 2.)
 template <int D>
-__device__ __forceinline__ int image_offset(int blk, int mt, int q4, int lane) {
-  return ((blk * (D / 32) + mt) * 4 + q4) * 256 + 4 * lane;
+__device__ __forceinline__ int image_offset(int blk, int mt, int pr, int lane) {
+  return ((blk * (D / 32) + mt) * 2 + pr) * 512 + 8 * lane;
+}
+
+// Values 8pr .. 8pr + 7 of an accumulator block (head dims 8q4 + 4hh + 0..3
+// for q4 = 2pr, 2pr + 1) as one 16-byte image piece, each scaled by sc.
+__device__ __forceinline__ u32x4 image_piece(const f32x16& o, int pr, float sc) {
+  return (u32x4){pack_bf16x2(o[8 * pr] * sc, o[8 * pr + 1] * sc), pack_bf16x2(o[8 * pr + 2] * sc, o[8 * pr + 3] * sc),
+                 pack_bf16x2(o[8 * pr + 4] * sc, o[8 * pr + 5] * sc), pack_bf16x2(o[8 * pr + 6] * sc, o[8 * pr + 7] * sc)};
 }
 
 // fp8 e4m3fn (OCP) -> bf16, exact.  Bytes b0..b3 of w -> 4 bf16 in a u32x2.

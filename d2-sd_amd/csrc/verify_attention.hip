@@ -888,11 +888,8 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4) {
-            const u32x2 val = {pack_bf16x2(o[rb][mt][4 * q4], o[rb][mt][4 * q4 + 1]),
-                               pack_bf16x2(o[rb][mt][4 * q4 + 2], o[rb][mt][4 * q4 + 3])};
-            __builtin_nontemporal_store(val, (u32x2*)(po + image_offset<D>(blk, mt, q4, lane)));
-          }
+          for (int pr = 0; pr < 2; ++pr)
+            __builtin_nontemporal_store(image_piece(o[rb][mt], pr, 1.f), (u32x4*)(po + image_offset<D>(blk, mt, pr, lane)));
         if (hh == 0) __builtin_nontemporal_store(lse_r[rb], pl);
       } else if (rv[rb]) {
         store_out<D>(p, w.q0 + n[rb], qh[rb], hh, o[rb], lse_r[rb]);
@@ -964,22 +961,19 @@ __device__ __forceinline__ void merge_rows(const VerifyParams& p, int slot0, int
   for (int s0 = 0; s0 < nslots; s0 += B) {
     const int cnt = min(B, nslots - s0);
     float ls[B];
-    u32x2 v[B][4];
+    u32x4 v[B][2];
 #pragma unroll
     for (int b = 0; b < B; ++b) {
       ls[b] = -INFINITY;
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) v[b][q4] = (u32x2){0u, 0u};
+      for (int pr = 0; pr < 2; ++pr) v[b][pr] = (u32x4){0u, 0u, 0u, 0u};
       if (b < cnt) {
         const long long s = slot0 + s0 + b;
         const float* pl = p.part_lse + s * ROWS + blk * 32 + l32;
         ls[b] = *pl;
         const bf16_t* po = (const bf16_t*)p.part_o + s * slot_elems;
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          const u32x2* src = (const u32x2*)(po + image_offset<D>(blk, mt, q4, lane));
-          v[b][q4] = *src;
-        }
+        for (int pr = 0; pr < 2; ++pr) v[b][pr] = *(const u32x4*)(po + image_offset<D>(blk, mt, pr, lane));
       }
     }
     float bm = -INFINITY;
@@ -995,11 +989,9 @@ __device__ __forceinline__ void merge_rows(const VerifyParams& p, int slot0, int
     for (int b = 0; b < B; ++b) {
       const float wt = (ls[b] == -INFINITY) ? 0.f : __expf(ls[b] - nm);
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        acc[4 * q4] += wt * bf16_lo(v[b][q4][0]);
-        acc[4 * q4 + 1] += wt * bf16_hi(v[b][q4][0]);
-        acc[4 * q4 + 2] += wt * bf16_lo(v[b][q4][1]);
-        acc[4 * q4 + 3] += wt * bf16_hi(v[b][q4][1]);
+      for (int e = 0; e < 8; ++e) {
+        acc[2 * e] += wt * bf16_lo(v[b][e >> 2][e & 3]);
+        acc[2 * e + 1] += wt * bf16_hi(v[b][e >> 2][e & 3]);
       }
       wsum += wt;
     }
