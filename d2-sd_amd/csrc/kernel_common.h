@@ -72,23 +72,16 @@ __device__ __forceinline__ u32x4 image_piece(const f32x16& o, int pr, float sc) 
                  pack_bf16x2(o[8 * pr + 4] * sc, o[8 * pr + 5] * sc), pack_bf16x2(o[8 * pr + 6] * sc, o[8 * pr + 7] * sc)};
 }
 
-// fp8 e4m3fn (OCP) -> bf16, exact.  Bytes b0..b3 of w -> 4 bf16 in a u32x2.
-// e4m3fn placed in the top of an fp16 gives value(fp16) * 2^8 == value(e4m3fn)
-// for normals and subnormals alike (exponent bias 15 vs 7); the 2^8 is folded
-// into the dequantisation scale by the caller.
+// fp8 e4m3fn (OCP) -> bf16, exact: every finite e4m3fn value is a bf16 value.
+// Bytes b0..b3 of w -> 4 bf16 in a u32x2, by the gfx950 converter
+// v_cvt_scalef32_pk_bf16_fp8 at scale 1 (word select 0: bytes 0, 1; 1: bytes
+// 2, 3).  Checked on the GPU against the exact value of all 254 finite bytes
+// (NaN bytes give NaN); one instruction per pair instead of ten VALU
+// operations of an expansion through fp16 (config 5 attention 1508 ->
+// 1271 us).
 __device__ __forceinline__ u32x2 fp8x4_to_bf16x4(unsigned w) {
-  u32x2 r;
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const unsigned b0 = (w >> (16 * h)) & 0xffu, b1 = (w >> (16 * h + 8)) & 0xffu;
-    const unsigned h0 = ((b0 & 0x80u) << 8) | ((b0 & 0x7fu) << 7);
-    const unsigned h1 = ((b1 & 0x80u) << 8) | ((b1 & 0x7fu) << 7);
-    const float f0 = (float)__builtin_bit_cast(_Float16, (unsigned short)h0);
-    const float f1 = (float)__builtin_bit_cast(_Float16, (unsigned short)h1);
-    // fp16 values with a 3-bit mantissa are exact in bf16: truncate.
-    r[h] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
-  }
-  return r;
+  return (u32x2){__builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.f, false)),
+                 __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.f, true))};
 }
 
 // One global_load_lds_dwordx4: lane l copies 16 bytes from `src` to LDS byte

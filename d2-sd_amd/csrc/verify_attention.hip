@@ -265,9 +265,9 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
 
   float kscale = 1.f, vscale = 1.f;
   if constexpr (FP8) {
-    // e4m3fn bytes are expanded as value / 2^8 (see fp8x4_to_bf16x4)
-    kscale = (S.k_scale ? S.k_scale[w.kvh] : 1.f) * 256.f;
-    vscale = (S.v_scale ? S.v_scale[w.kvh] : 1.f) * 256.f;
+    // e4m3fn bytes are expanded to their exact values (fp8x4_to_bf16x4)
+    kscale = S.k_scale ? S.k_scale[w.kvh] : 1.f;
+    vscale = S.v_scale ? S.v_scale[w.kvh] : 1.f;
   }
   const float c = p.sm_scale_log2 * kscale;  // raw score -> log2 domain
   const float cn = p.sm_scale * kscale;      // raw score -> natural domain
