@@ -77,8 +77,8 @@ struct VerifySmem {
       int pages[NPG];                  // page ids of the workgroup's key range
     } ring;
     struct {
-      bf16_t Ks[2][64 * (D + 8)];      // register-staged K tiles (row pitch D + 8)
-      bf16_t Vt[2][D * (64 + 8)];      // register-staged V^T tiles (row pitch 64 + 8)
+      bf16_t k[2][64 * D];             // register-staged K tiles (layout of the rings)
+      bf16_t v[2][64 * D];             // register-staged V tiles (layout of the rings)
       int pages[kMaxStagedPages];
     } st;
   };
@@ -777,67 +777,60 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
     }
   } else {
     // ============ register-staged tiles (fp8 e4m3fn -> bf16 in LDS) ============
+    // Each thread loads 16 fp8 bytes (head dims 16s .. 16s + 15 of one key),
+    // expands them to two bf16 chunks and stores those in the layout of the
+    // direct-to-LDS rings (row-major, chunk c of key row r at position
+    // c ^ swizzle(r)), so that K and V^T fragments are read exactly as there.
     wait_vmcnt<0>();  // Q / mask loads complete, visibly to the compiler (see above)
-    constexpr int KP = D + 8;          // K tile pitch (elements)
-    constexpr int VP = 64 + 8;         // V^T tile pitch (elements)
-    constexpr int KCH = D / 8;         // 8-element chunks per key row
-    constexpr int NK = 64 * KCH / NT;  // K chunks per thread == V keys per thread
-    constexpr int VKG = 64 / NK;       // V key groups per d-chunk
-    static_assert(NK == 1 || NK == 2 || NK == 4 || NK == 8, "tile/thread mismatch");
-    u32x2 kr[NK], vr[NK];  // 8 fp8 elements each
+    constexpr int SEG = D / 16;                  // 16-byte fp8 segments per key row
+    constexpr int NS = (64 * SEG + NT - 1) / NT;  // segments per thread and tile
+    u32x4 kr[NS], vr[NS];                        // 16 fp8 elements each
 
     auto load_tile = [&](int kb) {
 #pragma unroll
-      for (int i = 0; i < NK; ++i) {
-        const int c_ = tid + i * NT;
-        const int t = min(kb + c_ / KCH, kv_end - 1);
-        kr[i] = *(const u32x2*)(kbase + tok_off(t) + (c_ % KCH) * 8);
-      }
-      const int kg = tid % VKG, dc = tid / VKG;
-#pragma unroll
-      for (int i = 0; i < NK; ++i) {
-        const int t = min(kb + kg * NK + i, kv_end - 1);
-        vr[i] = *(const u32x2*)(vbase + tok_off(t) + dc * 8);
-      }
-    };
-    auto to_bf16 = [](const u32x2& r) -> u32x4 {
-      const u32x2 lo = fp8x4_to_bf16x4(r[0]), hi = fp8x4_to_bf16x4(r[1]);
-      return (u32x4){lo[0], lo[1], hi[0], hi[1]};
-    };
-    // K row-major; V transposed with the keys of each 16-key group in the
-    // order a lane of half h holds them in the S^T accumulator: keys
-    // 4h+{0..3} and 4h+8+{0..3} at slots 8h..8h+7.
-    auto store_tile = [&](int buf) {
-#pragma unroll
-      for (int i = 0; i < NK; ++i) {
-        const int c_ = tid + i * NT;
-        *(u32x4*)(&sm.st.Ks[buf][(c_ / KCH) * KP + (c_ % KCH) * 8]) = to_bf16(kr[i]);
-      }
-      const int kg = tid % VKG, dc = tid / VKG;
-      u32x4 vv[NK];
-#pragma unroll
-      for (int i = 0; i < NK; ++i) vv[i] = to_bf16(vr[i]);
-      auto slot_of = [](int kk) { return (kk & ~15) + 8 * ((kk >> 2) & 1) + (kk & 3) + 4 * ((kk >> 3) & 1); };
-#pragma unroll
-      for (int dd = 0; dd < 8; ++dd) {
-        const int wi = dd >> 1;
-        const int sh = (dd & 1) * 16;
-        bf16_t* rowp = &sm.st.Vt[buf][(dc * 8 + dd) * VP];
-        if constexpr (NK >= 4) {
-#pragma unroll
-          for (int q = 0; q < NK / 4; ++q) {
-            const unsigned e0 = (vv[4 * q][wi] >> sh) & 0xffffu, e1 = (vv[4 * q + 1][wi] >> sh) & 0xffffu;
-            const unsigned e2 = (vv[4 * q + 2][wi] >> sh) & 0xffffu, e3 = (vv[4 * q + 3][wi] >> sh) & 0xffffu;
-            *(u32x2*)(rowp + slot_of(kg * NK + 4 * q)) = (u32x2){e0 | (e1 << 16), e2 | (e3 << 16)};
-          }
-        } else if constexpr (NK == 2) {
-          const unsigned e0 = (vv[0][wi] >> sh) & 0xffffu, e1 = (vv[1][wi] >> sh) & 0xffffu;
-          *(unsigned*)(rowp + slot_of(kg * 2)) = e0 | (e1 << 16);
-        } else {
-          *(unsigned short*)(rowp + slot_of(kg)) = (unsigned short)((vv[0][wi] >> sh) & 0xffffu);
+      for (int i = 0; i < NS; ++i) {
+        const int s_ = tid + i * NT;
+        if (64 * SEG % NT == 0 || s_ < 64 * SEG) {
+          const long long off = tok_off(min(kb + s_ / SEG, kv_end - 1)) + (s_ % SEG) * 16;
+          kr[i] = *(const u32x4*)(kbase + off);
+          vr[i] = *(const u32x4*)(vbase + off);
         }
       }
     };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+      for (int i = 0; i < NS; ++i) {
+        const int s_ = tid + i * NT;
+        if (64 * SEG % NT == 0 || s_ < 64 * SEG) {
+          const int r = s_ / SEG, c0 = 2 * (s_ % SEG), sw = chunk_swizzle<D>(r);
+          bf16_t* krow = &sm.st.k[buf][r * D];
+          bf16_t* vrow = &sm.st.v[buf][r * D];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const u32x2 klo = fp8x4_to_bf16x4(kr[i][2 * h]), khi = fp8x4_to_bf16x4(kr[i][2 * h + 1]);
+            const u32x2 vlo = fp8x4_to_bf16x4(vr[i][2 * h]), vhi = fp8x4_to_bf16x4(vr[i][2 * h + 1]);
+            *(u32x4*)(krow + 8 * ((c0 + h) ^ sw)) = (u32x4){klo[0], klo[1], khi[0], khi[1]};
+            *(u32x4*)(vrow + 8 * ((c0 + h) ^ sw)) = (u32x4){vlo[0], vlo[1], vhi[0], vhi[1]};
+          }
+        }
+      }
+    };
+
+    // fragment offsets inside a tile (bytes), as for the direct-to-LDS rings
+    unsigned koff[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) koff[ks] = (l32 * D + 8 * ((2 * ks + hh) ^ chunk_swizzle<D>(l32))) * 2;
+    const int k16 = lane & 15;
+    const int krow = 4 * hh + (k16 >> 2);
+    const int dsub = 16 * ((lane >> 4) & 1) + 4 * (k16 & 3);
+    unsigned voff0[MT], voff1[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int d = 32 * mt + dsub;
+      voff0[mt] = (krow * D + 8 * ((d >> 3) ^ chunk_swizzle<D>(krow)) + (d & 7)) * 2;
+      voff1[mt] = ((krow + 8) * D + 8 * ((d >> 3) ^ chunk_swizzle<D>(krow + 8)) + (d & 7)) * 2;
+    }
+    typedef __attribute__((address_space(3))) char lds_char;
 
     if (ntiles > 0) {
       load_tile(kv_begin);
@@ -849,13 +842,17 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
       const int kb = kv_begin + it * 64;
       if (it + 1 < ntiles) load_tile(kb + 64);
       if (live) {
-        const bf16_t* ks_ = &sm.st.Ks[buf][0];
-        const bf16_t* vt_ = &sm.st.Vt[buf][0];
+        const lds_char* kst = (const lds_char*)(uintptr_t)lds_address(&sm.st.k[buf][0]);
+        const lds_char* vst = (const lds_char*)(uintptr_t)lds_address(&sm.st.v[buf][0]);
         auto kfrag = [&](int kt, int ks) -> bf16x8 {
-          return *(const bf16x8*)(ks_ + (l32 + 32 * kt) * KP + 8 * hh + 16 * ks);
+          return *(const __attribute__((address_space(3))) bf16x8*)(kst + koff[ks] + kt * 32 * D * 2);
         };
         auto vfrag = [&](int mt, int ks) -> bf16x8 {
-          return *(const bf16x8*)(vt_ + (l32 + 32 * mt) * VP + 8 * hh + 16 * ks);
+          typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vst + voff0[mt] + ks * 16 * D * 2));
+          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vst + voff1[mt] + ks * 16 * D * 2));
+          const u32x2 ulo = __builtin_bit_cast(u32x2, lo), uhi = __builtin_bit_cast(u32x2, hi);
+          return __builtin_bit_cast(bf16x8, (u32x4){ulo[0], ulo[1], uhi[0], uhi[1]});
         };
         compute_tile(kb, kfrag, vfrag, masked_tile);
       }
