@@ -529,11 +529,7 @@ __global__ __launch_bounds__(64) void merge_kernel(const AttnParams p, int rows_
   if (p.sinks) sc *= nonempty ? 1.f / (1.f + __expf(p.sinks[qh] - lse)) : 0.f;
   bf16_t* orow = (bf16_t*)p.o + (long long)req * p.o_stride_req + (long long)n * p.o_stride_n +
                  (long long)qh * p.o_stride_h;
-#pragma unroll
-  for (int q4 = 0; q4 < 4; ++q4)
-    *(u32x2*)(orow + 32 * mt + 8 * q4 + 4 * hh) =
-        (u32x2){pack_bf16x2(acc[4 * q4] * sc, acc[4 * q4 + 1] * sc),
-                pack_bf16x2(acc[4 * q4 + 2] * sc, acc[4 * q4 + 3] * sc)};
+  store_row_block32(orow + 32 * mt, acc, sc, hh);
   if (p.lse && mt == 0 && hh == 0) {
     float* lrow = p.lse + (long long)req * p.lse_stride_req + (long long)n * p.lse_stride_n + qh;
     *lrow = p.lse_base2 ? lse * kLog2e : lse;

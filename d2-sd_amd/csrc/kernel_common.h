@@ -72,6 +72,28 @@ __device__ __forceinline__ u32x4 image_piece(const f32x16& o, int pr, float sc) 
                  pack_bf16x2(o[8 * pr + 4] * sc, o[8 * pr + 5] * sc), pack_bf16x2(o[8 * pr + 6] * sc, o[8 * pr + 7] * sc)};
 }
 
+// Store of one row's 32 head dims from a lane pair: lane l (row l % 32,
+// hh = l / 32) holds acc[4q + e] = dim 8q + 4hh + e, q < 4, e < 4, scaled by
+// sc.  The pair exchanges halves (v_permlane32_swap) so that lane hh writes
+// dims 16hh .. 16hh + 15 as two 16-byte stores instead of four 8-byte ones
+// (merge launch at config 2: 4.17 -> 4.04 us).  Both lanes of a pair must be
+// active.
+__device__ __forceinline__ void store_row_block32(bf16_t* dst, const float (&acc)[16], float sc, int hh) {
+  unsigned wd[4][2];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    wd[q][0] = pack_bf16x2(acc[4 * q] * sc, acc[4 * q + 1] * sc);
+    wd[q][1] = pack_bf16x2(acc[4 * q + 2] * sc, acc[4 * q + 3] * sc);
+  }
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    // after the swaps lane hh holds both halves of chunk c + 2hh
+    const auto a0 = __builtin_amdgcn_permlane32_swap(wd[c][0], wd[c + 2][0], false, false);
+    const auto a1 = __builtin_amdgcn_permlane32_swap(wd[c][1], wd[c + 2][1], false, false);
+    *(u32x4*)(dst + 8 * (c + 2 * hh)) = (u32x4){a0[0], a1[0], a0[1], a1[1]};
+  }
+}
+
 // fp8 e4m3fn (OCP) -> bf16, exact: every finite e4m3fn value is a bf16 value.
 // Bytes b0..b3 of w -> 4 bf16 in a u32x2, by the gfx950 converter
 // v_cvt_scalef32_pk_bf16_fp8 at scale 1 (word select 0: bytes 0, 1; 1: bytes

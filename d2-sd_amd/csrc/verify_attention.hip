@@ -999,11 +999,7 @@ __device__ __forceinline__ void merge_rows(const VerifyParams& p, int slot0, int
   float sc = nonempty ? 1.f / wsum : 0.f;
   if (p.sinks) sc *= nonempty ? 1.f / (1.f + __expf(p.sinks[qh] - lse)) : 0.f;
   bf16_t* orow = (bf16_t*)p.o + (long long)(q0 + n) * p.o_stride_n + (long long)qh * p.o_stride_h;
-#pragma unroll
-  for (int q4 = 0; q4 < 4; ++q4)
-    *(u32x2*)(orow + 32 * mt + 8 * q4 + 4 * hh) =
-        (u32x2){pack_bf16x2(acc[4 * q4] * sc, acc[4 * q4 + 1] * sc),
-                pack_bf16x2(acc[4 * q4 + 2] * sc, acc[4 * q4 + 3] * sc)};
+  store_row_block32(orow + 32 * mt, acc, sc, hh);
   if (p.lse && mt == 0 && hh == 0)
     p.lse[(long long)(q0 + n) * p.lse_stride_n + qh] = p.lse_base2 ? lse * kLog2e : lse;
 }
