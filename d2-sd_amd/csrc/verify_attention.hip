@@ -836,11 +836,15 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
       load_tile(kv_begin);
       store_tile(0);
     }
+    if (1 < ntiles) load_tile(kv_begin + 64);
     __syncthreads();
     auto step = [&](int it, auto masked_tile) {
       const int buf = it & 1;
       const int kb = kv_begin + it * 64;
-      if (it + 1 < ntiles) load_tile(kb + 64);
+      // tile it + 1 (loaded during the previous step) into the free buffer,
+      // then the loads of tile it + 2, then the compute of tile it
+      if (it + 1 < ntiles) store_tile(buf ^ 1);
+      if (it + 2 < ntiles) load_tile(kb + 128);
       if (live) {
         const lds_char* kst = (const lds_char*)(uintptr_t)lds_address(&sm.st.k[buf][0]);
         const lds_char* vst = (const lds_char*)(uintptr_t)lds_address(&sm.st.v[buf][0]);
@@ -856,7 +860,6 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
         };
         compute_tile(kb, kfrag, vfrag, masked_tile);
       }
-      if (it + 1 < ntiles) store_tile(buf ^ 1);
       __syncthreads();
     };
     const int nfull = (kv_end - kv_begin) >> 6;
