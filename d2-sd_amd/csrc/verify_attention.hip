@@ -460,8 +460,10 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
   auto pipelined_tile = [&](f32x16 (&sc)[RB][2], auto&& kfrag_n, auto&& vfrag) {
     constexpr int Q1 = KS / 4;  // QK^T k-steps beside the row max
     // A wave computing a tile step wins instruction issue over a wave of its
-    // SIMD that is at its step's wait and DMA issue (config 2 attention
-    // -2.3%, config 4 -1.4%, the others within noise; A/B in one session).
+    // SIMD that is at its step's wait and DMA issue (attention launch of a
+    // 150-node Qwen3-8B tree over a 4096-key paged prefix -2.3%, of the
+    // GPT-OSS-20B head shape over 8192 keys -1.4%, other shapes within noise;
+    // A/B in one session).
     __builtin_amdgcn_s_setprio(1);
     f32x16 sn[RB][2];
     static_for<Q1>([&](auto ks) { qk_ks(sn, kfrag_n, decltype(ks)::value); });
