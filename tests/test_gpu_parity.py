@@ -548,6 +548,46 @@ def test_page_permutation_is_bit_invariant():
     assert torch.equal(o2, outs[0][0]) and torch.equal(l2, outs[0][1])
 
 
+@pytest.mark.parametrize("waves,d", [(4, 128), (8, 128), (4, 64)])
+def test_fp8_pool_equals_bf16_pool_of_the_same_values(waves, d):
+    """An fp8 e4m3fn pool and a bf16 pool holding exactly its values (every
+    finite byte, times a power-of-two scale) give bit-identical outputs: the
+    kernel's fp8 -> bf16 expansion is exact, and a power-of-two scale is
+    exact on either side (the fp8 path applies it to scores and O, the bf16
+    pool carries it in its values)."""
+    hq, hkv, P, L = (32 if d == 128 else 64), 8, 16, 1024
+    tr = dtree.d3_verify_tree(np.random.default_rng(5).uniform(size=15))
+    N = tr.num_nodes
+    g = torch.Generator().manual_seed(17)
+    pages = L // P
+    finite = torch.tensor([b for b in range(256) if b & 0x7F != 0x7F], dtype=torch.uint8)
+
+    def pool():
+        return finite[torch.randint(0, finite.numel(), (pages + 2, hkv, P, d), generator=g)].view(torch.float8_e4m3fn)
+
+    k8, v8 = pool(), pool()
+    s = 2.0 ** -6
+    kb, vb = (k8.float() * s).to(torch.bfloat16), (v8.float() * s).to(torch.bfloat16)
+    assert torch.equal(kb.float(), k8.float() * s) and torch.equal(vb.float(), v8.float() * s)
+    table = torch.randperm(pages + 2, generator=g)[:pages].to(torch.int32).to(DEV)
+    q = torch.randn(N, hq, d, generator=g).to(torch.bfloat16).to(DEV)
+    ksuf = torch.randn(N, hkv, d, generator=g).to(torch.bfloat16).to(DEV)
+    vsuf = torch.randn(N, hkv, d, generator=g).to(torch.bfloat16).to(DEV)
+    sc = torch.full((hkv,), s, dtype=torch.float32, device=DEV)
+    common = dict(tree_masks=[tr.ancestor_mask()], page_size=P, page_indptr=[0, pages], page_table=table,
+                  kv_layout="HND", waves_per_block=waves)
+    a8 = d2sd.CascadeVerifyAttention(DEV).plan([0, N], [L], hq, hkv, d, kv_dtype=torch.float8_e4m3fn,
+                                               k_scale=sc, v_scale=sc, **common)
+    ab = d2sd.CascadeVerifyAttention(DEV).plan([0, N], [L], hq, hkv, d, **common)
+    assert (a8.info.num_items, a8.info.max_splits_used) == (ab.info.num_items, ab.info.max_splits_used)
+    o8, l8 = a8.run(q, ksuf, vsuf, k8.to(DEV), v8.to(DEV))
+    ob, lb = ab.run(q, ksuf, vsuf, kb.to(DEV), vb.to(DEV))
+    torch.cuda.synchronize()
+    assert torch.isfinite(ob.float()).all()
+    assert torch.equal(o8, ob) and torch.equal(l8, lb), \
+        f"max |dO| {(o8.float() - ob.float()).abs().max().item():.3e}, max |dLSE| {(l8 - lb).abs().max().item():.3e}"
+
+
 def test_tree_flow_equals_reference_row_flow():
     """plan/run over unique nodes == the reference's row flow (single prefill +
     CascadeGraphRunner) gathered through node_index."""
