@@ -205,10 +205,12 @@ class CascadeVerifyAttention:
             raise ValueError("sinks must have num_qo_heads entries")
         self.kv_dtype = kv_dtype
         if fp8:
-            if k_scale is None or v_scale is None:
+            # the scales dequantise prefix keys / values; a plan without any
+            # prefix key needs none (as d2sd_cascade_run)
+            if any(int(x) > 0 for x in prefix_len) and (k_scale is None or v_scale is None):
                 raise ValueError("fp8 KV needs k_scale and v_scale")
-            self.k_scale = k_scale.to(device=dev, dtype=torch.float32).contiguous()
-            self.v_scale = v_scale.to(device=dev, dtype=torch.float32).contiguous()
+            self.k_scale = k_scale.to(device=dev, dtype=torch.float32).contiguous() if k_scale is not None else None
+            self.v_scale = v_scale.to(device=dev, dtype=torch.float32).contiguous() if v_scale is not None else None
         else:
             self.k_scale = self.v_scale = None
         self.lse_base2 = bool(lse_base2)

@@ -453,6 +453,17 @@ def test_cascade_random_problems(seed):
                                  f"waves {waves})")
 
 
+def test_fp8_plan_without_prefix_keys_needs_no_scales():
+    """fp8 scales dequantise prefix keys only: a plan whose requests have no
+    prefix key takes none (as d2sd_cascade_run) and matches the oracle."""
+    rng = np.random.default_rng(7)
+    reqs = [wl.Request(wl.random_branch_tree(rng, 3, 16), 0), wl.Request(wl.random_branch_tree(rng, 2, 8), 0)]
+    prob = wl.VerifyProblem("fp8_noprefix", 32, 8, 128, reqs, page_size=16, kv_dtype=torch.float8_e4m3fn, seed=7)
+    mp, _, outs = _run_problem(prob)
+    assert mp.k_scale is None and mp.v_scale is None
+    _check_problem(mp, outs, tag="fp8 plan without prefix keys")
+
+
 def test_dynamic_prefix_many_requests():
     """Ten requests (more than the kernel preloads with the work item): each
     at a ragged run-time length below its planned one, against the oracle."""
