@@ -12,6 +12,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libd2sd.so"
 TORCH_LIB_PATH = Path(__file__).resolve().parent / "libd2sd_torch.so"
 
 D2SD_OK = 0
+D2SD_ERR_WORKSPACE = 3
 D2SD_KV_BF16 = 0
 D2SD_KV_FP8_E4M3 = 1
 D2SD_MASK_NONE = 0

@@ -148,10 +148,18 @@ class CascadeVerifyAttention:
         desc.waves_per_block = waves_per_block
         desc.dynamic_prefix = int(bool(dynamic_prefix))
         info = _lib.PlanInfo()
-        check(lib.d2sd_cascade_plan(C.byref(desc), None, 0, C.byref(info)), "cascade_plan (size)")
-        host = np.zeros(max(info.plan_ints, 8), dtype=np.int32)
-        check(lib.d2sd_cascade_plan(C.byref(desc), host.ctypes.data_as(C.POINTER(C.c_int32)), host.size,
-                                    C.byref(info)), "cascade_plan")
+        # One planner pass into a buffer of the previous plan's capacity (or
+        # 16K entries); a plan that needs more is planned again at its size.
+        prev = getattr(self, "plan_host", None)
+        host = np.zeros(max(prev.size if prev is not None else 0, 1 << 14), dtype=np.int32)
+        rc = lib.d2sd_cascade_plan(C.byref(desc), host.ctypes.data_as(C.POINTER(C.c_int32)), host.size,
+                                   C.byref(info))
+        if rc == _lib.D2SD_ERR_WORKSPACE and info.plan_ints > host.size:
+            host = np.zeros(info.plan_ints, dtype=np.int32)
+            rc = lib.d2sd_cascade_plan(C.byref(desc), host.ctypes.data_as(C.POINTER(C.c_int32)), host.size,
+                                       C.byref(info))
+        check(rc, "cascade_plan")
+        host = host[:max(info.plan_ints, 8)]
         old = getattr(self, "info", None) if self._planned else None
         same = old is not None and all(
             getattr(old, f) == getattr(info, f) for f in
