@@ -705,6 +705,7 @@ def measure_qk_rope(args) -> int:
 # the other workloads of the verify path (parity cases of the tests), each
 # timed as a hipGraph of `layers` calls over distinct KV pools
 OTHER_WORKLOADS = {
+    "northstar": lambda wl, seed: (wl.northstar(seed), 36),  # 16.8 MB of KV per layer, 36 pools
     "config1": lambda wl, seed: (wl.config1(seed), 64),      # 4.2 MB of KV per call: 64 pools pass the MALL
     "config3": lambda wl, seed: (wl.config3(seed), 2),       # ~670 MB of KV per call
     "config4_full": lambda wl, seed: (wl.config4(seed), 12),
@@ -946,6 +947,7 @@ def measure_workload(args) -> int:
         attn_us = time_graph(graphs["attention"], reps, torch) * 1e3 / nl
         ab, af = wl.attention_launch_bytes_flops(prob)
         vb, vf = wl.verify_bytes_flops(prob)
+        pb, pf = wl.prefix_bytes_flops(prob)
         t_hbm, t_mfma = ab / (HBM_PEAK_GBPS * 1e9), af / (MFMA_BF16_PEAK_TFLOPS * 1e12)
         bound = "mfma" if t_mfma > t_hbm else "hbm"
         hbm = ab / (attn_us * 1e-6) / 1e9
@@ -961,6 +963,14 @@ def measure_workload(args) -> int:
             "roofline_floor_us": max(t_hbm, t_mfma) * 1e6,
             "frac": max(t_hbm, t_mfma) / (attn_us * 1e-6),
             "call_bytes": vb, "call_flops": vf, "queries_per_s": T / (call_us * 1e-6),
+            # the prefix level's algorithmic bytes / flops over the attention
+            # launch, which also runs the suffix level: a lower bound on the
+            # prefix level's own fractions
+            "prefix_level": {"bytes": pb, "flops": pf, "hbm_frac_lower_bound": pb / (attn_us * 1e-6) / 1e9 /
+                             HBM_PEAK_GBPS, "mfma_frac_lower_bound": pf / (attn_us * 1e-6) / 1e12 /
+                             MFMA_BF16_PEAK_TFLOPS, "hbm_ceiling": min(1.0, (pb / (HBM_PEAK_GBPS * 1e9)) /
+                                                                       max(pb / (HBM_PEAK_GBPS * 1e9),
+                                                                           pf / (MFMA_BF16_PEAK_TFLOPS * 1e12)))},
             "plan": {"workgroups": info.num_items, "waves": info.waves_per_block,
                      "splits": info.max_splits_used, "merges": info.num_merges},
             **({"cpu_baseline": cpu_baseline(mp, max(args.cpu_reps, 20), torch, prob.name)}

@@ -325,6 +325,22 @@ int d2sd_cascade_plan(const d2sd_cascade_plan_desc* desc, int32_t* host_plan, si
   if (desc->window_left < -1) return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: window_left must be >= -1");
   d2sd::VerifyPlanOutput out{};
   d2sd::plan_verify(in, out);
+  if (desc->page_size > 0) {
+    // every paged prefix chunk must fit the kernel's staged page ids (the
+    // planner bounds chunks by verify_max_chunk_tiles; this is the check)
+    int lg = 0;
+    while ((1 << lg) < desc->page_size) ++lg;
+    for (const auto& w : out.items) {
+      if (w.mode == d2sd::MODE_NOOP || w.src != d2sd::SRC_PREFIX) continue;
+      const long long pages = desc->dynamic_prefix
+                                  ? ((long long)w.kv_end - w.kv_begin + 63 + desc->page_size - 2) / desc->page_size + 1
+                                  : d2sd::pages_spanned(w.kv_begin, w.kv_end, lg);
+      if (pages > d2sd::kMaxStagedPages)
+        return fail(D2SD_ERR_UNSUPPORTED, "cascade_plan: a prefix chunk spans " + std::to_string(pages) +
+                                              " pages, more than the kernel stages (" +
+                                              std::to_string(d2sd::kMaxStagedPages) + ")");
+    }
+  }
   static_assert(sizeof(d2sd::VerifyItem) == 16 * sizeof(int32_t), "VerifyItem layout");
   static_assert(sizeof(d2sd::VerifyMerge) == 8 * sizeof(int32_t), "VerifyMerge layout");
   std::memset(info, 0, sizeof(*info));
@@ -354,6 +370,9 @@ int d2sd_cascade_plan(const d2sd_cascade_plan_desc* desc, int32_t* host_plan, si
           extent, (int64_t)(desc->prefix_tok_indptr ? desc->prefix_tok_indptr[r] : 0) + desc->prefix_len[r]);
   }
   info->prefix_extent = extent;
+  int max_q = 0;
+  for (int r = 0; r < desc->num_reqs; ++r) max_q = std::max(max_q, desc->qo_indptr[r + 1] - desc->qo_indptr[r]);
+  info->max_qo_len = max_q;
   if (host_plan) {
     if (host_plan_ints < (size_t)info->plan_ints)
       return fail(D2SD_ERR_WORKSPACE, "cascade_plan: host_plan too small (need " +
@@ -410,6 +429,10 @@ static int build_verify_params(const d2sd_cascade_plan_info* info, const d2sd_ca
     return fail(D2SD_ERR_INVALID_ARG, "cascade_run: mask_mode");
   if (a->mask_mode == D2SD_MASK_TREE && (!a->tree_mask || a->mask_words <= 0))
     return fail(D2SD_ERR_INVALID_ARG, "cascade_run: tree mask needs tree_mask and mask_words");
+  if (a->mask_mode == D2SD_MASK_TREE && (long long)a->mask_words * 64 < info->max_qo_len)
+    return fail(D2SD_ERR_INVALID_ARG, "cascade_run: mask_words (" + std::to_string(a->mask_words) +
+                                          ") must cover the widest request's " + std::to_string(info->max_qo_len) +
+                                          " nodes (" + std::to_string((info->max_qo_len + 63) / 64) + " words)");
   if (info->kv_dtype == D2SD_KV_FP8_E4M3 && has_prefix && (!a->k_scale || !a->v_scale))
     return fail(D2SD_ERR_INVALID_ARG, "cascade_run: fp8 prefix needs k_scale and v_scale");
   if (!(a->sm_scale > 0.f) || !std::isfinite(a->sm_scale))
@@ -474,10 +497,11 @@ static int build_verify_params(const d2sd_cascade_plan_info* info, const d2sd_ca
 // length as an argument, so a cache that grows step by step reuses one plan
 // per bucket.  Without a prefix (qo_len == kv_len, e.g. a row's local causal
 // attention) the plan has suffix items only, which write the output in one
-// launch.  The first
-// call of a shape plans and uploads (hipMalloc, hipMemcpy); under stream
-// capture, past kSinglePlanCap cached shapes, or for shapes the cascade form
-// does not cover, the caller falls back to the single-source kernels.
+// launch.  The first call of a shape plans and uploads (hipMalloc and a copy
+// on a library-owned stream, see upload_single_plan); when the caller's
+// stream is being captured, past kSinglePlanCap cached shapes, or for shapes
+// the cascade form does not cover, the caller falls back to the
+// single-source kernels.
 // ---------------------------------------------------------------------------
 namespace {
 
@@ -530,6 +554,51 @@ bool single_cascade_plan(int qo_len, int kv_len, int hq, int hkv, int d, d2sd_ca
   return ok;
 }
 
+// Device copy of a single-prefill plan (kept until the process ends).  The
+// upload may run while a stream of any thread is being captured: this thread
+// switches to relaxed capture mode for the allocation, so that it neither
+// fails nor invalidates another thread's global-mode capture, and the copy
+// goes through a library-owned non-blocking stream, never the legacy null
+// stream, which would synchronise with (and so break) a capturing stream.
+// *dev stays null (and the caller falls back to the single-source kernels)
+// when the allocation fails.
+int upload_single_plan(const std::vector<int32_t>& host, int32_t** dev) {
+  *dev = nullptr;
+  static std::vector<hipStream_t> streams;  // one per device, under g_single_mu
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) {
+    (void)hipGetLastError();
+    return D2SD_OK;
+  }
+  hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+  if (hipThreadExchangeStreamCaptureMode(&mode) != hipSuccess) {
+    (void)hipGetLastError();
+    return D2SD_OK;
+  }
+  int rc = D2SD_OK;
+  int32_t* p = nullptr;
+  if ((int)streams.size() <= device) streams.resize(device + 1, nullptr);
+  if (!streams[device] && hipStreamCreateWithFlags(&streams[device], hipStreamNonBlocking) != hipSuccess) {
+    (void)hipGetLastError();
+    streams[device] = nullptr;
+  } else if (hipMalloc((void**)&p, host.size() * sizeof(int32_t)) != hipSuccess) {
+    (void)hipGetLastError();
+    p = nullptr;
+  } else {
+    hipError_t e = hipMemcpyAsync(p, host.data(), host.size() * sizeof(int32_t), hipMemcpyHostToDevice,
+                                  streams[device]);
+    if (e == hipSuccess) e = hipStreamSynchronize(streams[device]);
+    if (e != hipSuccess) {
+      (void)hipFree(p);
+      p = nullptr;
+      rc = fail_hip(e, "single_prefill: plan upload");
+    }
+  }
+  (void)hipThreadExchangeStreamCaptureMode(&mode);
+  *dev = p;
+  return rc;
+}
+
 }  // namespace
 
 static size_t single_cascade_workspace(int qo_len, int kv_len, int hq, int hkv, int d, int window_left) {
@@ -576,14 +645,8 @@ static int single_prefill_cascade(const void* q, int64_t q_stride_n, int64_t q_s
       if (cs != hipStreamCaptureStatusNone || g_single_plans.size() >= kSinglePlanCap) return D2SD_OK;
       std::vector<int32_t> host;
       if (!single_cascade_plan(qo_len, kv_len, hq, hkv, d, &sp.info, &host)) return D2SD_OK;
-      if (hipMalloc((void**)&sp.plan_dev, host.size() * sizeof(int32_t)) != hipSuccess) {
-        (void)hipGetLastError();
-        return D2SD_OK;
-      }
-      if (hipError_t e = hipMemcpy(sp.plan_dev, host.data(), host.size() * sizeof(int32_t), hipMemcpyHostToDevice)) {
-        (void)hipFree(sp.plan_dev);
-        return fail_hip(e, "single_prefill: plan upload");
-      }
+      if (int rc = upload_single_plan(host, &sp.plan_dev)) return rc;
+      if (!sp.plan_dev) return D2SD_OK;
       g_single_plans.emplace(key, sp);
     }
   }

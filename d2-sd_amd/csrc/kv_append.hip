@@ -16,7 +16,8 @@
 // cascade kernels dequantise): each value becomes e4m3fn(x / scale), the
 // quotient correctly rounded in fp32, clamped to +-448 (the largest finite
 // e4m3fn) and rounded to nearest even - torch's float -> float8_e4m3fn cast
-// after a clamp (the cast alone turns |q| >= 480 into NaN).
+// after a clamp (the cast alone turns |q| >= 480 into NaN); a NaN quotient
+// becomes the e4m3fn NaN byte 0x7F with its sign, as torch's clamp and cast.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -77,9 +78,16 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const KvAppendParams p) 
       unsigned b[2] = {0u, 0u};
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const unsigned bits = (w[e >> 1] >> (16 * (e & 1))) << 16;
-        const float q = fminf(fmaxf(__fdiv_rn(__uint_as_float(bits & 0xFFFF0000u), s), -448.f), 448.f);
-        b[e >> 2] |= e4m3fn_byte(q) << (8 * (e & 3));
+        const unsigned bits = ((w[e >> 1] >> (16 * (e & 1))) << 16) & 0xFFFF0000u;
+        const float x = __uint_as_float(bits);
+        const float qr = __fdiv_rn(x, s);
+        const float q = fminf(fmaxf(qr, -448.f), 448.f);
+        // a NaN quotient stays NaN (torch's clamp keeps it; the cast makes it
+        // 0x7F with the NaN's sign: x's when x is NaN, else s's, else the
+        // negative default NaN of 0/0 and inf/inf); fminf / fmaxf would
+        // turn it into -448
+        const unsigned nan_byte = 0x7Fu | ((isnan(x) ? bits : isnan(s) ? __float_as_uint(s) : 0x80000000u) >> 24 & 0x80u);
+        b[e >> 2] |= (isnan(qr) ? nan_byte : e4m3fn_byte(q)) << (8 * (e & 3));
       }
       uint8_t* pool = (uint8_t*)(is_v ? p.v_pool[layer] : p.k_pool[layer]);
       *(uint2*)(pool + dst) = uint2{b[0], b[1]};

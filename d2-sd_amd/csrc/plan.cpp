@@ -120,8 +120,10 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
   const int cus_per_xcd = std::max(1, num_cus / 8);
   const int xcd_slots = cus_per_xcd * wpc;
   const int split_cap = in.max_splits > 0 ? std::min(in.max_splits, kMaxVerifySplits) : kMaxVerifySplits;
-  // a chunk's page ids must fit the kernel's LDS staging
-  const int max_chunk = in.page_size > 0 ? std::max(1, ((kMaxStagedPages - 8) * in.page_size) / 64) : (1 << 30);
+  // A chunk's page ids must fit the kernel's LDS staging; this bound wins over
+  // split_cap (a group then has more than split_cap chunks, which the merge
+  // takes in batches).
+  const int max_chunk = verify_max_chunk_tiles(in.page_size);
   constexpr int kMinChunk = 2;  // shorter chunks cost more in partials than they gain in balance
 
   std::vector<int> nq(R), qtiles(R), ptiles(R), stiles(R), kv0(R), kv1(R);
@@ -199,7 +201,7 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
       return n;
     };
     while (T < maxpt && count(T) > budget) ++T;
-    T = std::min(T, std::max(max_chunk, tmin));
+    T = std::min(T, max_chunk);
     long long used = 0;
     std::vector<int> n(cells.size());
     for (size_t i = 0; i < cells.size(); ++i) {

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime_api.h>
 #include <stddef.h>
 
+#include <algorithm>
 #include <vector>
 
 #include "d2sd_internal.h"
@@ -37,6 +38,24 @@ struct VerifyPlanOutput {
 };
 
 int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out);
+
+// Pages that keys [b, e) of a pool with 2^log2_page keys per page span.
+inline long long pages_spanned(long long b, long long e, int log2_page) {
+  return e > b ? ((e - 1) >> log2_page) - (b >> log2_page) + 1 : 0;
+}
+
+// Longest prefix chunk (64-key tiles) whose page ids fit the kernel's LDS
+// staging (kMaxStagedPages) for page size P (0: contiguous, no bound).  A
+// dynamic plan's run-time chunk may start at any key and be up to 63 keys
+// longer than planned (its boundaries are rescaled and rounded to 64 keys,
+// the last one kept at the current length), so T tiles may read
+// 64 T + 63 keys: that spans at most (64 T + 61 + P) / P pages, which stays
+// <= kMaxStagedPages iff 64 T <= (kMaxStagedPages - 1) P - 62.
+inline int verify_max_chunk_tiles(int page_size) {
+  if (page_size <= 0) return 1 << 30;
+  const long long t = ((long long)(kMaxStagedPages - 1) * page_size - 62) / 64;
+  return (int)std::max<long long>(1, std::min<long long>(t, 1 << 30));
+}
 // Workgroups of the attention launch resident per CU (LDS bound) and packed
 // rows per workgroup, by waves per workgroup (2: 64-row waves; 4, 8: 32-row
 // waves).

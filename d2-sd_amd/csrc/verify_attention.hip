@@ -222,7 +222,10 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
   if constexpr (STAGED) {
     if (ntiles > 0) {
       pg_first = kv_begin >> log2p;
-      npg = ((kv_end - 1) >> log2p) - pg_first + 1;  // <= kMaxStagedPages (planner)
+      // the planner keeps every chunk within kMaxStagedPages pages; the clamp
+      // only bounds what a bad plan can reach (keys past the staged pages
+      // then read the last staged page, never an unstaged LDS word)
+      npg = min(((kv_end - 1) >> log2p) - pg_first + 1, kMaxStagedPages);
       const int* pt = S.page_table + w.base + pg_first;
       // unconditional (index clamped into the range) so that the wait before
       // the LDS stores below counts exactly the loads issued after these
@@ -279,7 +282,8 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
 
   auto tok_off = [&](int t) -> long long {
     if constexpr (STAGED)
-      return (long long)pages[(t >> log2p) - pg_first] * page_b + (long long)(t & pmask) * tok_b;
+      return (long long)pages[min((unsigned)((t >> log2p) - pg_first), (unsigned)max(npg - 1, 0))] * page_b +
+             (long long)(t & pmask) * tok_b;
     else if constexpr (PAGED)
       return (long long)min((unsigned)S.page_table[w.base + (t >> log2p)], (unsigned)S.num_pages - 1u) * page_b +
              (long long)(t & pmask) * tok_b;
@@ -548,7 +552,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
         auto page_of = [&](int row) -> int {
           const int pi = min(row >> log2p, last_page);
           if constexpr (STAGED) {
-            return pages[min(max(pi - pg_first, 0), kMaxStagedPages - 1)];
+            return pages[min(max(pi - pg_first, 0), max(npg - 1, 0))];
           } else {
             typedef const __attribute__((address_space(4))) int const_int;
             return ntiles > 0

@@ -88,6 +88,7 @@ class PlanInfo(C.Structure):
         ("dynamic_prefix", C.c_int),
         ("window_left", C.c_int),
         ("prefix_extent", C.c_int64),
+        ("max_qo_len", C.c_int),
     ]
 
 

@@ -17,11 +17,18 @@ plan() does all host work and device uploads; run() only launches kernels
 partial states, then their merge), allocates nothing when `out`/`lse` are
 given, and can be captured into a HipGraph.
 
-Device buffers (plan, workspace, tree mask, page table, prefix lengths) are
-kept across plan() calls: a re-plan with the same shape (work items, merges,
-partial slots, mask width) rewrites them in place, so a graph captured
-earlier replays the new plan; a re-plan of another shape allocates new
-buffers, and a graph captured earlier keeps (and keeps using) its own.  With
+Device buffers.  The plan, workspace, tree mask and prefix lengths are
+always plan-owned.  A page table, sinks or fp8 scales given as a contiguous
+device tensor of the kernel's dtype (int32 / float32) are used in place (the
+caller may update them between replays); given any other way they are
+copied into a plan-owned buffer.  A re-plan with the same shape (work items,
+merges, partial slots, mask width, the same optional inputs) rewrites every
+plan-owned buffer in place, so a graph captured earlier replays the new plan;
+after a run() has been captured, such a re-plan raises rather than hand a
+buffer of another identity to the kernels (a caller tensor other than the
+one used in place before, or a changed mask width), since the graph would go
+on reading the old one.  A re-plan of another shape allocates new buffers,
+and a graph captured earlier keeps (and keeps using) its own.  With
 dynamic_prefix=True, prefix_len is each request's largest prefix and the
 kernels read the current lengths from `prefix_len_dev` (int32, on the
 device), so one captured step replays while the cache grows.
@@ -60,6 +67,42 @@ class CascadeVerifyAttention:
     def __init__(self, device: Union[str, torch.device, None] = None):
         self.device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
         self._planned = False
+        self._captured = False   # a run() was recorded into a graph
+        self._owned = set()      # names of the optional-input buffers the plan owns
+
+    def _in_place(self, t: torch.Tensor, dtype: torch.dtype) -> bool:
+        return t.device == self.device and t.dtype == dtype and t.is_contiguous()
+
+    def _keeps(self, name: str, src, dtype: torch.dtype) -> bool:
+        """Whether _input_buffer(name, src, ...) of a same-shape re-plan
+        returns the buffer the kernels read now."""
+        old = getattr(self, name, None)
+        if src is None or old is None:
+            return src is None and old is None
+        t = src if isinstance(src, torch.Tensor) else None
+        if t is not None and self._in_place(t, dtype):
+            return name not in self._owned and t.data_ptr() == old.data_ptr() and t.numel() == old.numel()
+        n = t.numel() if t is not None else int(np.asarray(src).size)
+        return name in self._owned and old.numel() == n
+
+    def _input_buffer(self, name: str, src, dtype: torch.dtype, same: bool) -> Optional[torch.Tensor]:
+        """Device buffer for an optional input (page table, sinks, scales):
+        a contiguous device tensor of `dtype` is used in place; anything else
+        goes into a plan-owned buffer, rewritten in place by a same-shape
+        re-plan when the sizes agree."""
+        old = getattr(self, name, None)
+        if src is None:
+            self._owned.discard(name)
+            return None
+        t = src if isinstance(src, torch.Tensor) else torch.from_numpy(np.ascontiguousarray(np.asarray(src)))
+        if self._in_place(t, dtype):
+            self._owned.discard(name)
+            return t
+        if same and name in self._owned and old is not None and old.numel() == t.numel():
+            old.copy_(t.reshape(-1).to(dtype))
+            return old
+        self._owned.add(name)
+        return t.to(device=self.device, dtype=dtype).reshape(-1).contiguous().clone()
 
     # ------------------------------------------------------------------ plan
     def plan(
@@ -148,23 +191,71 @@ class CascadeVerifyAttention:
         desc.waves_per_block = waves_per_block
         desc.dynamic_prefix = int(bool(dynamic_prefix))
         info = _lib.PlanInfo()
-        # One planner pass into a buffer of the previous plan's capacity (or
-        # 16K entries); a plan that needs more is planned again at its size.
-        prev = getattr(self, "plan_host", None)
-        host = np.zeros(max(prev.size if prev is not None else 0, 1 << 14), dtype=np.int32)
-        rc = lib.d2sd_cascade_plan(C.byref(desc), host.ctypes.data_as(C.POINTER(C.c_int32)), host.size,
+        # One planner pass into a host buffer kept across plans (16K entries at
+        # first); a plan that needs more is planned again into a larger one.
+        buf = getattr(self, "_plan_host_buf", None)
+        if buf is None:
+            buf = np.zeros(1 << 14, dtype=np.int32)
+        rc = lib.d2sd_cascade_plan(C.byref(desc), buf.ctypes.data_as(C.POINTER(C.c_int32)), buf.size,
                                    C.byref(info))
-        if rc == _lib.D2SD_ERR_WORKSPACE and info.plan_ints > host.size:
-            host = np.zeros(info.plan_ints, dtype=np.int32)
-            rc = lib.d2sd_cascade_plan(C.byref(desc), host.ctypes.data_as(C.POINTER(C.c_int32)), host.size,
+        if rc == _lib.D2SD_ERR_WORKSPACE and info.plan_ints > buf.size:
+            buf = np.zeros(info.plan_ints, dtype=np.int32)
+            rc = lib.d2sd_cascade_plan(C.byref(desc), buf.ctypes.data_as(C.POINTER(C.c_int32)), buf.size,
                                        C.byref(info))
         check(rc, "cascade_plan")
-        host = host[:max(info.plan_ints, 8)]
+        self._plan_host_buf = buf
+        host = buf[:max(info.plan_ints, 8)].copy()
+
+        # ---- inputs, checked before any buffer is touched ----
+        mode = _MASK_MODES[mask_mode]
+        packed = None
+        if mode == _lib.D2SD_MASK_TREE:
+            if tree_masks is None or len(tree_masks) != R:
+                raise ValueError("mask_mode 'tree' needs one ancestor mask per request")
+            for r, m in enumerate(tree_masks):
+                n = int(qo[r + 1] - qo[r])
+                if m.shape != (n, n):
+                    raise ValueError(f"tree_masks[{r}] must be [{n}, {n}], got {m.shape}")
+            packed = pack_tree_masks([np.asarray(m, dtype=bool) for m in tree_masks])
+        pt = None
+        if int(page_size) > 0:
+            pt = (page_table if isinstance(page_table, torch.Tensor) else torch.from_numpy(_i32(page_table))).reshape(-1)
+            if pt.numel() < int(pi[-1]):
+                raise ValueError("page_table shorter than page_indptr[-1]")
+        if sinks is not None and sinks.numel() != num_qo_heads:
+            raise ValueError("sinks must have num_qo_heads entries")
+        if fp8:
+            # the scales dequantise prefix keys / values; a plan without any
+            # prefix key needs none (as d2sd_cascade_run)
+            if any(int(x) > 0 for x in prefix_len) and (k_scale is None or v_scale is None):
+                raise ValueError("fp8 KV needs k_scale and v_scale")
+        else:
+            k_scale = v_scale = None
+
         old = getattr(self, "info", None) if self._planned else None
         same = old is not None and all(
             getattr(old, f) == getattr(info, f) for f in
             ("num_items", "num_merges", "waves_per_block", "rows_per_tile", "num_slots", "num_reqs",
              "num_qo_heads", "num_kv_heads", "head_dim", "kv_dtype", "page_size", "dynamic_prefix"))
+        mask_words = int(packed.shape[1]) if packed is not None else 0
+        same_mask = same and packed is not None and getattr(self, "tree_mask_dev", None) is not None \
+            and self.mask_words == mask_words and self.tree_mask_dev.numel() >= packed.size
+        if same and self._captured:
+            # a graph captured earlier reads these buffers: refuse a re-plan
+            # that would give the kernels others
+            changed = [n for n, src, dt in (("page_table_dev", pt, torch.int32), ("sinks", sinks, torch.float32),
+                                            ("k_scale", k_scale, torch.float32), ("v_scale", v_scale, torch.float32))
+                       if not self._keeps(n, src, dt)]
+            if (packed is not None) != (getattr(self, "tree_mask_dev", None) is not None) or \
+                    (packed is not None and not same_mask):
+                changed.append("tree_mask_dev")
+            if changed:
+                raise RuntimeError(
+                    "CascadeVerifyAttention.plan: a graph captured earlier reads this plan's buffers, and this "
+                    f"re-plan would hand other ones to the kernels ({', '.join(changed)}); pass the same device "
+                    "tensors (or host data), or plan a new CascadeVerifyAttention and capture again")
+
+        # ---- device buffers ----
         self.info = info
         self.info_bytes = torch.frombuffer(bytearray(bytes(info)), dtype=torch.uint8)
         self.plan_host = host
@@ -175,52 +266,27 @@ class CascadeVerifyAttention:
         self.workspace = (self.workspace if same and getattr(self, "workspace", None) is not None
                           and self.workspace.numel() >= ws else torch.empty(ws, dtype=torch.uint8, device=dev))
         self.prefix_len_dev = _reuse(getattr(self, "prefix_len_dev", None), torch.from_numpy(pl.copy()).to(dev), same)
-        self.mask_mode = _MASK_MODES[mask_mode]
+        self.mask_mode = mode
         self.total_q = int(qo[-1])
-        if self.mask_mode == _lib.D2SD_MASK_TREE:
-            if tree_masks is None or len(tree_masks) != R:
-                raise ValueError("mask_mode 'tree' needs one ancestor mask per request")
-            for r, m in enumerate(tree_masks):
-                n = int(qo[r + 1] - qo[r])
-                if m.shape != (n, n):
-                    raise ValueError(f"tree_masks[{r}] must be [{n}, {n}], got {m.shape}")
-            packed = pack_tree_masks([np.asarray(m, dtype=bool) for m in tree_masks])
-            same_mask = same and getattr(self, "mask_words", None) == int(packed.shape[1])
-            self.mask_words = int(packed.shape[1])
+        self.mask_words = mask_words
+        if packed is not None:
             self.tree_mask_dev = _reuse(getattr(self, "tree_mask_dev", None),
                                         torch.from_numpy(packed.view(np.int64)).to(dev), same_mask)
         else:
-            self.mask_words = 0
             self.tree_mask_dev = None
         self.page_size = int(page_size)
-        if self.page_size > 0:
-            pt = page_table if isinstance(page_table, torch.Tensor) else torch.from_numpy(_i32(page_table))
-            if pt.numel() < int(pi[-1]):
-                raise ValueError("page_table shorter than page_indptr[-1]")
-            # a device int32 table is used in place (the caller may update it
-            # between replays); anything else is uploaded
-            self.page_table_dev = pt.to(device=dev, dtype=torch.int32).contiguous()
+        self.page_table_dev = self._input_buffer("page_table_dev", pt, torch.int32, same)
+        if pt is not None:
             ids = pt[:int(pi[-1])].to("cpu", torch.int64)
             self._page_id_range = (int(ids.min()), int(ids.max())) if ids.numel() else (0, -1)
-        else:
-            self.page_table_dev = None
         self.kv_layout = kv_layout
         self.num_qo_heads, self.num_kv_heads, self.head_dim = num_qo_heads, num_kv_heads, head_dim
         self.sm_scale = float(sm_scale) if sm_scale is not None else head_dim ** -0.5
         self.window_left = window_left
-        self.sinks = sinks.to(device=dev, dtype=torch.float32).contiguous() if sinks is not None else None
-        if self.sinks is not None and self.sinks.numel() != num_qo_heads:
-            raise ValueError("sinks must have num_qo_heads entries")
+        self.sinks = self._input_buffer("sinks", sinks, torch.float32, same)
         self.kv_dtype = kv_dtype
-        if fp8:
-            # the scales dequantise prefix keys / values; a plan without any
-            # prefix key needs none (as d2sd_cascade_run)
-            if any(int(x) > 0 for x in prefix_len) and (k_scale is None or v_scale is None):
-                raise ValueError("fp8 KV needs k_scale and v_scale")
-            self.k_scale = k_scale.to(device=dev, dtype=torch.float32).contiguous() if k_scale is not None else None
-            self.v_scale = v_scale.to(device=dev, dtype=torch.float32).contiguous() if v_scale is not None else None
-        else:
-            self.k_scale = self.v_scale = None
+        self.k_scale = self._input_buffer("k_scale", k_scale, torch.float32, same)
+        self.v_scale = self._input_buffer("v_scale", v_scale, torch.float32, same)
         self.lse_base2 = bool(lse_base2)
         self._planned = True
         return self
@@ -320,6 +386,8 @@ class CascadeVerifyAttention:
             raise ValueError("out must be bf16 [total_q, Hq, D] with contiguous head_dim")
         if lse.shape != (T, hq) or lse.dtype != torch.float32 or lse.stride(-1) != 1:
             raise ValueError("lse must be float32 [total_q, Hq] with contiguous heads")
+        if torch.cuda.is_current_stream_capturing():
+            self._captured = True
         a = _lib.RunArgs()
         a.plan = self.plan_dev.data_ptr()
         a.q = q.data_ptr()

@@ -114,6 +114,18 @@ def config2(seed: int = 0, layers: int = 36) -> VerifyProblem:
                          page_size=16, layers=layers, seed=seed, meta={"conf": conf.tolist()})
 
 
+def northstar(seed: int = 0, layers: int = 36) -> VerifyProblem:
+    """The north-star shape: Qwen3-8B heads (32/8, head_dim 128), paged prefix
+    4096 (page 16, random page permutation) and the "4 x 16 + 32" tree of the
+    d3 geometry (generation/d3_generator.py:123-147): a 32-token main row
+    (the DFlash block of 16 and its DTA continuation to block_size_2 = 32) and
+    four branches that each share the main row's first 16 tokens and add 16
+    of their own, N = 32 + 4 x 16 = 96 nodes."""
+    tree = tree_from_branches(32, [0, 0, 0, 0, 0], [32, 16, 16, 16, 16])
+    return VerifyProblem("northstar_qwen3_8b_L4096_paged16_tree4x16+32", 32, 8, 128, [Request(tree, 4096)],
+                         page_size=16, layers=layers, seed=seed)
+
+
 def config3(seed: int = 0, num_reqs: int = 8) -> VerifyProblem:
     """8 requests, prefix ~ U{8192..32768}, paged 16, 4 x 16 trees."""
     rng = np.random.default_rng(seed)

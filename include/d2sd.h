@@ -5,8 +5,15 @@
  * Every entry point takes raw device pointers, element strides (int64, in
  * units of elements, not bytes), plain sizes and a hipStream_t, and returns
  * 0 (D2SD_OK) or a non-zero status; d2sd_last_error() then holds a message.
- * Nothing here allocates device memory except d2sd_graph_end_capture (the
- * graph executable) — scratch space is always caller-provided.  The launch
+ * Scratch space is caller-provided (d2sd_cascade_run_noalloc uses a
+ * library-owned array instead).  Device memory is allocated in two places
+ * only: d2sd_graph_end_capture (the graph executable) and the first
+ * d2sd_single_prefill_with_kv_cache call of each shape, which plans and
+ * uploads that shape's work list once (hipMalloc plus a synchronous copy on a
+ * library-owned stream, in relaxed capture mode so that a capture running on
+ * another thread is not disturbed; kept until the process ends, at most 512
+ * shapes).  When the caller's stream is being captured that first call takes
+ * the single-source kernels instead, which allocate nothing.  The other launch
  * entry points never synchronise the host, so they may be captured into a
  * hipGraph.
  *
@@ -218,6 +225,8 @@ typedef struct {
   int64_t prefix_extent;  /* contiguous prefix: tokens k_prefix must hold
                              (max_r prefix_tok_indptr[r] + prefix_len[r]);
                              paged: page_table entries the plan reads */
+  int max_qo_len;         /* nodes of the widest request: a tree mask needs
+                             mask_words >= ceil(max_qo_len / 64) */
 } d2sd_cascade_plan_info;
 
 /* Fills host_plan (capacity host_plan_ints int32) with the work list; the
@@ -234,7 +243,7 @@ typedef struct {
   const void* v_suffix;
   int64_t suffix_stride_n, suffix_stride_h;
   int mask_mode;            /* D2SD_MASK_* for the suffix level */
-  int mask_words;           /* 64-bit words per tree-mask row */
+  int mask_words;           /* 64-bit words per tree-mask row (>= ceil(info.max_qo_len / 64)) */
   const uint64_t* tree_mask;
   const void* k_prefix;     /* bf16 or fp8 bytes; NULL when no request has a prefix */
   const void* v_prefix;

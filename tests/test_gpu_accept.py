@@ -16,6 +16,23 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_scaled_logits_ref_is_torch_gpu_division(dtype):
+    """The oracle's logits / T (what the sampled walk draws from,
+    model/utils.py:34) equals torch's own division of a device tensor by a
+    Python scalar, bit for bit, over 8 x 32000 logits of widely spread
+    magnitudes (subnormal to 1e4) at several temperatures."""
+    gen = torch.Generator().manual_seed(34)
+    lg = torch.randn(8, 32000, generator=gen) * torch.exp2(torch.randint(-140, 14, (8, 32000), generator=gen).float())
+    lg = lg.to(dtype)
+    lg_dev = lg.to(DEV)
+    for t in (1e-4, 0.3, 0.7, 1.0, 1.3, 2.5, 7.0):
+        got = (lg_dev / t).cpu().double().numpy()
+        want = orc.scaled_logits_ref(lg, t)
+        diff = got != want
+        assert not diff.any(), f"T={t}: {int(diff.sum())} of {diff.size} values differ"
+
+
 def _drafts_following(node_logits, node_index, keep, gen):
     """Draft tokens per (row, position): row r repeats the target's argmax
     chain for its first keep[r] positions, then random tokens."""

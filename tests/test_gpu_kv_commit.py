@@ -105,20 +105,21 @@ def test_commit_replays_in_a_graph():
 
 # ---- fp8 e4m3fn pools (the cascade kernels' fp8 format, value / scale) ----
 
-def _every_finite_bf16(rows, hkv, d):
+def _every_bf16(rows, hkv, d):
     bits = torch.arange(65536, dtype=torch.int32).to(torch.int16)
-    x = bits.view(torch.bfloat16)
-    x = torch.where(torch.isfinite(x), x, torch.zeros_like(x))
-    return x.view(rows, hkv, d)
+    return bits.view(torch.bfloat16).view(rows, hkv, d)
 
 
 def test_fp8_commit_quantises_every_bf16_value_like_the_oracle():
-    """All 65536 bf16 bit patterns (non-finite ones as 0) committed into an
-    fp8 pool, kv head 0 at scale 1 (the cast alone) and head 1 at 0.37 (the
-    fp32 quotient first): every byte equals the oracle's."""
+    """All 65536 bf16 bit patterns (infinities and NaNs of both signs
+    included) committed into an fp8 pool, kv head 0 at scale 1 (the cast
+    alone) and head 1 at 0.37 (the fp32 quotient first): every byte equals the
+    oracle's (a NaN stays the NaN byte 0x7F with its sign, an infinity
+    saturates at +-448)."""
     hkv, d, P = 2, 128, 16
     rows = 65536 // (hkv * d)
-    new = _every_finite_bf16(rows, hkv, d)
+    new = _every_bf16(rows, hkv, d)
+    assert torch.isnan(new).any() and torch.isinf(new).any()
     pages = rows // P
     g = torch.Generator().manual_seed(3)
     pool = (torch.randn(pages + 2, hkv, P, d, generator=g)).to(torch.float8_e4m3fn)

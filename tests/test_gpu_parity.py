@@ -281,6 +281,23 @@ def test_cascade_config5_subset():
     _check_problem(mp, outs, reqs=[0, 31], dtype=torch.float32, tag="cfg5")
 
 
+@pytest.mark.parametrize("hq,hkv,d,fp8,waves", [(64, 8, 128, True, 4), (64, 8, 64, False, 4),
+                                                (32, 8, 128, False, 8)])
+def test_page_size_1_prefix_beyond_staged_pages(hq, hkv, d, fp8, waves):
+    """A 16384-key prefix at one key per page: a group's key range holds more
+    page ids than one workgroup stages (1024), so the plan cuts it into more
+    than 15 chunks.  fp8 at D = 128 (register-staged tiles), bf16 at D = 64 and
+    8-wave D = 128 tiles (page ids staged for the DMA path), each against the
+    oracle."""
+    rng = np.random.default_rng(16384 + d + waves)
+    tree = wl.random_branch_tree(rng, 3, 16)
+    prob = wl.VerifyProblem(f"page1_{d}", hq, hkv, d, [wl.Request(tree, 16384)], page_size=1,
+                            kv_dtype=torch.float8_e4m3fn if fp8 else torch.bfloat16, seed=d + waves)
+    mp, attn, outs = _run_problem(prob, waves_per_block=waves)
+    assert attn.info.max_splits_used > 15
+    _check_problem(mp, outs, dtype=torch.float32, tag=f"page 1, L 16384, {hq}/{hkv}/{d}, fp8 {fp8}, waves {waves}")
+
+
 def _torch_fp32_request(mp, li, r):
     """fp32 torch reference of one request on the GPU, in the oracle's
     single-pass form: one masked softmax over [windowed prefix || suffix] with

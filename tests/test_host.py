@@ -36,7 +36,7 @@ def test_version_and_error_strings():
 
 
 def _plan(qo, pl, hq=32, hkv=8, d=128, window=-1, num_cus=256, waves=0, max_splits=0, page_size=16,
-          page_indptr=None, tok_indptr=None, dynamic=0):
+          page_indptr=None, tok_indptr=None, dynamic=0, kv_dtype=0):
     desc = _lib.PlanDesc()
     qo = np.asarray(qo, dtype=np.int32)
     pl = np.asarray(pl, dtype=np.int32)
@@ -51,7 +51,7 @@ def _plan(qo, pl, hq=32, hkv=8, d=128, window=-1, num_cus=256, waves=0, max_spli
     desc.prefix_tok_indptr = ti.ctypes.data_as(C.POINTER(C.c_int32)) if ti is not None else None
     desc.num_qo_heads, desc.num_kv_heads, desc.head_dim = hq, hkv, d
     desc.window_left = window
-    desc.kv_dtype = 0
+    desc.kv_dtype = kv_dtype
     desc.page_size = page_size
     desc.num_cus = num_cus
     desc.max_splits = max_splits
@@ -169,10 +169,76 @@ def test_plan_partitions_work(qo, pl, window, page, hq, waves):
                     assert mg[key][b][:4] == (s0, len(ch) + 1, qo[r], n)
                     if heads >= 8:
                         assert {mg[key][b][4]} == xcd_of[key]
-                assert len(ch) <= 15
+                # at most 15 chunks, unless the staged-page bound forces more
+                assert len(ch) <= 15 or (page and -(-(Leff + 63) // 64) > 15 * _max_chunk_tiles(page))
                 if page:
                     for a, b, _ in ch:
                         assert (b - 1) // page - a // page + 1 <= 1024
+
+
+def _max_chunk_tiles(page):
+    """The longest paged chunk (64-key tiles) the kernel can stage: 64 T + 63
+    keys from any start span at most 1024 pages."""
+    return max(1, (1023 * page - 62) // 64)
+
+
+@pytest.mark.parametrize("page", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("L", [1000, 16384, 32768, 131072, 262144])
+@pytest.mark.parametrize("d,hq,fp8,waves", [(128, 64, 1, 4), (128, 32, 0, 8), (64, 64, 0, 4), (64, 64, 1, 8)])
+@pytest.mark.parametrize("dynamic,window", [(0, -1), (1, -1), (1, 5000)])
+def test_plan_keeps_paged_chunks_within_staged_pages(page, L, d, hq, fp8, waves, dynamic, window):
+    """Every paged prefix item reads at most 1024 pages, the page ids one
+    workgroup stages in LDS, even where that needs more than 15 chunks per
+    group (page size 1 at 16K keys, 2 at 32K, 16 at 256K), and even for the
+    run-time chunks of a dynamic plan (up to 63 keys longer than planned,
+    from any start key); the chunks still cover each group's visible prefix
+    once."""
+    n = 40
+    info, items, merges = _plan([0, n], [L], hq=hq, hkv=8, d=d, window=window, waves=waves, page_size=page,
+                                dynamic=dynamic, kv_dtype=fp8)
+    live = items[items[:, MODE] != MODE_NOOP]
+    pre = live[live[:, SRC] == SRC_PREFIX]
+    assert len(pre) > 0
+    for it in pre.tolist():
+        keys = it[KE] - it[KB]
+        assert (it[KE] - 1) // page - it[KB] // page + 1 <= 1024
+        if dynamic:
+            assert (keys + 63 + page - 2) // page + 1 <= 1024
+    Leff = min(L, window) if window >= 0 else L
+    by_group = {}
+    for it in pre.tolist():
+        by_group.setdefault((it[KVH], it[QT]), []).append((it[KB], it[KE]))
+    for ch in by_group.values():
+        ch.sort()
+        assert ch[0][0] == L - Leff and ch[-1][1] == L
+        assert all(b == c for (_, b), (c, _) in zip(ch[:-1], ch[1:]))
+    # the merge covers every chunk plus the suffix partial of each group
+    nslots = {(m[1], m[2]): m[4] for m in merges.tolist() if m[4] > 0}
+    assert all(nslots[k] == len(v) + 1 for k, v in by_group.items())
+    need = -(-(-(-Leff // 64)) // _max_chunk_tiles(page))   # chunks the staged-page bound forces
+    assert max(len(v) for v in by_group.values()) >= need
+    if page == 1 and Leff >= 16384:
+        assert need > 15
+
+
+def test_cascade_run_rejects_a_mask_narrower_than_the_widest_request():
+    """A tree mask of fewer 64-bit words per row than the widest request's
+    nodes need is refused before any launch (the kernel would read the next
+    row's words)."""
+    info, _, _ = _plan([0, 10, 140], [300, 300], page_size=0)
+    assert info.max_qo_len == 130
+    fake = 1 << 20
+    a = _lib.RunArgs()
+    a.plan = a.q = a.k_suffix = a.v_suffix = a.out = a.k_prefix = a.v_prefix = a.tree_mask = fake
+    a.workspace, a.workspace_bytes = fake, info.workspace_bytes
+    a.q_stride_n, a.q_stride_h = 32 * 128, 128
+    a.suffix_stride_n, a.suffix_stride_h = 8 * 128, 128
+    a.o_stride_n, a.o_stride_h = 32 * 128, 128
+    a.prefix_stride_tok, a.prefix_stride_head = 128, 1024 * 128
+    a.prefix_extent, a.sm_scale = 1024, 0.088
+    a.mask_mode, a.mask_words = _lib.D2SD_MASK_TREE, 2
+    rc = _lib.lib.d2sd_cascade_run(C.byref(info), C.byref(a), None)
+    assert rc == 1 and b"mask_words" in _lib.lib.d2sd_last_error()
 
 
 def test_plan_chooses_waves():
