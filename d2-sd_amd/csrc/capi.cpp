@@ -331,7 +331,7 @@ int d2sd_cascade_plan(const d2sd_cascade_plan_desc* desc, int32_t* host_plan, si
     int lg = 0;
     while ((1 << lg) < desc->page_size) ++lg;
     for (const auto& w : out.items) {
-      if (w.mode == d2sd::MODE_NOOP || w.src != d2sd::SRC_PREFIX) continue;
+      if (w.mode == d2sd::MODE_NOOP || w.src == d2sd::SRC_SUFFIX) continue;
       const long long pages = desc->dynamic_prefix
                                   ? ((long long)w.kv_end - w.kv_begin + 63 + desc->page_size - 2) / desc->page_size + 1
                                   : d2sd::pages_spanned(w.kv_begin, w.kv_end, lg);
@@ -361,6 +361,7 @@ int d2sd_cascade_plan(const d2sd_cascade_plan_desc* desc, int32_t* host_plan, si
   info->num_groups = out.num_groups;
   info->dynamic_prefix = desc->dynamic_prefix;
   info->window_left = desc->window_left;
+  info->fused = out.fused;
   int64_t extent = 0;
   for (int r = 0; r < desc->num_reqs; ++r) {
     if (desc->page_size > 0)
@@ -686,7 +687,8 @@ static int single_prefill_cascade(const void* q, int64_t q_stride_n, int64_t q_s
   p.prefix_len = nullptr;
   p.prefix_len_set = has_prefix ? 1 : 0;
   p.prefix_len_value = L;
-  hipError_t e = d2sd::launch_verify_attention(p, d, sp.info.waves_per_block, false, false, sp.info.num_items, stream);
+  hipError_t e = d2sd::launch_verify_attention(p, d, sp.info.waves_per_block, false, false, sp.info.fused != 0,
+                                               sp.info.num_items, stream);
   if (e != hipSuccess) return fail_hip(e, "single_prefill attention launch");
   if (sp.info.num_merges > 0) {
     e = d2sd::launch_verify_merge(p, d, sp.info.rows_per_tile, sp.info.num_merges, stream);
@@ -702,7 +704,7 @@ int d2sd_cascade_attention(const d2sd_cascade_plan_info* info, const d2sd_cascad
   d2sd::VerifyParams p{};
   if (int rc = build_verify_params(info, a, p)) return rc;
   hipError_t e = d2sd::launch_verify_attention(p, info->head_dim, info->waves_per_block, info->page_size > 0,
-                                               info->kv_dtype == D2SD_KV_FP8_E4M3, info->num_items,
+                                               info->kv_dtype == D2SD_KV_FP8_E4M3, info->fused != 0, info->num_items,
                                                (hipStream_t)stream);
   return e == hipSuccess ? D2SD_OK : fail_hip(e, "cascade attention launch");
 }

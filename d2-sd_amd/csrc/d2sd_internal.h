@@ -92,7 +92,9 @@ struct AttnParams {
 // (32 per wave; 64 per wave of a two-wave workgroup) and either one key chunk
 // of the shared prefix or the whole suffix tree, then one merge launch.
 // ---------------------------------------------------------------------------
-enum : int { SRC_PREFIX = 0, SRC_SUFFIX = 1 };
+// Keys an item reads: a chunk of the shared prefix, the suffix tree, or
+// (SRC_BOTH) its group's whole visible prefix and then its suffix tree.
+enum : int { SRC_PREFIX = 0, SRC_SUFFIX = 1, SRC_BOTH = 2 };
 
 // 64 bytes; everything a workgroup needs is baked in by the planner so that
 // the kernel's first dependent load is the item itself.

@@ -232,11 +232,16 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
     const Piece& pc = sets[s][0];
     for (int qt = 0; qt < qtiles[pc.req]; ++qt) gchunks[grp0[pc.req] + pc.kvh * qtiles[pc.req] + qt] += nchunk[s][qt];
   }
+  // When no group's prefix is split, one item per group reads the group's
+  // prefix and then its suffix tree (SRC_BOTH) and writes the output: the
+  // plan has no partial states and no merge launch.
+  bool fuse = true;
+  for (int gi = 0; gi < ngroups; ++gi) fuse = fuse && gchunks[gi] <= 1;
   std::vector<int> slot0(ngroups, -1), next_slot(ngroups, 0);
   int slot = 0, max_splits_used = 0;
   for (int gi = 0; gi < ngroups; ++gi) {
     max_splits_used = std::max(max_splits_used, gchunks[gi]);
-    if (gchunks[gi] > 0) {
+    if (gchunks[gi] > 0 && !fuse) {
       slot0[gi] = slot;
       next_slot[gi] = slot;
       slot += gchunks[gi] + 1;
@@ -266,22 +271,23 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
         w.req = r;
         w.kvh = h;
         w.qtile = qt;
-        w.src = SRC_PREFIX;
+        w.src = fuse ? SRC_BOTH : SRC_PREFIX;
         w.kv0 = kv0[r];
         w.plan_len = kv1[r];
         w.kv_begin = kv0[r] + 64 * a;
         w.kv_end = std::min(kv1[r], kv0[r] + 64 * b);
-        w.slot = next_slot[gi]++;
-        w.mode = MODE_PARTIAL;
+        w.slot = fuse ? -1 : next_slot[gi]++;
+        w.mode = fuse ? MODE_FINAL : MODE_PARTIAL;
         w.q0 = q0;
         w.nq = nq[r];
         w.base = pbase;
-        lists[x].push_back({w, b - a});
+        lists[x].push_back({w, (b - a) + (fuse ? 2 * stiles[r] : 0)});
       }
     }
     if (!pc.suffix) continue;
     for (int qt = 0; qt < qtiles[r]; ++qt) {
       const int gi = grp0[r] + h * qtiles[r] + qt;
+      if (fuse && gchunks[gi] == 1) continue;  // its SRC_BOTH item reads the suffix
       const bool split = gchunks[gi] > 0;
       VerifyItem w{};
       w.req = r;
@@ -351,6 +357,7 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
   out.num_slots = slot;
   out.max_splits_used = max_splits_used;
   out.num_groups = ngroups;
+  out.fused = fuse && max_splits_used > 0 ? 1 : 0;
   // bf16 partial O + fp32 LSE per (slot, row)
   out.workspace_bytes = (size_t)slot * ROWS * ((size_t)in.head_dim * 2 + sizeof(float));
   return 0;

@@ -34,6 +34,7 @@ struct VerifyPlanOutput {
   int num_slots;
   int max_splits_used;
   int num_groups;                   // (request, kv head, q-tile) groups
+  int fused;                        // 1: no group is split; SRC_BOTH items, no partials, no merge
   size_t workspace_bytes;
 };
 
@@ -63,8 +64,9 @@ int verify_wgs_per_cu(int waves);
 int verify_rows(int waves);
 int verify_auto_waves(const VerifyPlanInput& in, int num_cus);
 
-hipError_t launch_verify_attention(const VerifyParams& p, int head_dim, int waves, bool paged, bool fp8, int nitems,
-                                   hipStream_t s);
+// fused: the plan's prefix items are SRC_BOTH items (VerifyPlanOutput::fused)
+hipError_t launch_verify_attention(const VerifyParams& p, int head_dim, int waves, bool paged, bool fp8, bool fused,
+                                   int nitems, hipStream_t s);
 hipError_t launch_verify_merge(const VerifyParams& p, int head_dim, int rows, int nmerges, hipStream_t s);
 // Device address of this GPU's library-owned workspace (kVerifyScratchBytes).
 hipError_t verify_scratch(void** ptr);

@@ -118,6 +118,16 @@ __device__ __forceinline__ float xor32(float x, int hh) {
   return __uint_as_float(hh ? r[0] : r[1]);
 }
 
+// Online-softmax state of a wave's RB row blocks: O^T accumulators, the
+// running max (raw-score units of the source being read) and this lane's part
+// of the row sums, and the rows' Q fragments.
+template <int RB, int MT, int KS>
+struct VerifyState {
+  f32x16 o[RB][MT];
+  float m_run[RB], l_run[RB];
+  bf16x8 qf[RB][KS];
+};
+
 // One workgroup: rows [qtile*ROWS, +ROWS) of (req, kvh) against keys
 // [kv_begin, kv_end) of source S.  Each of the W waves owns RB 32-row
 // blocks (ROWS = 32*RB*W).
@@ -125,9 +135,18 @@ __device__ __forceinline__ float xor32(float x, int hh) {
 //   MASKED : the suffix level (causal / tree / no mask; else only the
 //            key-range tail is masked)
 //   FP8    : S holds e4m3fn bytes, staged through registers
-template <int D, int W, int RB, int KST, int VST, int NPG, bool PAGED, bool MASKED, bool FP8>
+//   INIT   : start from an empty state and load the Q fragments; else
+//            continue the state of an earlier call (suffix level only)
+//   EPI    : normalise and store (partial slot or output); else leave the
+//            state for a following suffix-level call, O in value units and
+//            the running max in bf16 score units (prefix level only)
+template <int D, int W, int RB, int KST, int VST, int NPG, bool PAGED, bool MASKED, bool FP8, bool INIT = true,
+          bool EPI = true>
 __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyItem& w, const VerifySource& S,
-                                            VerifySmem<D, KST, VST, NPG>& sm) {
+                                            VerifySmem<D, KST, VST, NPG>& sm,
+                                            VerifyState<RB, D / 32, D / 16>& st) {
+  static_assert(INIT || MASKED, "only the suffix level continues a state");
+  static_assert(EPI || !MASKED, "the suffix level always ends a state");
   constexpr int ROWS = 32 * RB * W;
   constexpr int NT = 64 * W;
   constexpr int MT = D / 32;
@@ -240,8 +259,8 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
   // ---- Q fragments (B operand of S^T = K Q^T): lane holds 8 consecutive
   // head dims at offset 8*hh of every 16-wide k step, for row block rb.  The
   // bf16 prefix level stages Q through LDS (below); the others load it here ----
-  bf16x8 qf[RB][KS];
-  if constexpr (MASKED || FP8) {
+  auto& qf = st.qf;
+  auto load_q = [&]() {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       const bf16_t* qp = (const bf16_t*)p.q + (long long)(w.q0 + n[rb]) * p.q_stride_n +
@@ -251,7 +270,8 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
       // their results are never stored or merged
       for (int ks = 0; ks < KS; ++ks) qf[rb][ks] = *(const bf16x8*)(qp + 16 * ks);
     }
-  }
+  };
+  if constexpr ((MASKED || FP8) && INIT) load_q();
   __builtin_amdgcn_sched_barrier(0);
 
   if constexpr (STAGED) {
@@ -291,18 +311,19 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
       return (long long)t * tok_b;
   };
 
-  f32x16 o[RB][MT];
+  auto& o = st.o;
+  auto& m_run = st.m_run;
+  auto& l_run = st.l_run;
+  if constexpr (INIT) {
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb)
+    for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[rb][mt][r] = 0.f;
-  float m_run[RB], l_run[RB];
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-    m_run[rb] = -INFINITY;
-    l_run[rb] = 0.f;
+        for (int r = 0; r < 16; ++r) o[rb][mt][r] = 0.f;
+      m_run[rb] = -INFINITY;
+      l_run[rb] = 0.f;
+    }
   }
 
   // Whether any row of this wave sees a key of tile kb (suffix masks).
@@ -702,6 +723,10 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
       // all Q fragments are in registers before the slots are refilled
       __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
+      // an empty range staged no Q; a following suffix-level call needs it
+      if constexpr (!EPI) {
+        if (ntiles == 0) load_q();
+      }
       if (2 < ntiles) issue_k(2, wave_page(2));
       static_for<VST - 2>([&](auto j) {
         constexpr int st = decltype(j)::value - (VST - 2);
@@ -873,6 +898,20 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
     if (nfull < ntiles) step(nfull, std::true_type{});
   }
 
+  if constexpr (!EPI) {
+    // hand the state to the suffix level (bf16 keys and values): O in value
+    // units, the running max in score units of unscaled keys
+    if (live) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        if (m_run[rb] != -INFINITY) m_run[rb] *= kscale;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) o[rb][mt] *= vscale;
+      }
+    }
+    return;
+  }
+
   // ---- epilogue: normalise, then a partial slot or the final output ----
   float lse_r[RB];
   if (live) {
@@ -918,7 +957,10 @@ struct Shape<8> { static constexpr int W = 8, RB = 1, OCC = 2; };
 
 // The prefix level (paged or contiguous, bf16 or fp8) and the suffix level
 // (contiguous bf16, masked) share one launch; the item's src picks the body.
-template <int D, int WPB, bool PAGED, bool FP8>
+// FUSED plans (no group split) have SRC_BOTH and suffix items only; their
+// kernel is built apart so that the other plans' register allocation does not
+// carry the two-level path.
+template <int D, int WPB, bool PAGED, bool FP8, bool FUSED>
 __global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(Shape<WPB>::OCC, Shape<WPB>::OCC)))
 void verify_attn_kernel(const VerifyParams p) {
   constexpr int W = Shape<WPB>::W, RB = Shape<WPB>::RB;
@@ -935,10 +977,22 @@ void verify_attn_kernel(const VerifyParams p) {
                    "s"(p.pre.page_table), "s"(p.pre.stride_tok), "s"(p.pre.stride_head), "s"(p.pre.stride_page),
                    "s"(p.pre.log2_page), "s"(p.group), "s"(p.sm_scale_log2));
   if (w.mode == MODE_NOOP) return;
-  if (w.src == SRC_PREFIX)
-    verify_body<D, W, RB, R::KST, R::VST, R::NPG, PAGED, false, FP8>(p, w, p.pre, sm);
-  else
-    verify_body<D, W, RB, R::KST, R::VST, R::NPG, false, true, false>(p, w, p.suf, sm);
+  VerifyState<RB, D / 32, D / 16> st;
+  if (!FUSED && w.src == SRC_PREFIX) {
+    verify_body<D, W, RB, R::KST, R::VST, R::NPG, PAGED, false, FP8>(p, w, p.pre, sm, st);
+  } else if (w.src == SRC_SUFFIX) {
+    verify_body<D, W, RB, R::KST, R::VST, R::NPG, false, true, false>(p, w, p.suf, sm, st);
+  } else if constexpr (FUSED) {
+    // SRC_BOTH: the group's whole visible prefix, then its suffix tree, in
+    // one state, to the final output (no partial, no merge)
+    verify_body<D, W, RB, R::KST, R::VST, R::NPG, PAGED, false, FP8, true, false>(p, w, p.pre, sm, st);
+    __syncthreads();  // every wave is done with the prefix tiles in the rings
+    VerifyItem ws = w;
+    ws.kv_begin = 0;
+    ws.kv_end = w.nq;
+    ws.base = w.q0;  // the request's suffix keys are rows q0.. of k/v_suffix
+    verify_body<D, W, RB, R::KST, R::VST, R::NPG, false, true, false, false, true>(p, ws, p.suf, sm, st);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1035,29 +1089,39 @@ __global__ __launch_bounds__(64) void verify_merge_kernel(const VerifyParams p) 
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
-template <int D, int WPB, bool PAGED, bool FP8>
+template <int D, int WPB, bool PAGED, bool FP8, bool FUSED>
 static hipError_t launch_verify_t(const VerifyParams& p, int nitems, hipStream_t s) {
-  hipLaunchKernelGGL((verify_attn_kernel<D, WPB, PAGED, FP8>), dim3(nitems), dim3(64 * WPB), 0, s, p);
+  hipLaunchKernelGGL((verify_attn_kernel<D, WPB, PAGED, FP8, FUSED>), dim3(nitems), dim3(64 * WPB), 0, s, p);
   return hipGetLastError();
 }
 
-template <int D, int WPB>
-static hipError_t launch_verify_w(const VerifyParams& p, bool paged, bool fp8, int nitems, hipStream_t s) {
-  if (fp8) return paged ? launch_verify_t<D, WPB, true, true>(p, nitems, s) : launch_verify_t<D, WPB, false, true>(p, nitems, s);
-  return paged ? launch_verify_t<D, WPB, true, false>(p, nitems, s) : launch_verify_t<D, WPB, false, false>(p, nitems, s);
+template <int D, int WPB, bool FUSED>
+static hipError_t launch_verify_f(const VerifyParams& p, bool paged, bool fp8, int nitems, hipStream_t s) {
+  if (fp8)
+    return paged ? launch_verify_t<D, WPB, true, true, FUSED>(p, nitems, s)
+                 : launch_verify_t<D, WPB, false, true, FUSED>(p, nitems, s);
+  return paged ? launch_verify_t<D, WPB, true, false, FUSED>(p, nitems, s)
+               : launch_verify_t<D, WPB, false, false, FUSED>(p, nitems, s);
 }
 
-hipError_t launch_verify_attention(const VerifyParams& p, int head_dim, int waves, bool paged, bool fp8, int nitems,
-                                   hipStream_t s) {
+template <int D, int WPB>
+static hipError_t launch_verify_w(const VerifyParams& p, bool paged, bool fp8, bool fused, int nitems,
+                                  hipStream_t s) {
+  return fused ? launch_verify_f<D, WPB, true>(p, paged, fp8, nitems, s)
+               : launch_verify_f<D, WPB, false>(p, paged, fp8, nitems, s);
+}
+
+hipError_t launch_verify_attention(const VerifyParams& p, int head_dim, int waves, bool paged, bool fp8, bool fused,
+                                   int nitems, hipStream_t s) {
   if (nitems <= 0) return hipSuccess;
   if (head_dim == 128) {
-    if (waves == 2) return launch_verify_w<128, 2>(p, paged, fp8, nitems, s);
-    if (waves == 4) return launch_verify_w<128, 4>(p, paged, fp8, nitems, s);
-    if (waves == 8) return launch_verify_w<128, 8>(p, paged, fp8, nitems, s);
+    if (waves == 2) return launch_verify_w<128, 2>(p, paged, fp8, fused, nitems, s);
+    if (waves == 4) return launch_verify_w<128, 4>(p, paged, fp8, fused, nitems, s);
+    if (waves == 8) return launch_verify_w<128, 8>(p, paged, fp8, fused, nitems, s);
   } else if (head_dim == 64) {
-    if (waves == 2) return launch_verify_w<64, 2>(p, paged, fp8, nitems, s);
-    if (waves == 4) return launch_verify_w<64, 4>(p, paged, fp8, nitems, s);
-    if (waves == 8) return launch_verify_w<64, 8>(p, paged, fp8, nitems, s);
+    if (waves == 2) return launch_verify_w<64, 2>(p, paged, fp8, fused, nitems, s);
+    if (waves == 4) return launch_verify_w<64, 4>(p, paged, fp8, fused, nitems, s);
+    if (waves == 8) return launch_verify_w<64, 8>(p, paged, fp8, fused, nitems, s);
   }
   return hipErrorInvalidValue;
 }

@@ -89,6 +89,7 @@ class PlanInfo(C.Structure):
         ("window_left", C.c_int),
         ("prefix_extent", C.c_int64),
         ("max_qo_len", C.c_int),
+        ("fused", C.c_int),
     ]
 
 

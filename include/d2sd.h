@@ -227,6 +227,10 @@ typedef struct {
                              paged: page_table entries the plan reads */
   int max_qo_len;         /* nodes of the widest request: a tree mask needs
                              mask_words >= ceil(max_qo_len / 64) */
+  int fused;              /* 1: no request's prefix is split; each workgroup
+                             reads its rows' prefix and then their suffix tree
+                             and writes out / lse (run() is one launch, no
+                             workspace) */
 } d2sd_cascade_plan_info;
 
 /* Fills host_plan (capacity host_plan_ints int32) with the work list; the

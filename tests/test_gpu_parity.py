@@ -444,6 +444,64 @@ def test_dynamic_prefix_at_every_length(paged, window):
             check_close(o[a:b], o_ref, lse[a:b], lse_ref, f"lengths {lens} req {r}")
 
 
+def _fused_problem(name):
+    rng = np.random.default_rng(23)
+    if name == "cfg4_sliding":
+        return wl.config4(0, sliding=True)
+    if name == "fp8_window":       # fp8 prefix: the score / value scales change between the levels
+        reqs = [wl.Request(wl.random_branch_tree(rng, 4, 32), 3000), wl.Request(wl.random_branch_tree(rng, 3, 16), 90)]
+        return wl.VerifyProblem("fused_fp8", 64, 8, 128, reqs, page_size=16, window_left=100,
+                                kv_dtype=torch.float8_e4m3fn, with_sinks=True, seed=23)
+    if name == "d64_mixed":        # a request without prefix keys beside short ones, contiguous prefix
+        reqs = [wl.Request(wl.random_branch_tree(rng, 8, 32, chain_to_row0=False), 120),
+                wl.Request(wl.random_branch_tree(rng, 2, 16), 0), wl.Request(wl.random_branch_tree(rng, 3, 8), 1)]
+        return wl.VerifyProblem("fused_d64", 64, 8, 64, reqs, page_size=0, seed=24)
+    raise KeyError(name)
+
+
+@pytest.mark.parametrize("name", ["cfg4_sliding", "fp8_window", "d64_mixed"])
+def test_fused_plan_vs_oracle(name):
+    """Plans in which no request's prefix is split are fused: each workgroup
+    reads its rows' visible prefix and then their suffix tree in one
+    online-softmax state and writes O and LSE (the sink applied), with no
+    partial states and no merge launch; every request against the oracle."""
+    prob = _fused_problem(name)
+    mp, attn, outs = _run_problem(prob)
+    assert attn.info.fused == 1 and attn.info.num_merges == 0 and attn.info.num_slots == 0
+    _check_problem(mp, outs, dtype=torch.float32, tag=f"fused {name}")
+
+
+def test_fused_dynamic_plan_at_every_length():
+    """A fused dynamic-prefix plan (windowed GPT-OSS-style layer, prefixes
+    planned at 900 and 200) run at shorter and ragged lengths, empty included:
+    each request against the oracle at its run-time length."""
+    rng = np.random.default_rng(31)
+    reqs = [wl.Request(wl.random_branch_tree(rng, 4, 32), 900), wl.Request(wl.random_branch_tree(rng, 2, 16), 200)]
+    window = 128
+    prob = wl.VerifyProblem("fused_dyn", 64, 8, 64, reqs, page_size=16, window_left=window, with_sinks=True, seed=31)
+    mp = wl.materialize(prob, DEV, layers=1)
+    attn = d2sd.CascadeVerifyAttention(DEV)
+    wl.plan_for(attn, mp, dynamic_prefix=True)
+    assert attn.info.fused == 1
+    lt = mp.layers[0]
+    qo = prob.qo_indptr
+    for lens in ([900, 200], [899, 1], [129, 200], [128, 0], [0, 127], [64, 63]):
+        attn.set_prefix_len(lens)
+        o, lse = attn.run(lt.q, lt.k_suffix, lt.v_suffix, lt.k_prefix, lt.v_prefix)
+        torch.cuda.synchronize()
+        for r, L in enumerate(lens):
+            a, b = qo[r], qo[r + 1]
+            kp = vp = None
+            if L > 0:
+                pages = mp.page_table[mp.page_indptr[r]:mp.page_indptr[r + 1]].cpu().tolist()
+                kp = orc.gather_paged(lt.k_prefix.cpu(), pages, L)
+                vp = orc.gather_paged(lt.v_prefix.cpu(), pages, L)
+            o_ref, lse_ref = orc.cascade_tree_ref(lt.q.cpu()[a:b], lt.k_suffix.cpu()[a:b], lt.v_suffix.cpu()[a:b],
+                                                  kp, vp, torch.as_tensor(reqs[r].tree.ancestor_mask()),
+                                                  64 ** -0.5, window, sinks=mp.sinks.cpu())
+            check_close(o[a:b], o_ref, lse[a:b], lse_ref, f"fused dynamic lengths {lens} req {r}")
+
+
 @pytest.mark.parametrize("seed", range(32))
 def test_cascade_random_problems(seed):
     """Seeded random problems over the plan space: 1-4 requests with random

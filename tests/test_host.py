@@ -70,7 +70,7 @@ def _plan(qo, pl, hq=32, hkv=8, d=128, window=-1, num_cus=256, waves=0, max_spli
 
 
 MODE_PARTIAL, MODE_FINAL, MODE_NOOP = 0, 1, 3
-SRC_PREFIX, SRC_SUFFIX = 0, 1
+SRC_PREFIX, SRC_SUFFIX, SRC_BOTH = 0, 1, 2
 # VerifyItem fields
 REQ, KVH, QT, SRC, KB, KE, SLOT, MODE, Q0, NQ, BASE, COFF, KV0, PLAN_LEN = range(14)
 
@@ -95,7 +95,9 @@ def test_plan_partitions_work(qo, pl, window, page, hq, waves):
     naming the window start and the planned length), one suffix item covers
     its nodes, and the group's slots are merged exactly once, by one merge
     item per 32-row block; a group without prefix keys has a FINAL suffix item
-    and no merge."""
+    and no merge.  When no group's prefix is split the plan is fused: one
+    FINAL item per group reads its whole visible prefix and its suffix
+    (SRC_BOTH), with no slots and no merges."""
     hkv = 8
     g = hq // hkv
     page_indptr = None
@@ -116,8 +118,15 @@ def test_plan_partitions_work(qo, pl, window, page, hq, waves):
         key = (it[REQ], it[KVH], it[QT])
         r = it[REQ]
         assert it[Q0] == qo[r] and it[NQ] == qo[r + 1] - qo[r]
-        if it[SRC] == SRC_PREFIX:
-            assert it[MODE] == MODE_PARTIAL
+        if it[SRC] == SRC_BOTH:
+            assert info.fused == 1 and it[MODE] == MODE_FINAL and it[SLOT] == -1 and key not in suf
+            Leff = min(pl[r], window) if window >= 0 else pl[r]
+            assert (it[KB], it[KE], it[KV0], it[PLAN_LEN]) == (pl[r] - Leff, pl[r], pl[r] - Leff, pl[r])
+            assert it[BASE] == (page_indptr[r] if page else 0)
+            suf[key] = (-1, MODE_FINAL)
+            pre[key] = [(it[KB], it[KE], -1)]
+        elif it[SRC] == SRC_PREFIX:
+            assert info.fused == 0 and it[MODE] == MODE_PARTIAL
             assert it[BASE] == (page_indptr[r] if page else 0)
             Leff = min(pl[r], window) if window >= 0 else pl[r]
             assert it[KV0] == pl[r] - Leff and it[PLAN_LEN] == pl[r]
@@ -126,6 +135,17 @@ def test_plan_partitions_work(qo, pl, window, page, hq, waves):
             assert it[SRC] == SRC_SUFFIX and key not in suf
             assert (it[KB], it[KE], it[BASE]) == (0, qo[r + 1] - qo[r], qo[r])
             suf[key] = (it[SLOT], it[MODE])
+    if info.fused:
+        assert info.num_slots == 0 and info.num_merges == 0 and info.workspace_bytes == 0
+        assert info.max_splits_used == 1
+        # one item per group: SRC_BOTH where the request has prefix keys
+        want = {(r, h, qt) for r in range(len(pl)) for h in range(hkv)
+                for qt in range(-(-(qo[r + 1] - qo[r]) * g // info.rows_per_tile))}
+        assert set(suf) == want
+        for (r, h, qt) in want:
+            Leff = min(pl[r], window) if window >= 0 else pl[r]
+            assert ((r, h, qt) in pre) == (Leff > 0)
+        return
     all_slots = [c[2] for v in pre.values() for c in v] + [v[0] for v in suf.values() if v[1] == MODE_PARTIAL]
     assert len(all_slots) == len(set(all_slots)) == info.num_slots
     assert sorted(all_slots) == list(range(info.num_slots))
@@ -197,7 +217,7 @@ def test_plan_keeps_paged_chunks_within_staged_pages(page, L, d, hq, fp8, waves,
     info, items, merges = _plan([0, n], [L], hq=hq, hkv=8, d=d, window=window, waves=waves, page_size=page,
                                 dynamic=dynamic, kv_dtype=fp8)
     live = items[items[:, MODE] != MODE_NOOP]
-    pre = live[live[:, SRC] == SRC_PREFIX]
+    pre = live[live[:, SRC] != SRC_SUFFIX]
     assert len(pre) > 0
     for it in pre.tolist():
         keys = it[KE] - it[KB]

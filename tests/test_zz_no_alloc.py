@@ -34,10 +34,11 @@ def test_no_alloc_matches_workspace_run_on_two_calls():
 
 
 def test_no_alloc_rejects_plans_beyond_its_workspace():
-    prob = wl.config5(0)            # 32 requests: far more partial states than 32 MiB
+    prob = wl.config3(0)
     attn = d2sd.CascadeVerifyAttention(DEV)
     mp = wl.materialize(prob, DEV, layers=1)
-    wl.plan_for(attn, mp)
+    # 8 long requests split for 4x the CUs: ~57 MiB of partial states
+    wl.plan_for(attn, mp, num_cus=1024)
     assert attn.info.workspace_bytes > _lib.lib.d2sd_cascade_scratch_bytes()
     lt = mp.layers[0]
     with pytest.raises(RuntimeError, match="workspace"):
