@@ -79,6 +79,13 @@ static int single_prefill_cascade(const void* q, int64_t q_stride_n, int64_t q_s
                                   int lse_base2, void* workspace, size_t workspace_bytes, hipStream_t stream,
                                   bool* used);
 
+static int local_merge_cascade(const void* q, int64_t q_stride_b, int64_t q_stride_n, int64_t q_stride_h,
+                               const void* k, const void* v, int64_t kv_stride_b, int64_t kv_stride_n,
+                               int64_t kv_stride_h, void* out, int64_t o_stride_b, int64_t o_stride_n,
+                               int64_t o_stride_h, float* lse, int64_t lse_stride_b, int64_t lse_stride_n, int bsz,
+                               int block_len, int hq, int hkv, int d, int causal, float sm_scale, const float* sinks,
+                               int lse_base2, hipStream_t stream, bool* used);
+
 const char* d2sd_last_error(void) { return g_last_error.c_str(); }
 
 const char* d2sd_version(void) { return "d2sd-mi355x 0.1.0 (gfx950)"; }
@@ -199,6 +206,15 @@ int d2sd_local_attention_merge(const void* q, int64_t q_stride_b, int64_t q_stri
       !stride_ok(kv_stride_h) || !stride_ok(o_stride_b) || !stride_ok(o_stride_n) || !stride_ok(o_stride_h))
     return fail(D2SD_ERR_INVALID_ARG,
                 "local_attention_merge: tensors must be 16-byte aligned with strides % 8 == 0");
+  // the cascade kernels' suffix items when the batch is laid out row after row
+  bool used = false;
+  if (int rc = local_merge_cascade(q, q_stride_b, q_stride_n, q_stride_h, k, v, kv_stride_b, kv_stride_n, kv_stride_h,
+                                   out, o_stride_b, o_stride_n, o_stride_h, lse, lse_stride_b, lse_stride_n, bsz,
+                                   block_len, num_qo_heads, num_kv_heads, head_dim, causal, sm_scale, sinks,
+                                   lse_base2, (hipStream_t)stream, &used))
+    return rc;
+  if (used) return D2SD_OK;
+
   d2sd::AttnParams p{};
   const int g = num_qo_heads / num_kv_heads;
   const int waves = d2sd::choose_waves(block_len * g);
@@ -687,7 +703,8 @@ static int single_prefill_cascade(const void* q, int64_t q_stride_n, int64_t q_s
   p.prefix_len = nullptr;
   p.prefix_len_set = has_prefix ? 1 : 0;
   p.prefix_len_value = L;
-  hipError_t e = d2sd::launch_verify_attention(p, d, sp.info.waves_per_block, false, false, sp.info.fused != 0,
+  hipError_t e = d2sd::launch_verify_attention(p, d, sp.info.waves_per_block, false, false,
+                                               sp.info.fused ? d2sd::KIND_FUSED : d2sd::KIND_SPLIT,
                                                sp.info.num_items, stream);
   if (e != hipSuccess) return fail_hip(e, "single_prefill attention launch");
   if (sp.info.num_merges > 0) {
@@ -698,13 +715,115 @@ static int single_prefill_cascade(const void* q, int64_t q_stride_n, int64_t q_s
   return D2SD_OK;
 }
 
+// ---------------------------------------------------------------------------
+// local_attention_merge on the cascade kernels.  With every tensor laid out
+// row after row (batch stride = block_len x token stride), the bsz rows are
+// requests without a prefix whose suffix level is the row's own block
+// (causal or not): one suffix item per (row, kv head, q-tile), merged in
+// place into out / lse (MODE_INPLACE, the KIND_INPLACE kernel).  The plan is
+// cached per (device, bsz, block_len, heads, head_dim) and uploaded by the
+// first call of a shape (as single_prefill's; a call whose stream is being
+// captured, or past kSinglePlanCap shapes, takes the single-source kernel).
+// ---------------------------------------------------------------------------
+namespace {
+std::map<std::array<int, 6>, SinglePlan> g_local_plans;  // under g_single_mu
+}
+
+static int local_merge_cascade(const void* q, int64_t q_stride_b, int64_t q_stride_n, int64_t q_stride_h,
+                               const void* k, const void* v, int64_t kv_stride_b, int64_t kv_stride_n,
+                               int64_t kv_stride_h, void* out, int64_t o_stride_b, int64_t o_stride_n,
+                               int64_t o_stride_h, float* lse, int64_t lse_stride_b, int64_t lse_stride_n, int bsz,
+                               int block_len, int hq, int hkv, int d, int causal, float sm_scale, const float* sinks,
+                               int lse_base2, hipStream_t stream, bool* used) {
+  *used = false;
+  const int64_t L = block_len;
+  if (q_stride_b != L * q_stride_n || kv_stride_b != L * kv_stride_n || o_stride_b != L * o_stride_n ||
+      lse_stride_b != L * lse_stride_n || (int64_t)bsz * L > INT32_MAX / 2)
+    return D2SD_OK;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return D2SD_OK;
+  }
+  const std::array<int, 6> key = {dev, bsz, block_len, hq, hkv, d};
+  SinglePlan sp{};
+  {
+    std::lock_guard<std::mutex> lk(g_single_mu);
+    auto it = g_local_plans.find(key);
+    if (it != g_local_plans.end()) {
+      sp = it->second;
+    } else {
+      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+      if (hipStreamIsCapturing(stream, &cs) != hipSuccess) {
+        (void)hipGetLastError();
+        return D2SD_OK;
+      }
+      if (cs != hipStreamCaptureStatusNone || g_local_plans.size() >= kSinglePlanCap) return D2SD_OK;
+      std::vector<int32_t> qo(bsz + 1), pl(bsz, 0);
+      for (int r = 0; r <= bsz; ++r) qo[r] = r * block_len;
+      d2sd_cascade_plan_desc desc{};
+      desc.num_reqs = bsz;
+      desc.qo_indptr = qo.data();
+      desc.prefix_len = pl.data();
+      desc.num_qo_heads = hq;
+      desc.num_kv_heads = hkv;
+      desc.head_dim = d;
+      desc.window_left = -1;
+      desc.kv_dtype = D2SD_KV_BF16;
+      const std::string saved = g_last_error;
+      std::vector<int32_t> host;
+      bool ok = d2sd_cascade_plan(&desc, nullptr, 0, &sp.info) == D2SD_OK;
+      if (ok) {
+        host.assign((size_t)sp.info.plan_ints, 0);
+        ok = d2sd_cascade_plan(&desc, host.data(), host.size(), &sp.info) == D2SD_OK;
+      }
+      g_last_error = saved;
+      if (!ok || sp.info.num_merges != 0 || sp.info.num_slots != 0) return D2SD_OK;
+      // every item is a suffix item writing the output: merge in place instead
+      for (int i = 0; i < sp.info.num_items; ++i) {
+        d2sd::VerifyItem* w = (d2sd::VerifyItem*)(host.data() + 16 * (size_t)i);
+        if (w->mode == d2sd::MODE_FINAL) w->mode = d2sd::MODE_INPLACE;
+      }
+      if (int rc = upload_single_plan(host, &sp.plan_dev)) return rc;
+      if (!sp.plan_dev) return D2SD_OK;
+      g_local_plans.emplace(key, sp);
+    }
+  }
+  d2sd_cascade_run_args a{};
+  a.plan = sp.plan_dev;
+  a.q = q;
+  a.q_stride_n = q_stride_n;
+  a.q_stride_h = q_stride_h;
+  a.k_suffix = k;
+  a.v_suffix = v;
+  a.suffix_stride_n = kv_stride_n;
+  a.suffix_stride_h = kv_stride_h;
+  a.mask_mode = causal ? D2SD_MASK_CAUSAL : D2SD_MASK_NONE;
+  a.out = out;
+  a.o_stride_n = o_stride_n;
+  a.o_stride_h = o_stride_h;
+  a.lse = lse;
+  a.lse_stride_n = lse_stride_n;
+  a.sm_scale = sm_scale;
+  a.sinks = sinks;
+  a.lse_base2 = lse_base2;
+  d2sd::VerifyParams p{};
+  if (int rc = build_verify_params(&sp.info, &a, p)) return rc;
+  hipError_t e = d2sd::launch_verify_attention(p, d, sp.info.waves_per_block, false, false, d2sd::KIND_INPLACE,
+                                               sp.info.num_items, stream);
+  if (e != hipSuccess) return fail_hip(e, "local_attention_merge launch");
+  *used = true;
+  return D2SD_OK;
+}
+
 int d2sd_cascade_attention(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* a,
                            d2sd_stream_t stream) {
   g_last_error.clear();
   d2sd::VerifyParams p{};
   if (int rc = build_verify_params(info, a, p)) return rc;
   hipError_t e = d2sd::launch_verify_attention(p, info->head_dim, info->waves_per_block, info->page_size > 0,
-                                               info->kv_dtype == D2SD_KV_FP8_E4M3, info->fused != 0, info->num_items,
+                                               info->kv_dtype == D2SD_KV_FP8_E4M3,
+                                               info->fused ? d2sd::KIND_FUSED : d2sd::KIND_SPLIT, info->num_items,
                                                (hipStream_t)stream);
   return e == hipSuccess ? D2SD_OK : fail_hip(e, "cascade attention launch");
 }

@@ -96,6 +96,11 @@ struct AttnParams {
 // (SRC_BOTH) its group's whole visible prefix and then its suffix tree.
 enum : int { SRC_PREFIX = 0, SRC_SUFFIX = 1, SRC_BOTH = 2 };
 
+// Kinds of cascade plans (one attention-kernel instantiation each): split
+// prefixes with partial states and a merge launch, fused (no split), and
+// in-place suffix items (the drop-in runner's per-row local level).
+enum : int { KIND_SPLIT = 0, KIND_FUSED = 1, KIND_INPLACE = 2 };
+
 // 64 bytes; everything a workgroup needs is baked in by the planner so that
 // the kernel's first dependent load is the item itself.
 struct VerifyItem {

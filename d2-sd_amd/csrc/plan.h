@@ -64,8 +64,8 @@ int verify_wgs_per_cu(int waves);
 int verify_rows(int waves);
 int verify_auto_waves(const VerifyPlanInput& in, int num_cus);
 
-// fused: the plan's prefix items are SRC_BOTH items (VerifyPlanOutput::fused)
-hipError_t launch_verify_attention(const VerifyParams& p, int head_dim, int waves, bool paged, bool fp8, bool fused,
+// kind: KIND_SPLIT, KIND_FUSED (VerifyPlanOutput::fused) or KIND_INPLACE
+hipError_t launch_verify_attention(const VerifyParams& p, int head_dim, int waves, bool paged, bool fp8, int kind,
                                    int nitems, hipStream_t s);
 hipError_t launch_verify_merge(const VerifyParams& p, int head_dim, int rows, int nmerges, hipStream_t s);
 // Device address of this GPU's library-owned workspace (kVerifyScratchBytes).

@@ -140,13 +140,17 @@ struct VerifyState {
 //   EPI    : normalise and store (partial slot or output); else leave the
 //            state for a following suffix-level call, O in value units and
 //            the running max in bf16 score units (prefix level only)
+//   INPLACE: the items merge into the (O, LSE) already stored at the output
+//            (MODE_INPLACE, suffix level only); the stored state is loaded
+//            with Q, so its round trip overlaps the first tiles
 template <int D, int W, int RB, int KST, int VST, int NPG, bool PAGED, bool MASKED, bool FP8, bool INIT = true,
-          bool EPI = true>
+          bool EPI = true, bool INPLACE = false>
 __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyItem& w, const VerifySource& S,
                                             VerifySmem<D, KST, VST, NPG>& sm,
                                             VerifyState<RB, D / 32, D / 16>& st) {
   static_assert(INIT || MASKED, "only the suffix level continues a state");
   static_assert(EPI || !MASKED, "the suffix level always ends a state");
+  static_assert(!INPLACE || (MASKED && INIT && EPI), "in-place merges end a suffix-level state");
   constexpr int ROWS = 32 * RB * W;
   constexpr int NT = 64 * W;
   constexpr int MT = D / 32;
@@ -272,6 +276,26 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
     }
   };
   if constexpr ((MASKED || FP8) && INIT) load_q();
+  // INPLACE: this lane's part of the stored output of its rows (head dims
+  // 32 mt + 8 q4 + 4 hh .. + 3) and their stored LSE (natural log)
+  u32x2 old_o[RB][INPLACE ? MT : 1][4];
+  float old_lse[RB];
+  if constexpr (INPLACE) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      old_lse[rb] = -INFINITY;
+      if (rv[rb]) {
+        const bf16_t* orow = (const bf16_t*)p.o + (long long)(w.q0 + n[rb]) * p.o_stride_n +
+                             (long long)qh[rb] * p.o_stride_h + 4 * hh;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) old_o[rb][mt][q4] = *(const u32x2*)(orow + 32 * mt + 8 * q4);
+        const float l = p.lse[(long long)(w.q0 + n[rb]) * p.lse_stride_n + qh[rb]];
+        old_lse[rb] = p.lse_base2 ? l * kLn2 : l;
+      }
+    }
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   if constexpr (STAGED) {
@@ -937,6 +961,32 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
             __builtin_nontemporal_store(image_piece(o[rb][mt], pr, 1.f), (u32x4*)(po + image_offset<D>(blk, mt, pr, lane)));
         if (hh == 0) __builtin_nontemporal_store(lse_r[rb], pl);
       } else if (rv[rb]) {
+        if constexpr (INPLACE) {
+          // flashinfer.merge_state_in_place of the stored state (O_s, LSE_s)
+          // with this one (model/cascade_graph.py:58-60); both empty keeps
+          // the stored state
+          const float m = fmaxf(old_lse[rb], lse_r[rb]);
+          float wa = 1.f, wb = 0.f;
+          if (m != -INFINITY) {
+            const float ea = __expf(old_lse[rb] - m), eb = __expf(lse_r[rb] - m);
+            const float sum = ea + eb;
+            wa = ea / sum;
+            wb = eb / sum;
+            lse_r[rb] = m + logf(sum);
+          } else {
+            lse_r[rb] = old_lse[rb];
+          }
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+              const u32x2 od = old_o[rb][mt][q4];
+              o[rb][mt][4 * q4] = o[rb][mt][4 * q4] * wb + wa * bf16_lo(od[0]);
+              o[rb][mt][4 * q4 + 1] = o[rb][mt][4 * q4 + 1] * wb + wa * bf16_hi(od[0]);
+              o[rb][mt][4 * q4 + 2] = o[rb][mt][4 * q4 + 2] * wb + wa * bf16_lo(od[1]);
+              o[rb][mt][4 * q4 + 3] = o[rb][mt][4 * q4 + 3] * wb + wa * bf16_hi(od[1]);
+            }
+        }
         store_out<D>(p, w.q0 + n[rb], qh[rb], hh, o[rb], lse_r[rb]);
       }
     }
@@ -957,10 +1007,12 @@ struct Shape<8> { static constexpr int W = 8, RB = 1, OCC = 2; };
 
 // The prefix level (paged or contiguous, bf16 or fp8) and the suffix level
 // (contiguous bf16, masked) share one launch; the item's src picks the body.
-// FUSED plans (no group split) have SRC_BOTH and suffix items only; their
-// kernel is built apart so that the other plans' register allocation does not
-// carry the two-level path.
-template <int D, int WPB, bool PAGED, bool FP8, bool FUSED>
+// Plans of each kind have a kernel of their own, so that no kind's register
+// allocation carries another kind's path: KIND_SPLIT (prefix-chunk and suffix
+// items), KIND_FUSED (no group split: SRC_BOTH and suffix items), KIND_INPLACE
+// (suffix items merging into the stored output: the per-row local level of
+// the drop-in runner).
+template <int D, int WPB, bool PAGED, bool FP8, int KIND>
 __global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(Shape<WPB>::OCC, Shape<WPB>::OCC)))
 void verify_attn_kernel(const VerifyParams p) {
   constexpr int W = Shape<WPB>::W, RB = Shape<WPB>::RB;
@@ -978,11 +1030,13 @@ void verify_attn_kernel(const VerifyParams p) {
                    "s"(p.pre.log2_page), "s"(p.group), "s"(p.sm_scale_log2));
   if (w.mode == MODE_NOOP) return;
   VerifyState<RB, D / 32, D / 16> st;
-  if (!FUSED && w.src == SRC_PREFIX) {
+  if constexpr (KIND == KIND_INPLACE) {
+    verify_body<D, W, RB, R::KST, R::VST, R::NPG, false, true, false, true, true, true>(p, w, p.suf, sm, st);
+  } else if (KIND == KIND_SPLIT && w.src == SRC_PREFIX) {
     verify_body<D, W, RB, R::KST, R::VST, R::NPG, PAGED, false, FP8>(p, w, p.pre, sm, st);
   } else if (w.src == SRC_SUFFIX) {
     verify_body<D, W, RB, R::KST, R::VST, R::NPG, false, true, false>(p, w, p.suf, sm, st);
-  } else if constexpr (FUSED) {
+  } else if constexpr (KIND == KIND_FUSED) {
     // SRC_BOTH: the group's whole visible prefix, then its suffix tree, in
     // one state, to the final output (no partial, no merge)
     verify_body<D, W, RB, R::KST, R::VST, R::NPG, PAGED, false, FP8, true, false>(p, w, p.pre, sm, st);
@@ -1089,39 +1143,41 @@ __global__ __launch_bounds__(64) void verify_merge_kernel(const VerifyParams p) 
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
-template <int D, int WPB, bool PAGED, bool FP8, bool FUSED>
+template <int D, int WPB, bool PAGED, bool FP8, int KIND>
 static hipError_t launch_verify_t(const VerifyParams& p, int nitems, hipStream_t s) {
-  hipLaunchKernelGGL((verify_attn_kernel<D, WPB, PAGED, FP8, FUSED>), dim3(nitems), dim3(64 * WPB), 0, s, p);
+  hipLaunchKernelGGL((verify_attn_kernel<D, WPB, PAGED, FP8, KIND>), dim3(nitems), dim3(64 * WPB), 0, s, p);
   return hipGetLastError();
 }
 
-template <int D, int WPB, bool FUSED>
-static hipError_t launch_verify_f(const VerifyParams& p, bool paged, bool fp8, int nitems, hipStream_t s) {
+template <int D, int WPB, int KIND>
+static hipError_t launch_verify_k(const VerifyParams& p, bool paged, bool fp8, int nitems, hipStream_t s) {
   if (fp8)
-    return paged ? launch_verify_t<D, WPB, true, true, FUSED>(p, nitems, s)
-                 : launch_verify_t<D, WPB, false, true, FUSED>(p, nitems, s);
-  return paged ? launch_verify_t<D, WPB, true, false, FUSED>(p, nitems, s)
-               : launch_verify_t<D, WPB, false, false, FUSED>(p, nitems, s);
+    return paged ? launch_verify_t<D, WPB, true, true, KIND>(p, nitems, s)
+                 : launch_verify_t<D, WPB, false, true, KIND>(p, nitems, s);
+  return paged ? launch_verify_t<D, WPB, true, false, KIND>(p, nitems, s)
+               : launch_verify_t<D, WPB, false, false, KIND>(p, nitems, s);
 }
 
 template <int D, int WPB>
-static hipError_t launch_verify_w(const VerifyParams& p, bool paged, bool fp8, bool fused, int nitems,
-                                  hipStream_t s) {
-  return fused ? launch_verify_f<D, WPB, true>(p, paged, fp8, nitems, s)
-               : launch_verify_f<D, WPB, false>(p, paged, fp8, nitems, s);
+static hipError_t launch_verify_w(const VerifyParams& p, bool paged, bool fp8, int kind, int nitems, hipStream_t s) {
+  if (kind == KIND_FUSED) return launch_verify_k<D, WPB, KIND_FUSED>(p, paged, fp8, nitems, s);
+  // in-place plans read no prefix: one instantiation
+  if (kind == KIND_INPLACE) return launch_verify_t<D, WPB, false, false, KIND_INPLACE>(p, nitems, s);
+  return launch_verify_k<D, WPB, KIND_SPLIT>(p, paged, fp8, nitems, s);
 }
 
-hipError_t launch_verify_attention(const VerifyParams& p, int head_dim, int waves, bool paged, bool fp8, bool fused,
+hipError_t launch_verify_attention(const VerifyParams& p, int head_dim, int waves, bool paged, bool fp8, int kind,
                                    int nitems, hipStream_t s) {
   if (nitems <= 0) return hipSuccess;
+  if (kind != KIND_SPLIT && kind != KIND_FUSED && kind != KIND_INPLACE) return hipErrorInvalidValue;
   if (head_dim == 128) {
-    if (waves == 2) return launch_verify_w<128, 2>(p, paged, fp8, fused, nitems, s);
-    if (waves == 4) return launch_verify_w<128, 4>(p, paged, fp8, fused, nitems, s);
-    if (waves == 8) return launch_verify_w<128, 8>(p, paged, fp8, fused, nitems, s);
+    if (waves == 2) return launch_verify_w<128, 2>(p, paged, fp8, kind, nitems, s);
+    if (waves == 4) return launch_verify_w<128, 4>(p, paged, fp8, kind, nitems, s);
+    if (waves == 8) return launch_verify_w<128, 8>(p, paged, fp8, kind, nitems, s);
   } else if (head_dim == 64) {
-    if (waves == 2) return launch_verify_w<64, 2>(p, paged, fp8, fused, nitems, s);
-    if (waves == 4) return launch_verify_w<64, 4>(p, paged, fp8, fused, nitems, s);
-    if (waves == 8) return launch_verify_w<64, 8>(p, paged, fp8, fused, nitems, s);
+    if (waves == 2) return launch_verify_w<64, 2>(p, paged, fp8, kind, nitems, s);
+    if (waves == 4) return launch_verify_w<64, 4>(p, paged, fp8, kind, nitems, s);
+    if (waves == 8) return launch_verify_w<64, 8>(p, paged, fp8, kind, nitems, s);
   }
   return hipErrorInvalidValue;
 }
