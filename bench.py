@@ -153,7 +153,7 @@ def traffic_workload(args) -> int:
     dst = torch.empty_like(src)
     wbuf = torch.empty(CAL_BYTES // 4, dtype=torch.float32, device=dev)
     rbuf = torch.ones(CAL_BYTES // 4, dtype=torch.float32, device=dev)
-    prob = wl.config2(args.seed, layers=args.layers)
+    prob = _traffic_problem(wl, args)
     mp = wl.materialize(prob, dev)
     attn = d2sd.CascadeVerifyAttention(dev)
     wl.plan_for(attn, mp)
@@ -170,6 +170,20 @@ def traffic_workload(args) -> int:
         torch.cuda.synchronize()
     print(f"traffic workload done: {attn.info.num_slots} partial slots, {attn.info.num_items} items", flush=True)
     return 0
+
+
+def _traffic_problem(wl, args):
+    """The workload of the traffic passes: config 2 (36 layers, one KV pool
+    each) or config 3 (8 requests of 8K-32K keys: one 670 MB pool already
+    passes the 256 MB MALL)."""
+    if args.traffic_config == "config3":
+        return wl.config3(args.seed)
+    return wl.config2(args.seed, layers=args.layers)
+
+
+def _traffic_file(args) -> Path:
+    return ROOT / "profiles" / ("verify_attn_cfg3_traffic.txt" if args.traffic_config == "config3"
+                                else "verify_attn_cfg2_traffic.txt")
 
 
 def _kernel_class(name: str):
@@ -211,7 +225,7 @@ def _pmc_pass(counters, outdir: Path, args, kernel_trace: bool = False):
     cmd += ["--kernel-include-regex", TRAFFIC_KERNELS,
             "-d", str(outdir), "-o", "run", "--output-format", "csv", "--",
             sys.executable, str(Path(__file__).resolve()), "--traffic-workload",
-            "--layers", str(args.layers), "--seed", str(args.seed)]
+            "--layers", str(args.layers), "--seed", str(args.seed), "--traffic-config", args.traffic_config]
     log("running " + " ".join(cmd))
     r = subprocess.run(cmd, capture_output=True, text=True)
     _PMC_STDOUT.append(r.stdout)
@@ -389,7 +403,8 @@ def measure_mix(args) -> int:
 def measure_traffic(args) -> int:
     """HBM traffic of the attention launch: four counter passes of the
     traffic workload (FETCH_SIZE; WRITE_SIZE; the L2-to-fabric read requests
-    by size; write requests), each a child process; writes TRAFFIC_FILE.
+    by size; write requests), each a child process; writes the summary
+    under profiles/ (verify_attn_cfg2_traffic.txt or ..._cfg3_traffic.txt).
 
     Calibration: the 1 GiB fill writes and the 1 GiB sum reads known bytes
     with no reuse, so measured / known is what the counters see of a
@@ -415,18 +430,18 @@ def measure_traffic(args) -> int:
                 return 1
             for c in counters:
                 res[c] = _counter_means(files[0], c)
-    prob = wl.config2(args.seed, layers=args.layers)
+    prob = _traffic_problem(wl, args)
     hq, hkv, d, T = prob.num_qo_heads, prob.num_kv_heads, prob.head_dim, prob.total_q
-    L, P = prob.requests[0].prefix_len, prob.page_size
+    P = prob.page_size
     ab, _ = wl.attention_launch_bytes_flops(prob)
     slots, nitems = slots_seen[0]
     rows = 128
     items = {
-        "prefix_kv_unique": 2 * L * hkv * d * 2,
+        "prefix_kv_unique": sum(2 * r.prefix_len * hkv * d * 2 for r in prob.requests),
         "suffix_kv": 2 * T * hkv * d * 2,
         "q": T * hq * d * 2,
-        "page_table": 4 * ((L + P - 1) // P),
-        "tree_mask": T * ((T + 63) // 64) * 8,
+        "page_table": sum(4 * ((r.prefix_len + P - 1) // P) for r in prob.requests),
+        "tree_mask": sum(r.n * ((r.n + 63) // 64) * 8 for r in prob.requests),
         "plan_items": nitems * 64,
     }
     w_items = {"partial_slots": slots * (rows * d * 2 + rows * 4)}
@@ -446,8 +461,9 @@ def measure_traffic(args) -> int:
     a_reads = hist_reads("attention") / read_cov
     a_writes = hist_writes("attention") / write_cov
     lines = [
-        "# HBM traffic of the cascade verify attention launch, config 2 (Qwen3-8B, L=4096 paged, 36 layers)",
-        f"# command: python bench.py --measure-traffic --layers {args.layers} --seed {args.seed}",
+        f"# HBM traffic of the cascade verify attention launch, {prob.name}",
+        f"# command: python bench.py --measure-traffic --traffic-config {args.traffic_config} --layers {args.layers} "
+        f"--seed {args.seed}",
         "#   = four passes, each: timeout -s KILL 120 rocprofv3 --pmc <counters>",
         f"#     --kernel-include-regex '{TRAFFIC_KERNELS}' --output-format csv -- python bench.py --traffic-workload",
         "#   passes: " + " | ".join(" ".join(c) for c in TRAFFIC_PASSES),
@@ -487,8 +503,9 @@ def measure_traffic(args) -> int:
         "",
         f"traffic_bytes_per_launch: {a_reads + a_writes:.0f}",
     ]
-    TRAFFIC_FILE.parent.mkdir(exist_ok=True)
-    TRAFFIC_FILE.write_text("\n".join(lines) + "\n")
+    out_file = _traffic_file(args)
+    out_file.parent.mkdir(exist_ok=True)
+    out_file.write_text("\n".join(lines) + "\n")
     print("\n".join(lines))
     return 0
 
@@ -1005,6 +1022,8 @@ def main() -> int:
     ap.add_argument("--measure-traffic", action="store_true",
                     help="run the two rocprofv3 counter passes and write the traffic summary")
     ap.add_argument("--traffic-workload", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--traffic-config", default="config2", choices=("config2", "config3"),
+                    help="workload of --measure-traffic (its summary: profiles/verify_attn_<cfg>_traffic.txt)")
     ap.add_argument("--measure-mix", action="store_true",
                     help="run two rocprofv3 passes of SQ instruction counters and write the instruction-mix summary")
     ap.add_argument("--measure-mfma", action="store_true",
