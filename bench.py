@@ -723,10 +723,12 @@ def measure_qk_rope(args) -> int:
 # timed as a hipGraph of `layers` calls over distinct KV pools
 OTHER_WORKLOADS = {
     "northstar": lambda wl, seed: (wl.northstar(seed), 36),  # 16.8 MB of KV per layer, 36 pools
-    "config1": lambda wl, seed: (wl.config1(seed), 64),      # 4.2 MB of KV per call: 64 pools pass the MALL
-    "config3": lambda wl, seed: (wl.config3(seed), 2),       # ~670 MB of KV per call
-    "config4_full": lambda wl, seed: (wl.config4(seed), 12),
-    "config4_sliding": lambda wl, seed: (wl.config4(seed, sliding=True), 12),
+    # KV pools per workload: together well past the 256 MB Infinity Cache, so
+    # each call's prefix comes from HBM
+    "config1": lambda wl, seed: (wl.config1(seed), 96),      # 4.2 MB of KV per pool: 403 MB
+    "config3": lambda wl, seed: (wl.config3(seed), 2),       # ~670 MB of KV per pool
+    "config4_full": lambda wl, seed: (wl.config4(seed), 24),  # 16.8 MB per pool: 403 MB
+    "config4_sliding": lambda wl, seed: (wl.config4(seed, sliding=True), 24),
     "config5": lambda wl, seed: (wl.config5(seed), 2),       # ~540 MB of fp8 KV per call
 }
 

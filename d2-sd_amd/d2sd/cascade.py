@@ -43,7 +43,7 @@ import torch
 
 from . import _lib
 from ._lib import check, lib
-from .graph import keep_alive
+from .graph import capturing, keep_alive
 from .tree import pack_tree_masks
 
 _MASK_MODES = {"none": _lib.D2SD_MASK_NONE, "causal": _lib.D2SD_MASK_CAUSAL, "tree": _lib.D2SD_MASK_TREE}
@@ -65,7 +65,10 @@ def _reuse(old: Optional[torch.Tensor], new: torch.Tensor, same_shape: bool) -> 
 
 class CascadeVerifyAttention:
     def __init__(self, device: Union[str, torch.device, None] = None):
-        self.device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        if dev.type == "cuda" and dev.index is None:  # "cuda" names the current device: compare by index
+            dev = torch.device("cuda", torch.cuda.current_device())
+        self.device = dev
         self._planned = False
         self._captured = False   # a run() was recorded into a graph
         self._owned = set()      # names of the optional-input buffers the plan owns
@@ -386,7 +389,7 @@ class CascadeVerifyAttention:
             raise ValueError("out must be bf16 [total_q, Hq, D] with contiguous head_dim")
         if lse.shape != (T, hq) or lse.dtype != torch.float32 or lse.stride(-1) != 1:
             raise ValueError("lse must be float32 [total_q, Hq] with contiguous heads")
-        if torch.cuda.is_current_stream_capturing():
+        if capturing():
             self._captured = True
         a = _lib.RunArgs()
         a.plan = self.plan_dev.data_ptr()

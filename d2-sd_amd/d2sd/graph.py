@@ -19,6 +19,11 @@ from ._lib import check, lib
 _CAPTURING: list = []
 
 
+def capturing() -> bool:
+    """Whether a HipGraph (or a torch graph on the current stream) is capturing."""
+    return bool(_CAPTURING) or torch.cuda.is_current_stream_capturing()
+
+
 def keep_alive(*objs) -> None:
     """Called by d2sd ops with the device buffers a launch reads or writes:
     while a HipGraph is capturing, it holds references to them for as long as

@@ -775,6 +775,53 @@ def test_hipgraph_replays_match_eager():
         _ = (torch.randn(1000, device=DEV) * 2).sum().item()   # eager work between replays
 
 
+def test_same_shape_replan_replays_in_captured_graph():
+    """A graph captured before a same-shape re-plan replays the new plan:
+    plan with a host page table, capture run(), re-plan with a host table of
+    another permutation of the pool (copied into the same plan-owned buffer)
+    and new sinks, replay; the result matches the oracle on the new pages.
+    A re-plan that would hand the kernels another device tensor raises."""
+    rng = np.random.default_rng(41)
+    tree = wl.random_branch_tree(rng, 4, 16)
+    prob = wl.VerifyProblem("replan", 32, 8, 128, [wl.Request(tree, 2000)], page_size=16, with_sinks=True, seed=41)
+    mp = wl.materialize(prob, DEV, layers=1)
+    lt = mp.layers[0]
+    npages = int(mp.page_indptr[-1])
+    pool_pages = lt.k_prefix.shape[0]
+    gen = torch.Generator().manual_seed(41)
+    table_a = torch.randperm(pool_pages, generator=gen)[:npages].to(torch.int32)
+    table_b = torch.randperm(pool_pages, generator=gen)[:npages].to(torch.int32)
+    assert not torch.equal(table_a, table_b)
+    sinks_b = torch.randn(32, generator=gen)
+
+    def plan(attn, table, sinks):
+        return attn.plan(prob.qo_indptr, prob.prefix_lens, 32, 8, 128, tree_masks=prob.tree_masks(), page_size=16,
+                         page_indptr=mp.page_indptr, page_table=table.tolist(), kv_layout="HND", sinks=sinks.cpu())
+
+    attn = d2sd.CascadeVerifyAttention(DEV)
+    plan(attn, table_a, mp.sinks)
+    out = torch.empty(prob.total_q, 32, 128, dtype=torch.bfloat16, device=DEV)
+    lse = torch.empty(prob.total_q, 32, dtype=torch.float32, device=DEV)
+    g = d2sd.HipGraph()
+    with g.capture():
+        attn.run(lt.q, lt.k_suffix, lt.v_suffix, lt.k_prefix, lt.v_prefix, out=out, lse=lse)
+    pt_buf = attn.page_table_dev
+    plan(attn, table_b, sinks_b)
+    assert attn.page_table_dev is pt_buf
+    out.zero_()
+    g.replay()
+    torch.cuda.synchronize()
+    pages = table_b.tolist()
+    kp = orc.gather_paged(lt.k_prefix.cpu(), pages, 2000)
+    vp = orc.gather_paged(lt.v_prefix.cpu(), pages, 2000)
+    o_ref, lse_ref = orc.cascade_tree_ref(lt.q.cpu(), lt.k_suffix.cpu(), lt.v_suffix.cpu(), kp, vp,
+                                          torch.as_tensor(tree.ancestor_mask()), 128 ** -0.5, sinks=sinks_b)
+    check_close(out, o_ref, lse, lse_ref, "captured graph after a same-shape re-plan")
+    with pytest.raises(RuntimeError, match="captured"):
+        attn.plan(prob.qo_indptr, prob.prefix_lens, 32, 8, 128, tree_masks=prob.tree_masks(), page_size=16,
+                  page_indptr=mp.page_indptr, page_table=table_a.to(DEV), kv_layout="HND", sinks=sinks_b.cpu())
+
+
 # ------------------------------------------- DTA draft reuse (model/dflash.py:92-133)
 def test_dta_draft_cascade_through_plan_run():
     """The DTA draft's cascade (model/dflash.py:96-133; runner built with
