@@ -733,7 +733,7 @@ OTHER_WORKLOADS = {
 }
 
 
-SYSTEM_WORKLOADS = ("dropin", "step")
+SYSTEM_WORKLOADS = ("dropin", "dta", "step")
 
 
 def _events_us(fn, reps: int, torch) -> float:
@@ -749,6 +749,102 @@ def _events_us(fn, reps: int, torch) -> float:
     e1.record(s)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) * 1e3 / reps
+
+
+def measure_dta(args) -> int:
+    """The DTA draft's cascade (model/dflash.py:96-133) at Qwen3-8B heads: 4
+    rows of 16 noise tokens, a DynamicCache draft layer of 4096 tokens and 17
+    projected context tokens, one distinct cache per layer (36) so nothing
+    stays in L2.  Three forms per layer: the reference's call site over the
+    drop-ins (torch.cat of [cache | context], the NHD copies, single_prefill,
+    the causal=False runner), eager; one plan whose shared level is the
+    concatenation made by torch.cat each call; one plan reading the two
+    segments in place (no concatenation).  The plan forms replay one hipGraph
+    of all layers."""
+    import numpy as np
+    import torch
+    import d2sd
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    bsz, ql, hq, hkv, d, lc, cap, ctx, nl = 4, 16, 32, 8, 128, 4096, 4096 + 256, 17, args.layers
+    gen = torch.Generator(device=dev).manual_seed(args.seed + 2)
+
+    def rnd(*shape):
+        return torch.randn(shape, generator=gen, device=dev).to(torch.bfloat16)
+
+    # per layer: q [bsz, Hq, q_len, D], the k/v projection [bsz, Hkv, ctx + q_len, D]
+    # (dflash.py:87), the draft cache layer [1, Hkv, cap, D] holding lc tokens
+    layers = [dict(q=rnd(bsz, hq, ql, d), k=rnd(bsz, hkv, ctx + ql, d), v=rnd(bsz, hkv, ctx + ql, d),
+                   kc=rnd(1, hkv, cap, d), vc=rnd(1, hkv, cap, d)) for _ in range(nl)]
+    scale = d ** -0.5
+    n = bsz * ql
+    runner = d2sd.CascadeGraphRunner(ql, hq, hkv, d, torch.bfloat16, dev, scale, causal=False)
+
+    def call_site(x):
+        k_sh = torch.cat([x["kc"][0, :, :lc], x["k"][0, :, :ctx]], dim=1)
+        v_sh = torch.cat([x["vc"][0, :, :lc], x["v"][0, :, :ctx]], dim=1)
+        q_fi = x["q"].transpose(1, 2)
+        out, lse = d2sd.single_prefill_with_kv_cache(q_fi.reshape(n, hq, d), k_sh.transpose(0, 1).contiguous(),
+                                                     v_sh.transpose(0, 1).contiguous(), causal=False,
+                                                     return_lse=True, sm_scale=scale)
+        runner.run(q_fi, x["k"][:, :, ctx:].transpose(1, 2).contiguous(),
+                   x["v"][:, :, ctx:].transpose(1, 2).contiguous(), out.view(bsz, ql, hq, d), lse.view(bsz, ql, hq))
+        return out
+
+    mask = np.zeros((n, n), dtype=bool)
+    for b in range(bsz):
+        mask[b * ql:(b + 1) * ql, b * ql:(b + 1) * ql] = True
+    two = d2sd.CascadeVerifyAttention(dev).plan([0, n], [lc + ctx], hq, hkv, d, tree_masks=[mask], page_size=0,
+                                                kv_layout="HND", prefix_split=[lc])
+    one = d2sd.CascadeVerifyAttention(dev).plan([0, n], [lc + ctx], hq, hkv, d, tree_masks=[mask], page_size=0,
+                                                kv_layout="HND")
+    # plan inputs made once: queries / noise K,V in the node layout
+    prep = [dict(q=x["q"].transpose(1, 2).reshape(n, hq, d).contiguous(),
+                 kn=x["k"][:, :, ctx:].transpose(1, 2).reshape(n, hkv, d).contiguous(),
+                 vn=x["v"][:, :, ctx:].transpose(1, 2).reshape(n, hkv, d).contiguous(),
+                 kcat=torch.empty(hkv, lc + ctx, d, dtype=torch.bfloat16, device=dev),
+                 vcat=torch.empty(hkv, lc + ctx, d, dtype=torch.bfloat16, device=dev),
+                 o=torch.empty(n, hq, d, dtype=torch.bfloat16, device=dev),
+                 lse=torch.empty(n, hq, dtype=torch.float32, device=dev)) for x in layers]
+
+    def run_two():
+        for x, y in zip(layers, prep):
+            two.run(y["q"], y["kn"], y["vn"], (x["kc"], x["k"][0, :, :ctx]), (x["vc"], x["v"][0, :, :ctx]),
+                    out=y["o"], lse=y["lse"])
+
+    def run_cat():
+        for x, y in zip(layers, prep):
+            torch.cat([x["kc"][0, :, :lc], x["k"][0, :, :ctx]], dim=1, out=y["kcat"])
+            torch.cat([x["vc"][0, :, :lc], x["v"][0, :, :ctx]], dim=1, out=y["vcat"])
+            one.run(y["q"], y["kn"], y["vn"], y["kcat"], y["vcat"], out=y["o"], lse=y["lse"])
+
+    reps = max(5, args.kernel_reps // 5)
+    for _ in range(3):
+        for x in layers:
+            call_site(x)
+    site_us = _events_us(lambda: [call_site(x) for x in layers], reps, torch) / nl
+    graphs = {}
+    for key, fn in (("two", run_two), ("cat", run_cat)):
+        fn()
+        torch.cuda.synchronize()
+        g = d2sd.HipGraph()
+        with g.capture():
+            fn()
+        for _ in range(3):
+            g.replay()
+        graphs[key] = _events_us(g.replay, reps, torch) / nl
+    print(json.dumps({
+        "workload": "dta_draft_qwen3_8b_cache4096_ctx17_rows4x16", "value": graphs["two"], "unit": "us/layer",
+        "higher_is_better": False, "rows": bsz, "row_len": ql, "queries": n, "cache_len": lc, "context_len": ctx,
+        "layers": nl, "two_segment_us": graphs["two"], "concat_then_run_us": graphs["cat"],
+        "reference_call_site_us": site_us,
+        "note": "value: one plan reading [draft cache | context] in place, hipGraph of all layers; "
+                "concat_then_run: the same plan shape over torch.cat's concatenation made each call (graph); "
+                "reference_call_site: dflash.py:103-133 eager over the drop-ins (cat, NHD copies, "
+                "single_prefill, causal=False runner)",
+    }), flush=True)
+    return 0
 
 
 def measure_dropin(args) -> int:
@@ -934,6 +1030,9 @@ def measure_workload(args) -> int:
     for name in args.workload.split(","):
         if name == "dropin":
             measure_dropin(args)
+            continue
+        if name == "dta":
+            measure_dta(args)
             continue
         if name == "step":
             measure_step(args)

@@ -322,6 +322,16 @@ int d2sd_cascade_plan(const d2sd_cascade_plan_desc* desc, int32_t* host_plan, si
         return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: page_indptr gives a request fewer pages than prefix_len needs");
     }
   }
+  if (desc->prefix_split) {
+    if (desc->page_size != 0 || desc->dynamic_prefix)
+      return fail(D2SD_ERR_UNSUPPORTED, "cascade_plan: a two-segment prefix needs a contiguous prefix and a static plan");
+    for (int r = 0; r < desc->num_reqs; ++r) {
+      if (desc->prefix_split[r] < 0 || desc->prefix_split[r] > desc->prefix_len[r])
+        return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: prefix_split[r] must lie in [0, prefix_len[r]]");
+      if (desc->prefix2_tok_indptr && desc->prefix2_tok_indptr[r] < 0)
+        return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: negative prefix2_tok_indptr");
+    }
+  }
   d2sd::VerifyPlanInput in{};
   in.num_reqs = desc->num_reqs;
   in.qo_indptr = desc->qo_indptr;
@@ -336,6 +346,8 @@ int d2sd_cascade_plan(const d2sd_cascade_plan_desc* desc, int32_t* host_plan, si
   in.max_splits = desc->max_splits;
   in.waves = desc->waves_per_block;
   in.page_size = desc->page_size;
+  in.prefix_split = desc->prefix_split;
+  in.prefix2_tok_indptr = desc->prefix2_tok_indptr;
   if (desc->dynamic_prefix != 0 && desc->dynamic_prefix != 1)
     return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: dynamic_prefix must be 0 or 1");
   if (desc->window_left < -1) return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: window_left must be >= -1");
@@ -378,15 +390,21 @@ int d2sd_cascade_plan(const d2sd_cascade_plan_desc* desc, int32_t* host_plan, si
   info->dynamic_prefix = desc->dynamic_prefix;
   info->window_left = desc->window_left;
   info->fused = out.fused;
-  int64_t extent = 0;
+  int64_t extent = 0, extent2 = 0;
   for (int r = 0; r < desc->num_reqs; ++r) {
+    const int len1 = desc->prefix_split ? desc->prefix_split[r] : desc->prefix_len[r];
+    const int len2 = desc->prefix_len[r] - len1;
     if (desc->page_size > 0)
       extent = desc->page_indptr[desc->num_reqs];
-    else if (desc->prefix_len[r] > 0)
-      extent = std::max<int64_t>(
-          extent, (int64_t)(desc->prefix_tok_indptr ? desc->prefix_tok_indptr[r] : 0) + desc->prefix_len[r]);
+    else if (len1 > 0)
+      extent = std::max<int64_t>(extent, (int64_t)(desc->prefix_tok_indptr ? desc->prefix_tok_indptr[r] : 0) + len1);
+    if (len2 > 0)
+      extent2 = std::max<int64_t>(extent2,
+                                  (int64_t)(desc->prefix2_tok_indptr ? desc->prefix2_tok_indptr[r] : 0) + len2);
   }
   info->prefix_extent = extent;
+  info->prefix2_extent = extent2;
+  for (const auto& w : out.items) info->two_segment |= w.mode != d2sd::MODE_NOOP && w.src == d2sd::SRC_PREFIX2;
   int max_q = 0;
   for (int r = 0; r < desc->num_reqs; ++r) max_q = std::max(max_q, desc->qo_indptr[r + 1] - desc->qo_indptr[r]);
   info->max_qo_len = max_q;
@@ -421,7 +439,8 @@ static int build_verify_params(const d2sd_cascade_plan_info* info, const d2sd_ca
   if (info->workspace_bytes > 0 && !aligned16(a->workspace))
     return fail(D2SD_ERR_INVALID_ARG, "cascade_run: workspace must be 16-byte aligned");
   const bool has_prefix = a->k_prefix != nullptr;
-  if (info->max_splits_used > 0 && !has_prefix)
+  // (a two-segment plan whose first segment is empty everywhere reads none of k_prefix)
+  if (info->max_splits_used > 0 && !has_prefix && !(info->two_segment && info->prefix_extent == 0))
     return fail(D2SD_ERR_INVALID_ARG, "cascade_run: the plan has prefix keys but k_prefix is null");
   if (has_prefix) {
     if (info->page_size > 0 ? (a->prefix_extent <= 0 || a->prefix_extent > INT32_MAX)
@@ -452,6 +471,21 @@ static int build_verify_params(const d2sd_cascade_plan_info* info, const d2sd_ca
                                           " nodes (" + std::to_string((info->max_qo_len + 63) / 64) + " words)");
   if (info->kv_dtype == D2SD_KV_FP8_E4M3 && has_prefix && (!a->k_scale || !a->v_scale))
     return fail(D2SD_ERR_INVALID_ARG, "cascade_run: fp8 prefix needs k_scale and v_scale");
+  if (info->two_segment) {
+    const int esz = info->kv_dtype == D2SD_KV_FP8_E4M3 ? 1 : 2;
+    if (info->page_size != 0 || info->dynamic_prefix)
+      return fail(D2SD_ERR_INVALID_ARG, "cascade_run: info does not come from d2sd_cascade_plan");
+    if (!a->k_prefix2 || !a->v_prefix2)
+      return fail(D2SD_ERR_INVALID_ARG, "cascade_run: the plan reads a second prefix segment; k_prefix2 / v_prefix2 are null");
+    if (!aligned16(a->k_prefix2) || !aligned16(a->v_prefix2) || (a->prefix2_stride_tok * esz) % 16 != 0 ||
+        (a->prefix2_stride_head * esz) % 16 != 0)
+      return fail(D2SD_ERR_INVALID_ARG, "cascade_run: second prefix segment must be 16-byte aligned with 16-byte strides");
+    if (a->prefix2_extent < info->prefix2_extent)
+      return fail(D2SD_ERR_INVALID_ARG, "cascade_run: k_prefix2 holds fewer tokens than the plan reads (need " +
+                                            std::to_string(info->prefix2_extent) + ")");
+    if (info->kv_dtype == D2SD_KV_FP8_E4M3 && (!a->k2_scale || !a->v2_scale))
+      return fail(D2SD_ERR_INVALID_ARG, "cascade_run: fp8 second prefix segment needs k2_scale and v2_scale");
+  }
   if (!(a->sm_scale > 0.f) || !std::isfinite(a->sm_scale))
     return fail(D2SD_ERR_INVALID_ARG, "cascade_run: bad sm_scale");
 
@@ -487,6 +521,16 @@ static int build_verify_params(const d2sd_cascade_plan_info* info, const d2sd_ca
   pre.log2_page = lg;
   pre.fp8 = info->kv_dtype == D2SD_KV_FP8_E4M3;
   pre.num_pages = info->page_size > 0 ? (int)a->prefix_extent : 0;
+  if (info->two_segment) {
+    d2sd::VerifySource& pre2 = p.pre2;
+    pre2.k = a->k_prefix2;
+    pre2.v = a->v_prefix2;
+    pre2.stride_tok = a->prefix2_stride_tok;
+    pre2.stride_head = a->prefix2_stride_head;
+    pre2.k_scale = a->k2_scale;
+    pre2.v_scale = a->v2_scale;
+    pre2.fp8 = pre.fp8;
+  }
   d2sd::VerifySource& suf = p.suf;
   suf.k = a->k_suffix;
   suf.v = a->v_suffix;
@@ -823,7 +867,10 @@ int d2sd_cascade_attention(const d2sd_cascade_plan_info* info, const d2sd_cascad
   if (int rc = build_verify_params(info, a, p)) return rc;
   hipError_t e = d2sd::launch_verify_attention(p, info->head_dim, info->waves_per_block, info->page_size > 0,
                                                info->kv_dtype == D2SD_KV_FP8_E4M3,
-                                               info->fused ? d2sd::KIND_FUSED : d2sd::KIND_SPLIT, info->num_items,
+                                               info->two_segment ? d2sd::KIND_SEGMENTS
+                                               : info->fused     ? d2sd::KIND_FUSED
+                                                                 : d2sd::KIND_SPLIT,
+                                               info->num_items,
                                                (hipStream_t)stream);
   return e == hipSuccess ? D2SD_OK : fail_hip(e, "cascade attention launch");
 }

@@ -92,14 +92,17 @@ struct AttnParams {
 // (32 per wave; 64 per wave of a two-wave workgroup) and either one key chunk
 // of the shared prefix or the whole suffix tree, then one merge launch.
 // ---------------------------------------------------------------------------
-// Keys an item reads: a chunk of the shared prefix, the suffix tree, or
-// (SRC_BOTH) its group's whole visible prefix and then its suffix tree.
-enum : int { SRC_PREFIX = 0, SRC_SUFFIX = 1, SRC_BOTH = 2 };
+// Keys an item reads: a chunk of the shared prefix, the suffix tree,
+// (SRC_BOTH) its group's whole visible prefix and then its suffix tree, or a
+// chunk of the second segment of a two-segment contiguous prefix (kv_begin,
+// kv_end and base in that segment's own key numbering).
+enum : int { SRC_PREFIX = 0, SRC_SUFFIX = 1, SRC_BOTH = 2, SRC_PREFIX2 = 3 };
 
 // Kinds of cascade plans (one attention-kernel instantiation each): split
-// prefixes with partial states and a merge launch, fused (no split), and
-// in-place suffix items (the drop-in runner's per-row local level).
-enum : int { KIND_SPLIT = 0, KIND_FUSED = 1, KIND_INPLACE = 2 };
+// prefixes with partial states and a merge launch, fused (no split), in-place
+// suffix items (the drop-in runner's per-row local level), and split plans
+// over a two-segment contiguous prefix.
+enum : int { KIND_SPLIT = 0, KIND_FUSED = 1, KIND_INPLACE = 2, KIND_SEGMENTS = 3 };
 
 // 64 bytes; everything a workgroup needs is baked in by the planner so that
 // the kernel's first dependent load is the item itself.
@@ -151,6 +154,7 @@ struct VerifyParams {
   const float* sinks;      // nullable, [Hq]
   const unsigned long long* tree_mask;  // [total_q][mask_words]
   VerifySource pre, suf;
+  VerifySource pre2;       // second prefix segment (SRC_PREFIX2 items; contiguous)
   float sm_scale;
   float sm_scale_log2;
   int group;               // Hq / Hkv

@@ -126,7 +126,13 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
   const int max_chunk = verify_max_chunk_tiles(in.page_size);
   constexpr int kMinChunk = 2;  // shorter chunks cost more in partials than they gain in balance
 
-  std::vector<int> nq(R), qtiles(R), ptiles(R), stiles(R), kv0(R), kv1(R);
+  // A two-segment prefix (in.prefix_split) is tiled segment by segment: the
+  // first segment's tiles start at the window start kv0 (its last tile ends
+  // at the split, possibly partial), the second's at its own first visible
+  // key, so no tile holds keys of both segments.  Tile boundaries of request
+  // r: key kv0 + 64 t for t <= ta[r], then second-segment key b0[r] + 64 (t - ta[r]).
+  std::vector<int> nq(R), qtiles(R), ptiles(R), stiles(R), kv0(R), kv1(R), sp(R), ta(R), b0(R);
+  bool second = false;  // some request sees keys of the second segment
   for (int r = 0; r < R; ++r) {
     nq[r] = in.qo_indptr[r + 1] - in.qo_indptr[r];
     qtiles[r] = (nq[r] * g + ROWS - 1) / ROWS;
@@ -134,7 +140,12 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
     const int Leff = in.window_left >= 0 ? std::min(L, in.window_left) : L;
     kv0[r] = L - Leff;
     kv1[r] = L;
-    ptiles[r] = nq[r] > 0 ? (Leff + 63) / 64 : 0;
+    sp[r] = in.prefix_split ? std::min(std::max(in.prefix_split[r], 0), L) : L;
+    ta[r] = sp[r] > kv0[r] ? (sp[r] - kv0[r] + 63) / 64 : 0;
+    b0[r] = std::max(kv0[r], sp[r]) - sp[r];
+    const int tb = (L - sp[r] - b0[r] + 63) / 64;
+    ptiles[r] = nq[r] > 0 ? ta[r] + tb : 0;
+    second = second || (nq[r] > 0 && tb > 0);
     stiles[r] = (nq[r] + 63) / 64;
   }
   std::vector<int> grp0(R + 1, 0);
@@ -227,15 +238,31 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
   }
 
   // ---- partial slots: per group its prefix chunks in key order, then the suffix ----
+  // Chunk c of S over tiles [t0, t1): tiles [t0 + span c / S, t0 + span (c+1) / S).
+  // A chunk holding tiles of both segments is cut at the split: two items.
+  auto chunk_tiles = [](const Piece& pc, int S, int c, int& a, int& b) {
+    const int span = pc.t1 - pc.t0;
+    a = pc.t0 + (int)((long long)span * c / S);
+    b = pc.t0 + (int)((long long)span * (c + 1) / S);
+  };
   std::vector<int> gchunks(ngroups, 0);
   for (size_t s = 0; s < sets.size(); ++s) {
     const Piece& pc = sets[s][0];
-    for (int qt = 0; qt < qtiles[pc.req]; ++qt) gchunks[grp0[pc.req] + pc.kvh * qtiles[pc.req] + qt] += nchunk[s][qt];
+    for (int qt = 0; qt < qtiles[pc.req]; ++qt) {
+      int& gc = gchunks[grp0[pc.req] + pc.kvh * qtiles[pc.req] + qt];
+      gc += nchunk[s][qt];
+      for (int c = 0; c < nchunk[s][qt]; ++c) {
+        int a, b;
+        chunk_tiles(pc, nchunk[s][qt], c, a, b);
+        gc += a < ta[pc.req] && ta[pc.req] < b;
+      }
+    }
   }
   // When no group's prefix is split, one item per group reads the group's
   // prefix and then its suffix tree (SRC_BOTH) and writes the output: the
-  // plan has no partial states and no merge launch.
-  bool fuse = true;
+  // plan has no partial states and no merge launch.  Plans that read a
+  // second prefix segment are never fused.
+  bool fuse = !second;
   for (int gi = 0; gi < ngroups; ++gi) fuse = fuse && gchunks[gi] <= 1;
   std::vector<int> slot0(ngroups, -1), next_slot(ngroups, 0);
   int slot = 0, max_splits_used = 0;
@@ -261,27 +288,43 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
     const int r = pc.req, h = pc.kvh, x = set_xcd[s];
     const int q0 = in.qo_indptr[r];
     const int pbase = in.page_size > 0 ? in.page_indptr[r] : (in.prefix_tok_indptr ? in.prefix_tok_indptr[r] : 0);
+    const int pbase2 = in.prefix2_tok_indptr ? in.prefix2_tok_indptr[r] : 0;
     for (int qt = 0; qt < qtiles[r]; ++qt) {
       const int gi = grp0[r] + h * qtiles[r] + qt;
       const int S = nchunk[s][qt];
-      const int span = pc.t1 - pc.t0;
       for (int c = 0; c < S; ++c) {
-        const int a = pc.t0 + (int)((long long)span * c / S), b = pc.t0 + (int)((long long)span * (c + 1) / S);
+        int a, b;
+        chunk_tiles(pc, S, c, a, b);
         VerifyItem w{};
         w.req = r;
         w.kvh = h;
         w.qtile = qt;
-        w.src = fuse ? SRC_BOTH : SRC_PREFIX;
-        w.kv0 = kv0[r];
-        w.plan_len = kv1[r];
-        w.kv_begin = kv0[r] + 64 * a;
-        w.kv_end = std::min(kv1[r], kv0[r] + 64 * b);
-        w.slot = fuse ? -1 : next_slot[gi]++;
         w.mode = fuse ? MODE_FINAL : MODE_PARTIAL;
         w.q0 = q0;
         w.nq = nq[r];
-        w.base = pbase;
-        lists[x].push_back({w, (b - a) + (fuse ? 2 * stiles[r] : 0)});
+        if (a < ta[r]) {  // first segment: keys [kv0 + 64 a, min(kv0 + 64 b, split))
+          const int e = std::min(b, ta[r]);
+          w.src = fuse ? SRC_BOTH : SRC_PREFIX;
+          w.kv0 = kv0[r];
+          w.plan_len = kv1[r];
+          w.kv_begin = kv0[r] + 64 * a;
+          w.kv_end = std::min(sp[r], kv0[r] + 64 * e);
+          w.slot = fuse ? -1 : next_slot[gi]++;
+          w.base = pbase;
+          lists[x].push_back({w, (e - a) + (fuse ? 2 * stiles[r] : 0)});
+        }
+        if (b > ta[r]) {  // second segment, in its own key numbering
+          const int f = std::max(a, ta[r]);
+          const int len2 = kv1[r] - sp[r];
+          w.src = SRC_PREFIX2;
+          w.kv0 = b0[r];
+          w.plan_len = len2;
+          w.kv_begin = b0[r] + 64 * (f - ta[r]);
+          w.kv_end = std::min(len2, b0[r] + 64 * (b - ta[r]));
+          w.slot = next_slot[gi]++;
+          w.base = pbase2;
+          lists[x].push_back({w, b - f});
+        }
       }
     }
     if (!pc.suffix) continue;

@@ -24,6 +24,12 @@ struct VerifyPlanInput {
   int max_splits;  // 0: no limit beyond kMaxVerifySplits
   int waves;       // 0: choose; else 2, 4 or 8
   int page_size;   // 0: contiguous prefix
+  // Two-segment contiguous prefix (nullable): keys [0, prefix_split[r]) of
+  // request r are the first segment (prefix_tok_indptr), keys
+  // [prefix_split[r], prefix_len[r]) the second (SRC_PREFIX2 items, token
+  // prefix2_tok_indptr[r] + key - prefix_split[r]; nullable => 0).
+  const int* prefix_split;
+  const int* prefix2_tok_indptr;
 };
 
 struct VerifyPlanOutput {
@@ -64,7 +70,8 @@ int verify_wgs_per_cu(int waves);
 int verify_rows(int waves);
 int verify_auto_waves(const VerifyPlanInput& in, int num_cus);
 
-// kind: KIND_SPLIT, KIND_FUSED (VerifyPlanOutput::fused) or KIND_INPLACE
+// kind: KIND_SPLIT, KIND_FUSED (VerifyPlanOutput::fused), KIND_INPLACE or
+// KIND_SEGMENTS (a plan with SRC_PREFIX2 items)
 hipError_t launch_verify_attention(const VerifyParams& p, int head_dim, int waves, bool paged, bool fp8, int kind,
                                    int nitems, hipStream_t s);
 hipError_t launch_verify_merge(const VerifyParams& p, int head_dim, int rows, int nmerges, hipStream_t s);

@@ -141,7 +141,9 @@ void cascade(bool no_alloc, const at::Tensor& info, const at::Tensor& plan, cons
              const c10::optional<at::Tensor>& tree_mask, int64_t mask_mode, int64_t mask_words,
              const c10::optional<at::Tensor>& prefix_len, const c10::optional<at::Tensor>& k_scale,
              const c10::optional<at::Tensor>& v_scale, const c10::optional<at::Tensor>& sinks, double sm_scale,
-             bool lse_base2, at::Tensor& out, at::Tensor& lse) {
+             bool lse_base2, at::Tensor& out, at::Tensor& lse, const c10::optional<at::Tensor>& k_prefix2,
+             const c10::optional<at::Tensor>& v_prefix2, at::IntArrayRef prefix2,
+             const c10::optional<at::Tensor>& k2_scale, const c10::optional<at::Tensor>& v2_scale) {
   TORCH_CHECK(info.device().is_cpu() && info.scalar_type() == at::kByte && info.is_contiguous() &&
                   (size_t)info.numel() == sizeof(d2sd_cascade_plan_info),
               "d2sd: info must hold the bytes of a d2sd_cascade_plan_info");
@@ -190,6 +192,16 @@ void cascade(bool no_alloc, const at::Tensor& info, const at::Tensor& plan, cons
   a.lse_stride_n = lse.stride(0);
   a.sm_scale = (float)sm_scale;
   a.lse_base2 = lse_base2 ? 1 : 0;
+  if (k_prefix2.has_value()) {
+    TORCH_CHECK(prefix2.size() == 3, "d2sd: prefix2 = (stride_tok, stride_head, extent)");
+    a.k_prefix2 = k_prefix2->data_ptr();
+    a.v_prefix2 = ptr_or_null(v_prefix2);
+    a.prefix2_stride_tok = prefix2[0];
+    a.prefix2_stride_head = prefix2[1];
+    a.prefix2_extent = prefix2[2];
+    a.k2_scale = (const float*)ptr_or_null(k2_scale);
+    a.v2_scale = (const float*)ptr_or_null(v2_scale);
+  }
   if (!no_alloc) {
     need_device(workspace, "workspace");
     a.workspace = workspace.data_ptr();
@@ -207,10 +219,13 @@ void cascade(bool no_alloc, const at::Tensor& info, const at::Tensor& plan, cons
       const c10::optional<at::Tensor>&page_table, const c10::optional<at::Tensor>&tree_mask, int64_t mask_mode,    \
       int64_t mask_words, const c10::optional<at::Tensor>&prefix_len, const c10::optional<at::Tensor>&k_scale,     \
       const c10::optional<at::Tensor>&v_scale, const c10::optional<at::Tensor>&sinks, double sm_scale,             \
-      bool lse_base2, at::Tensor &out, at::Tensor &lse
+      bool lse_base2, at::Tensor &out, at::Tensor &lse, const c10::optional<at::Tensor>&k_prefix2,               \
+      const c10::optional<at::Tensor>&v_prefix2, at::IntArrayRef prefix2, const c10::optional<at::Tensor>&k2_scale, \
+      const c10::optional<at::Tensor>&v2_scale
 #define CASCADE_PASS                                                                                       \
   info, plan, workspace, q, k_suffix, v_suffix, k_prefix, v_prefix, prefix, page_table, tree_mask, mask_mode, \
-      mask_words, prefix_len, k_scale, v_scale, sinks, sm_scale, lse_base2, out, lse
+      mask_words, prefix_len, k_scale, v_scale, sinks, sm_scale, lse_base2, out, lse, k_prefix2, v_prefix2,   \
+      prefix2, k2_scale, v2_scale
 
 void cascade_run(CASCADE_ARGS) { cascade(false, CASCADE_PASS); }
 void cascade_run_no_alloc(CASCADE_ARGS) { cascade(true, CASCADE_PASS); }
@@ -228,7 +243,8 @@ TORCH_LIBRARY(d2sd, m) {
       "(Tensor info, Tensor plan, Tensor workspace, Tensor q, Tensor k_suffix, Tensor v_suffix, Tensor? k_prefix, "
       "Tensor? v_prefix, int[] prefix, Tensor? page_table, Tensor? tree_mask, int mask_mode, int mask_words, "
       "Tensor? prefix_len, Tensor? k_scale, Tensor? v_scale, Tensor? sinks, float sm_scale, bool lse_base2, "
-      "Tensor(a!) out, Tensor(b!) lse) -> ()";
+      "Tensor(a!) out, Tensor(b!) lse, Tensor? k_prefix2=None, Tensor? v_prefix2=None, int[] prefix2=[], "
+      "Tensor? k2_scale=None, Tensor? v2_scale=None) -> ()";
   m.def((std::string("cascade_run") + cascade_schema).c_str());
   m.def((std::string("cascade_run_no_alloc") + cascade_schema).c_str());
 }

@@ -1011,7 +1011,8 @@ struct Shape<8> { static constexpr int W = 8, RB = 1, OCC = 2; };
 // allocation carries another kind's path: KIND_SPLIT (prefix-chunk and suffix
 // items), KIND_FUSED (no group split: SRC_BOTH and suffix items), KIND_INPLACE
 // (suffix items merging into the stored output: the per-row local level of
-// the drop-in runner).
+// the drop-in runner), KIND_SEGMENTS (split plans over a two-segment
+// contiguous prefix: SRC_PREFIX, SRC_PREFIX2 and suffix items).
 template <int D, int WPB, bool PAGED, bool FP8, int KIND>
 __global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(Shape<WPB>::OCC, Shape<WPB>::OCC)))
 void verify_attn_kernel(const VerifyParams p) {
@@ -1034,6 +1035,10 @@ void verify_attn_kernel(const VerifyParams p) {
     verify_body<D, W, RB, R::KST, R::VST, R::NPG, false, true, false, true, true, true>(p, w, p.suf, sm, st);
   } else if (KIND == KIND_SPLIT && w.src == SRC_PREFIX) {
     verify_body<D, W, RB, R::KST, R::VST, R::NPG, PAGED, false, FP8>(p, w, p.pre, sm, st);
+  } else if (KIND == KIND_SEGMENTS && w.src != SRC_SUFFIX) {
+    // a chunk of the contiguous prefix's first or second segment
+    verify_body<D, W, RB, R::KST, R::VST, R::NPG, false, false, FP8>(p, w, w.src == SRC_PREFIX2 ? p.pre2 : p.pre,
+                                                                      sm, st);
   } else if (w.src == SRC_SUFFIX) {
     verify_body<D, W, RB, R::KST, R::VST, R::NPG, false, true, false>(p, w, p.suf, sm, st);
   } else if constexpr (KIND == KIND_FUSED) {
@@ -1163,13 +1168,19 @@ static hipError_t launch_verify_w(const VerifyParams& p, bool paged, bool fp8, i
   if (kind == KIND_FUSED) return launch_verify_k<D, WPB, KIND_FUSED>(p, paged, fp8, nitems, s);
   // in-place plans read no prefix: one instantiation
   if (kind == KIND_INPLACE) return launch_verify_t<D, WPB, false, false, KIND_INPLACE>(p, nitems, s);
+  // two-segment prefixes are contiguous
+  if (kind == KIND_SEGMENTS)
+    return paged ? hipErrorInvalidValue
+           : fp8 ? launch_verify_t<D, WPB, false, true, KIND_SEGMENTS>(p, nitems, s)
+                 : launch_verify_t<D, WPB, false, false, KIND_SEGMENTS>(p, nitems, s);
   return launch_verify_k<D, WPB, KIND_SPLIT>(p, paged, fp8, nitems, s);
 }
 
 hipError_t launch_verify_attention(const VerifyParams& p, int head_dim, int waves, bool paged, bool fp8, int kind,
                                    int nitems, hipStream_t s) {
   if (nitems <= 0) return hipSuccess;
-  if (kind != KIND_SPLIT && kind != KIND_FUSED && kind != KIND_INPLACE) return hipErrorInvalidValue;
+  if (kind != KIND_SPLIT && kind != KIND_FUSED && kind != KIND_INPLACE && kind != KIND_SEGMENTS)
+    return hipErrorInvalidValue;
   if (head_dim == 128) {
     if (waves == 2) return launch_verify_w<128, 2>(p, paged, fp8, kind, nitems, s);
     if (waves == 4) return launch_verify_w<128, 4>(p, paged, fp8, kind, nitems, s);

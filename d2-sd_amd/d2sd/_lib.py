@@ -65,6 +65,8 @@ class PlanDesc(C.Structure):
         ("max_splits", C.c_int),
         ("waves_per_block", C.c_int),
         ("dynamic_prefix", C.c_int),
+        ("prefix_split", C.POINTER(C.c_int32)),
+        ("prefix2_tok_indptr", C.POINTER(C.c_int32)),
     ]
 
 
@@ -90,6 +92,8 @@ class PlanInfo(C.Structure):
         ("prefix_extent", C.c_int64),
         ("max_qo_len", C.c_int),
         ("fused", C.c_int),
+        ("two_segment", C.c_int),
+        ("prefix2_extent", C.c_int64),
     ]
 
 
@@ -127,6 +131,13 @@ class RunArgs(C.Structure):
         ("lse_base2", C.c_int),
         ("workspace", C.c_void_p),
         ("workspace_bytes", C.c_size_t),
+        ("k_prefix2", C.c_void_p),
+        ("v_prefix2", C.c_void_p),
+        ("prefix2_stride_tok", C.c_int64),
+        ("prefix2_stride_head", C.c_int64),
+        ("prefix2_extent", C.c_int64),
+        ("k2_scale", C.c_void_p),
+        ("v2_scale", C.c_void_p),
     ]
 
 

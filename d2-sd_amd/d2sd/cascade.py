@@ -134,6 +134,8 @@ class CascadeVerifyAttention:
         waves_per_block: int = 0,
         num_cus: int = 0,
         dynamic_prefix: bool = False,
+        prefix_split: Optional[Sequence[int]] = None,
+        prefix2_tok_indptr: Optional[Sequence[int]] = None,
     ) -> "CascadeVerifyAttention":
         """Plan one verify call.
 
@@ -153,6 +155,14 @@ class CascadeVerifyAttention:
         the current lengths in self.prefix_len_dev (set_prefix_len(), or any
         device write, e.g. PagedKVCommit's advance), each clamped to
         [0, planned length].
+        prefix_split [R]: a two-segment contiguous prefix (static plans): keys
+        [0, prefix_split[r]) of request r come from the first prefix tensor,
+        keys [prefix_split[r], prefix_len[r]) from the second, at token
+        prefix2_tok_indptr[r] (default 0) of it; run() then takes
+        k_prefix = (k_first, k_second) and v_prefix likewise, both in
+        kv_layout.  This is the DTA draft's shared level [draft cache |
+        projected target context] (model/dflash.py:103-106) without the
+        concatenation.
         """
         qo = _i32(qo_indptr)
         pl = _i32(prefix_len)
@@ -177,6 +187,13 @@ class CascadeVerifyAttention:
         pti = _i32(prefix_tok_indptr) if (prefix_tok_indptr is not None and int(page_size) == 0) else None
         if pti is not None and pti.shape[0] != R:
             raise ValueError("prefix_tok_indptr must have R entries")
+        psplit = _i32(prefix_split) if prefix_split is not None else None
+        pti2 = _i32(prefix2_tok_indptr) if (prefix2_tok_indptr is not None and psplit is not None) else None
+        if psplit is not None:
+            if psplit.shape[0] != R or (pti2 is not None and pti2.shape[0] != R):
+                raise ValueError("prefix_split and prefix2_tok_indptr must have R entries")
+            if int(page_size) > 0 or dynamic_prefix:
+                raise ValueError("a two-segment prefix needs a contiguous prefix and a static plan")
         desc = _lib.PlanDesc()
         desc.num_reqs = R
         desc.qo_indptr = qo.ctypes.data_as(C.POINTER(C.c_int32))
@@ -193,6 +210,8 @@ class CascadeVerifyAttention:
         desc.max_splits = max_splits
         desc.waves_per_block = waves_per_block
         desc.dynamic_prefix = int(bool(dynamic_prefix))
+        desc.prefix_split = psplit.ctypes.data_as(C.POINTER(C.c_int32)) if psplit is not None else None
+        desc.prefix2_tok_indptr = pti2.ctypes.data_as(C.POINTER(C.c_int32)) if pti2 is not None else None
         info = _lib.PlanInfo()
         # One planner pass into a host buffer kept across plans (16K entries at
         # first); a plan that needs more is planned again into a larger one.
@@ -227,19 +246,31 @@ class CascadeVerifyAttention:
                 raise ValueError("page_table shorter than page_indptr[-1]")
         if sinks is not None and sinks.numel() != num_qo_heads:
             raise ValueError("sinks must have num_qo_heads entries")
+        k2_scale = v2_scale = None
         if fp8:
             # the scales dequantise prefix keys / values; a plan without any
-            # prefix key needs none (as d2sd_cascade_run)
+            # prefix key needs none (as d2sd_cascade_run).  A two-segment
+            # prefix takes one scale pair for both segments or a (first,
+            # second) pair of each.
+            if isinstance(k_scale, (tuple, list)):
+                k_scale, k2_scale = k_scale
+            if isinstance(v_scale, (tuple, list)):
+                v_scale, v2_scale = v_scale
+            if info.two_segment:
+                k2_scale = k_scale if k2_scale is None else k2_scale
+                v2_scale = v_scale if v2_scale is None else v2_scale
             if any(int(x) > 0 for x in prefix_len) and (k_scale is None or v_scale is None):
                 raise ValueError("fp8 KV needs k_scale and v_scale")
         else:
             k_scale = v_scale = None
+        if not info.two_segment:
+            k2_scale = v2_scale = None
 
         old = getattr(self, "info", None) if self._planned else None
         same = old is not None and all(
             getattr(old, f) == getattr(info, f) for f in
             ("num_items", "num_merges", "waves_per_block", "rows_per_tile", "num_slots", "num_reqs",
-             "num_qo_heads", "num_kv_heads", "head_dim", "kv_dtype", "page_size", "dynamic_prefix"))
+             "num_qo_heads", "num_kv_heads", "head_dim", "kv_dtype", "page_size", "dynamic_prefix", "two_segment"))
         mask_words = int(packed.shape[1]) if packed is not None else 0
         same_mask = same and packed is not None and getattr(self, "tree_mask_dev", None) is not None \
             and self.mask_words == mask_words and self.tree_mask_dev.numel() >= packed.size
@@ -247,7 +278,9 @@ class CascadeVerifyAttention:
             # a graph captured earlier reads these buffers: refuse a re-plan
             # that would give the kernels others
             changed = [n for n, src, dt in (("page_table_dev", pt, torch.int32), ("sinks", sinks, torch.float32),
-                                            ("k_scale", k_scale, torch.float32), ("v_scale", v_scale, torch.float32))
+                                            ("k_scale", k_scale, torch.float32), ("v_scale", v_scale, torch.float32),
+                                            ("k2_scale", k2_scale, torch.float32),
+                                            ("v2_scale", v2_scale, torch.float32))
                        if not self._keeps(n, src, dt)]
             if (packed is not None) != (getattr(self, "tree_mask_dev", None) is not None) or \
                     (packed is not None and not same_mask):
@@ -290,6 +323,8 @@ class CascadeVerifyAttention:
         self.kv_dtype = kv_dtype
         self.k_scale = self._input_buffer("k_scale", k_scale, torch.float32, same)
         self.v_scale = self._input_buffer("v_scale", v_scale, torch.float32, same)
+        self.k2_scale = self._input_buffer("k2_scale", k2_scale, torch.float32, same)
+        self.v2_scale = self._input_buffer("v2_scale", v2_scale, torch.float32, same)
         self.lse_base2 = bool(lse_base2)
         self._planned = True
         return self
@@ -303,10 +338,11 @@ class CascadeVerifyAttention:
         self.prefix_len_dev.copy_(v)
 
     # ------------------------------------------------------------------- run
-    def _prefix_strides(self, k_prefix: torch.Tensor) -> Tuple[int, int, int, int]:
+    def _prefix_strides(self, k_prefix: torch.Tensor, second: bool = False) -> Tuple[int, int, int, int]:
         """(stride_tok, stride_head, stride_page, extent) in elements; extent =
-        pages of a paged pool or tokens of a contiguous prefix."""
-        if self.page_size > 0:
+        pages of a paged pool or tokens of a contiguous prefix (second: the
+        second segment of a two-segment prefix)."""
+        if self.page_size > 0 and not second:
             if k_prefix.dim() != 4:
                 raise ValueError("paged prefix pool must be 4-D")
             if self.kv_layout == "HND":   # [pages, Hkv, P, D]
@@ -332,8 +368,10 @@ class CascadeVerifyAttention:
             else:
                 extent, hkv, D = k_prefix.shape
                 st, sh, sp = k_prefix.stride(0), k_prefix.stride(1), 0
-            if extent < int(self.info.prefix_extent):
-                raise ValueError(f"k_prefix holds {extent} tokens; the plan reads {int(self.info.prefix_extent)}")
+            need = int(self.info.prefix2_extent if second else self.info.prefix_extent)
+            if extent < need:
+                raise ValueError(f"k_prefix{' (second segment)' if second else ''} holds {extent} tokens; "
+                                 f"the plan reads {need}")
         if hkv != self.num_kv_heads or D != self.head_dim or k_prefix.stride(-1) != 1:
             raise ValueError("prefix KV head count / head_dim / contiguity mismatch")
         return st, sh, sp, extent
@@ -400,6 +438,29 @@ class CascadeVerifyAttention:
         a.mask_mode = self.mask_mode
         a.mask_words = self.mask_words
         a.tree_mask = self.tree_mask_dev.data_ptr() if self.tree_mask_dev is not None else None
+        k_prefix2 = v_prefix2 = None
+        prefix2 = []
+        if isinstance(k_prefix, (tuple, list)) or isinstance(v_prefix, (tuple, list)):
+            if not (isinstance(k_prefix, (tuple, list)) and isinstance(v_prefix, (tuple, list))
+                    and len(k_prefix) == 2 and len(v_prefix) == 2):
+                raise ValueError("a two-segment prefix takes k_prefix = (first, second) and v_prefix likewise")
+            if not self.info.two_segment:
+                raise ValueError("this plan has a one-segment prefix (plan(prefix_split=...) makes two)")
+            (k_prefix, k_prefix2), (v_prefix, v_prefix2) = k_prefix, v_prefix
+            if k_prefix2 is None or v_prefix2 is None:
+                raise ValueError("the plan reads the second prefix segment; it is None")
+            if v_prefix2.shape != k_prefix2.shape or v_prefix2.stride() != k_prefix2.stride():
+                raise ValueError("v_prefix's second segment must match k_prefix's in shape and strides")
+            if k_prefix2.dtype != self.kv_dtype or v_prefix2.dtype != self.kv_dtype or not k_prefix2.is_cuda:
+                raise TypeError(f"prefix KV must be {self.kv_dtype} device tensors")
+            st2, sh2, _, extent2 = self._prefix_strides(k_prefix2, second=True)
+            a.k_prefix2, a.v_prefix2 = k_prefix2.data_ptr(), v_prefix2.data_ptr()
+            a.prefix2_stride_tok, a.prefix2_stride_head, a.prefix2_extent = st2, sh2, extent2
+            a.k2_scale = self.k2_scale.data_ptr() if self.k2_scale is not None else None
+            a.v2_scale = self.v2_scale.data_ptr() if self.v2_scale is not None else None
+            prefix2 = [st2, sh2, extent2]
+        elif self.info.two_segment:
+            raise ValueError("the plan has a two-segment prefix: pass k_prefix = (first, second) and v_prefix likewise")
         if k_prefix is not None:
             if v_prefix is None or v_prefix.shape != k_prefix.shape or v_prefix.stride() != k_prefix.stride():
                 raise ValueError("v_prefix must match k_prefix in shape and strides")
@@ -429,11 +490,13 @@ class CascadeVerifyAttention:
                 self.info_bytes, self.plan_dev, self.workspace, q, k_suffix, v_suffix, k_prefix, v_prefix,
                 [a.prefix_stride_tok, a.prefix_stride_head, a.prefix_stride_page, a.prefix_extent],
                 self.page_table_dev, self.tree_mask_dev, self.mask_mode, self.mask_words, self.prefix_len_dev,
-                self.k_scale, self.v_scale, self.sinks, self.sm_scale, self.lse_base2, out, lse)
+                self.k_scale, self.v_scale, self.sinks, self.sm_scale, self.lse_base2, out, lse,
+                k_prefix2, v_prefix2, prefix2, self.k2_scale, self.v2_scale)
         else:
             fn = getattr(lib, fn_name)
             check(fn(C.byref(self.info), C.byref(a), C.c_void_p(torch.cuda.current_stream().cuda_stream)),
                   fn_name)
         keep_alive(self.plan_dev, self.workspace if workspace else None, self.tree_mask_dev, self.page_table_dev, self.prefix_len_dev,
-                   self.sinks, self.k_scale, self.v_scale, q, k_suffix, v_suffix, k_prefix, v_prefix, out, lse)
+                   self.sinks, self.k_scale, self.v_scale, self.k2_scale, self.v2_scale, q, k_suffix, v_suffix,
+                   k_prefix, v_prefix, k_prefix2, v_prefix2, out, lse)
         return out, lse

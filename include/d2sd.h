@@ -161,6 +161,16 @@ int d2sd_graph_destroy(void* graph_exec);
  *            + (t % page_size)*prefix_stride_tok + h*prefix_stride_head.
  * window_left >= 0 keeps the last window_left prefix keys (all queries).
  *
+ * Two-segment prefix (prefix_split != NULL; contiguous first segment, static
+ * plans): the prefix of request r is the concatenation
+ *   [keys 0 .. prefix_split[r]) of k_prefix as above
+ *   | keys 0 .. prefix_len[r] - prefix_split[r]) of k_prefix2,
+ * key u of the second segment at
+ *   k_prefix2 + (prefix2_tok_indptr[r] + u)*prefix2_stride_tok + h*prefix2_stride_head
+ * (prefix2_tok_indptr may be NULL: 0).  This is the DTA draft's shared level
+ * [draft cache | projected target context] (model/dflash.py:103-106) read in
+ * place instead of concatenated; the window applies to the concatenation.
+ *
  * plan() bakes every per-request offset into a work list the caller uploads;
  * run() is the attention launch (prefix key chunks and suffix trees, each
  * writing a partial state to the workspace, or the output directly when a
@@ -202,6 +212,11 @@ typedef struct {
                           waves, 128-row tiles) or 8 (32-row waves, 256-row tiles) */
   int dynamic_prefix;  /* 1: prefix_len is each request's largest prefix; run()
                           reads the current lengths from args.prefix_len */
+  const int32_t* prefix_split;       /* host [num_reqs], nullable: two-segment
+                                        prefix, 0 <= prefix_split[r] <= prefix_len[r]
+                                        (page_size 0, dynamic_prefix 0) */
+  const int32_t* prefix2_tok_indptr; /* host [num_reqs], nullable: token of the
+                                        second segment's key 0 of request r */
 } d2sd_cascade_plan_desc;
 
 typedef struct {
@@ -231,6 +246,10 @@ typedef struct {
                              reads its rows' prefix and then their suffix tree
                              and writes out / lse (run() is one launch, no
                              workspace) */
+  int two_segment;        /* 1: the plan reads keys of a second prefix segment
+                             (run() then needs k_prefix2 / v_prefix2) */
+  int64_t prefix2_extent; /* tokens k_prefix2 must hold
+                             (max_r prefix2_tok_indptr[r] + prefix_len[r] - prefix_split[r]) */
 } d2sd_cascade_plan_info;
 
 /* Fills host_plan (capacity host_plan_ints int32) with the work list; the
@@ -269,6 +288,13 @@ typedef struct {
   int lse_base2;
   void* workspace;          /* >= info.workspace_bytes */
   size_t workspace_bytes;
+  const void* k_prefix2;    /* second prefix segment (info.two_segment): contiguous,
+                               the prefix's dtype; NULL otherwise */
+  const void* v_prefix2;
+  int64_t prefix2_stride_tok, prefix2_stride_head;
+  int64_t prefix2_extent;   /* tokens in k_prefix2 (>= info.prefix2_extent) */
+  const float* k2_scale;    /* fp8: [Hkv] scales of the second segment */
+  const float* v2_scale;
 } d2sd_cascade_run_args;
 
 /* run = attention launch then merge launch; both halves are also exported. */

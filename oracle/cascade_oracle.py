@@ -24,6 +24,8 @@ It restates the reference's verify-attention algorithm on the CPU in float64
   Philox4x32-10 (the counter-based generator the sampled walk draws from)
                                                    philox4x32_10
   verification.py:113-123 (QK RMSNorm + RoPE)       qk_norm_rope_ref
+  model/dflash.py:103-108 (DTA shared level, [draft cache | context])
+                                                   dta_shared_prefix_ref
 
 FlashInfer itself (flashinfer-python>=0.2.0, requirements.txt:13) is not
 vendored in the reference and not installed here.  Its published algorithm for
@@ -44,6 +46,9 @@ pure tree attention; chain tree == causal; constant V -> that V; page-table
 permutation invariance); against the reference's three-step row-layout
 algorithm vs. the single-pass tree form; and, for the sink, against the
 installed transformers GPT-OSS eager attention (a library routine).
+dta_shared_prefix_ref is pinned token by token to the reference's cat order
+and by the split-KV identity (its attention == the merge of the two
+segments' attentions).
 philox4x32_10 is pinned to the published known-answer vectors of Random123
 (the generator's authors' reference release); sample_scores_ref to the
 mathematics it restates: sampled frequencies follow softmax(x) (chi-square),
@@ -210,6 +215,16 @@ def cascade_tree_ref(q: Tensor, k_suffix: Tensor, v_suffix: Tensor, k_prefix: Op
     if sinks is not None:
         o = o * torch.sigmoid(lse.to(dtype) - sinks.to(dtype))[..., None]
     return o, lse
+
+
+def dta_shared_prefix_ref(k_cache: Tensor, v_cache: Tensor, k_ctx: Tensor, v_ctx: Tensor) -> Tuple[Tensor, Tensor]:
+    """The DTA draft's shared level (model/dflash.py:103-108): the draft
+    cache [Hkv, Lc, D] and the projected target context [Hkv, C, D] joined
+    along tokens (torch.cat(..., dim=1)), then made NHD [Lc + C, Hkv, D]
+    (transpose(0, 1).contiguous()), the layout single_prefill reads."""
+    k = torch.cat([k_cache, k_ctx], dim=1).transpose(0, 1).contiguous()
+    v = torch.cat([v_cache, v_ctx], dim=1).transpose(0, 1).contiguous()
+    return k, v
 
 
 def ancestor_mask_from_rows(node_index: np.ndarray, num_nodes: int) -> np.ndarray:

@@ -850,3 +850,116 @@ def test_dta_draft_cascade_through_plan_run():
                       kp, vp)
     torch.cuda.synchronize()
     check_close(o.view(bsz, q_len, hq, d), o_ref, lse.view(bsz, q_len, hq), lse_ref, "dta draft")
+
+
+def test_dta_draft_two_segment_prefix_in_place():
+    """model/dflash.py:96-133 without the [cache | context] concatenation: the
+    shared level reads the draft cache (a DynamicCache layer [1, Hkv, cap, D]
+    holding cache_len tokens) and the projected context (k[0, :, :ctx_len], a
+    strided view of the [bsz, Hkv, ctx + q_len, D] projection, dflash.py:87)
+    as the two segments of one plan; the noise tokens are the suffix with a
+    block-diagonal all-ones mask.  Against the oracle on the reference's
+    concatenated prefix, and against the one-segment plan over that
+    concatenation (the reference's own flow)."""
+    gen = torch.Generator().manual_seed(22)
+    bsz, q_len, hq, hkv, d, cache_len, cap, ctx_len = 4, 16, 32, 8, 128, 1500, 1600, 17
+    L = cache_len + ctx_len
+    q = bf16_randn(gen, bsz, q_len, hq, d)
+    k_proj, v_proj = bf16_randn(gen, bsz, hkv, ctx_len + q_len, d), bf16_randn(gen, bsz, hkv, ctx_len + q_len, d)
+    k_cache, v_cache = bf16_randn(gen, 1, hkv, cap, d), bf16_randn(gen, 1, hkv, cap, d)
+    kn = k_proj[:, :, ctx_len:].transpose(1, 2).contiguous()     # [bsz, q_len, Hkv, D]
+    vn = v_proj[:, :, ctx_len:].transpose(1, 2).contiguous()
+    k_sh, v_sh = orc.dta_shared_prefix_ref(k_cache[0, :, :cache_len], v_cache[0, :, :cache_len],
+                                           k_proj[0, :, :ctx_len], v_proj[0, :, :ctx_len])
+    o_ref, lse_ref = orc.cascade_verify_rows_ref(q, kn, vn, k_sh, v_sh, d ** -0.5, -1, None, causal=False)
+    n = bsz * q_len
+    mask = np.zeros((n, n), dtype=bool)
+    for b in range(bsz):
+        mask[b * q_len:(b + 1) * q_len, b * q_len:(b + 1) * q_len] = True
+    qd, knd, vnd = q.reshape(n, hq, d).to(DEV), kn.reshape(n, hkv, d).to(DEV), vn.reshape(n, hkv, d).to(DEV)
+    kc, vc, kp, vp = k_cache.to(DEV), v_cache.to(DEV), k_proj.to(DEV), v_proj.to(DEV)
+    two = d2sd.CascadeVerifyAttention(DEV).plan([0, n], [L], hq, hkv, d, tree_masks=[mask], page_size=0,
+                                                kv_layout="HND", prefix_split=[cache_len])
+    assert two.info.two_segment == 1 and two.info.fused == 0
+    o2, lse2 = two.run(qd, knd, vnd, (kc, kp[0, :, :ctx_len]), (vc, vp[0, :, :ctx_len]))
+    one = d2sd.CascadeVerifyAttention(DEV).plan([0, n], [L], hq, hkv, d, tree_masks=[mask], page_size=0,
+                                                kv_layout="HND")
+    kcat = torch.cat([kc[0, :, :cache_len], kp[0, :, :ctx_len]], dim=1)   # dflash.py:103-104
+    vcat = torch.cat([vc[0, :, :cache_len], vp[0, :, :ctx_len]], dim=1)
+    o1, lse1 = one.run(qd, knd, vnd, kcat, vcat)
+    torch.cuda.synchronize()
+    check_close(o2.view(bsz, q_len, hq, d), o_ref, lse2.view(bsz, q_len, hq), lse_ref, "dta draft, two segments")
+    check_close(o1.view(bsz, q_len, hq, d), o_ref, lse1.view(bsz, q_len, hq), lse_ref, "dta draft, concatenated")
+
+
+def _two_segment_problem(name, rng, gen):
+    """(hq, hkv, d, window, sinks, fp8, requests): per request its tree, first
+    and second segment lengths; segments are NHD [T, Hkv, D] tensors holding
+    the requests back to back after a few unused tokens."""
+    if name == "multi":
+        return 32, 8, 128, -1, False, False, [(wl.random_branch_tree(rng, 4, 16), 1000, 37),
+                                               (wl.random_branch_tree(rng, 3, 32), 0, 900),
+                                               (wl.random_branch_tree(rng, 2, 8), 2500, 0),
+                                               (wl.random_branch_tree(rng, 5, 16), 64, 64)]
+    if name == "window_sinks":     # the window straddles the split in one request, lies in the second in another
+        return 64, 8, 64, 100, True, False, [(wl.random_branch_tree(rng, 4, 32), 3000, 40),
+                                              (wl.random_branch_tree(rng, 2, 16), 700, 300)]
+    if name == "fp8":              # each segment dequantised with its own per-head scales
+        return 32, 8, 128, -1, False, True, [(wl.random_branch_tree(rng, 4, 16), 1900, 21),
+                                              (wl.random_branch_tree(rng, 2, 32), 130, 500)]
+    raise KeyError(name)
+
+
+@pytest.mark.parametrize("name", ["multi", "window_sinks", "fp8"])
+def test_two_segment_prefix_vs_oracle(name):
+    """Plans with a two-segment contiguous prefix (per request: keys of the
+    first tensor, then keys of the second, at their own token offsets): empty
+    first or second segments, splits inside a 64-key tile, windows across the
+    split, sinks, fp8 segments with scales of their own; each request against
+    the oracle on its concatenated prefix."""
+    rng = np.random.default_rng(77)
+    gen = torch.Generator().manual_seed(77)
+    hq, hkv, d, window, with_sinks, fp8, reqs = _two_segment_problem(name, rng, gen)
+    n_r = [t.num_nodes for t, _, _ in reqs]
+    qo = np.concatenate([[0], np.cumsum(n_r)]).tolist()
+    T = qo[-1]
+    tok1, tok2, t1, t2 = [], [], 5, 3
+    for _, a, b in reqs:
+        tok1.append(t1)
+        tok2.append(t2)
+        t1, t2 = t1 + a + 2, t2 + b + 1
+    kf1, vf1 = torch.randn(t1, hkv, d, generator=gen), torch.randn(t1, hkv, d, generator=gen)
+    kf2, vf2 = torch.randn(t2, hkv, d, generator=gen), torch.randn(t2, hkv, d, generator=gen)
+    scales = {}
+    if fp8:
+        for key, x in (("k1", kf1), ("v1", vf1), ("k2", kf2), ("v2", vf2)):
+            # the second segment's step is 1.7x coarser (its codes stay within +-448 / 1.7)
+            scales[key] = (x.abs().amax(dim=(0, 2)) / 448.0 * (1.0 if key[1] == "1" else 1.7)).float()
+        k1, v1 = (kf1 / scales["k1"][None, :, None]).to(torch.float8_e4m3fn), \
+            (vf1 / scales["v1"][None, :, None]).to(torch.float8_e4m3fn)
+        k2, v2 = (kf2 / scales["k2"][None, :, None]).to(torch.float8_e4m3fn), \
+            (vf2 / scales["v2"][None, :, None]).to(torch.float8_e4m3fn)
+        deq = lambda x, s: x.float() * s[None, :, None]   # noqa: E731
+    else:
+        k1, v1, k2, v2 = (x.to(torch.bfloat16) for x in (kf1, vf1, kf2, vf2))
+        deq = lambda x, s: x   # noqa: E731
+    q, ks, vs = bf16_randn(gen, T, hq, d), bf16_randn(gen, T, hkv, d), bf16_randn(gen, T, hkv, d)
+    sinks = torch.randn(hq, generator=gen) if with_sinks else None
+    attn = d2sd.CascadeVerifyAttention(DEV).plan(
+        qo, [a + b for _, a, b in reqs], hq, hkv, d, tree_masks=[t.ancestor_mask() for t, _, _ in reqs],
+        page_size=0, kv_layout="NHD", prefix_tok_indptr=tok1, prefix_split=[a for _, a, _ in reqs],
+        prefix2_tok_indptr=tok2, window_left=window, sinks=sinks.to(DEV) if sinks is not None else None,
+        kv_dtype=torch.float8_e4m3fn if fp8 else torch.bfloat16,
+        k_scale=(scales["k1"].to(DEV), scales["k2"].to(DEV)) if fp8 else None,
+        v_scale=(scales["v1"].to(DEV), scales["v2"].to(DEV)) if fp8 else None)
+    assert attn.info.two_segment == 1 and attn.info.fused == 0
+    o, lse = attn.run(q.to(DEV), ks.to(DEV), vs.to(DEV), (k1.to(DEV), k2.to(DEV)), (v1.to(DEV), v2.to(DEV)))
+    torch.cuda.synchronize()
+    for r, (tree, a, b) in enumerate(reqs):
+        kp = torch.cat([deq(k1[tok1[r]:tok1[r] + a], scales.get("k1")), deq(k2[tok2[r]:tok2[r] + b], scales.get("k2"))])
+        vp = torch.cat([deq(v1[tok1[r]:tok1[r] + a], scales.get("v1")), deq(v2[tok2[r]:tok2[r] + b], scales.get("v2"))])
+        x, y = qo[r], qo[r + 1]
+        o_ref, lse_ref = orc.cascade_tree_ref(q[x:y], ks[x:y], vs[x:y], kp if a + b else None, vp if a + b else None,
+                                              torch.as_tensor(tree.ancestor_mask()), d ** -0.5, window, sinks,
+                                              dtype=torch.float32 if fp8 else torch.float64)
+        check_close(o[x:y], o_ref, lse[x:y], lse_ref, f"two segments {name} req {r}")

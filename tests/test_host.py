@@ -36,7 +36,7 @@ def test_version_and_error_strings():
 
 
 def _plan(qo, pl, hq=32, hkv=8, d=128, window=-1, num_cus=256, waves=0, max_splits=0, page_size=16,
-          page_indptr=None, tok_indptr=None, dynamic=0, kv_dtype=0):
+          page_indptr=None, tok_indptr=None, dynamic=0, kv_dtype=0, split=None, tok2=None):
     desc = _lib.PlanDesc()
     qo = np.asarray(qo, dtype=np.int32)
     pl = np.asarray(pl, dtype=np.int32)
@@ -57,6 +57,10 @@ def _plan(qo, pl, hq=32, hkv=8, d=128, window=-1, num_cus=256, waves=0, max_spli
     desc.max_splits = max_splits
     desc.waves_per_block = waves
     desc.dynamic_prefix = dynamic
+    sp = np.asarray(split, dtype=np.int32) if split is not None else None
+    t2 = np.asarray(tok2, dtype=np.int32) if tok2 is not None else None
+    desc.prefix_split = sp.ctypes.data_as(C.POINTER(C.c_int32)) if sp is not None else None
+    desc.prefix2_tok_indptr = t2.ctypes.data_as(C.POINTER(C.c_int32)) if t2 is not None else None
     info = _lib.PlanInfo()
     assert _lib.lib.d2sd_cascade_plan(C.byref(desc), None, 0, C.byref(info)) == 0, _lib.lib.d2sd_last_error()
     host = np.zeros(max(info.plan_ints, 8), dtype=np.int32)
@@ -70,7 +74,7 @@ def _plan(qo, pl, hq=32, hkv=8, d=128, window=-1, num_cus=256, waves=0, max_spli
 
 
 MODE_PARTIAL, MODE_FINAL, MODE_NOOP = 0, 1, 3
-SRC_PREFIX, SRC_SUFFIX, SRC_BOTH = 0, 1, 2
+SRC_PREFIX, SRC_SUFFIX, SRC_BOTH, SRC_PREFIX2 = 0, 1, 2, 3
 # VerifyItem fields
 REQ, KVH, QT, SRC, KB, KE, SLOT, MODE, Q0, NQ, BASE, COFF, KV0, PLAN_LEN = range(14)
 
@@ -194,6 +198,116 @@ def test_plan_partitions_work(qo, pl, window, page, hq, waves):
                 if page:
                     for a, b, _ in ch:
                         assert (b - 1) // page - a // page + 1 <= 1024
+
+
+@pytest.mark.parametrize("qo,pl,split,window,tok1,tok2", [
+    ([0, 80], [4096 + 17], [4096], -1, None, None),                 # DTA draft: cache 4096 | context 17
+    ([0, 80], [4000 + 5], [4000], -1, [7], [3]),                    # split inside a tile, token offsets
+    ([0, 80], [300], [0], -1, None, None),                          # all keys in the second segment
+    ([0, 80], [300], [300], -1, None, None),                        # all keys in the first segment
+    ([0, 80], [5000], [4990], 100, None, None),                     # window straddles the split
+    ([0, 80], [5000], [4000], 100, None, None),                     # window inside the second segment
+    ([0, 40, 120, 150], [1000, 9000, 64], [999, 100, 64], -1, [0, 1000, 9000], [0, 1, 9000]),
+    ([0, 256], [8192 + 31], [8192], -1, None, None),
+])
+def test_plan_two_segment_prefix_partitions_keys(qo, pl, split, window, tok1, tok2):
+    """A two-segment prefix: per group, the first segment's items and the
+    second's (keys shifted by the split) cover the visible keys of the
+    concatenation exactly once, in slot order, no item holds keys of both
+    segments, each segment's chunks start on 64-key tiles of its own, items
+    name their segment's token offset, and no such plan is fused."""
+    hkv, hq = 8, 32
+    g = hq // hkv
+    info, items, merges = _plan(qo, pl, hq, hkv, 128, window, page_size=0, tok_indptr=tok1, split=split, tok2=tok2)
+    R = len(pl)
+    t1 = tok1 or [0] * R
+    t2 = tok2 or [0] * R
+    kv0 = [pl[r] - (min(pl[r], window) if window >= 0 else pl[r]) for r in range(R)]
+    sees2 = any(qo[r + 1] > qo[r] and pl[r] > max(split[r], kv0[r]) for r in range(R))
+    assert info.two_segment == int(sees2)
+    assert info.fused == 0 or not sees2
+    assert info.prefix_extent == max([t1[r] + split[r] for r in range(R) if split[r] > 0] + [0])
+    assert info.prefix2_extent == max([t2[r] + pl[r] - split[r] for r in range(R) if pl[r] > split[r]] + [0])
+    live = items[items[:, MODE] != MODE_NOOP].tolist()
+    pre = {}
+    for it in live:
+        r = it[REQ]
+        key = (r, it[KVH], it[QT])
+        if it[SRC] in (SRC_PREFIX, SRC_BOTH):
+            assert it[BASE] == t1[r] and it[KE] <= split[r] and (it[KB] - kv0[r]) % 64 == 0
+            pre.setdefault(key, []).append((it[KB], it[KE], it[SLOT], 1))
+        elif it[SRC] == SRC_PREFIX2:
+            b0 = max(kv0[r], split[r]) - split[r]
+            assert it[BASE] == t2[r] and it[MODE] == MODE_PARTIAL and 0 <= it[KB] < it[KE] <= pl[r] - split[r]
+            assert (it[KB] - b0) % 64 == 0
+            pre.setdefault(key, []).append((it[KB] + split[r], it[KE] + split[r], it[SLOT], 2))
+    for r in range(R):
+        n = qo[r + 1] - qo[r]
+        for h in range(hkv):
+            for qt in range(-(-n * g // info.rows_per_tile)):
+                ch = sorted(pre.get((r, h, qt), []))
+                if kv0[r] == pl[r]:
+                    assert ch == []
+                    continue
+                assert ch[0][0] == kv0[r] and ch[-1][1] == pl[r]
+                assert all(b == c for (_, b, _, _), (c, _, _, _) in zip(ch[:-1], ch[1:]))
+                assert all(e <= split[r] for _, e, _, s in ch if s == 1)
+                assert all(b >= split[r] for b, _, _, s in ch if s == 2)
+                if not info.fused:
+                    s0 = ch[0][2]
+                    assert [c[2] for c in ch] == list(range(s0, s0 + len(ch)))
+    blocks = {}
+    for m in merges.tolist():
+        if m[4]:
+            blocks[(m[0], m[1], m[2])] = m[4]
+    for key, ch in pre.items():
+        if not info.fused:
+            assert blocks[key] == len(ch) + 1   # the chunks of both segments and the suffix
+
+
+def test_plan_rejects_bad_two_segment_prefixes():
+    """A second segment needs a contiguous first one and a static plan, and
+    each split must lie in [0, prefix_len]."""
+    qo = np.asarray([0, 10], dtype=np.int32)
+    pl = np.asarray([100], dtype=np.int32)
+    for page, dyn, sp, code, msg in ((16, 0, 50, 2, b"contiguous"), (0, 1, 50, 2, b"static"),
+                                     (0, 0, 101, 1, b"prefix_split"), (0, 0, -1, 1, b"prefix_split")):
+        desc = _lib.PlanDesc()
+        desc.num_reqs = 1
+        desc.qo_indptr = qo.ctypes.data_as(C.POINTER(C.c_int32))
+        desc.prefix_len = pl.ctypes.data_as(C.POINTER(C.c_int32))
+        desc.num_qo_heads, desc.num_kv_heads, desc.head_dim = 32, 8, 128
+        pi = np.asarray([0, 7], dtype=np.int32)
+        desc.page_indptr = pi.ctypes.data_as(C.POINTER(C.c_int32))
+        desc.page_size, desc.dynamic_prefix = page, dyn
+        s = np.asarray([sp], dtype=np.int32)
+        desc.prefix_split = s.ctypes.data_as(C.POINTER(C.c_int32))
+        info = _lib.PlanInfo()
+        assert _lib.lib.d2sd_cascade_plan(C.byref(desc), None, 0, C.byref(info)) == code
+        assert msg in _lib.lib.d2sd_last_error()
+
+
+@pytest.mark.parametrize("field,value,msg", [("k_prefix2", 0, b"k_prefix2"), ("prefix2_extent", 16, b"fewer tokens"),
+                                             ("k_prefix2", 8, b"aligned")])
+def test_cascade_run_rejects_a_missing_second_segment_without_launching(field, value, msg):
+    """A plan that reads a second prefix segment refuses a null, misaligned
+    or short second segment before any launch (pointers never dereferenced)."""
+    info, _, _ = _plan([0, 10], [300], page_size=0, split=[280])
+    assert info.two_segment == 1 and info.prefix2_extent == 20 and info.prefix_extent == 280
+    fake = 1 << 20
+    a = _lib.RunArgs()
+    a.plan = a.q = a.k_suffix = a.v_suffix = a.out = a.k_prefix = a.v_prefix = fake
+    a.k_prefix2 = a.v_prefix2 = fake
+    a.workspace, a.workspace_bytes = fake, info.workspace_bytes
+    a.q_stride_n, a.q_stride_h = 32 * 128, 128
+    a.suffix_stride_n, a.suffix_stride_h = 8 * 128, 128
+    a.o_stride_n, a.o_stride_h = 32 * 128, 128
+    a.prefix_stride_tok, a.prefix_stride_head = 128, 300 * 128
+    a.prefix2_stride_tok, a.prefix2_stride_head, a.prefix2_extent = 128, 20 * 128, 20
+    a.prefix_extent, a.sm_scale = 300, 0.088
+    setattr(a, field, (fake + value) if (field == "k_prefix2" and value) else value)
+    rc = _lib.lib.d2sd_cascade_run(C.byref(info), C.byref(a), None)
+    assert rc == 1 and msg in _lib.lib.d2sd_last_error()
 
 
 def _max_chunk_tiles(page):

@@ -109,6 +109,29 @@ def test_split_prefix_merge_equals_unsplit(splits):
     _close(l_acc, l_ref, 1e-12)
 
 
+def test_dta_shared_prefix_is_cache_then_context():
+    """dflash.py:103-108: key t of the DTA shared level is draft-cache token t
+    for t < Lc and context token t - Lc after it, keys and values alike; and
+    the shared level's attention equals the merge of the two segments'
+    attentions (the split-KV identity a two-segment plan relies on)."""
+    gen = torch.Generator().manual_seed(5)
+    hkv, lc, c, d = 2, 13, 5, 16
+    kc, vc, kx, vx = (_rand(gen, hkv, n, d) for n in (lc, lc, c, c))
+    k, v = orc.dta_shared_prefix_ref(kc, vc, kx, vx)
+    assert k.shape == v.shape == (lc + c, hkv, d) and k.is_contiguous()
+    for t in range(lc + c):
+        for h in range(hkv):
+            src_k, src_v = (kc[h, t], vc[h, t]) if t < lc else (kx[h, t - lc], vx[h, t - lc])
+            assert torch.equal(k[t, h], src_k) and torch.equal(v[t, h], src_v)
+    q = _rand(gen, 7, 4, d)
+    o_ref, l_ref = orc.single_prefill_ref(q, k, v, False, 0.25)
+    o_a, l_a = orc.single_prefill_ref(q, kc.transpose(0, 1), vc.transpose(0, 1), False, 0.25)
+    o_b, l_b = orc.single_prefill_ref(q, kx.transpose(0, 1), vx.transpose(0, 1), False, 0.25)
+    o_m, l_m = orc.merge_state_ref(o_a, l_a, o_b, l_b)
+    _close(o_m, o_ref, 1e-12)
+    _close(l_m, l_ref, 1e-12)
+
+
 def test_merge_commutative_associative():
     gen = torch.Generator().manual_seed(3)
     st = [(_rand(gen, 3, 2, 8), _rand(gen, 3, 2) * 3) for _ in range(3)]
