@@ -814,6 +814,7 @@ static int local_merge_cascade(const void* q, int64_t q_stride_b, int64_t q_stri
       desc.head_dim = d;
       desc.window_left = -1;
       desc.kv_dtype = D2SD_KV_BF16;
+      desc.waves_per_block = 4;  // the in-place kernel's one shape
       const std::string saved = g_last_error;
       std::vector<int32_t> host;
       bool ok = d2sd_cascade_plan(&desc, nullptr, 0, &sp.info) == D2SD_OK;

@@ -93,6 +93,36 @@ __device__ __forceinline__ void wait_vmcnt_units(int k) {
   });
 }
 
+// Element offset of packed row `row` = (node row / g, head row % g) of a
+// group, stepped `step` rows at a time without a division per step; rows
+// past the group's end (R rows) give the last row's offset (valid() false).
+struct RowWalk {
+  int row, j, step, dj, g, R;
+  long long off, dstep, wrap, last;
+  __device__ __forceinline__ RowWalk(int row0, int step_, int R_, int g_, long long sn, long long sh)
+      : row(row0), step(step_), g(g_), R(R_) {
+    const int n0 = row0 / g_;
+    j = row0 - n0 * g_;
+    off = (long long)n0 * sn + (long long)j * sh;
+    dj = step_ % g_;
+    dstep = (long long)(step_ / g_) * sn + (long long)dj * sh;
+    wrap = sn - (long long)g_ * sh;
+    const int nl = (R_ - 1) / g_;
+    last = (long long)nl * sn + (long long)(R_ - 1 - nl * g_) * sh;
+  }
+  __device__ __forceinline__ bool valid() const { return row < R; }
+  __device__ __forceinline__ long long offset() const { return row < R ? off : last; }
+  __device__ __forceinline__ void next() {
+    row += step;
+    off += dstep;
+    j += dj;
+    if (j >= g) {
+      j -= g;
+      off += wrap;
+    }
+  }
+};
+
 template <int D>
 __device__ __forceinline__ void store_out(const VerifyParams& p, int qrow, int qh, int hh,
                                           const f32x16 (&o)[D / 32], float lse) {
@@ -276,24 +306,27 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
     }
   };
   if constexpr ((MASKED || FP8) && INIT) load_q();
-  // INPLACE: this lane's part of the stored output of its rows (head dims
-  // 32 mt + 8 q4 + 4 hh .. + 3) and their stored LSE (natural log)
-  u32x2 old_o[RB][INPLACE ? MT : 1][4];
+  // INPLACE: the stored output of this wave's rows, read row by row (lane:
+  // 16-byte piece lane % OCH of row ORPI i + lane / OCH of each 32-row block,
+  // so that one instruction reads whole rows) and their stored LSE; the
+  // epilogue moves the pieces into the MFMA layout through LDS
+  constexpr int OCH = D / 8, ORPI = 64 / OCH, OIPB = 32 / ORPI;
+  u32x4 old_o[RB][INPLACE ? OIPB : 1];
   float old_lse[RB];
   if constexpr (INPLACE) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
+      // raw (base-2 when lse_base2): converted in the epilogue, so that no
+      // instruction waits for this load before the key tiles are issued
       old_lse[rb] = -INFINITY;
-      if (rv[rb]) {
-        const bf16_t* orow = (const bf16_t*)p.o + (long long)(w.q0 + n[rb]) * p.o_stride_n +
-                             (long long)qh[rb] * p.o_stride_h + 4 * hh;
+      if (rv[rb]) old_lse[rb] = p.lse[(long long)(w.q0 + n[rb]) * p.lse_stride_n + qh[rb]];
+      // unconditional (rows past the group's end read its last row, never
+      // stored): a load under a branch would be waited for at the join
+      RowWalk rw(wrow0 + 32 * rb + lane / OCH, ORPI, R, g, p.o_stride_n, p.o_stride_h);
+      const bf16_t* obase = (const bf16_t*)p.o + (long long)w.q0 * p.o_stride_n +
+                            (long long)(w.kvh * g) * p.o_stride_h + 8 * (lane % OCH);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4) old_o[rb][mt][q4] = *(const u32x2*)(orow + 32 * mt + 8 * q4);
-        const float l = p.lse[(long long)(w.q0 + n[rb]) * p.lse_stride_n + qh[rb]];
-        old_lse[rb] = p.lse_base2 ? l * kLn2 : l;
-      }
+      for (int i = 0; i < OIPB; ++i, rw.next()) old_o[rb][i] = *(const u32x4*)(obase + rw.offset());
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -936,6 +969,91 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
     return;
   }
 
+  if constexpr (INPLACE) {
+    // The stored state (O_s, LSE_s) merged with this one
+    // (flashinfer.merge_state_in_place, model/cascade_graph.py:58-60; both
+    // empty keeps the stored state), the sink applied, through this wave's
+    // rows of the ring (chunks swizzled by row as in the key tiles): the
+    // stored pieces go in row by row, each lane merges its MFMA-layout part
+    // and writes the bf16 result back in place, and the rows go out row by
+    // row (whole rows per store instruction).
+    static_assert(ROWS * D <= (KST + VST) * 64 * D, "the rows must fit the ring");
+    __syncthreads();  // every wave is done with the key / value tiles
+    bf16_t* reg = &sm.ring.k[0][0] + wv * RB * 32 * D;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int i = 0; i < OIPB; ++i) {
+        const int r = ORPI * i + lane / OCH;  // row in the 32-row block
+        *(u32x4*)(reg + (32 * rb + r) * D + 8 * ((lane % OCH) ^ chunk_swizzle<D>(r))) = old_o[rb][i];
+      }
+    if (live) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        const float l_tot = l_run[rb] + xor32(l_run[rb], hh);
+        const bool nonempty = l_tot > 0.f;
+        const float inv = nonempty ? __builtin_amdgcn_rcpf(l_tot) : 0.f;  // l_tot >= 1 (below)
+        const float lse_n = nonempty ? m_run[rb] * cn + logf(l_tot) : -INFINITY;
+        const float ol = p.lse_base2 ? old_lse[rb] * kLn2 : old_lse[rb];
+        const float m = fmaxf(ol, lse_n);
+        float wa = 1.f, wb = 0.f, lse = ol;
+        if (m != -INFINITY) {
+          const float ea = __expf(ol - m), eb = __expf(lse_n - m);
+          const float sum = ea + eb;  // in [1, 2]
+          const float rs = __builtin_amdgcn_rcpf(sum);
+          wa = ea * rs;
+          wb = eb * rs * inv;
+          lse = m + logf(sum);
+        }
+        if (p.sinks) {
+          const float sc = (lse == -INFINITY || !rv[rb]) ? 0.f : 1.f / (1.f + __expf(p.sinks[qh[rb]] - lse));
+          wa *= sc;
+          wb *= sc;
+        }
+        // all reads, then all writes: the LDS reads issue back to back
+        bf16_t* myrow = reg + (32 * rb + l32) * D + 4 * hh;
+        u32x2 od[MT][4];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) od[mt][q4] = *(const u32x2*)(myrow + 8 * ((4 * mt + q4) ^ chunk_swizzle<D>(l32)));
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4)
+            *(u32x2*)(myrow + 8 * ((4 * mt + q4) ^ chunk_swizzle<D>(l32))) =
+                (u32x2){pack_bf16x2(o[rb][mt][4 * q4] * wb + wa * bf16_lo(od[mt][q4][0]),
+                                    o[rb][mt][4 * q4 + 1] * wb + wa * bf16_hi(od[mt][q4][0])),
+                        pack_bf16x2(o[rb][mt][4 * q4 + 2] * wb + wa * bf16_lo(od[mt][q4][1]),
+                                    o[rb][mt][4 * q4 + 3] * wb + wa * bf16_hi(od[mt][q4][1]))};
+        if (p.lse && rv[rb] && hh == 0)
+          p.lse[(long long)(w.q0 + n[rb]) * p.lse_stride_n + qh[rb]] = p.lse_base2 ? lse * kLog2e : lse;
+      }
+    }
+    // (the reads below see this wave's own LDS writes above: a wave's LDS
+    // operations complete in order).  The row addresses are recomputed from
+    // an opaque copy of the lane index: reusing the prologue's would keep
+    // them live across the tile loop.
+    int olane;
+    __asm__ volatile("v_mov_b32 %0, %1" : "=v"(olane) : "v"(lane));
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      RowWalk rw(wrow0 + 32 * rb + olane / OCH, ORPI, R, g, p.o_stride_n, p.o_stride_h);
+      bf16_t* obase = (bf16_t*)p.o + (long long)w.q0 * p.o_stride_n + (long long)(w.kvh * g) * p.o_stride_h +
+                      8 * (olane % OCH);
+      u32x4 piece[OIPB];  // all reads first, then the stores
+#pragma unroll
+      for (int i = 0; i < OIPB; ++i) {
+        const int r = ORPI * i + olane / OCH;
+        piece[i] = *(const u32x4*)(reg + (32 * rb + r) * D + 8 * ((olane % OCH) ^ chunk_swizzle<D>(r)));
+      }
+#pragma unroll
+      for (int i = 0; i < OIPB; ++i, rw.next())
+        if (rw.valid()) *(u32x4*)(obase + rw.offset()) = piece[i];
+    }
+    return;
+  }
+
   // ---- epilogue: normalise, then a partial slot or the final output ----
   float lse_r[RB];
   if (live) {
@@ -943,7 +1061,9 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
     for (int rb = 0; rb < RB; ++rb) {
       const float l_tot = l_run[rb] + xor32(l_run[rb], hh);
       const bool nonempty = l_tot > 0.f;
-      const float inv = nonempty ? vscale / l_tot : 0.f;
+      // l_tot >= 1 when nonempty (the running max never exceeds the row's
+      // maximum, whose term is then >= 1): the reciprocal is within 1 ulp
+      const float inv = nonempty ? vscale * __builtin_amdgcn_rcpf(l_tot) : 0.f;
       lse_r[rb] = nonempty ? m_run[rb] * cn + logf(l_tot) : -INFINITY;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) o[rb][mt] *= inv;
@@ -961,32 +1081,6 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
             __builtin_nontemporal_store(image_piece(o[rb][mt], pr, 1.f), (u32x4*)(po + image_offset<D>(blk, mt, pr, lane)));
         if (hh == 0) __builtin_nontemporal_store(lse_r[rb], pl);
       } else if (rv[rb]) {
-        if constexpr (INPLACE) {
-          // flashinfer.merge_state_in_place of the stored state (O_s, LSE_s)
-          // with this one (model/cascade_graph.py:58-60); both empty keeps
-          // the stored state
-          const float m = fmaxf(old_lse[rb], lse_r[rb]);
-          float wa = 1.f, wb = 0.f;
-          if (m != -INFINITY) {
-            const float ea = __expf(old_lse[rb] - m), eb = __expf(lse_r[rb] - m);
-            const float sum = ea + eb;
-            wa = ea / sum;
-            wb = eb / sum;
-            lse_r[rb] = m + logf(sum);
-          } else {
-            lse_r[rb] = old_lse[rb];
-          }
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) {
-              const u32x2 od = old_o[rb][mt][q4];
-              o[rb][mt][4 * q4] = o[rb][mt][4 * q4] * wb + wa * bf16_lo(od[0]);
-              o[rb][mt][4 * q4 + 1] = o[rb][mt][4 * q4 + 1] * wb + wa * bf16_hi(od[0]);
-              o[rb][mt][4 * q4 + 2] = o[rb][mt][4 * q4 + 2] * wb + wa * bf16_lo(od[1]);
-              o[rb][mt][4 * q4 + 3] = o[rb][mt][4 * q4 + 3] * wb + wa * bf16_hi(od[1]);
-            }
-        }
         store_out<D>(p, w.q0 + n[rb], qh[rb], hh, o[rb], lse_r[rb]);
       }
     }
@@ -1013,8 +1107,12 @@ struct Shape<8> { static constexpr int W = 8, RB = 1, OCC = 2; };
 // (suffix items merging into the stored output: the per-row local level of
 // the drop-in runner), KIND_SEGMENTS (split plans over a two-segment
 // contiguous prefix: SRC_PREFIX, SRC_PREFIX2 and suffix items).
+// The in-place kind serves the drop-in runner's few workgroups (rows x kv
+// heads): one wave per SIMD, so that its state, the stored output and the
+// tree-mask words all stay in registers.
 template <int D, int WPB, bool PAGED, bool FP8, int KIND>
-__global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(Shape<WPB>::OCC, Shape<WPB>::OCC)))
+__global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(KIND == KIND_INPLACE ? 1 : Shape<WPB>::OCC,
+                                                                            KIND == KIND_INPLACE ? 1 : Shape<WPB>::OCC)))
 void verify_attn_kernel(const VerifyParams p) {
   constexpr int W = Shape<WPB>::W, RB = Shape<WPB>::RB;
   using R = RingCfg<D, WPB>;
@@ -1166,8 +1264,11 @@ static hipError_t launch_verify_k(const VerifyParams& p, bool paged, bool fp8, i
 template <int D, int WPB>
 static hipError_t launch_verify_w(const VerifyParams& p, bool paged, bool fp8, int kind, int nitems, hipStream_t s) {
   if (kind == KIND_FUSED) return launch_verify_k<D, WPB, KIND_FUSED>(p, paged, fp8, nitems, s);
-  // in-place plans read no prefix: one instantiation
-  if (kind == KIND_INPLACE) return launch_verify_t<D, WPB, false, false, KIND_INPLACE>(p, nitems, s);
+  // in-place plans read no prefix and are planned with four waves: one instantiation
+  if (kind == KIND_INPLACE) {
+    if constexpr (WPB == 4) return launch_verify_t<D, 4, false, false, KIND_INPLACE>(p, nitems, s);
+    return hipErrorInvalidValue;
+  }
   // two-segment prefixes are contiguous
   if (kind == KIND_SEGMENTS)
     return paged ? hipErrorInvalidValue
