@@ -123,22 +123,6 @@ struct RowWalk {
   }
 };
 
-template <int D>
-__device__ __forceinline__ void store_out(const VerifyParams& p, int qrow, int qh, int hh,
-                                          const f32x16 (&o)[D / 32], float lse) {
-  bf16_t* orow = (bf16_t*)p.o + (long long)qrow * p.o_stride_n + (long long)qh * p.o_stride_h;
-  float sc = 1.f;
-  if (p.sinks) sc = (lse == -INFINITY) ? 0.f : 1.f / (1.f + __expf(p.sinks[qh] - lse));
-#pragma unroll
-  for (int mt = 0; mt < D / 32; ++mt)
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4)
-      *(u32x2*)(orow + 32 * mt + 8 * q4 + 4 * hh) =
-          (u32x2){pack_bf16x2(o[mt][4 * q4] * sc, o[mt][4 * q4 + 1] * sc),
-                  pack_bf16x2(o[mt][4 * q4 + 2] * sc, o[mt][4 * q4 + 3] * sc)};
-  if (p.lse && hh == 0) p.lse[(long long)qrow * p.lse_stride_n + qh] = p.lse_base2 ? lse * kLog2e : lse;
-}
-
 // Row value of the partner lane l ^ 32 (the other half of the wave), by
 // v_permlane32_swap: after swapping the upper half of `a` with the lower half
 // of `b` (both copies of x), lane l < 32 finds x[l + 32] in b and lane l >= 32
@@ -969,63 +953,83 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
     return;
   }
 
-  if constexpr (INPLACE) {
-    // The stored state (O_s, LSE_s) merged with this one
-    // (flashinfer.merge_state_in_place, model/cascade_graph.py:58-60; both
-    // empty keeps the stored state), the sink applied, through this wave's
-    // rows of the ring (chunks swizzled by row as in the key tiles): the
-    // stored pieces go in row by row, each lane merges its MFMA-layout part
-    // and writes the bf16 result back in place, and the rows go out row by
-    // row (whole rows per store instruction).
+  // ---- epilogue ----
+  // Final outputs (and the in-place merge) go through this wave's rows of the
+  // ring, chunks swizzled by row as in the key tiles: each lane writes its
+  // MFMA-layout part of the bf16 result, and the rows go out row by row (whole
+  // rows per store instruction).  In place, the stored state (O_s, LSE_s),
+  // read row by row in the prologue, goes in first and each lane merges its
+  // part with this state (flashinfer.merge_state_in_place,
+  // model/cascade_graph.py:58-60; both empty keeps the stored state).  The
+  // sink (verification.py:173-176) scales the result.
+  if (INPLACE || w.mode != MODE_PARTIAL) {
     static_assert(ROWS * D <= (KST + VST) * 64 * D, "the rows must fit the ring");
     __syncthreads();  // every wave is done with the key / value tiles
     bf16_t* reg = &sm.ring.k[0][0] + wv * RB * 32 * D;
+    if constexpr (INPLACE) {
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
+      for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-      for (int i = 0; i < OIPB; ++i) {
-        const int r = ORPI * i + lane / OCH;  // row in the 32-row block
-        *(u32x4*)(reg + (32 * rb + r) * D + 8 * ((lane % OCH) ^ chunk_swizzle<D>(r))) = old_o[rb][i];
-      }
+        for (int i = 0; i < OIPB; ++i) {
+          const int r = ORPI * i + lane / OCH;  // row in the 32-row block
+          *(u32x4*)(reg + (32 * rb + r) * D + 8 * ((lane % OCH) ^ chunk_swizzle<D>(r))) = old_o[rb][i];
+        }
+    }
     if (live) {
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
         const float l_tot = l_run[rb] + xor32(l_run[rb], hh);
         const bool nonempty = l_tot > 0.f;
-        const float inv = nonempty ? __builtin_amdgcn_rcpf(l_tot) : 0.f;  // l_tot >= 1 (below)
+        // l_tot >= 1 when nonempty (the running max never exceeds the row's
+        // maximum, whose term is then >= 1): the reciprocal is within 1 ulp
+        const float inv = nonempty ? vscale * __builtin_amdgcn_rcpf(l_tot) : 0.f;
         const float lse_n = nonempty ? m_run[rb] * cn + logf(l_tot) : -INFINITY;
-        const float ol = p.lse_base2 ? old_lse[rb] * kLn2 : old_lse[rb];
-        const float m = fmaxf(ol, lse_n);
-        float wa = 1.f, wb = 0.f, lse = ol;
-        if (m != -INFINITY) {
-          const float ea = __expf(ol - m), eb = __expf(lse_n - m);
-          const float sum = ea + eb;  // in [1, 2]
-          const float rs = __builtin_amdgcn_rcpf(sum);
-          wa = ea * rs;
-          wb = eb * rs * inv;
-          lse = m + logf(sum);
+        float wa = 0.f, wb = inv, lse = lse_n;  // out = wa O_s + wb O
+        if constexpr (INPLACE) {
+          const float ol = p.lse_base2 ? old_lse[rb] * kLn2 : old_lse[rb];
+          const float m = fmaxf(ol, lse_n);
+          wa = 1.f;
+          wb = 0.f;
+          lse = ol;
+          if (m != -INFINITY) {
+            const float ea = __expf(ol - m), eb = __expf(lse_n - m);
+            const float sum = ea + eb;  // in [1, 2]
+            const float rs = __builtin_amdgcn_rcpf(sum);
+            wa = ea * rs;
+            wb = eb * rs * inv;
+            lse = m + logf(sum);
+          }
         }
         if (p.sinks) {
           const float sc = (lse == -INFINITY || !rv[rb]) ? 0.f : 1.f / (1.f + __expf(p.sinks[qh[rb]] - lse));
           wa *= sc;
           wb *= sc;
         }
-        // all reads, then all writes: the LDS reads issue back to back
         bf16_t* myrow = reg + (32 * rb + l32) * D + 4 * hh;
-        u32x2 od[MT][4];
+        u32x2 od[INPLACE ? MT : 1][4];  // all reads, then all writes: the reads issue back to back
+        if constexpr (INPLACE) {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4)
+              od[mt][q4] = *(const u32x2*)(myrow + 8 * ((4 * mt + q4) ^ chunk_swizzle<D>(l32)));
+        }
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4) od[mt][q4] = *(const u32x2*)(myrow + 8 * ((4 * mt + q4) ^ chunk_swizzle<D>(l32)));
+          for (int q4 = 0; q4 < 4; ++q4) {
+            float v[4];
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4)
+            for (int e = 0; e < 4; ++e) v[e] = o[rb][mt][4 * q4 + e] * wb;
+            if constexpr (INPLACE) {
+              v[0] += wa * bf16_lo(od[mt][q4][0]);
+              v[1] += wa * bf16_hi(od[mt][q4][0]);
+              v[2] += wa * bf16_lo(od[mt][q4][1]);
+              v[3] += wa * bf16_hi(od[mt][q4][1]);
+            }
             *(u32x2*)(myrow + 8 * ((4 * mt + q4) ^ chunk_swizzle<D>(l32))) =
-                (u32x2){pack_bf16x2(o[rb][mt][4 * q4] * wb + wa * bf16_lo(od[mt][q4][0]),
-                                    o[rb][mt][4 * q4 + 1] * wb + wa * bf16_hi(od[mt][q4][0])),
-                        pack_bf16x2(o[rb][mt][4 * q4 + 2] * wb + wa * bf16_lo(od[mt][q4][1]),
-                                    o[rb][mt][4 * q4 + 3] * wb + wa * bf16_hi(od[mt][q4][1]))};
+                (u32x2){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+          }
         if (p.lse && rv[rb] && hh == 0)
           p.lse[(long long)(w.q0 + n[rb]) * p.lse_stride_n + qh[rb]] = p.lse_base2 ? lse * kLog2e : lse;
       }
@@ -1054,35 +1058,28 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
     return;
   }
 
-  // ---- epilogue: normalise, then a partial slot or the final output ----
-  float lse_r[RB];
+  // partial state of a key chunk: normalised O and LSE to the workspace slot
   if (live) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       const float l_tot = l_run[rb] + xor32(l_run[rb], hh);
       const bool nonempty = l_tot > 0.f;
-      // l_tot >= 1 when nonempty (the running max never exceeds the row's
-      // maximum, whose term is then >= 1): the reciprocal is within 1 ulp
-      const float inv = nonempty ? vscale * __builtin_amdgcn_rcpf(l_tot) : 0.f;
-      lse_r[rb] = nonempty ? m_run[rb] * cn + logf(l_tot) : -INFINITY;
+      const float inv = nonempty ? vscale * __builtin_amdgcn_rcpf(l_tot) : 0.f;  // l_tot >= 1 (above)
+      const float lse_r = nonempty ? m_run[rb] * cn + logf(l_tot) : -INFINITY;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) o[rb][mt] *= inv;
-      if (w.mode == MODE_PARTIAL) {
-        // streaming stores: the merge launch reads each partial once, and
-        // lines that leave L2 during the epilogue are not written back at
-        // the kernel's end
-        const int blk = RB * wv + rb;
-        bf16_t* po = (bf16_t*)p.part_o + (long long)w.slot * ROWS * D;
-        float* pl = p.part_lse + (long long)w.slot * ROWS + blk * 32 + l32;
+      // streaming stores: the merge launch reads each partial once, and
+      // lines that leave L2 during the epilogue are not written back at the
+      // kernel's end
+      const int blk = RB * wv + rb;
+      bf16_t* po = (bf16_t*)p.part_o + (long long)w.slot * ROWS * D;
+      float* pl = p.part_lse + (long long)w.slot * ROWS + blk * 32 + l32;
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-          for (int pr = 0; pr < 2; ++pr)
-            __builtin_nontemporal_store(image_piece(o[rb][mt], pr, 1.f), (u32x4*)(po + image_offset<D>(blk, mt, pr, lane)));
-        if (hh == 0) __builtin_nontemporal_store(lse_r[rb], pl);
-      } else if (rv[rb]) {
-        store_out<D>(p, w.q0 + n[rb], qh[rb], hh, o[rb], lse_r[rb]);
-      }
+        for (int pr = 0; pr < 2; ++pr)
+          __builtin_nontemporal_store(image_piece(o[rb][mt], pr, 1.f), (u32x4*)(po + image_offset<D>(blk, mt, pr, lane)));
+      if (hh == 0) __builtin_nontemporal_store(lse_r, pl);
     }
   }
 }
