@@ -1110,11 +1110,11 @@ struct Shape<8> { static constexpr int W = 8, RB = 1, OCC = 2; };
 template <int D, int WPB, bool PAGED, bool FP8, int KIND>
 __global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(KIND == KIND_INPLACE ? 1 : Shape<WPB>::OCC,
                                                                             KIND == KIND_INPLACE ? 1 : Shape<WPB>::OCC)))
-void verify_attn_kernel(const VerifyParams p) {
+void verify_attn_kernel(const VerifyItem* __restrict__ items, const VerifyParams p) {
   constexpr int W = Shape<WPB>::W, RB = Shape<WPB>::RB;
   using R = RingCfg<D, WPB>;
   __shared__ __attribute__((aligned(16))) VerifySmem<D, R::KST, R::VST, R::NPG> sm;
-  const VerifyItem w = p.items[blockIdx.x];
+  const VerifyItem w = items[blockIdx.x];
   // Load the whole item and the prefix-level arguments in one round of
   // scalar loads (the compiler would otherwise fetch the fields used after
   // the mode test in later rounds): the Q loads and the first page ids
@@ -1227,14 +1227,14 @@ __device__ __forceinline__ void merge_rows(const VerifyParams& p, int slot0, int
 // has linear index m + nm8 * mt, so merge m stays on XCD m % 8, the XCD of its
 // partials.
 template <int D, int ROWS>
-__global__ __launch_bounds__(64) void verify_merge_kernel(const VerifyParams p) {
+__global__ __launch_bounds__(64) void verify_merge_kernel(const VerifyMerge* __restrict__ merges, const VerifyParams p) {
   const int mi = blockIdx.x, mt = blockIdx.y;
   // the arguments in one round of scalar loads, then the whole record in one
-  __asm__ volatile("" ::"s"(p.merges), "s"(p.num_merges), "s"(p.part_o), "s"(p.part_lse), "s"(p.o),
+  __asm__ volatile("" ::"s"(merges), "s"(p.num_merges), "s"(p.part_o), "s"(p.part_lse), "s"(p.o),
                    "s"(p.o_stride_n), "s"(p.o_stride_h), "s"(p.lse), "s"(p.lse_stride_n), "s"(p.group),
                    "s"(p.sinks), "s"(p.lse_base2));
   if (mi >= p.num_merges) return;
-  const VerifyMerge m = p.merges[mi];
+  const VerifyMerge m = merges[mi];
   __asm__ volatile("" ::"s"(m.kvh), "s"(m.qtile), "s"(m.slot0), "s"(m.nslots), "s"(m.q0), "s"(m.nq), "s"(m.blk));
   if (m.nslots == 0) return;  // padding
   merge_rows<D, ROWS>(p, m.slot0, m.nslots, m.blk, mt, threadIdx.x, m.q0, m.nq, m.kvh, m.qtile);
@@ -1245,7 +1245,7 @@ __global__ __launch_bounds__(64) void verify_merge_kernel(const VerifyParams p) 
 // ---------------------------------------------------------------------------
 template <int D, int WPB, bool PAGED, bool FP8, int KIND>
 static hipError_t launch_verify_t(const VerifyParams& p, int nitems, hipStream_t s) {
-  hipLaunchKernelGGL((verify_attn_kernel<D, WPB, PAGED, FP8, KIND>), dim3(nitems), dim3(64 * WPB), 0, s, p);
+  hipLaunchKernelGGL((verify_attn_kernel<D, WPB, PAGED, FP8, KIND>), dim3(nitems), dim3(64 * WPB), 0, s, p.items, p);
   return hipGetLastError();
 }
 
@@ -1296,10 +1296,10 @@ hipError_t launch_verify_merge(const VerifyParams& p, int head_dim, int rows, in
   if (p.num_merges != nmerges) return hipErrorInvalidValue;
   const int nm8 = (nmerges + 7) & ~7;
   const dim3 grid((unsigned)nm8, (unsigned)(head_dim / 32)), block(64);
-  if (head_dim == 128 && rows == 128) hipLaunchKernelGGL((verify_merge_kernel<128, 128>), grid, block, 0, s, p);
-  else if (head_dim == 128 && rows == 256) hipLaunchKernelGGL((verify_merge_kernel<128, 256>), grid, block, 0, s, p);
-  else if (head_dim == 64 && rows == 128) hipLaunchKernelGGL((verify_merge_kernel<64, 128>), grid, block, 0, s, p);
-  else if (head_dim == 64 && rows == 256) hipLaunchKernelGGL((verify_merge_kernel<64, 256>), grid, block, 0, s, p);
+  if (head_dim == 128 && rows == 128) hipLaunchKernelGGL((verify_merge_kernel<128, 128>), grid, block, 0, s, p.merges, p);
+  else if (head_dim == 128 && rows == 256) hipLaunchKernelGGL((verify_merge_kernel<128, 256>), grid, block, 0, s, p.merges, p);
+  else if (head_dim == 64 && rows == 128) hipLaunchKernelGGL((verify_merge_kernel<64, 128>), grid, block, 0, s, p.merges, p);
+  else if (head_dim == 64 && rows == 256) hipLaunchKernelGGL((verify_merge_kernel<64, 256>), grid, block, 0, s, p.merges, p);
   else return hipErrorInvalidValue;
   return hipGetLastError();
 }

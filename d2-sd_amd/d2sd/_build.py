@@ -35,7 +35,10 @@ DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-p
 # of per-tile AGPR<->VGPR copies.  Its inputs are NaN-free by contract (scores
 # use -inf, never NaN): without NaN semantics the row maxima need no
 # canonicalising v_max x, x of every MFMA result (one VALU op per score).
-EXTRA = {"verify_attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1", "-fno-honor-nans"]}
+# The work-list pointer is the kernels' first argument: preloaded into SGPRs
+# at wave launch, so a workgroup's first load (its item) depends on nothing.
+EXTRA = {"verify_attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1", "-fno-honor-nans",
+                                  "-mllvm", "-amdgpu-kernarg-preload-count=2"]}
 
 
 def hipcc() -> str:
