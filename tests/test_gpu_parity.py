@@ -177,6 +177,43 @@ def test_reference_row_flow(bsz, causal, with_sinks):
     assert bsz in staged._graphs and not runner._graphs
 
 
+@pytest.mark.parametrize("bsz,lb,hq,hkv,d,causal,with_sinks,base2", [
+    (4, 32, 64, 8, 64, False, True, False),   # GPT-OSS heads: 256 rows per (row, kv head), two q-tiles
+    (3, 20, 32, 8, 128, True, False, True),   # 80 rows: a partial 32-row block, rows past the group's end
+    (2, 24, 16, 2, 128, True, True, False),   # 8 query heads per kv head at D = 128: 192 rows
+])
+def test_local_attention_merge_in_place(bsz, lb, hq, hkv, d, causal, with_sinks, base2):
+    """The in-place kind that serves the drop-in runner (model/cascade_graph.py:
+    52-60) across head shapes and row counts: each row's local attention
+    merged into the stored (O, LSE) (flashinfer.merge_state_in_place), then
+    the sink, against the oracle; the stored and returned LSE in base 2 when
+    asked."""
+    gen = torch.Generator().manual_seed(100 + lb)
+    q = bf16_randn(gen, bsz, lb, hq, d)
+    kl, vl = bf16_randn(gen, bsz, lb, hkv, d), bf16_randn(gen, bsz, lb, hkv, d)
+    o_st = bf16_randn(gen, bsz, lb, hq, d)
+    lse_st = torch.randn(bsz, lb, hq, generator=gen) * 2 + 4
+    sinks = torch.randn(hq, generator=gen) if with_sinks else None
+    scale = d ** -0.5
+    o_ref, lse_ref = [], []
+    for b in range(bsz):
+        o_l, lse_l = orc.single_prefill_ref(q[b], kl[b], vl[b], causal=causal, sm_scale=scale)
+        o_m, lse_m = orc.merge_state_ref(o_st[b].double(), lse_st[b].double(), o_l, lse_l)
+        o_ref.append(o_m)
+        lse_ref.append(lse_m)
+    o_ref, lse_ref = torch.stack(o_ref), torch.stack(lse_ref)
+    if sinks is not None:
+        o_ref = orc.sink_rescale_ref(o_ref, lse_ref, sinks)
+    log2e = 1.0 / math.log(2.0)
+    o_dev = o_st.to(DEV)
+    lse_dev = (lse_st * log2e if base2 else lse_st).to(DEV)
+    d2sd.local_attention_merge(q.to(DEV), kl.to(DEV), vl.to(DEV), o_dev, lse_dev, causal, scale,
+                               sinks=sinks.to(DEV) if sinks is not None else None, lse_base2=base2)
+    torch.cuda.synchronize()
+    lse_out = lse_dev.cpu() / log2e if base2 else lse_dev.cpu()
+    check_close(o_dev, o_ref, lse_out, lse_ref, f"in place {bsz}x{lb} {hq}/{hkv}/{d}")
+
+
 # --------------------------------------------------- cascade plan / run
 def _run_problem(prob, layers=1, **plan_kw):
     mp = wl.materialize(prob, DEV, layers=layers)
