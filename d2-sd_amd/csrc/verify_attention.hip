@@ -140,6 +140,11 @@ struct VerifyState {
   f32x16 o[RB][MT];
   float m_run[RB], l_run[RB];
   bf16x8 qf[RB][KS];
+  // handed from a fused item's prefix level to its suffix level: the suffix's
+  // first tiles were issued into the ring rotated by ring_off (handoff != 0)
+  // and its rows' tree-mask words loaded
+  int handoff, ring_off;
+  unsigned long long mreg[RB][kMaskRegWords];
 };
 
 // One workgroup: rows [qtile*ROWS, +ROWS) of (req, kvh) against keys
@@ -157,8 +162,11 @@ struct VerifyState {
 //   INPLACE: the items merge into the (O, LSE) already stored at the output
 //            (MODE_INPLACE, suffix level only); the stored state is loaded
 //            with Q, so its round trip overlaps the first tiles
+// SEAM (fused items, bf16 prefix): 1 = the prefix level issues the suffix
+// level's first tiles and mask words during its last tile; 2 = the suffix
+// level continues from them.
 template <int D, int W, int RB, int KST, int VST, int NPG, bool PAGED, bool MASKED, bool FP8, bool INIT = true,
-          bool EPI = true, bool INPLACE = false>
+          bool EPI = true, bool INPLACE = false, int SEAM = 0>
 __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyItem& w, const VerifySource& S,
                                             VerifySmem<D, KST, VST, NPG>& sm,
                                             VerifyState<RB, D / 32, D / 16>& st) {
@@ -230,7 +238,8 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
         if (rv[rb]) {
           mrow[rb] = p.tree_mask + (long long)(w.q0 + n[rb]) * p.mask_words;
 #pragma unroll
-          for (int k = 0; k < kMaskRegWords; ++k) mreg[rb][k] = (k < p.mask_words) ? mrow[rb][k] : 0ull;
+          for (int k = 0; k < kMaskRegWords; ++k)
+            mreg[rb][k] = (SEAM == 2 && st.handoff) ? st.mreg[rb][k] : (k < p.mask_words) ? mrow[rb][k] : 0ull;
         }
     }
   }
@@ -654,8 +663,12 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
         }
       }
     };
-    auto issue_k = [&](int it, PagePair pg) { issue(it, pg, kbase, kring + (it % KST) * TB); };
-    auto issue_v = [&](int it, PagePair pg) { issue(it, pg, vbase, vring + (it % VST) * TB); };
+    // ring slots: K(it) in (it + roff) % KST, V(it) in (it + roff) % VST
+    // (roff != 0 only for a suffix level continuing a fused item's ring)
+    int roff = 0;
+    if constexpr (SEAM == 2) roff = st.handoff ? st.ring_off : 0;
+    auto issue_k = [&](int it, PagePair pg) { issue(it, pg, kbase, kring + ((it + roff) % KST) * TB); };
+    auto issue_v = [&](int it, PagePair pg) { issue(it, pg, vbase, vring + ((it + roff) % VST) * TB); };
 
     // LDS byte offsets (inside a tile) of this lane's fragments; the
     // key-row / head-dim steps are immediate offsets.  K: key row l32 (+32 for
@@ -679,13 +692,13 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
 
     // Fragment readers of the ring slots holding K(it) / V(it).
     auto kfrag_at = [&](int it) {
-      const lds_char* kst = (const lds_char*)(uintptr_t)(kring + (it % KST) * TB);
+      const lds_char* kst = (const lds_char*)(uintptr_t)(kring + ((it + roff) % KST) * TB);
       return [&, kst](int kt, int ks) -> bf16x8 {
         return *(const __attribute__((address_space(3))) bf16x8*)(kst + koff[ks] + kt * 32 * D * 2);
       };
     };
     auto vfrag_at = [&](int it) {
-      const lds_char* vst = (const lds_char*)(uintptr_t)(vring + (it % VST) * TB);
+      const lds_char* vst = (const lds_char*)(uintptr_t)(vring + ((it + roff) % VST) * TB);
       return [&, vst](int mt, int ks) -> bf16x8 {
         typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
         const lds_char* p0 = vst + voff0[mt] + ks * 16 * D * 2;
@@ -805,20 +818,61 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
       if (ntiles > 0) {
         // last tile: keys past kv_end (a partial tile) are masked
         pstep_wait(ntiles - 1);
+        if constexpr (SEAM == 1) {
+          // Every K slot and all V slots but V(ntiles - 1)'s are free now
+          // (the barrier above): issue the suffix level's prologue tiles
+          // (rows q0.. of k/v_suffix, the order of its own prologue) into
+          // the ring rotated by ntiles, and its rows' tree-mask words, so
+          // that they land during this last tile.
+          if (p.mask_mode == MASK_TREE) {
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb)
+              if (rv[rb]) {
+                const unsigned long long* mr = p.tree_mask + (long long)(w.q0 + n[rb]) * p.mask_words;
+#pragma unroll
+                for (int k = 0; k < kMaskRegWords; ++k) st.mreg[rb][k] = (k < p.mask_words) ? mr[k] : 0ull;
+              }
+          }
+          const int nts = (w.nq + 63) >> 6;
+          const long long stok = p.suf.stride_tok * 2;
+          const long long soff = (long long)w.kvh * p.suf.stride_head * 2 + (long long)w.q0 * stok;
+          auto issue_s = [&](const void* src, int j, unsigned slot) {
+#pragma unroll
+            for (int i = 0; i < IPW; ++i) {
+              const int inst = wv * IPW + i;
+              const int r = inst * RPI + lrow;
+              dma16((const char*)src + soff + min(j * 64 + r, w.nq - 1) * stok + (cs ^ chunk_swizzle<D>(r)) * 16,
+                    slot + inst * 1024);
+            }
+          };
+          static_for<KST - 1>([&](auto jj) {
+            constexpr int st_ = decltype(jj)::value - (KST - 1);
+            if (st_ + VST - 1 >= 0 && st_ + VST - 1 < nts)
+              issue_s(p.suf.v, st_ + VST - 1, vring + ((st_ + VST - 1 + ntiles) % VST) * TB);
+            if (st_ + KST - 1 < nts) issue_s(p.suf.k, st_ + KST - 1, kring + ((st_ + KST - 1 + ntiles) % KST) * TB);
+          });
+        }
         if (live) {
           mask_scores(sc, kv_begin + (ntiles - 1) * 64, std::true_type{});
           finish_tile(sc, vfrag_at(ntiles - 1));
         }
       }
+      if constexpr (SEAM == 1) {
+        st.handoff = ntiles > 0;
+        st.ring_off = ntiles;
+      }
     } else {
       // ---- suffix level: masked tiles, skipped where no row sees a key ----
       // Issue order: step s issues V(s + VST - 1) then K(s + KST - 1); the
       // prologue plays steps -(KST - 1) .. -1.
-      static_for<KST - 1>([&](auto j) {
-        constexpr int st = decltype(j)::value - (KST - 1);
-        if (st + VST - 1 >= 0 && st + VST - 1 < ntiles) issue_v(st + VST - 1, wave_page(st + VST - 1));
-        if (st + KST - 1 < ntiles) issue_k(st + KST - 1, wave_page(st + KST - 1));
-      });
+      // (a fused item's prefix level already issued them: SEAM 2 with handoff)
+      if (!(SEAM == 2 && st.handoff)) {
+        static_for<KST - 1>([&](auto j) {
+          constexpr int st_ = decltype(j)::value - (KST - 1);
+          if (st_ + VST - 1 >= 0 && st_ + VST - 1 < ntiles) issue_v(st_ + VST - 1, wave_page(st_ + VST - 1));
+          if (st_ + KST - 1 < ntiles) issue_k(st_ + KST - 1, wave_page(st_ + KST - 1));
+        });
+      }
       auto pk_next = wave_page(KST - 1), pv_next = wave_page(VST - 1);
       wait_vmcnt<0>();  // Q / mask loads and the first tiles (see above)
 
@@ -1139,13 +1193,15 @@ void verify_attn_kernel(const VerifyItem* __restrict__ items, const VerifyParams
   } else if constexpr (KIND == KIND_FUSED) {
     // SRC_BOTH: the group's whole visible prefix, then its suffix tree, in
     // one state, to the final output (no partial, no merge)
-    verify_body<D, W, RB, R::KST, R::VST, R::NPG, PAGED, false, FP8, true, false>(p, w, p.pre, sm, st);
+    verify_body<D, W, RB, R::KST, R::VST, R::NPG, PAGED, false, FP8, true, false, false, FP8 ? 0 : 1>(p, w, p.pre,
+                                                                                                       sm, st);
     __syncthreads();  // every wave is done with the prefix tiles in the rings
     VerifyItem ws = w;
     ws.kv_begin = 0;
     ws.kv_end = w.nq;
     ws.base = w.q0;  // the request's suffix keys are rows q0.. of k/v_suffix
-    verify_body<D, W, RB, R::KST, R::VST, R::NPG, false, true, false, false, true>(p, ws, p.suf, sm, st);
+    verify_body<D, W, RB, R::KST, R::VST, R::NPG, false, true, false, false, true, false, FP8 ? 0 : 2>(p, ws, p.suf,
+                                                                                                       sm, st);
   }
 }
 
