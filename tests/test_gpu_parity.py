@@ -508,6 +508,27 @@ def test_fused_plan_vs_oracle(name):
     _check_problem(mp, outs, dtype=torch.float32, tag=f"fused {name}")
 
 
+@pytest.mark.parametrize("d,hq,waves,page,window", [(128, 32, 4, 16, -1), (128, 32, 8, 16, 100), (128, 32, 2, 0, -1),
+                                                     (64, 64, 4, 16, -1), (64, 64, 8, 0, 100)])
+def test_fused_seam_every_ring(d, hq, waves, page, window):
+    """Fused items hand the suffix level's first tiles and mask words over
+    during the prefix level's last tile, into the ring rotated by the prefix's
+    tile count: every ring depth (K / V slots 3 / 2, 4 / 3, 5 / 4, 6 / 5),
+    prefixes of 0..11 tiles (so every rotation), partial last tiles, windows,
+    and suffix trees of one to four tiles, against the oracle (a plan with at
+    most one chunk per group is fused)."""
+    rng = np.random.default_rng(7 + d + waves)
+    lens = [0, 1, 63, 64, 65, 130, 200, 257, 450, 700]
+    shapes = [(1, 8), (2, 16), (3, 32), (5, 32), (12, 32), (2, 8), (4, 16), (6, 32), (1, 16), (7, 32)]
+    reqs = [wl.Request(wl.random_branch_tree(rng, nr, rl, chain_to_row0=bool(i % 2)), L)
+            for i, (L, (nr, rl)) in enumerate(zip(lens, shapes))]
+    prob = wl.VerifyProblem(f"seam_{d}_{waves}", hq, 8, d, reqs, page_size=page, window_left=window,
+                            with_sinks=True, seed=d + waves)
+    mp, attn, outs = _run_problem(prob, waves_per_block=waves, max_splits=1)
+    assert attn.info.fused == 1 and attn.info.num_merges == 0
+    _check_problem(mp, outs, tag=f"seam d{d} w{waves} page{page} window{window}")
+
+
 def test_fused_dynamic_plan_at_every_length():
     """A fused dynamic-prefix plan (windowed GPT-OSS-style layer, prefixes
     planned at 900 and 200) run at shorter and ragged lengths, empty included:
