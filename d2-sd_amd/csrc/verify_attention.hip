@@ -1125,15 +1125,19 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
       // streaming stores: the merge launch reads each partial once, and
       // lines that leave L2 during the epilogue are not written back at the
       // kernel's end
+      // (rows past the group's end are never merged: not stored)
       const int blk = RB * wv + rb;
       bf16_t* po = (bf16_t*)p.part_o + (long long)w.slot * ROWS * D;
       float* pl = p.part_lse + (long long)w.slot * ROWS + blk * 32 + l32;
+      if (rv[rb]) {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int pr = 0; pr < 2; ++pr)
-          __builtin_nontemporal_store(image_piece(o[rb][mt], pr, 1.f), (u32x4*)(po + image_offset<D>(blk, mt, pr, lane)));
-      if (hh == 0) __builtin_nontemporal_store(lse_r, pl);
+          for (int pr = 0; pr < 2; ++pr)
+            __builtin_nontemporal_store(image_piece(o[rb][mt], pr, 1.f),
+                                        (u32x4*)(po + image_offset<D>(blk, mt, pr, lane)));
+        if (hh == 0) __builtin_nontemporal_store(lse_r, pl);
+      }
     }
   }
 }
