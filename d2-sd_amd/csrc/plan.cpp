@@ -101,6 +101,7 @@ struct Piece {            // the q-tiles of one (request, kv head) over prefix t
 struct PlanItem {
   VerifyItem w;
   int cost;               // in prefix-tile units
+  int c = -1;             // dynamic plans: the chunk's index among its group's chunks (else -1)
 };
 
 int ceil_div(long long a, long long b) { return (int)((a + b - 1) / b); }
@@ -238,10 +239,20 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
   }
 
   // ---- partial slots: per group its prefix chunks in key order, then the suffix ----
-  // Chunk c of S over tiles [t0, t1): tiles [t0 + span c / S, t0 + span (c+1) / S).
+  // Chunk c of S over tiles [t0, t1): tiles [t0 + span c / S, t0 + span (c+1) / S);
+  // in dynamic plans a chunk of a request's whole visible prefix takes the
+  // partition the device repeats at the run-time length (dyn_chunk_start).
   // A chunk holding tiles of both segments is cut at the split: two items.
-  auto chunk_tiles = [](const Piece& pc, int S, int c, int& a, int& b) {
+  auto whole = [&](const Piece& pc) {
+    return in.dynamic && !in.prefix_split && pc.t0 == 0 && pc.t1 == ptiles[pc.req];
+  };
+  auto chunk_tiles = [&](const Piece& pc, int S, int c, int& a, int& b) {
     const int span = pc.t1 - pc.t0;
+    if (whole(pc)) {
+      a = pc.t0 + dyn_chunk_start(c, S, span);
+      b = pc.t0 + dyn_chunk_start(c + 1, S, span);
+      return;
+    }
     a = pc.t0 + (int)((long long)span * c / S);
     b = pc.t0 + (int)((long long)span * (c + 1) / S);
   };
@@ -311,7 +322,11 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
           w.kv_end = std::min(sp[r], kv0[r] + 64 * e);
           w.slot = fuse ? -1 : next_slot[gi]++;
           w.base = pbase;
-          lists[x].push_back({w, (e - a) + (fuse ? 2 * stiles[r] : 0)});
+          // dynamic plans: a chunk of the whole visible prefix is re-partitioned
+          // on the device (dyn_chunk_start); pieces of a range keep the scaling
+          const bool wh = whole(pc);
+          w.chunk = wh ? c | S << 16 : 0;
+          lists[x].push_back({w, (e - a) + (fuse ? 2 * stiles[r] : 0), wh ? c : -1});
         }
         if (b > ta[r]) {  // second segment, in its own key numbering
           const int f = std::max(a, ta[r]);
@@ -365,7 +380,12 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
   std::vector<std::vector<VerifyItem>> ordered(8);
   for (int x = 0; x < 8; ++x) {
     auto& L = lists[x];
-    std::stable_sort(L.begin(), L.end(), [](const PlanItem& a, const PlanItem& b) { return a.cost > b.cost; });
+    // longest first; in dynamic plans ties go to lower chunk indices first, so
+    // a group's first chunks (the ones the run-time partition lengthens first)
+    // run in the first round, each paired with a later chunk
+    std::stable_sort(L.begin(), L.end(), [](const PlanItem& a, const PlanItem& b) {
+      return a.cost != b.cost ? a.cost > b.cost : a.c < b.c;
+    });
     const int m = (int)L.size(), K = cus_per_xcd;
     auto& o = ordered[x];
     if (wpc == 2 && m > K && m <= 2 * K) {

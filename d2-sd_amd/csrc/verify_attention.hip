@@ -145,6 +145,9 @@ struct VerifyState {
   // and its rows' tree-mask words loaded
   int handoff, ring_off;
   unsigned long long mreg[RB][kMaskRegWords];
+  // dynamic plans: request 0's run-time prefix length, loaded at kernel entry
+  // together with the item (the other requests' lengths are loaded after it)
+  int len0;
 };
 
 // One workgroup: rows [qtile*ROWS, +ROWS) of (req, kvh) against keys
@@ -200,22 +203,31 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
   }
   int kv_begin = w.kv_begin, kv_end = w.kv_end;
   if constexpr (!MASKED) {
-    // dynamic plan: the planned chunks of the span [kv0, plan_len) scaled to
-    // the run-time span [k0, L) (L never beyond the planned length), each
-    // boundary rounded down to a 64-key tile and the last one kept at L, so
-    // the chunks stay contiguous, keep their relative sizes (the plan's
-    // balance over XCDs and CUs) and no workgroup idles on keys past L
+    // dynamic plan: the run-time span [k0, L) (L never beyond the planned
+    // length) in 64-key tiles from k0, the last one ending at L.  A chunk of
+    // the whole span takes its share of the equal partition (dyn_chunk_start:
+    // the planner pairs chunks 2j and 2j + 1 on a CU); a chunk of a piece
+    // scales its planned boundaries, rounded down to a tile, so the chunks stay
+    // contiguous, keep their relative sizes (the plan's balance over XCDs and
+    // CUs) and no workgroup idles on keys past L
     if (p.prefix_len || p.prefix_len_set) {
-      const int L = min(max(p.prefix_len_set ? p.prefix_len_value : p.prefix_len[w.req], 0), w.plan_len);
+      const int L = min(max(p.prefix_len_set ? p.prefix_len_value : w.req == 0 ? st.len0 : p.prefix_len[w.req], 0),
+                        w.plan_len);
       const int span = p.window_left >= 0 ? min(L, p.window_left) : L;
       const int k0 = L - span;
-      const long long pspan = (long long)w.plan_len - w.kv0;
-      auto scale = [&](int x) -> int {
-        if (pspan <= 0 || x >= pspan) return span;
-        return min(span, (int)(((long long)x * span / pspan) & ~63ll));
-      };
-      kv_begin = k0 + scale(w.kv_begin - w.kv0);
-      kv_end = k0 + scale(w.kv_end - w.kv0);
+      if (w.chunk) {
+        const int c = w.chunk & 0xffff, S = w.chunk >> 16, nt = (span + 63) >> 6;
+        kv_begin = k0 + min(span, 64 * dyn_chunk_start(c, S, nt));
+        kv_end = k0 + min(span, 64 * dyn_chunk_start(c + 1, S, nt));
+      } else {
+        const long long pspan = (long long)w.plan_len - w.kv0;
+        auto scale = [&](int x) -> int {
+          if (pspan <= 0 || x >= pspan) return span;
+          return min(span, (int)(((long long)x * span / pspan) & ~63ll));
+        };
+        kv_begin = k0 + scale(w.kv_begin - w.kv0);
+        kv_end = k0 + scale(w.kv_end - w.kv0);
+      }
     }
   }
   const int ntiles = kv_end > kv_begin ? (kv_end - kv_begin + 63) >> 6 : 0;
@@ -1168,11 +1180,17 @@ struct Shape<8> { static constexpr int W = 8, RB = 1, OCC = 2; };
 template <int D, int WPB, bool PAGED, bool FP8, int KIND>
 __global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(KIND == KIND_INPLACE ? 1 : Shape<WPB>::OCC,
                                                                             KIND == KIND_INPLACE ? 1 : Shape<WPB>::OCC)))
-void verify_attn_kernel(const VerifyItem* __restrict__ items, const VerifyParams p) {
+void verify_attn_kernel(const VerifyItem* __restrict__ items, const int* __restrict__ prefix_len,
+                        const VerifyParams p) {
   constexpr int W = Shape<WPB>::W, RB = Shape<WPB>::RB;
   using R = RingCfg<D, WPB>;
   __shared__ __attribute__((aligned(16))) VerifySmem<D, R::KST, R::VST, R::NPG> sm;
   const VerifyItem w = items[blockIdx.x];
+  // prefix_len (p.prefix_len, preloaded like items): request 0's length is
+  // fetched in the same round as the item, so a single-request dynamic plan
+  // knows its key range when the item lands
+  int len0 = 0;
+  if (prefix_len) len0 = prefix_len[0];
   // Load the whole item and the prefix-level arguments in one round of
   // scalar loads (the compiler would otherwise fetch the fields used after
   // the mode test in later rounds): the Q loads and the first page ids
@@ -1184,6 +1202,7 @@ void verify_attn_kernel(const VerifyItem* __restrict__ items, const VerifyParams
                    "s"(p.pre.log2_page), "s"(p.group), "s"(p.sm_scale_log2));
   if (w.mode == MODE_NOOP) return;
   VerifyState<RB, D / 32, D / 16> st;
+  st.len0 = len0;
   if constexpr (KIND == KIND_INPLACE) {
     verify_body<D, W, RB, R::KST, R::VST, R::NPG, false, true, false, true, true, true>(p, w, p.suf, sm, st);
   } else if (KIND == KIND_SPLIT && w.src == SRC_PREFIX) {
@@ -1305,7 +1324,7 @@ __global__ __launch_bounds__(64) void verify_merge_kernel(const VerifyMerge* __r
 // ---------------------------------------------------------------------------
 template <int D, int WPB, bool PAGED, bool FP8, int KIND>
 static hipError_t launch_verify_t(const VerifyParams& p, int nitems, hipStream_t s) {
-  hipLaunchKernelGGL((verify_attn_kernel<D, WPB, PAGED, FP8, KIND>), dim3(nitems), dim3(64 * WPB), 0, s, p.items, p);
+  hipLaunchKernelGGL((verify_attn_kernel<D, WPB, PAGED, FP8, KIND>), dim3(nitems), dim3(64 * WPB), 0, s, p.items, p.prefix_len, p);
   return hipGetLastError();
 }
 

@@ -35,10 +35,12 @@ DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-p
 # of per-tile AGPR<->VGPR copies.  Its inputs are NaN-free by contract (scores
 # use -inf, never NaN): without NaN semantics the row maxima need no
 # canonicalising v_max x, x of every MFMA result (one VALU op per score).
-# The work-list pointer is the kernels' first argument: preloaded into SGPRs
-# at wave launch, so a workgroup's first load (its item) depends on nothing.
+# The work-list pointer is the kernels' first argument (and the attention
+# kernel's run-time prefix lengths its second): preloaded into SGPRs at wave
+# launch, so a workgroup's first loads (its item, request 0's prefix length)
+# depend on nothing.
 EXTRA = {"verify_attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1", "-fno-honor-nans",
-                                  "-mllvm", "-amdgpu-kernarg-preload-count=2"]}
+                                  "-mllvm", "-amdgpu-kernarg-preload-count=4"]}
 
 
 def hipcc() -> str:

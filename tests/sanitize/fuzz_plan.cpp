@@ -2,9 +2,12 @@
 // with AddressSanitizer and UBSan on the host by tests/test_plan_sanitize.py:
 // every emitted item reads keys inside its request and segment, paged chunks
 // stay within the staged page bound, partial slots are unique and every merge
-// names slots that exist.
+// names slots that exist; in dynamic plans the chunks of a group's whole
+// prefix are numbered 0..S-1 and their run-time partition (dyn_chunk_start)
+// tiles every shorter prefix exactly, within the staged page bound.
 #include <cstdio>
 #include <cstdlib>
+#include <map>
 #include <random>
 #include <set>
 #include <vector>
@@ -46,14 +49,44 @@ int main(int argc, char** argv) {
     in.page_size = page;
     in.prefix_split = two ? sp.data() : nullptr;
     in.prefix2_tok_indptr = two && U(0, 1) ? t2.data() : nullptr;
+    in.dynamic = !two && U(0, 1);
     VerifyPlanOutput out{};
     plan_verify(in, out);
     std::set<int> slots;
     int lg = 0;
     while (page && (1 << lg) < page) ++lg;
+    std::map<long long, std::set<int>> chunks;  // group -> chunk indices
+    std::map<long long, int> nchunks;
     for (const auto& w : out.items) {
       if (w.mode == MODE_NOOP) continue;
       ++checked;
+      if (w.chunk) {
+        const int c = w.chunk & 0xffff, S = w.chunk >> 16;
+        const long long key = ((long long)w.req * hkv + w.kvh) * 100000 + w.qtile;
+        if (!in.dynamic || (w.src != SRC_PREFIX && w.src != SRC_BOTH) || c >= S || !chunks[key].insert(c).second ||
+            (nchunks.count(key) && nchunks[key] != S)) { printf("bad chunk index\n"); return 1; }
+        nchunks[key] = S;
+        // the run-time partition of every length up to the planned one
+        for (int k = 0; k < 6; ++k) {
+          const int L = k == 0 ? pl[w.req] : k == 1 ? 0 : U(0, pl[w.req]);
+          const int span = in.window_left >= 0 ? std::min(L, in.window_left) : L, k0 = L - span;
+          const int nt = (span + 63) / 64;
+          const int b = k0 + std::min(span, 64 * dyn_chunk_start(c, S, nt));
+          const int e = k0 + std::min(span, 64 * dyn_chunk_start(c + 1, S, nt));
+          const int b0 = k0 + std::min(span, 64 * dyn_chunk_start(0, S, nt));
+          const int eS = k0 + std::min(span, 64 * dyn_chunk_start(S, S, nt));
+          const int t = (e - b + 63) / 64;
+          if (b0 != k0 || eS != L || e < b || t > nt / S + 1 || (nt % S == 0 && t != nt / S) ||
+              (k == 0 && (b != w.kv_begin || e != w.kv_end)) ||  // the planned chunk at the planned length
+              (page && pages_spanned(b, e, lg) > kMaxStagedPages)) {
+            printf("bad run-time chunk L=%d c=%d S=%d [%d, %d)\n", L, c, S, b, e); return 1;
+          }
+          if (c + 1 < S) {  // contiguous with the next chunk
+            const int nb = k0 + std::min(span, 64 * dyn_chunk_start(c + 1, S, nt));
+            if (nb != e) { printf("gap\n"); return 1; }
+          }
+        }
+      }
       if (w.req < 0 || w.req >= R || w.kvh < 0 || w.kvh >= hkv) { printf("bad req/kvh\n"); return 1; }
       if (w.src == SRC_SUFFIX) {
         if (w.kv_begin != 0 || w.kv_end != qo[w.req + 1] - qo[w.req]) { printf("bad suffix range\n"); return 1; }
@@ -70,6 +103,8 @@ int main(int argc, char** argv) {
     }
     for (const auto& m : out.merges)
       if (m.nslots && (m.slot0 < 0 || m.slot0 + m.nslots > out.num_slots)) { printf("bad merge\n"); return 1; }
+    for (const auto& kv : chunks)
+      if ((int)kv.second.size() != nchunks[kv.first]) { printf("missing chunk index\n"); return 1; }
   }
   printf("ok: %d plans, %lld items checked\n", iters, checked);
   return 0;

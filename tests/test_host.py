@@ -265,6 +265,41 @@ def test_plan_two_segment_prefix_partitions_keys(qo, pl, split, window, tok1, to
             assert blocks[key] == len(ch) + 1   # the chunks of both segments and the suffix
 
 
+@pytest.mark.parametrize("qo,pl,window", [([0, 150], [4608], -1), ([0, 156], [4096], -1), ([0, 64, 100], [9000, 700], -1),
+                                          ([0, 150], [4608], 3000), ([64 * i for i in range(9)], [6000] * 8, -1)])
+def test_dynamic_plan_numbers_chunks_first_round_first(qo, pl, window):
+    """A dynamic plan numbers the chunks of each group's whole visible prefix
+    0..S-1 in key order, sized as the device partitions a run-time prefix
+    (the first nt % S chunks one tile longer), and runs a group's first
+    chunks in the first resident round of its XCD's CUs: every first-round
+    chunk of a group precedes its second-round chunks.  A static plan of the
+    same shape numbers nothing."""
+    info, items, _ = _plan(qo, pl, window=window, dynamic=1)
+    _, sitems, _ = _plan(qo, pl, window=window)
+    CHUNK = 14
+    assert (sitems[:, CHUNK] == 0).all()
+    groups = {}
+    for i, it in enumerate(items.tolist()):
+        if it[MODE] == MODE_NOOP or it[SRC] == SRC_SUFFIX:
+            continue
+        assert it[CHUNK] != 0
+        c, S = it[CHUNK] & 0xFFFF, it[CHUNK] >> 16
+        groups.setdefault((it[REQ], it[KVH], it[QT]), []).append((c, S, it[KB], it[KE], i))
+    K = 256 // 8
+    for (r, h, qt), v in groups.items():
+        v.sort()
+        S = v[0][1]
+        assert [c for c, *_ in v] == list(range(S)) and {x[1] for x in v} == {S}
+        L = pl[r]
+        k0 = L - (min(L, window) if window >= 0 else L)
+        nt = -(-(L - k0) // 64)
+        sizes = [-(-(e - b) // 64) for _, _, b, e, _ in v]
+        assert v[0][2] == k0 and v[-1][3] == L
+        assert sizes == [nt // S + (c < nt % S) for c in range(S)]
+        rounds = [(i // 8) // K for *_, i in v]           # workgroup i runs on XCD i % 8, round (i // 8) // K
+        assert rounds == sorted(rounds)
+
+
 def test_plan_rejects_bad_two_segment_prefixes():
     """A second segment needs a contiguous first one and a static plan, and
     each split must lie in [0, prefix_len]."""
