@@ -117,15 +117,16 @@ struct VerifyItem {
   int causal_off;        // MASK_CAUSAL: key j visible to query i iff j <= i + causal_off
   int kv0;               // prefix: first visible key at the planned length (window start)
   int plan_len;          // prefix: the request's planned prefix length
-  int chunk;             // dynamic plans: c | S << 16 for chunk c of the S chunks that split the
-                         // request's whole visible prefix for this q-tile (0: the planned
-                         // boundaries are scaled to the run-time length instead)
+  int chunk;             // c | S << 16 for chunk c of the S chunks that split the request's
+                         // whole visible prefix for this q-tile (dynamic plans re-partition
+                         // it at the run-time length); 0: a piece of the prefix (dynamic
+                         // plans scale its planned boundaries instead)
   int pad;
 };
 
-// Dynamic plans: first 64-key tile of chunk i of the S chunks that split nt
-// tiles (the planned prefix, or the run-time one): nt / S tiles each and one
-// more for the first nt % S chunks.  The planner runs a group's first chunks
+// First 64-key tile of chunk i of the S chunks that split nt tiles (a planned
+// prefix, or a dynamic plan's run-time one): nt / S tiles each and one more
+// for the first nt % S chunks.  The planner runs a group's first chunks
 // in a CU's first round, each paired with a later chunk, so while a group's
 // extra tiles fit its first-round chunks no CU holds two.  (constexpr: also
 // compiled for the device.)

@@ -240,12 +240,11 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
 
   // ---- partial slots: per group its prefix chunks in key order, then the suffix ----
   // Chunk c of S over tiles [t0, t1): tiles [t0 + span c / S, t0 + span (c+1) / S);
-  // in dynamic plans a chunk of a request's whole visible prefix takes the
-  // partition the device repeats at the run-time length (dyn_chunk_start).
-  // A chunk holding tiles of both segments is cut at the split: two items.
-  auto whole = [&](const Piece& pc) {
-    return in.dynamic && !in.prefix_split && pc.t0 == 0 && pc.t1 == ptiles[pc.req];
-  };
+  // a chunk of a request's whole visible prefix takes the partition
+  // dyn_chunk_start (the first span % S chunks one tile longer), which a
+  // dynamic plan's kernels repeat at the run-time length.  A chunk holding
+  // tiles of both segments is cut at the split: two items.
+  auto whole = [&](const Piece& pc) { return !in.prefix_split && pc.t0 == 0 && pc.t1 == ptiles[pc.req]; };
   auto chunk_tiles = [&](const Piece& pc, int S, int c, int& a, int& b) {
     const int span = pc.t1 - pc.t0;
     if (whole(pc)) {
@@ -322,8 +321,9 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
           w.kv_end = std::min(sp[r], kv0[r] + 64 * e);
           w.slot = fuse ? -1 : next_slot[gi]++;
           w.base = pbase;
-          // dynamic plans: a chunk of the whole visible prefix is re-partitioned
-          // on the device (dyn_chunk_start); pieces of a range keep the scaling
+          // a chunk of the whole visible prefix names its place in the
+          // partition (dynamic plans repeat it on the device); a dynamic
+          // plan's pieces of a range scale their planned boundaries instead
           const bool wh = whole(pc);
           w.chunk = wh ? c | S << 16 : 0;
           lists[x].push_back({w, (e - a) + (fuse ? 2 * stiles[r] : 0), wh ? c : -1});
@@ -380,9 +380,9 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
   std::vector<std::vector<VerifyItem>> ordered(8);
   for (int x = 0; x < 8; ++x) {
     auto& L = lists[x];
-    // longest first; in dynamic plans ties go to lower chunk indices first, so
-    // a group's first chunks (the ones the run-time partition lengthens first)
-    // run in the first round, each paired with a later chunk
+    // longest first, ties to lower chunk indices first: a group's first
+    // chunks (the ones the partition lengthens first) run in the first round,
+    // each paired with a later chunk
     std::stable_sort(L.begin(), L.end(), [](const PlanItem& a, const PlanItem& b) {
       return a.cost != b.cost ? a.cost > b.cost : a.c < b.c;
     });

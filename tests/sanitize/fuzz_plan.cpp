@@ -2,9 +2,10 @@
 // with AddressSanitizer and UBSan on the host by tests/test_plan_sanitize.py:
 // every emitted item reads keys inside its request and segment, paged chunks
 // stay within the staged page bound, partial slots are unique and every merge
-// names slots that exist; in dynamic plans the chunks of a group's whole
-// prefix are numbered 0..S-1 and their run-time partition (dyn_chunk_start)
-// tiles every shorter prefix exactly, within the staged page bound.
+// names slots that exist; the chunks of a group's whole prefix are numbered
+// 0..S-1 and their partition (dyn_chunk_start) gives the planned chunks at the
+// planned length and tiles every shorter prefix exactly (a dynamic plan's
+// run-time chunks), within the staged page bound.
 #include <cstdio>
 #include <cstdlib>
 #include <map>
@@ -63,7 +64,7 @@ int main(int argc, char** argv) {
       if (w.chunk) {
         const int c = w.chunk & 0xffff, S = w.chunk >> 16;
         const long long key = ((long long)w.req * hkv + w.kvh) * 100000 + w.qtile;
-        if (!in.dynamic || (w.src != SRC_PREFIX && w.src != SRC_BOTH) || c >= S || !chunks[key].insert(c).second ||
+        if ((w.src != SRC_PREFIX && w.src != SRC_BOTH) || c >= S || !chunks[key].insert(c).second ||
             (nchunks.count(key) && nchunks[key] != S)) { printf("bad chunk index\n"); return 1; }
         nchunks[key] = S;
         // the run-time partition of every length up to the planned one
