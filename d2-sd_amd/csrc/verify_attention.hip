@@ -205,11 +205,11 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
   if constexpr (!MASKED) {
     // dynamic plan: the run-time span [k0, L) (L never beyond the planned
     // length) in 64-key tiles from k0, the last one ending at L.  A chunk of
-    // the whole span takes its share of the equal partition (dyn_chunk_start:
-    // the planner pairs chunks 2j and 2j + 1 on a CU); a chunk of a piece
-    // scales its planned boundaries, rounded down to a tile, so the chunks stay
-    // contiguous, keep their relative sizes (the plan's balance over XCDs and
-    // CUs) and no workgroup idles on keys past L
+    // the whole span takes its share of the partition the planner made at the
+    // planned length (dyn_chunk_start: even shares, the first chunks one tile
+    // longer); a chunk of a piece scales its planned boundaries, rounded down
+    // to a tile, so the chunks stay contiguous, keep their relative sizes (the
+    // plan's balance over XCDs and CUs) and no workgroup idles on keys past L
     if (p.prefix_len || p.prefix_len_set) {
       const int L = min(max(p.prefix_len_set ? p.prefix_len_value : w.req == 0 ? st.len0 : p.prefix_len[w.req], 0),
                         w.plan_len);

@@ -270,7 +270,8 @@ class CascadeVerifyAttention:
         same = old is not None and all(
             getattr(old, f) == getattr(info, f) for f in
             ("num_items", "num_merges", "waves_per_block", "rows_per_tile", "num_slots", "num_reqs",
-             "num_qo_heads", "num_kv_heads", "head_dim", "kv_dtype", "page_size", "dynamic_prefix", "two_segment"))
+             "num_qo_heads", "num_kv_heads", "head_dim", "kv_dtype", "page_size", "dynamic_prefix", "two_segment",
+             "fused"))
         mask_words = int(packed.shape[1]) if packed is not None else 0
         same_mask = same and packed is not None and getattr(self, "tree_mask_dev", None) is not None \
             and self.mask_words == mask_words and self.tree_mask_dev.numel() >= packed.size

@@ -2,7 +2,8 @@
 // with AddressSanitizer and UBSan on the host by tests/test_plan_sanitize.py:
 // every emitted item reads keys inside its request and segment, paged chunks
 // stay within the staged page bound, partial slots are unique and every merge
-// names slots that exist; the chunks of a group's whole prefix are numbered
+// names slots that each one item of its group writes, every group's suffix
+// tree is read once; the chunks of a group's whole prefix are numbered
 // 0..S-1 and their partition (dyn_chunk_start) gives the planned chunks at the
 // planned length and tiles every shorter prefix exactly (a dynamic plan's
 // run-time chunks), within the staged page bound.
@@ -19,6 +20,7 @@ int main(int argc, char** argv) {
   std::mt19937_64 rng(12345);
   auto U = [&](int a, int b) { return (int)std::uniform_int_distribution<int>(a, b)(rng); };
   long long checked = 0;
+  int fused_plans = 0;
   for (int t = 0; t < iters; ++t) {
     const int R = U(1, 40);
     std::vector<int> qo(R + 1, 0), pl(R), pi(R + 1, 0), ti(R), sp(R), t2(R);
@@ -53,11 +55,14 @@ int main(int argc, char** argv) {
     in.dynamic = !two && U(0, 1);
     VerifyPlanOutput out{};
     plan_verify(in, out);
+    fused_plans += out.fused;
     std::set<int> slots;
     int lg = 0;
     while (page && (1 << lg) < page) ++lg;
     std::map<long long, std::set<int>> chunks;  // group -> chunk indices
     std::map<long long, int> nchunks;
+    std::map<long long, int> suffix_readers;    // group -> items reading its suffix tree
+    std::map<int, long long> slot_group;        // partial slot -> its writer's group
     for (const auto& w : out.items) {
       if (w.mode == MODE_NOOP) continue;
       ++checked;
@@ -98,15 +103,34 @@ int main(int argc, char** argv) {
         if (w.kv_begin < 0 || w.kv_end > hi || w.kv_begin >= w.kv_end) { printf("bad prefix range %d %d %d\n", w.kv_begin, w.kv_end, hi); return 1; }
         if (page && pages_spanned(w.kv_begin, w.kv_end, lg) > kMaxStagedPages) { printf("page bound\n"); return 1; }
       }
+      const long long gkey = ((long long)w.req * hkv + w.kvh) * 100000 + w.qtile;
+      if (w.src == SRC_SUFFIX || w.src == SRC_BOTH) ++suffix_readers[gkey];
+      if (w.src == SRC_BOTH && !out.fused) { printf("SRC_BOTH in a split plan\n"); return 1; }
       if (w.mode == MODE_PARTIAL) {
         if (w.slot < 0 || w.slot >= out.num_slots || !slots.insert(w.slot).second) { printf("bad slot\n"); return 1; }
+        slot_group[w.slot] = gkey;
       }
     }
-    for (const auto& m : out.merges)
+    for (const auto& m : out.merges) {
       if (m.nslots && (m.slot0 < 0 || m.slot0 + m.nslots > out.num_slots)) { printf("bad merge\n"); return 1; }
+      const long long gkey = ((long long)m.req * hkv + m.kvh) * 100000 + m.qtile;
+      for (int k = 0; k < m.nslots; ++k)  // every merged slot is written by one item of the group
+        if (!slot_group.count(m.slot0 + k) || slot_group[m.slot0 + k] != gkey) { printf("unwritten slot\n"); return 1; }
+    }
+    if ((int)slots.size() != out.num_slots) { printf("slot count\n"); return 1; }
+    for (int r = 0; r < R; ++r) {  // every group's suffix tree is read exactly once
+      const int n = qo[r + 1] - qo[r];
+      if (n == 0) continue;
+      const int qt = (n * g + out.rows - 1) / out.rows;
+      for (int h = 0; h < hkv; ++h)
+        for (int t = 0; t < qt; ++t) {
+          const long long gkey = ((long long)r * hkv + h) * 100000 + t;
+          if (suffix_readers[gkey] != 1) { printf("suffix read %d times\n", suffix_readers[gkey]); return 1; }
+        }
+    }
     for (const auto& kv : chunks)
       if ((int)kv.second.size() != nchunks[kv.first]) { printf("missing chunk index\n"); return 1; }
   }
-  printf("ok: %d plans, %lld items checked\n", iters, checked);
+  printf("ok: %d plans (%d fused), %lld items checked\n", iters, fused_plans, checked);
   return 0;
 }
