@@ -407,6 +407,29 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
     return true;
   };
 
+  // Suffix level: some row of this wave sees a key of kb + 32 .. kb + 63
+  // (else the in-place kind skips the tile's upper half: past the range, or
+  // masked for every row, as for the drop-in runner's blocks of up to 32
+  // tokens)
+  auto upper_visible = [&](int kb) -> bool {
+    if (kv_end - kb <= 32) return false;
+    if constexpr (MASKED) {
+      if (mask_mode == MASK_TREE) {
+        unsigned long long any = 0ull;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) any |= tile_word(rb, kb >> 6);
+        return __any((any >> 32) != 0ull);
+      }
+      if (mask_mode == MASK_CAUSAL) {
+        bool any = false;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) any = any || (rv[rb] && kb + 32 <= n[rb] + w.causal_off);
+        return __any(any);
+      }
+    }
+    return true;
+  };
+
   // Pieces of one 64-key tile.  kfrag(kt, ks) is the A operand of keys
   // 32kt..32kt+31, head dims 16ks.. (this lane's part); vfrag(mt, ks) the A
   // operand of head dims 32mt.., keys 16ks.. in P^T order.
@@ -533,6 +556,38 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
   // One whole 64-key tile: QK^T, masking, online softmax, PV.
   auto compute_tile = [&](int kb, auto&& kfrag, auto&& vfrag, auto masked_tile) {
     f32x16 s[RB][2];
+    // (the in-place kind only: one wave per SIMD leaves room for the second
+    // path; in the split kinds it would spill registers of the prefix loop)
+    if constexpr (INPLACE && RB == 1) {
+      if (!upper_visible(kb)) {
+        // half a tile: QK^T, softmax and PV of keys kb .. kb + 31 only
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const bf16x8 a0 = kfrag(0, ks);
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb)
+            s[rb][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[rb][ks], ks == 0 ? f32x16{} : s[rb][0], 0, 0, 0);
+        }
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[rb][1][r] = -INFINITY;
+        mask_scores(s, kb, masked_tile);
+        float mc[RB];
+        max_rescale(s, mc);
+        bf16x8 pb[RB][4];
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+          float ls[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int j = 0; j < 2; ++j) pb[rb][j] = p_chunk(s, rb, j, mc[rb], ls);
+          l_run[rb] += (ls[0] + ls[1]) + (ls[2] + ls[3]);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) pv_chunk(vfrag, pb, j);
+        return;
+      }
+    }
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) qk_ks(s, kfrag, ks);
     mask_scores(s, kb, masked_tile);
