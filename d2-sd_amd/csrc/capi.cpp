@@ -294,8 +294,12 @@ int d2sd_graph_destroy(void* graph_exec) {
   return e == hipSuccess ? D2SD_OK : fail_hip(e, "hipGraphExecDestroy");
 }
 
-int d2sd_cascade_plan(const d2sd_cascade_plan_desc* desc, int32_t* host_plan, size_t host_plan_ints,
-                      d2sd_cascade_plan_info* info) {
+// one_wave: the drop-in runner's in-place plans (local_merge_cascade), whose
+// suffix items run as one-wave workgroups of 32 rows (waves_per_block 1,
+// which the public entry point does not accept: only the in-place kind has
+// that shape)
+static int cascade_plan_impl(const d2sd_cascade_plan_desc* desc, int32_t* host_plan, size_t host_plan_ints,
+                             d2sd_cascade_plan_info* info, bool one_wave) {
   g_last_error.clear();
   if (!desc || !info) return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: null desc/info");
   if (int rc = check_heads(desc->num_qo_heads, desc->num_kv_heads, desc->head_dim)) return rc;
@@ -304,7 +308,7 @@ int d2sd_cascade_plan(const d2sd_cascade_plan_desc* desc, int32_t* host_plan, si
   if (desc->kv_dtype != D2SD_KV_BF16 && desc->kv_dtype != D2SD_KV_FP8_E4M3)
     return fail(D2SD_ERR_UNSUPPORTED, "cascade_plan: kv_dtype");
   if (desc->waves_per_block != 0 && desc->waves_per_block != 2 && desc->waves_per_block != 4 &&
-      desc->waves_per_block != 8)
+      desc->waves_per_block != 8 && !(one_wave && desc->waves_per_block == 1))
     return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: waves_per_block must be 0, 2, 4 or 8");
   if (desc->qo_indptr[0] != 0) return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: qo_indptr[0] must be 0");
   for (int r = 0; r < desc->num_reqs; ++r) {
@@ -420,12 +424,19 @@ int d2sd_cascade_plan(const d2sd_cascade_plan_desc* desc, int32_t* host_plan, si
   return D2SD_OK;
 }
 
+int d2sd_cascade_plan(const d2sd_cascade_plan_desc* desc, int32_t* host_plan, size_t host_plan_ints,
+                      d2sd_cascade_plan_info* info) {
+  return cascade_plan_impl(desc, host_plan, host_plan_ints, info, false);
+}
+
+// one_wave: the drop-in runner's in-place plans (one-wave workgroups)
 static int build_verify_params(const d2sd_cascade_plan_info* info, const d2sd_cascade_run_args* a,
-                               d2sd::VerifyParams& p) {
+                               d2sd::VerifyParams& p, bool one_wave = false) {
   if (!info || !a) return fail(D2SD_ERR_INVALID_ARG, "cascade_run: null info/args");
   const int D = info->head_dim;
   if (int rc = check_heads(info->num_qo_heads, info->num_kv_heads, D)) return rc;
-  if ((info->waves_per_block != 2 && info->waves_per_block != 4 && info->waves_per_block != 8) ||
+  if ((info->waves_per_block != 2 && info->waves_per_block != 4 && info->waves_per_block != 8 &&
+       !(one_wave && info->waves_per_block == 1)) ||
       info->rows_per_tile != d2sd::verify_rows(info->waves_per_block))
     return fail(D2SD_ERR_INVALID_ARG, "cascade_run: info does not come from d2sd_cascade_plan");
   if (!a->plan || !a->q || !a->k_suffix || !a->v_suffix || !a->out)
@@ -815,13 +826,15 @@ static int local_merge_cascade(const void* q, int64_t q_stride_b, int64_t q_stri
       desc.head_dim = d;
       desc.window_left = -1;
       desc.kv_dtype = D2SD_KV_BF16;
-      desc.waves_per_block = 4;  // the in-place kernel's one shape
+      // one-wave workgroups of 32 rows: four times the workgroups of a
+      // 128-row tile, each loading a quarter of the stored output and Q
+      desc.waves_per_block = 1;
       const std::string saved = g_last_error;
       std::vector<int32_t> host;
-      bool ok = d2sd_cascade_plan(&desc, nullptr, 0, &sp.info) == D2SD_OK;
+      bool ok = cascade_plan_impl(&desc, nullptr, 0, &sp.info, true) == D2SD_OK;
       if (ok) {
         host.assign((size_t)sp.info.plan_ints, 0);
-        ok = d2sd_cascade_plan(&desc, host.data(), host.size(), &sp.info) == D2SD_OK;
+        ok = cascade_plan_impl(&desc, host.data(), host.size(), &sp.info, true) == D2SD_OK;
       }
       g_last_error = saved;
       if (!ok || sp.info.num_merges != 0 || sp.info.num_slots != 0) return D2SD_OK;
@@ -854,7 +867,7 @@ static int local_merge_cascade(const void* q, int64_t q_stride_b, int64_t q_stri
   a.sinks = sinks;
   a.lse_base2 = lse_base2;
   d2sd::VerifyParams p{};
-  if (int rc = build_verify_params(&sp.info, &a, p)) return rc;
+  if (int rc = build_verify_params(&sp.info, &a, p, true)) return rc;
   hipError_t e = d2sd::launch_verify_attention(p, d, sp.info.waves_per_block, false, false, d2sd::KIND_INPLACE,
                                                sp.info.num_items, stream);
   if (e != hipSuccess) return fail_hip(e, "local_attention_merge launch");

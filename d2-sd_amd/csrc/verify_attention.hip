@@ -54,11 +54,15 @@ namespace d2sd {
 template <int D, int WPB>
 struct RingCfg;
 template <>
+struct RingCfg<128, 1> { static constexpr int KST = 3, VST = 2, NPG = 0; };  // 80 KB
+template <>
 struct RingCfg<128, 2> { static constexpr int KST = 3, VST = 2, NPG = 0; };  // 80 KB
 template <>
 struct RingCfg<128, 4> { static constexpr int KST = 3, VST = 2, NPG = 0; };  // 80 KB
 template <>
 struct RingCfg<128, 8> { static constexpr int KST = 4, VST = 3, NPG = kMaxStagedPages; };  // 116 KB
+template <>
+struct RingCfg<64, 1> { static constexpr int KST = 5, VST = 4, NPG = kMaxStagedPages; };  // 76 KB
 template <>
 struct RingCfg<64, 2> { static constexpr int KST = 5, VST = 4, NPG = kMaxStagedPages; };  // 76 KB
 template <>
@@ -1215,6 +1219,8 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
 template <int WPB>
 struct Shape;
 template <>
+struct Shape<1> { static constexpr int W = 1, RB = 1, OCC = 1; };  // the in-place kind's 32-row workgroups
+template <>
 struct Shape<2> { static constexpr int W = 2, RB = 2, OCC = 1; };
 template <>
 struct Shape<4> { static constexpr int W = 4, RB = 1, OCC = 2; };
@@ -1229,9 +1235,9 @@ struct Shape<8> { static constexpr int W = 8, RB = 1, OCC = 2; };
 // (suffix items merging into the stored output: the per-row local level of
 // the drop-in runner), KIND_SEGMENTS (split plans over a two-segment
 // contiguous prefix: SRC_PREFIX, SRC_PREFIX2 and suffix items).
-// The in-place kind serves the drop-in runner's few workgroups (rows x kv
-// heads): one wave per SIMD, so that its state, the stored output and the
-// tree-mask words all stay in registers.
+// The in-place kind serves the drop-in runner's workgroups (rows x kv heads
+// x 32-row blocks, one wave each): one wave per SIMD, so that its state, the
+// stored output and the tree-mask words all stay in registers.
 template <int D, int WPB, bool PAGED, bool FP8, int KIND>
 __global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(KIND == KIND_INPLACE ? 1 : Shape<WPB>::OCC,
                                                                             KIND == KIND_INPLACE ? 1 : Shape<WPB>::OCC)))
@@ -1394,18 +1400,21 @@ static hipError_t launch_verify_k(const VerifyParams& p, bool paged, bool fp8, i
 
 template <int D, int WPB>
 static hipError_t launch_verify_w(const VerifyParams& p, bool paged, bool fp8, int kind, int nitems, hipStream_t s) {
-  if (kind == KIND_FUSED) return launch_verify_k<D, WPB, KIND_FUSED>(p, paged, fp8, nitems, s);
-  // in-place plans read no prefix and are planned with four waves: one instantiation
-  if (kind == KIND_INPLACE) {
-    if constexpr (WPB == 4) return launch_verify_t<D, 4, false, false, KIND_INPLACE>(p, nitems, s);
-    return hipErrorInvalidValue;
+  // in-place plans (the drop-in runner's) read no prefix and are planned with
+  // one wave per workgroup, a shape no other kind has
+  if constexpr (WPB == 1) {
+    return kind == KIND_INPLACE ? launch_verify_t<D, 1, false, false, KIND_INPLACE>(p, nitems, s)
+                                : hipErrorInvalidValue;
+  } else {
+    if (kind == KIND_INPLACE) return hipErrorInvalidValue;
+    if (kind == KIND_FUSED) return launch_verify_k<D, WPB, KIND_FUSED>(p, paged, fp8, nitems, s);
+    // two-segment prefixes are contiguous
+    if (kind == KIND_SEGMENTS)
+      return paged ? hipErrorInvalidValue
+             : fp8 ? launch_verify_t<D, WPB, false, true, KIND_SEGMENTS>(p, nitems, s)
+                   : launch_verify_t<D, WPB, false, false, KIND_SEGMENTS>(p, nitems, s);
+    return launch_verify_k<D, WPB, KIND_SPLIT>(p, paged, fp8, nitems, s);
   }
-  // two-segment prefixes are contiguous
-  if (kind == KIND_SEGMENTS)
-    return paged ? hipErrorInvalidValue
-           : fp8 ? launch_verify_t<D, WPB, false, true, KIND_SEGMENTS>(p, nitems, s)
-                 : launch_verify_t<D, WPB, false, false, KIND_SEGMENTS>(p, nitems, s);
-  return launch_verify_k<D, WPB, KIND_SPLIT>(p, paged, fp8, nitems, s);
 }
 
 hipError_t launch_verify_attention(const VerifyParams& p, int head_dim, int waves, bool paged, bool fp8, int kind,
@@ -1414,10 +1423,12 @@ hipError_t launch_verify_attention(const VerifyParams& p, int head_dim, int wave
   if (kind != KIND_SPLIT && kind != KIND_FUSED && kind != KIND_INPLACE && kind != KIND_SEGMENTS)
     return hipErrorInvalidValue;
   if (head_dim == 128) {
+    if (waves == 1) return launch_verify_w<128, 1>(p, paged, fp8, kind, nitems, s);
     if (waves == 2) return launch_verify_w<128, 2>(p, paged, fp8, kind, nitems, s);
     if (waves == 4) return launch_verify_w<128, 4>(p, paged, fp8, kind, nitems, s);
     if (waves == 8) return launch_verify_w<128, 8>(p, paged, fp8, kind, nitems, s);
   } else if (head_dim == 64) {
+    if (waves == 1) return launch_verify_w<64, 1>(p, paged, fp8, kind, nitems, s);
     if (waves == 2) return launch_verify_w<64, 2>(p, paged, fp8, kind, nitems, s);
     if (waves == 4) return launch_verify_w<64, 4>(p, paged, fp8, kind, nitems, s);
     if (waves == 8) return launch_verify_w<64, 8>(p, paged, fp8, kind, nitems, s);
