@@ -352,7 +352,6 @@ static int cascade_plan_impl(const d2sd_cascade_plan_desc* desc, int32_t* host_p
   in.page_size = desc->page_size;
   in.prefix_split = desc->prefix_split;
   in.prefix2_tok_indptr = desc->prefix2_tok_indptr;
-  in.dynamic = desc->dynamic_prefix;
   if (desc->dynamic_prefix != 0 && desc->dynamic_prefix != 1)
     return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: dynamic_prefix must be 0 or 1");
   if (desc->window_left < -1) return fail(D2SD_ERR_INVALID_ARG, "cascade_plan: window_left must be >= -1");

@@ -101,7 +101,7 @@ struct Piece {            // the q-tiles of one (request, kv head) over prefix t
 struct PlanItem {
   VerifyItem w;
   int cost;               // in prefix-tile units
-  int c = -1;             // dynamic plans: the chunk's index among its group's chunks (else -1)
+  int c = -1;             // a whole-prefix chunk's index among its group's chunks (else -1)
 };
 
 int ceil_div(long long a, long long b) { return (int)((a + b - 1) / b); }

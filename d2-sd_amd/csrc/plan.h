@@ -30,10 +30,6 @@ struct VerifyPlanInput {
   // prefix2_tok_indptr[r] + key - prefix_split[r]; nullable => 0).
   const int* prefix_split;
   const int* prefix2_tok_indptr;
-  // 1: run-time prefix lengths up to prefix_len (a dynamic plan; the chunks of
-  // a request's whole visible prefix are re-partitioned on the device by their
-  // VerifyItem::chunk, dyn_chunk_start)
-  int dynamic;
 };
 
 struct VerifyPlanOutput {

@@ -52,7 +52,6 @@ int main(int argc, char** argv) {
     in.page_size = page;
     in.prefix_split = two ? sp.data() : nullptr;
     in.prefix2_tok_indptr = two && U(0, 1) ? t2.data() : nullptr;
-    in.dynamic = !two && U(0, 1);
     VerifyPlanOutput out{};
     plan_verify(in, out);
     fused_plans += out.fused;
