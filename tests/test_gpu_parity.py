@@ -181,6 +181,8 @@ def test_reference_row_flow(bsz, causal, with_sinks):
     (4, 32, 64, 8, 64, False, True, False),   # GPT-OSS heads: 256 rows per (row, kv head), two q-tiles
     (3, 20, 32, 8, 128, True, False, True),   # 80 rows: a partial 32-row block, rows past the group's end
     (2, 24, 16, 2, 128, True, True, False),   # 8 query heads per kv head at D = 128: 192 rows
+    (2, 100, 32, 8, 128, True, False, False),  # two key tiles per row (the second of 36 keys)
+    (2, 90, 64, 8, 64, False, True, True),     # two key tiles, the second a half tile (26 keys), D = 64
 ])
 def test_local_attention_merge_in_place(bsz, lb, hq, hkv, d, causal, with_sinks, base2):
     """The in-place kind that serves the drop-in runner (model/cascade_graph.py:
