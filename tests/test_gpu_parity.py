@@ -448,14 +448,16 @@ def test_run_rejects_a_prefix_the_plan_overruns(paged):
     _check_problem(mp, [(o, lse)], tag="overrun")
 
 
-@pytest.mark.parametrize("paged,window", [(True, -1), (True, 300), (False, -1)])
-def test_dynamic_prefix_at_every_length(paged, window):
+@pytest.mark.parametrize("paged,window,hkv", [(True, -1, 8), (True, 300, 8), (False, -1, 8), (True, -1, 2)])
+def test_dynamic_prefix_at_every_length(paged, window, hkv):
     """One dynamic-prefix plan (planned for prefixes 3000 and 700) run at
     shorter and ragged lengths, empty included: each request against the
-    oracle at its run-time length (the planned chunks are scaled to it)."""
+    oracle at its run-time length (each group's chunks re-partitioned at it;
+    with 2 kv heads, fewer than 8 (request, kv head) sets, the prefix is cut
+    into pieces whose planned boundaries are scaled instead)."""
     rng = np.random.default_rng(5)
     reqs = [wl.Request(wl.random_branch_tree(rng, 4, 16), 3000), wl.Request(wl.random_branch_tree(rng, 2, 16), 700)]
-    prob = wl.VerifyProblem("dyn", 32, 8, 128, reqs, page_size=16 if paged else 0, window_left=window, seed=9)
+    prob = wl.VerifyProblem("dyn", 32, hkv, 128, reqs, page_size=16 if paged else 0, window_left=window, seed=9)
     mp = wl.materialize(prob, DEV, layers=1)
     attn = d2sd.CascadeVerifyAttention(DEV)
     wl.plan_for(attn, mp, dynamic_prefix=True)
