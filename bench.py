@@ -79,9 +79,10 @@ def time_graph(graph, reps: int, torch) -> float:
 
 
 def cpu_threads() -> dict:
-    """Host threads for the CPU baseline: os.cpu_count() (BASELINE.md's
-    recipe), bounded by the process's CPU affinity and by OMP_NUM_THREADS when
-    the environment sets it (a GPU box grants a share of its host cores)."""
+    """Host threads for the CPU baseline: os.cpu_count() (the baseline
+    recipe: torch on every host core), bounded by the process's CPU affinity
+    and by OMP_NUM_THREADS when the environment sets it (a host may grant a
+    share of its cores)."""
     count = os.cpu_count() or 1
     try:
         affinity = len(os.sched_getaffinity(0))
