@@ -834,8 +834,12 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
         issue_v(0, pg0);
       }
       if (1 < ntiles) issue_k(1, wave_page(1));
-      // Q and K(0) have landed once at most V(0) and K(1) are outstanding
-      wait_vmcnt_units<IPW, 2>((0 < ntiles ? 1 : 0) + (1 < ntiles ? 1 : 0));
+      // two-tile ranges (a 128-key window) whose Q staging leaves the V ring
+      // free: V(1) goes out now, after K(1), instead of after the Q fragments
+      const bool early_v1 = W * QB <= FREE1 && ntiles == 2;
+      if (early_v1) issue_v(1, wave_page(1));
+      // Q and K(0) have landed once at most V(0), K(1) (and V(1)) are outstanding
+      wait_vmcnt_units<IPW, 3>((0 < ntiles ? 1 : 0) + (1 < ntiles ? 1 : 0) + (early_v1 ? 1 : 0));
       __builtin_amdgcn_s_barrier();  // every wave's share of K(0) is visible
       if (ntiles > 0) {
         const lds_char* qs = (const lds_char*)(uintptr_t)qdst;
@@ -855,7 +859,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& p, const VerifyI
       if (2 < ntiles) issue_k(2, wave_page(2));
       static_for<VST - 2>([&](auto j) {
         constexpr int st = decltype(j)::value - (VST - 2);
-        if (st + VST - 1 < ntiles) issue_v(st + VST - 1, wave_page(st + VST - 1));
+        if (st + VST - 1 < ntiles && !(early_v1 && st + VST - 1 == 1)) issue_v(st + VST - 1, wave_page(st + VST - 1));
         if (st + KST < ntiles) issue_k(st + KST, wave_page(st + KST));
       });
       auto pv_next = wave_page(VST - 1), pk_next = wave_page(KST);
