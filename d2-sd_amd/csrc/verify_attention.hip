@@ -66,7 +66,7 @@ struct RingCfg<64, 1> { static constexpr int KST = 5, VST = 4, NPG = kMaxStagedP
 template <>
 struct RingCfg<64, 2> { static constexpr int KST = 5, VST = 4, NPG = kMaxStagedPages; };  // 76 KB
 template <>
-struct RingCfg<64, 4> { static constexpr int KST = 5, VST = 4, NPG = kMaxStagedPages; };  // 76 KB
+struct RingCfg<64, 4> { static constexpr int KST = 5, VST = 4, NPG = 0; };  // 76 KB (page ids by scalar loads)
 template <>
 struct RingCfg<64, 8> { static constexpr int KST = 6, VST = 5, NPG = kMaxStagedPages; };  // 92 KB
 
