@@ -88,7 +88,10 @@ int verify_auto_waves(const VerifyPlanInput& in, int num_cus) {
 // Balance.  Per XCD the prefix chunks are sized to fill its workgroup slots
 // (CUs per XCD x workgroups per CU) after the suffix items: the largest chunk
 // T is the smallest that fits, then the remaining slots split the groups whose
-// chunks are longest.  With one or two rounds of workgroups per XCD, the
+// chunks are longest.  Where one workgroup per CU (the suffix items paired
+// with each other) needs chunks less than 1.6x as long, the chunks are sized
+// for that instead: a lone workgroup steps through tiles faster than two that
+// share a CU.  With one or two rounds of workgroups per XCD, the
 // longest items run alone and the rest are paired longest-with-shortest on a
 // CU; beyond two rounds items go longest first.
 namespace {
@@ -200,19 +203,39 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
       }
     }
     if (cells.empty()) continue;
-    const long long budget = std::max<long long>((long long)xcd_slots - suffix_items, (long long)cells.size());
     int maxpt = 1, tmin = 1;
     for (auto& c : cells) {
       maxpt = std::max(maxpt, c.pt);
       tmin = std::max(tmin, ceil_div(c.pt, c.cap));
     }
-    int T = std::max(tmin, std::min(kMinChunk, maxpt));
     auto count = [&](int t) {
       long long n = 0;
       for (auto& c : cells) n += ceil_div(c.pt, t);
       return n;
     };
-    while (T < maxpt && count(T) > budget) ++T;
+    // the longest chunk that fits `slots` items
+    auto chunk_len = [&](long long slots) {
+      int t = std::max(tmin, std::min(kMinChunk, maxpt));
+      while (t < maxpt && count(t) > slots) ++t;
+      return t;
+    };
+    long long budget = std::max<long long>((long long)xcd_slots - suffix_items, (long long)cells.size());
+    int T = chunk_len(budget);
+    if (wpc == 2) {
+      // One workgroup per CU (the suffix items paired with each other)
+      // instead of two: a tile step of a CU's lone workgroup takes about
+      // 0.55 of a step shared by two (measured on MI355X: 4096 keys, 96
+      // nodes, 24 q-tile groups: chunks of 7 tiles alone 12.3 us per
+      // attention launch against 4-5 tiles paired 13.2 us), so the longer
+      // chunks of the lone plan win below 1.6 x the paired length.
+      const long long alone = std::max<long long>((long long)cus_per_xcd - (suffix_items + 1) / 2,
+                                                  (long long)cells.size());
+      const int Ta = chunk_len(alone);
+      if (5 * Ta < 8 * T) {
+        budget = alone;
+        T = Ta;
+      }
+    }
     T = std::min(T, max_chunk);
     long long used = 0;
     std::vector<int> n(cells.size());

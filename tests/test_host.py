@@ -300,6 +300,33 @@ def test_plan_numbers_chunks_first_round_first(qo, pl, window):
         assert rounds == sorted(rounds)
 
 
+@pytest.mark.parametrize("nodes,lone", [(96, True), (150, False)])
+def test_plan_lone_workgroups_where_chunks_stay_short(nodes, lone):
+    """Prefix 4096 keys (64 tiles), 24 or 40 q-tile groups.  Where one
+    workgroup per CU keeps the longest prefix chunk under 1.6x the chunk that
+    two workgroups per CU would need, the plan leaves each CU one workgroup:
+    96 nodes get 10 chunks of 6-7 tiles per group on 33 items per XCD, whose
+    one CU pair holds two suffix items.  Otherwise every CU runs two
+    workgroups: 150 nodes get 12 chunks of 5-6 tiles, 64 items per XCD."""
+    info, items, _ = _plan([0, nodes], [4096])
+    its = items.tolist()
+    K = 256 // 8
+    per_xcd = [0] * 8
+    for i, it in enumerate(its):
+        if it[MODE] != MODE_NOOP:
+            per_xcd[i % 8] += 1
+    chunks = [it for it in its if it[MODE] != MODE_NOOP and it[SRC] != SRC_SUFFIX]
+    longest = max(-(-(it[KE] - it[KB]) // 64) for it in chunks)
+    # workgroup i runs on XCD i % 8; i and i + 8K share a CU
+    pairs = [(it[SRC], its[i - 8 * K][SRC]) for i, it in enumerate(its) if i // 8 >= K and it[MODE] != MODE_NOOP]
+    if lone:
+        assert per_xcd == [K + 1] * 8 and longest == 7 and len(chunks) == 24 * 10
+        assert pairs == [(SRC_SUFFIX, SRC_SUFFIX)] * 8
+    else:
+        assert per_xcd == [2 * K] * 8 and longest == 6
+        assert any(a == SRC_PREFIX and b == SRC_PREFIX for a, b in pairs)
+
+
 def test_plan_rejects_bad_two_segment_prefixes():
     """A second segment needs a contiguous first one and a static plan, and
     each split must lie in [0, prefix_len]."""
