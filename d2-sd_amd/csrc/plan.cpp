@@ -88,10 +88,10 @@ int verify_auto_waves(const VerifyPlanInput& in, int num_cus) {
 // Balance.  Per XCD the prefix chunks are sized to fill its workgroup slots
 // (CUs per XCD x workgroups per CU) after the suffix items: the largest chunk
 // T is the smallest that fits, then the remaining slots split the groups whose
-// chunks are longest.  Where one workgroup per CU (the suffix items paired
-// with each other) needs chunks less than 1.6x as long, the chunks are sized
-// for that instead: a lone workgroup steps through tiles faster than two that
-// share a CU.  With one or two rounds of workgroups per XCD, the
+// chunks are longest.  Where those chunks are at least 4 tiles long and one
+// workgroup per CU (the suffix items paired with each other) needs chunks
+// less than 1.6x as long, the chunks are sized for that instead: a lone
+// workgroup steps through tiles faster than two that share a CU.  With one or two rounds of workgroups per XCD, the
 // longest items run alone and the rest are paired longest-with-shortest on a
 // CU; beyond two rounds items go longest first.
 namespace {
@@ -221,13 +221,16 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
     };
     long long budget = std::max<long long>((long long)xcd_slots - suffix_items, (long long)cells.size());
     int T = chunk_len(budget);
-    if (wpc == 2) {
+    if (wpc == 2 && T >= 4) {
       // One workgroup per CU (the suffix items paired with each other)
       // instead of two: a tile step of a CU's lone workgroup takes about
-      // 0.55 of a step shared by two (measured on MI355X: 4096 keys, 96
-      // nodes, 24 q-tile groups: chunks of 7 tiles alone 12.3 us per
-      // attention launch against 4-5 tiles paired 13.2 us), so the longer
-      // chunks of the lone plan win below 1.6 x the paired length.
+      // 0.55 of a step shared by two, so the longer chunks of the lone plan
+      // win below 1.6x the paired length.  Measured on MI355X, 96 nodes, 24
+      // q-tile groups: 4096 keys, 7 tiles alone 12.3 us per attention launch
+      // against 4-5 paired 13.2 us; 8192 keys, 13 alone 20.6 us against 9
+      // paired 22.0 us.  Below 4 tiles per paired chunk the per-item fixed
+      // cost, which two workgroups of a CU overlap, dominates (2048 keys: 3
+      // paired 14.5 us per call against 4 alone 14.9 us).
       const long long alone = std::max<long long>((long long)cus_per_xcd - (suffix_items + 1) / 2,
                                                   (long long)cells.size());
       const int Ta = chunk_len(alone);

@@ -300,15 +300,17 @@ def test_plan_numbers_chunks_first_round_first(qo, pl, window):
         assert rounds == sorted(rounds)
 
 
-@pytest.mark.parametrize("nodes,lone", [(96, True), (150, False)])
-def test_plan_lone_workgroups_where_chunks_stay_short(nodes, lone):
-    """Prefix 4096 keys (64 tiles), 24 or 40 q-tile groups.  Where one
-    workgroup per CU keeps the longest prefix chunk under 1.6x the chunk that
-    two workgroups per CU would need, the plan leaves each CU one workgroup:
-    96 nodes get 10 chunks of 6-7 tiles per group on 33 items per XCD, whose
-    one CU pair holds two suffix items.  Otherwise every CU runs two
-    workgroups: 150 nodes get 12 chunks of 5-6 tiles, 64 items per XCD."""
-    info, items, _ = _plan([0, nodes], [4096])
+@pytest.mark.parametrize("nodes,L,lone,longest_tiles", [(96, 4096, True, 7), (150, 4096, False, 6),
+                                                          (96, 2048, False, 3), (96, 8192, True, 13)])
+def test_plan_lone_workgroups_where_chunks_stay_short(nodes, L, lone, longest_tiles):
+    """24 or 40 q-tile groups.  Where paired chunks would be at least 4 tiles
+    and one workgroup per CU keeps the longest prefix chunk under 1.6x that
+    length, the plan leaves each CU one workgroup: 96 nodes at 4096 keys get
+    10 chunks of 6-7 tiles per group on 33 items per XCD, whose one CU pair
+    holds two suffix items.  Otherwise CUs run two workgroups: 150 nodes get
+    12 chunks of 5-6 tiles, 64 items per XCD; 96 nodes at 2048 keys keep 15
+    chunks of 2-3 tiles (the per-item fixed cost dominates there)."""
+    info, items, _ = _plan([0, nodes], [L])
     its = items.tolist()
     K = 256 // 8
     per_xcd = [0] * 8
@@ -319,11 +321,12 @@ def test_plan_lone_workgroups_where_chunks_stay_short(nodes, lone):
     longest = max(-(-(it[KE] - it[KB]) // 64) for it in chunks)
     # workgroup i runs on XCD i % 8; i and i + 8K share a CU
     pairs = [(it[SRC], its[i - 8 * K][SRC]) for i, it in enumerate(its) if i // 8 >= K and it[MODE] != MODE_NOOP]
+    assert longest == longest_tiles
     if lone:
-        assert per_xcd == [K + 1] * 8 and longest == 7 and len(chunks) == 24 * 10
+        assert per_xcd == [K + 1] * 8 and len(chunks) == 24 * 10
         assert pairs == [(SRC_SUFFIX, SRC_SUFFIX)] * 8
     else:
-        assert per_xcd == [2 * K] * 8 and longest == 6
+        assert min(per_xcd) > K + 1
         assert any(a == SRC_PREFIX and b == SRC_PREFIX for a, b in pairs)
 
 
