@@ -223,14 +223,16 @@ int plan_verify(const VerifyPlanInput& in, VerifyPlanOutput& out) {
     int T = chunk_len(budget);
     if (wpc == 2 && T >= 4) {
       // One workgroup per CU (the suffix items paired with each other)
-      // instead of two: a tile step of a CU's lone workgroup takes about
-      // 0.55 of a step shared by two, so the longer chunks of the lone plan
-      // win below 1.6x the paired length.  Measured on MI355X, 96 nodes, 24
+      // instead of two: a lone workgroup steps through a tile in about 1.45
+      // us, each of two sharing a CU in 1.8-2.0 us, so the lone plan's
+      // longer chunks can end first.  Measured on MI355X, 96 nodes, 24
       // q-tile groups: 4096 keys, 7 tiles alone 12.3 us per attention launch
-      // against 4-5 paired 13.2 us; 8192 keys, 13 alone 20.6 us against 9
-      // paired 22.0 us.  Below 4 tiles per paired chunk the per-item fixed
-      // cost, which two workgroups of a CU overlap, dominates (2048 keys: 3
-      // paired 14.5 us per call against 4 alone 14.9 us).
+      // against 4-5 paired 13.2 us (1.4x the length); 8192 keys, 13 alone
+      // 20.6 us against 9 paired 22.0 us (1.44x); at 2x and 2.2x (128 and
+      // 150 nodes) the lone plan lost, so the bound is 1.6x.  Below 4 tiles
+      // per paired chunk the per-item fixed cost, which two workgroups of a
+      // CU overlap, dominates (2048 keys: 3 paired 14.5 us per call against
+      // 4 alone 14.9 us).
       const long long alone = std::max<long long>((long long)cus_per_xcd - (suffix_items + 1) / 2,
                                                   (long long)cells.size());
       const int Ta = chunk_len(alone);
