@@ -304,6 +304,19 @@ def test_cascade_config2_two_layers():
     _check_problem(mp, outs, tag="cfg2")
 
 
+@pytest.mark.parametrize("L", [4096, 8192])
+def test_cascade_northstar_one_workgroup_per_cu(L):
+    """The north-star tree (a 32-token main row and four 16-token branches,
+    N = 96) over a paged prefix of 4096 and 8192 keys: the plan gives each CU
+    one workgroup (10 prefix chunks per q-tile group, 264 workgroups), and the
+    result matches the oracle."""
+    tree = wl.tree_from_branches(32, [0, 0, 0, 0, 0], [32, 16, 16, 16, 16])
+    prob = wl.VerifyProblem(f"northstar_L{L}", 32, 8, 128, [wl.Request(tree, L)], page_size=16, seed=L)
+    mp, attn, outs = _run_problem(prob)
+    assert attn.info.num_items == 264 and attn.info.max_splits_used == 10
+    _check_problem(mp, outs, dtype=torch.float32, tag=f"northstar L{L}")
+
+
 def test_cascade_config3_subset():
     mp, _, outs = _run_problem(wl.config3(0, num_reqs=8))
     _check_problem(mp, outs, reqs=[0, 5], dtype=torch.float32, tag="cfg3")
